@@ -1,0 +1,496 @@
+// enchip.hip -- libenchip.so: the C ABI declared in include/enchip.h.
+//
+// Context = one device + one HIP stream + registered weights + growable device
+// scratch. Host-pointer entry points are synchronous and serialised by the
+// context mutex; *_dev entry points only enqueue.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "enchip.h"
+#include "kernels.h"
+
+namespace {
+
+constexpr int64_t kMaxK = 131072;  // K*127*127 stays below 2^31: the int32 dot cannot wrap
+constexpr int64_t kRowPad = 256;   // quantized-activation scratch rows are padded to this
+constexpr int64_t kColPad = 256;   // weight output channels are padded to this
+
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+struct Weight {
+    int8_t *d_w = nullptr;  // fragment-major, [Np/32][Kp/32][1024]
+    float *d_s = nullptr;   // [N]
+    int64_t N = 0, K = 0, Np = 0, Kp = 0;
+};
+
+thread_local std::string g_open_error = "no error";
+
+}  // namespace
+
+struct enchip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int num_cus = 0, clock_khz = 0;
+    std::string arch;
+    std::mutex mu;
+    std::string err = "no error";
+    std::unordered_map<uint64_t, Weight> weights;
+    uint64_t next_handle = 1;
+    int64_t small_m = 32;
+    // device scratch (grown on demand, freed by enchip_close)
+    int8_t *d_aq = nullptr;
+    size_t aq_cap = 0;
+    float *d_as = nullptr;
+    size_t as_cap = 0;
+    float *d_a = nullptr;
+    size_t a_cap = 0;
+    float *d_dst = nullptr;
+    size_t dst_cap = 0;
+    float *d_bias = nullptr;
+    size_t bias_cap = 0;
+    int32_t *d_acc = nullptr;
+    size_t acc_cap = 0;
+};
+
+namespace {
+
+int fail(enchip_ctx *c, int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    c->err = buf;
+    return code;
+}
+
+#define HIP_TRY(ctx, expr)                                                                  \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess)                                                               \
+            return fail((ctx), ENCHIP_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+// Grows a device buffer to at least `bytes`. Contents are not preserved.
+template <typename T>
+int ensure(enchip_ctx *c, T **p, size_t *cap, size_t bytes) {
+    if (bytes <= *cap && *p) return ENCHIP_OK;
+    if (*p) {
+        hipError_t e = hipFree(*p);
+        *p = nullptr;
+        *cap = 0;
+        if (e != hipSuccess) return fail(c, ENCHIP_ERR_HIP, "hipFree: %s", hipGetErrorString(e));
+    }
+    size_t want = std::max<size_t>(bytes, 256);
+    hipError_t e = hipMalloc((void **)p, want);
+    if (e != hipSuccess) {
+        *p = nullptr;
+        (void)hipGetLastError();
+        return fail(c, ENCHIP_ERR_OOM, "hipMalloc(%zu): %s", want, hipGetErrorString(e));
+    }
+    *cap = want;
+    return ENCHIP_OK;
+}
+
+int check_launch(enchip_ctx *c, const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(c, ENCHIP_ERR_HIP, "launch %s: %s", what, hipGetErrorString(e));
+    return ENCHIP_OK;
+}
+
+// Quantizes d_a[M,K] into q[M][ldq] (zero-padded to ldq) and scale[M].
+int launch_quant(enchip_ctx *c, const float *d_a, int64_t M, int64_t K, int8_t *q, int64_t ldq,
+                 float *scale, hipStream_t s) {
+    if (M == 0) return ENCHIP_OK;
+    const dim3 grid((unsigned)((M + 3) / 4)), block(256);
+    const bool vec = (K % 4 == 0) && (ldq % 4 == 0) && ((uintptr_t)d_a % 16 == 0) &&
+                     ((uintptr_t)q % 4 == 0) && K > 0 && K <= 256 * 16;
+    if (vec) {
+        const int ch = (int)((K + 255) / 256);
+        const int k = (int)K;
+        switch (ch) {
+#define QCASE(N) \
+    case N: hipLaunchKernelGGL(enchip::quant_rows_vec<N>, grid, block, 0, s, d_a, q, ldq, scale, M, k); break;
+            QCASE(1) QCASE(2) QCASE(3) QCASE(4) QCASE(5) QCASE(6) QCASE(7) QCASE(8)
+            QCASE(9) QCASE(10) QCASE(11) QCASE(12) QCASE(13) QCASE(14) QCASE(15) QCASE(16)
+#undef QCASE
+            default: return fail(c, ENCHIP_ERR_ARG, "quant: bad chunk count %d", ch);
+        }
+    } else {
+        hipLaunchKernelGGL(enchip::quant_rows_scalar, grid, block, 0, s, d_a, q, ldq, scale, M, K);
+    }
+    return check_launch(c, "quant_rows");
+}
+
+template <int BM, int BN, int EPI>
+void launch_gemm_t(const Weight &w, const int8_t *aq, int64_t lda, const float *as, const float *bias,
+                   void *out, int64_t ldo, int64_t M, hipStream_t s) {
+    const int tilesM = (int)((M + BM - 1) / BM), tilesN = (int)((w.N + BN - 1) / BN);
+    hipLaunchKernelGGL((enchip::gemm_w8a8<BM, BN, EPI>), dim3((unsigned)(tilesM * tilesN)), dim3(256), 0,
+                       s, aq, lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp, tilesN);
+}
+
+template <int EPI>
+void launch_gemm_epi(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, const float *as,
+                     const float *bias, void *out, int64_t ldo, int64_t M, hipStream_t s) {
+    if (M <= c->small_m) {
+        hipLaunchKernelGGL((enchip::gemv_w8a8<EPI>), dim3((unsigned)((w.N + 31) / 32)), dim3(256), 0, s, aq,
+                           lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp);
+        return;
+    }
+    // Largest tile that still gives every CU at least one block.
+    auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((w.N + bn - 1) / bn); };
+    if (tiles(256, 128) >= c->num_cus)
+        launch_gemm_t<256, 128, EPI>(w, aq, lda, as, bias, out, ldo, M, s);
+    else if (tiles(128, 128) >= c->num_cus)
+        launch_gemm_t<128, 128, EPI>(w, aq, lda, as, bias, out, ldo, M, s);
+    else
+        launch_gemm_t<128, 64, EPI>(w, aq, lda, as, bias, out, ldo, M, s);
+}
+
+int launch_gemm(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, const float *as,
+                const float *bias, int epi, void *out, int64_t ldo, int64_t M, hipStream_t s) {
+    if (M == 0) return ENCHIP_OK;
+    switch (epi) {
+        case enchip::EPI_I32: launch_gemm_epi<enchip::EPI_I32>(c, w, aq, lda, as, bias, out, ldo, M, s); break;
+        case enchip::EPI_F32: launch_gemm_epi<enchip::EPI_F32>(c, w, aq, lda, as, bias, out, ldo, M, s); break;
+        case enchip::EPI_F32_GELU:
+            launch_gemm_epi<enchip::EPI_F32_GELU>(c, w, aq, lda, as, bias, out, ldo, M, s);
+            break;
+        default: return fail(c, ENCHIP_ERR_ARG, "bad epilogue %d", epi);
+    }
+    return check_launch(c, "gemm_w8a8");
+}
+
+int find_weight(enchip_ctx *c, enchip_weight h, Weight **out) {
+    auto it = c->weights.find(h);
+    if (it == c->weights.end()) return fail(c, ENCHIP_ERR_HANDLE, "unknown weight handle %llu", (unsigned long long)h);
+    *out = &it->second;
+    return ENCHIP_OK;
+}
+
+// Scratch for the quantized activations of M rows at pitch Kp.
+int ensure_act_scratch(enchip_ctx *c, int64_t M, int64_t Kp) {
+    const int64_t Mp = round_up(std::max<int64_t>(M, 1), kRowPad);
+    int rc = ensure(c, &c->d_aq, &c->aq_cap, (size_t)(Mp * Kp));
+    if (rc) return rc;
+    return ensure(c, &c->d_as, &c->as_cap, (size_t)Mp * sizeof(float));
+}
+
+int act_code(int act) {
+    return act == ENCHIP_ACT_GELU ? enchip::EPI_F32_GELU : enchip::EPI_F32;
+}
+
+}  // namespace
+
+extern "C" {
+
+int enchip_abi_version(void) { return ENCHIP_ABI_VERSION; }
+
+const char *enchip_last_error(const enchip_ctx *ctx) {
+    return ctx ? ctx->err.c_str() : g_open_error.c_str();
+}
+
+int enchip_open(int device, enchip_ctx **out) {
+    if (!out) {
+        g_open_error = "enchip_open: out is NULL";
+        return ENCHIP_ERR_ARG;
+    }
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        g_open_error = std::string("enchip_open: no HIP device (") + hipGetErrorString(e) + ")";
+        (void)hipGetLastError();
+        return ENCHIP_ERR_NO_DEVICE;
+    }
+    if (device < 0 || device >= n) {
+        g_open_error = "enchip_open: device index " + std::to_string(device) + " out of range (have " +
+                       std::to_string(n) + ")";
+        return ENCHIP_ERR_NO_DEVICE;
+    }
+    hipDeviceProp_t prop;
+    if ((e = hipSetDevice(device)) != hipSuccess || (e = hipGetDeviceProperties(&prop, device)) != hipSuccess) {
+        g_open_error = std::string("enchip_open: ") + hipGetErrorString(e);
+        return ENCHIP_ERR_HIP;
+    }
+    auto *c = new enchip_ctx();
+    c->device = device;
+    c->num_cus = prop.multiProcessorCount;
+    c->clock_khz = prop.clockRate;
+    c->arch = prop.gcnArchName;
+    if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) {
+        g_open_error = std::string("enchip_open: hipStreamCreate: ") + hipGetErrorString(e);
+        delete c;
+        return ENCHIP_ERR_HIP;
+    }
+    *out = c;
+    return ENCHIP_OK;
+}
+
+int enchip_close(enchip_ctx *ctx) {
+    if (!ctx) return ENCHIP_OK;
+    {
+        std::lock_guard<std::mutex> g(ctx->mu);
+        (void)hipSetDevice(ctx->device);
+        if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+        for (auto &kv : ctx->weights) {
+            (void)hipFree(kv.second.d_w);
+            (void)hipFree(kv.second.d_s);
+        }
+        ctx->weights.clear();
+        void *bufs[] = {ctx->d_aq, ctx->d_as, ctx->d_a, ctx->d_dst, ctx->d_bias, ctx->d_acc};
+        for (void *p : bufs)
+            if (p) (void)hipFree(p);
+        if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    }
+    delete ctx;
+    return ENCHIP_OK;
+}
+
+int enchip_device_info(enchip_ctx *ctx, int *num_cus, int *clock_khz, char *name, int name_len) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    if (num_cus) *num_cus = ctx->num_cus;
+    if (clock_khz) *clock_khz = ctx->clock_khz;
+    if (name && name_len > 0) {
+        std::strncpy(name, ctx->arch.c_str(), (size_t)name_len - 1);
+        name[name_len - 1] = 0;
+    }
+    return ENCHIP_OK;
+}
+
+int enchip_set_small_m(enchip_ctx *ctx, int64_t max_m) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (max_m < 0 || max_m > 32) return fail(ctx, ENCHIP_ERR_ARG, "small_m must be in [0,32], got %lld", (long long)max_m);
+    ctx->small_m = max_m;
+    return ENCHIP_OK;
+}
+
+int enchip_quant_rows_dev(enchip_ctx *ctx, const float *d_a, int64_t M, int64_t K, int8_t *d_aq, int64_t ldq,
+                          float *d_ascale, void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (M < 0 || K < 0 || K > kMaxK || ldq < K || ldq < 1)
+        return fail(ctx, ENCHIP_ERR_ARG, "quant: bad shape M=%lld K=%lld ldq=%lld", (long long)M, (long long)K, (long long)ldq);
+    if (M == 0) return ENCHIP_OK;
+    if ((K > 0 && !d_a) || !d_aq || !d_ascale) return fail(ctx, ENCHIP_ERR_ARG, "quant: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    return launch_quant(ctx, d_a, M, K, d_aq, ldq, d_ascale, s);
+}
+
+int enchip_w8a8_pre_dev(enchip_ctx *ctx, enchip_weight h, const int8_t *d_aq, int64_t ldq, int64_t M,
+                        const float *d_ascale, const float *d_bias, int act, float *d_dst, void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    Weight *w;
+    int rc = find_weight(ctx, h, &w);
+    if (rc) return rc;
+    if (M < 0 || M > ((int64_t)1 << 30)) return fail(ctx, ENCHIP_ERR_ARG, "pre: bad M=%lld", (long long)M);
+    if (ldq % 64 != 0 || ldq < w->Kp)
+        return fail(ctx, ENCHIP_ERR_ARG, "pre: ldq=%lld must be a multiple of 64 and >= %lld", (long long)ldq, (long long)w->Kp);
+    if (act != ENCHIP_ACT_NONE && act != ENCHIP_ACT_GELU) return fail(ctx, ENCHIP_ERR_ARG, "pre: bad act %d", act);
+    if (M == 0) return ENCHIP_OK;
+    if (!d_aq || !d_ascale || !d_dst) return fail(ctx, ENCHIP_ERR_ARG, "pre: null pointer");
+    if ((uintptr_t)d_aq % 16 != 0) return fail(ctx, ENCHIP_ERR_ARG, "pre: d_aq must be 16-byte aligned");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    return launch_gemm(ctx, *w, d_aq, ldq, d_ascale, d_bias, act_code(act), d_dst, w->N, M, s);
+}
+
+int enchip_quant_rows(enchip_ctx *ctx, const float *a, int64_t M, int64_t K, int8_t *aq, float *ascale) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (M < 0 || K < 0 || K > kMaxK) return fail(ctx, ENCHIP_ERR_ARG, "quant: bad shape M=%lld K=%lld", (long long)M, (long long)K);
+    if (M == 0) return ENCHIP_OK;
+    if (!aq || !ascale || (K > 0 && !a)) return fail(ctx, ENCHIP_ERR_ARG, "quant: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    int rc;
+    const int64_t ldq = std::max<int64_t>(K, 1);
+    if ((rc = ensure(ctx, &ctx->d_a, &ctx->a_cap, (size_t)(M * K) * sizeof(float)))) return rc;
+    if ((rc = ensure(ctx, &ctx->d_aq, &ctx->aq_cap, (size_t)(M * ldq)))) return rc;
+    if ((rc = ensure(ctx, &ctx->d_as, &ctx->as_cap, (size_t)M * sizeof(float)))) return rc;
+    if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, ldq, ctx->d_as, ctx->stream))) return rc;
+    if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(aq, ctx->d_aq, (size_t)(M * K), hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(ctx, hipMemcpyAsync(ascale, ctx->d_as, (size_t)M * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return ENCHIP_OK;
+}
+
+int enchip_weight_register(enchip_ctx *ctx, const int8_t *wq, const float *wscale, int64_t N, int64_t K,
+                           enchip_weight *out) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (!out) return fail(ctx, ENCHIP_ERR_ARG, "weight_register: out is NULL");
+    *out = 0;
+    if (N <= 0 || K < 0 || K > kMaxK || N > (int64_t)1 << 30)
+        return fail(ctx, ENCHIP_ERR_ARG, "weight_register: bad shape N=%lld K=%lld", (long long)N, (long long)K);
+    if ((K > 0 && !wq) || !wscale) return fail(ctx, ENCHIP_ERR_ARG, "weight_register: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    Weight w;
+    w.N = N;
+    w.K = K;
+    w.Np = round_up(N, kColPad);
+    w.Kp = round_up(std::max<int64_t>(K, 1), 64);
+    // Pre-swizzle on the host into the fragment-major MFMA operand layout.
+    const int64_t nk32 = w.Kp / 32;
+    std::vector<int8_t> frag((size_t)(w.Np * w.Kp), 0);
+    for (int64_t n = 0; n < N; ++n) {
+        const int8_t *src = wq + n * K;
+        const int64_t nb = n >> 5, nl = n & 31;
+        for (int64_t k = 0; k < K; ++k) {
+            const int64_t kb = k >> 5, kh = (k >> 4) & 1, j = k & 15;
+            frag[(size_t)((nb * nk32 + kb) * 1024 + (nl + 32 * kh) * 16 + j)] = src[k];
+        }
+    }
+    int rc;
+    size_t wcap = 0, scap = 0;
+    if ((rc = ensure(ctx, &w.d_w, &wcap, frag.size()))) return rc;
+    if ((rc = ensure(ctx, &w.d_s, &scap, (size_t)N * sizeof(float)))) {
+        (void)hipFree(w.d_w);
+        return rc;
+    }
+    hipError_t e1 = hipMemcpy(w.d_w, frag.data(), frag.size(), hipMemcpyHostToDevice);
+    hipError_t e2 = hipMemcpy(w.d_s, wscale, (size_t)N * sizeof(float), hipMemcpyHostToDevice);
+    if (e1 != hipSuccess || e2 != hipSuccess) {
+        (void)hipFree(w.d_w);
+        (void)hipFree(w.d_s);
+        return fail(ctx, ENCHIP_ERR_HIP, "weight upload: %s", hipGetErrorString(e1 != hipSuccess ? e1 : e2));
+    }
+    const uint64_t h = ctx->next_handle++;
+    ctx->weights[h] = w;
+    *out = h;
+    return ENCHIP_OK;
+}
+
+int enchip_weight_release(enchip_ctx *ctx, enchip_weight h) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    Weight *w;
+    int rc = find_weight(ctx, h, &w);
+    if (rc) return rc;
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    (void)hipFree(w->d_w);
+    (void)hipFree(w->d_s);
+    ctx->weights.erase(h);
+    return ENCHIP_OK;
+}
+
+int enchip_weight_shape(enchip_ctx *ctx, enchip_weight h, int64_t *N, int64_t *K) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    Weight *w;
+    int rc = find_weight(ctx, h, &w);
+    if (rc) return rc;
+    if (N) *N = w->N;
+    if (K) *K = w->K;
+    return ENCHIP_OK;
+}
+
+int enchip_w8a8_linear_dev(enchip_ctx *ctx, enchip_weight h, const float *d_a, int64_t M, const float *d_bias,
+                           int act, float *d_dst, void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    Weight *w;
+    int rc = find_weight(ctx, h, &w);
+    if (rc) return rc;
+    if (M < 0 || M > ((int64_t)1 << 30)) return fail(ctx, ENCHIP_ERR_ARG, "linear: bad M=%lld", (long long)M);
+    if (act != ENCHIP_ACT_NONE && act != ENCHIP_ACT_GELU) return fail(ctx, ENCHIP_ERR_ARG, "linear: bad act %d", act);
+    if (M == 0) return ENCHIP_OK;
+    if ((w->K > 0 && !d_a) || !d_dst) return fail(ctx, ENCHIP_ERR_ARG, "linear: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    if ((rc = ensure_act_scratch(ctx, M, w->Kp))) return rc;
+    if ((rc = launch_quant(ctx, d_a, M, w->K, ctx->d_aq, w->Kp, ctx->d_as, s))) return rc;
+    return launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, d_bias, act_code(act), d_dst, w->N, M, s);
+}
+
+int enchip_w8a8_linear(enchip_ctx *ctx, enchip_weight h, const float *a, int64_t M, const float *bias, int act,
+                       float *dst, int32_t *acc_debug) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    Weight *w;
+    int rc = find_weight(ctx, h, &w);
+    if (rc) return rc;
+    if (M < 0 || M > ((int64_t)1 << 30)) return fail(ctx, ENCHIP_ERR_ARG, "linear: bad M=%lld", (long long)M);
+    if (act != ENCHIP_ACT_NONE && act != ENCHIP_ACT_GELU) return fail(ctx, ENCHIP_ERR_ARG, "linear: bad act %d", act);
+    if (M == 0) return ENCHIP_OK;
+    if ((w->K > 0 && !a) || !dst) return fail(ctx, ENCHIP_ERR_ARG, "linear: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    const int64_t K = w->K, N = w->N;
+    const size_t out_bytes = (size_t)(M * N) * sizeof(float);
+    if ((rc = ensure(ctx, &ctx->d_a, &ctx->a_cap, (size_t)(M * K) * sizeof(float)))) return rc;
+    if ((rc = ensure(ctx, &ctx->d_dst, &ctx->dst_cap, out_bytes))) return rc;
+    if ((rc = ensure_act_scratch(ctx, M, w->Kp))) return rc;
+    if (bias && (rc = ensure(ctx, &ctx->d_bias, &ctx->bias_cap, (size_t)N * sizeof(float)))) return rc;
+    if (acc_debug && (rc = ensure(ctx, &ctx->d_acc, &ctx->acc_cap, out_bytes))) return rc;
+    hipStream_t s = ctx->stream;
+    if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
+    if (bias) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_bias, bias, (size_t)N * sizeof(float), hipMemcpyHostToDevice, s));
+    if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, w->Kp, ctx->d_as, s))) return rc;
+    if ((rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, bias ? ctx->d_bias : nullptr, act_code(act),
+                          ctx->d_dst, N, M, s)))
+        return rc;
+    if (acc_debug &&
+        (rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, nullptr, enchip::EPI_I32, ctx->d_acc, N, M, s)))
+        return rc;
+    HIP_TRY(ctx, hipMemcpyAsync(dst, ctx->d_dst, out_bytes, hipMemcpyDeviceToHost, s));
+    if (acc_debug) HIP_TRY(ctx, hipMemcpyAsync(acc_debug, ctx->d_acc, out_bytes, hipMemcpyDeviceToHost, s));
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    return ENCHIP_OK;
+}
+
+int enchip_w8a8_batch(enchip_ctx *ctx, const float *a, int64_t M, int64_t K, const enchip_op *ops, int nops) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (nops < 0 || (nops > 0 && !ops)) return fail(ctx, ENCHIP_ERR_ARG, "batch: bad ops");
+    if (M < 0 || M > ((int64_t)1 << 30) || K < 0) return fail(ctx, ENCHIP_ERR_ARG, "batch: bad shape");
+    // Validate every op before any work (linalg/quant.go:330-339 does the same).
+    std::vector<Weight *> ws((size_t)nops);
+    int64_t maxN = 0;
+    for (int i = 0; i < nops; ++i) {
+        int rc = find_weight(ctx, ops[i].w, &ws[(size_t)i]);
+        if (rc) return rc;
+        if (ws[(size_t)i]->K != K) return fail(ctx, ENCHIP_ERR_ARG, "batch: op %d has K=%lld, want %lld", i, (long long)ws[(size_t)i]->K, (long long)K);
+        if (ops[i].act != ENCHIP_ACT_NONE && ops[i].act != ENCHIP_ACT_GELU) return fail(ctx, ENCHIP_ERR_ARG, "batch: bad act");
+        if (!ops[i].dst) return fail(ctx, ENCHIP_ERR_ARG, "batch: op %d dst is NULL", i);
+        maxN = std::max(maxN, ws[(size_t)i]->N);
+    }
+    if (M == 0 || nops == 0) return ENCHIP_OK;
+    if (K > 0 && !a) return fail(ctx, ENCHIP_ERR_ARG, "batch: a is NULL");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    const int64_t Kp = ws[0]->Kp;
+    int rc;
+    if ((rc = ensure(ctx, &ctx->d_a, &ctx->a_cap, (size_t)(M * K) * sizeof(float)))) return rc;
+    if ((rc = ensure(ctx, &ctx->d_dst, &ctx->dst_cap, (size_t)(M * maxN) * sizeof(float)))) return rc;
+    if ((rc = ensure(ctx, &ctx->d_bias, &ctx->bias_cap, (size_t)maxN * sizeof(float)))) return rc;
+    if ((rc = ensure_act_scratch(ctx, M, Kp))) return rc;
+    hipStream_t s = ctx->stream;
+    if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
+    if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, Kp, ctx->d_as, s))) return rc;
+    for (int i = 0; i < nops; ++i) {
+        const Weight &w = *ws[(size_t)i];
+        if (ops[i].bias)
+            HIP_TRY(ctx, hipMemcpyAsync(ctx->d_bias, ops[i].bias, (size_t)w.N * sizeof(float), hipMemcpyHostToDevice, s));
+        if ((rc = launch_gemm(ctx, w, ctx->d_aq, Kp, ctx->d_as, ops[i].bias ? ctx->d_bias : nullptr,
+                              act_code(ops[i].act), ctx->d_dst, w.N, M, s)))
+            return rc;
+        HIP_TRY(ctx, hipMemcpyAsync(ops[i].dst, ctx->d_dst, (size_t)(M * w.N) * sizeof(float), hipMemcpyDeviceToHost, s));
+        // The next op reuses d_bias / d_dst: wait for this op's download.
+        HIP_TRY(ctx, hipStreamSynchronize(s));
+    }
+    return ENCHIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,79 @@
+// gelu_f32.h -- exact-erf GELU for the fused GEMM epilogue, bit-identical to
+// aikit's linalg.GELUF32 in the default amd64 build.
+//
+// The reference evaluates a fixed sequence of IEEE float32 operations with no
+// multiply-add fusion (linalg/exp.go:81-117 expF32Core, :207-244 ErfF32,
+// :260-263 GELUF32). Reproducing that sequence operation for operation, with
+// contraction disabled, gives the same bits on gfx950: every v_mul/v_add/v_sub
+// rounds to nearest even, and f32 division is compiled to the correctly rounded
+// v_div_scale/v_div_fmas/v_div_fixup sequence. The constants are the same
+// correctly rounded float32 values the Go compiler derives from the untyped
+// constants.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#pragma clang fp contract(off)
+
+namespace enchip {
+
+// linalg/exp.go:81-117 expF32Core. Only reached from the erf tail, where the
+// argument is -x*x with x in [1,4], so k stays in [-24,-1] and the int32
+// conversion is exact.
+__device__ __forceinline__ float exp_f32_core(float x) {
+    float z = x * 1.4426950408889634f;
+    float t = z + 12582912.0f;
+    float kf = t - 12582912.0f;
+    int k = (int)kf;
+    float r = x - kf * 0.693145751953125f - kf * 1.428606820309417e-06f;
+    float p = 1.9875691500e-4f;
+    p = p * r + 1.3981999507e-3f;
+    p = p * r + 8.3334519073e-3f;
+    p = p * r + 4.1665795894e-2f;
+    p = p * r + 1.6666665459e-1f;
+    p = p * r + 5.0000001201e-1f;
+    p = p * r * r + r + 1.0f;
+    int e = k + 127;
+    if (e <= 0) return 0.0f;
+    if (e >= 255) return p * __uint_as_float((unsigned)(e - 1) << 23) * 2.0f;
+    return p * __uint_as_float((unsigned)e << 23);
+}
+
+// linalg/exp.go:207-244 ErfF32.
+__device__ __forceinline__ float erf_f32(float x) {
+    float sign = 1.0f;
+    if (x < 0) {
+        sign = -1.0f;
+        x = -x;
+    }
+    if (x > 4) return sign;
+    if (x < 1) {
+        float z = x * x;
+        float p = 1.3122532963802806e-08f;
+        p = p * z - 1.4503852223150468e-07f;
+        p = p * z + 1.4589169000933706e-06f;
+        p = p * z - 1.3227513227513228e-05f;
+        p = p * z + 1.0683760683760684e-04f;
+        p = p * z - 7.5757575757575758e-04f;
+        p = p * z + 4.6296296296296294e-03f;
+        p = p * z - 2.3809523809523808e-02f;
+        p = p * z + 1.0000000000000001e-01f;
+        p = p * z - 3.3333333333333331e-01f;
+        p = p * z + 1.0f;
+        return sign * 1.1283791670955126f * x * p;
+    }
+    float t = 1.0f / (1.0f + 0.3275911f * x);
+    float p = 1.061405429f;
+    p = p * t - 1.453152027f;
+    p = p * t + 1.421413741f;
+    p = p * t - 0.284496736f;
+    p = p * t + 0.254829592f;
+    return sign * (1.0f - p * t * exp_f32_core(-x * x));
+}
+
+// linalg/exp.go:260-263 GELUF32.
+__device__ __forceinline__ float gelu_f32(float x) {
+    return 0.5f * x * (1.0f + erf_f32(x * 0.7071067811865476f));
+}
+
+}  // namespace enchip

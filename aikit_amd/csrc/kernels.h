@@ -1,0 +1,355 @@
+// kernels.h -- gfx950 kernels of the W8A8 linear path.
+//
+//   quant_rows_vec / quant_rows_scalar  per-token dynamic int8 quantization
+//   gemm_w8a8                           tiled int8 MFMA GEMM + fused dequant epilogue
+//   gemv_w8a8                           small-M (HBM-bound) split-K MFMA variant
+//
+// Data layout in HBM
+//   activations (f32, caller)   a[M][K] row-major
+//   quantized activations       aq[M][lda] int8 row-major, lda a multiple of 64 >= K,
+//                               columns [K,lda) zero (the GEMMs read rows past M as
+//                               row M-1 and never store them)
+//   activation scales           as[Mp] f32
+//   weights (pre-swizzled once) wf[Np/32][Kp/32][64 lanes][16 B] int8 -- one 1 KiB
+//                               "fragment" per 32 output channels x 32 k; lane l holds
+//                               W[n0 + l%32][k0 + 16*(l/32) .. +16], the operand
+//                               layout of v_mfma_i32_32x32x32_i8. Np = roundup(N,256),
+//                               padding rows/columns zero.
+//   weight scales / bias        f32 [N]
+//   output                      dst[M][ldo] f32 (or int32 accumulators in debug mode)
+//
+// Exactness: the int8 products are summed in int32 by the MFMA unit, exactly, in
+// whatever order; the only roundings are the epilogue's, done in the reference's
+// order with contraction disabled (see gelu_f32.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gelu_f32.h"
+
+#pragma clang fp contract(off)
+
+namespace enchip {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+enum Epi { EPI_I32 = 0, EPI_F32 = 1, EPI_F32_GELU = 2 };
+
+// ----------------------------------------------------------------------------
+// Quantization (linalg/quant.go:43-71, activations' all-zero row -> scale 0).
+
+// One code: math.Round(float64(v*inv)) clamped to +-127. v*inv is a single f32
+// multiply; roundf is round-half-away-from-zero like Go's math.Round, and exact
+// for every float32. A NaN (from an Inf or NaN input) converts to 0 as Go's
+// int8(NaN) does on amd64.
+__device__ __forceinline__ int quant_code(float v, float inv) {
+    float x = roundf(v * inv);
+    if (x > 127.0f) x = 127.0f;
+    else if (x < -127.0f) x = -127.0f;
+    return (x == x) ? (int)x : 0;
+}
+
+// Max of |v| ignoring NaN, as the reference's `if v > maxAbs` does.
+__device__ __forceinline__ float absmax_step(float m, float v) {
+    float t = fabsf(v);
+    return t > m ? t : m;
+}
+
+__device__ __forceinline__ float wave_absmax(float m) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        float o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    return m;
+}
+
+// One wavefront per row, 4 rows per 256-thread block. Each lane holds CH float4 of
+// the row in registers (K <= 256*CH, K % 4 == 0, rows 16-byte aligned), so the
+// row is read from HBM exactly once. Codes are written as packed 32-bit words;
+// columns [K, ldq) are zero-filled.
+template <int CH>
+__global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ a,
+                                                      int8_t *__restrict__ q, int64_t ldq,
+                                                      float *__restrict__ scale, int64_t M,
+                                                      int K) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const float4 *src = reinterpret_cast<const float4 *>(a + row * (int64_t)K);
+    const int K4 = K >> 2;
+    float4 v[CH];
+    float m = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int k4 = lane + 64 * c;
+        v[c] = (k4 < K4) ? src[k4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        m = absmax_step(m, v[c].x);
+        m = absmax_step(m, v[c].y);
+        m = absmax_step(m, v[c].z);
+        m = absmax_step(m, v[c].w);
+    }
+    m = wave_absmax(m);
+    int *dst = reinterpret_cast<int *>(q + row * ldq);
+    const int ldq4 = (int)(ldq >> 2);
+    if (m == 0.0f) {
+        for (int k4 = lane; k4 < ldq4; k4 += 64) dst[k4] = 0;
+        if (lane == 0) scale[row] = 0.0f;
+        return;
+    }
+    const float s = m / 127.0f;
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int k4 = lane + 64 * c;
+        if (k4 < K4) {
+            const int c0 = quant_code(v[c].x, inv), c1 = quant_code(v[c].y, inv);
+            const int c2 = quant_code(v[c].z, inv), c3 = quant_code(v[c].w, inv);
+            dst[k4] = (c0 & 0xff) | ((c1 & 0xff) << 8) | ((c2 & 0xff) << 16) | ((int)((unsigned)c3 << 24));
+        }
+    }
+    for (int k4 = K4 + lane; k4 < ldq4; k4 += 64) dst[k4] = 0;
+    if (lane == 0) scale[row] = s;
+}
+
+// Any K and alignment: one wavefront per row, two passes over the row.
+__global__ __launch_bounds__(256) void quant_rows_scalar(const float *__restrict__ a,
+                                                         int8_t *__restrict__ q, int64_t ldq,
+                                                         float *__restrict__ scale, int64_t M,
+                                                         int64_t K) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const float *src = a + row * K;
+    int8_t *dst = q + row * ldq;
+    float m = 0.0f;
+    for (int64_t k = lane; k < K; k += 64) m = absmax_step(m, src[k]);
+    m = wave_absmax(m);
+    if (m == 0.0f) {
+        for (int64_t k = lane; k < ldq; k += 64) dst[k] = 0;
+        if (lane == 0) scale[row] = 0.0f;
+        return;
+    }
+    const float s = m / 127.0f;
+    const float inv = 1.0f / s;
+    for (int64_t k = lane; k < K; k += 64) dst[k] = (int8_t)quant_code(src[k], inv);
+    for (int64_t k = K + lane; k < ldq; k += 64) dst[k] = 0;
+    if (lane == 0) scale[row] = s;
+}
+
+// ----------------------------------------------------------------------------
+// Epilogue of one output element (linalg/quant.go:291-295, encoder/linalg.go:130-140,
+// linalg/exp.go:260-263): float32(acc)*aS*wS left to right, +0 for an all-zero
+// activation row, then the bias as a separate rounding, then GELU.
+template <int EPI>
+__device__ __forceinline__ float epilogue(int acc, float as, float ws, bool has_bias, float b) {
+    float y = (as == 0.0f) ? 0.0f : (float)acc * as * ws;
+    if (has_bias) y = y + b;
+    if (EPI == EPI_F32_GELU) y = gelu_f32(y);
+    return y;
+}
+
+// Row of a 32x32 i32 MFMA accumulator held by lane `lane` in register r.
+__device__ __forceinline__ int acc_row(int r, int lane) {
+    return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+}
+
+// XOR swizzle of the four 16-byte chunks of a 64-byte LDS row of A: any 16
+// consecutive rows read at one logical chunk hit 16 distinct 16-byte bank groups
+// (so do any 8-row aligned groups on a 32-bank LDS).
+__device__ __forceinline__ int a_swz(int r) {
+    return (((r >> 2) ^ (r >> 1)) & 1) | ((((r >> 3) ^ (r >> 1)) & 1) << 1);
+}
+
+// Map the hardware's round-robin XCD dispatch (block b runs on XCD b % 8) to a
+// contiguous range of logical tiles per XCD, so tiles that share an A row-block
+// run on the same XCD and share its L2.
+__device__ __forceinline__ int xcd_logical_tile(int pid, int nblocks) {
+    const int xcd = pid & 7, idx = pid >> 3;
+    const int q = nblocks >> 3, r = nblocks & 7;
+    return (xcd < r) ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+}
+
+// ----------------------------------------------------------------------------
+// Tiled GEMM: block tile BM x BN, BK = 64, 4 waves in a 2x2 grid, each wave a
+// (BM/2) x (BN/2) tile of 32x32 MFMA accumulators. A and W stages are staged
+// through LDS, double-buffered: the global loads of stage k+1 are issued before
+// the MFMAs of stage k.
+template <int BM, int BN, int EPI>
+__global__ __launch_bounds__(256, 2) void gemm_w8a8(
+    const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ Wf,
+    const float *__restrict__ aS, const float *__restrict__ wS, const float *__restrict__ bias,
+    void *__restrict__ out, int64_t ldo, int M, int N, int Kp, int tilesN) {
+    constexpr int WTM = BM / 2, WTN = BN / 2;
+    constexpr int TM = WTM / 32, TN = WTN / 32;
+    constexpr int A_STAGE = BM * 64, B_STAGE = BN * 64;
+    constexpr int A_CH = BM * 4 / 256;  // 16-byte chunks per thread per stage
+    constexpr int B_CH = BN * 4 / 256;
+    static_assert(TM >= 1 && TN >= 1 && A_CH >= 1 && B_CH >= 1, "tile too small");
+
+    __shared__ __attribute__((aligned(16))) int8_t smem[2 * (A_STAGE + B_STAGE)];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int logical = xcd_logical_tile(blockIdx.x, gridDim.x);
+    const int m0 = (logical / tilesN) * BM, n0 = (logical % tilesN) * BN;
+    const int nk = Kp >> 6, nk32 = Kp >> 5;
+
+    i32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    // Global -> register staging of one K stage.
+    i32x4 ra[A_CH], rb[B_CH];
+    auto load_stage = [&](int kt) {
+        const int k0 = kt * 64;
+#pragma unroll
+        for (int i = 0; i < A_CH; ++i) {
+            const int c = tid + 256 * i, r = c >> 2, qc = c & 3;
+            const int gr = min(m0 + r, M - 1);  // rows past M re-read row M-1; never stored
+            ra[i] = *reinterpret_cast<const i32x4 *>(A + (int64_t)gr * lda + k0 + qc * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < B_CH; ++i) {
+            const int c = tid + 256 * i, f = c >> 6, l = c & 63;
+            const int nb = (n0 >> 5) + (f >> 1), kb = (k0 >> 5) + (f & 1);
+            rb[i] = *reinterpret_cast<const i32x4 *>(Wf + ((int64_t)nb * nk32 + kb) * 1024 + l * 16);
+        }
+    };
+    auto store_stage = [&](int buf) {
+        int8_t *As = smem + buf * (A_STAGE + B_STAGE);
+        int8_t *Bs = As + A_STAGE;
+#pragma unroll
+        for (int i = 0; i < A_CH; ++i) {
+            const int c = tid + 256 * i, r = c >> 2, qc = c & 3;
+            *reinterpret_cast<i32x4 *>(As + r * 64 + ((qc ^ a_swz(r)) << 4)) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < B_CH; ++i) {
+            const int c = tid + 256 * i;
+            *reinterpret_cast<i32x4 *>(Bs + c * 16) = rb[i];
+        }
+    };
+
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) load_stage(kt + 1);
+        const int8_t *As = smem + cur * (A_STAGE + B_STAGE);
+        const int8_t *Bs = As + A_STAGE;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            i32x4 af[TM], bf[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int rr = wm * WTM + i * 32 + (lane & 31);
+                const int qc = 2 * s + (lane >> 5);
+                af[i] = *reinterpret_cast<const i32x4 *>(As + rr * 64 + ((qc ^ a_swz(rr)) << 4));
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int f = ((wn * WTN >> 5) + j) * 2 + s;
+                bf[j] = *reinterpret_cast<const i32x4 *>(Bs + f * 1024 + lane * 16);
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) store_stage(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue straight from the accumulators: for a fixed register, lanes 0-31
+    // and 32-63 each write 32 consecutive outputs (128 bytes) of one row.
+    const bool has_bias = bias != nullptr;
+    float ws[TN], bb[TN];
+    int cols[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        cols[j] = n0 + wn * WTN + j * 32 + (lane & 31);
+        ws[j] = cols[j] < N ? wS[cols[j]] : 0.0f;
+        bb[j] = (has_bias && cols[j] < N) ? bias[cols[j]] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wm * WTM + i * 32 + acc_row(r, lane);
+            if (row >= M) continue;
+            if (EPI == EPI_I32) {
+                int *o = reinterpret_cast<int *>(out) + (int64_t)row * ldo;
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    if (cols[j] < N) o[cols[j]] = acc[i][j][r];
+            } else {
+                const float as = aS[row];
+                float *o = reinterpret_cast<float *>(out) + (int64_t)row * ldo;
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    if (cols[j] < N) o[cols[j]] = epilogue<EPI>(acc[i][j][r], as, ws[j], has_bias, bb[j]);
+            }
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Small-M variant (M <= 32): HBM-bound on the weight stream, so every weight
+// byte is read once and the whole M tile (zero-padded to 32 rows) rides along in
+// the MFMA. One block per 32 output channels; its 4 waves split K and their int32
+// partial sums are added exactly through LDS.
+template <int EPI>
+__global__ __launch_bounds__(256) void gemv_w8a8(
+    const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ Wf,
+    const float *__restrict__ aS, const float *__restrict__ wS, const float *__restrict__ bias,
+    void *__restrict__ out, int64_t ldo, int M, int N, int Kp) {
+    __shared__ int red[4 * 16 * 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nb = blockIdx.x, nk32 = Kp >> 5;
+    const int8_t *arow = A + (int64_t)min(lane & 31, M - 1) * lda + (lane >> 5) * 16;
+    const int8_t *wfr = Wf + (int64_t)nb * nk32 * 1024 + lane * 16;
+
+    i32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0;
+#pragma unroll 4
+    for (int kk = wave; kk < nk32; kk += 4) {
+        const i32x4 a = *reinterpret_cast<const i32x4 *>(arow + kk * 32);
+        const i32x4 b = *reinterpret_cast<const i32x4 *>(wfr + (int64_t)kk * 1024);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
+    __syncthreads();
+
+    const int col = nb * 32 + (lane & 31);
+    const bool has_bias = bias != nullptr;
+    const float ws = col < N ? wS[col] : 0.0f;
+    const float bb = (has_bias && col < N) ? bias[col] : 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+        const int r = wave * 4 + rr;
+        const int sum = red[(0 * 16 + r) * 64 + lane] + red[(1 * 16 + r) * 64 + lane] +
+                        red[(2 * 16 + r) * 64 + lane] + red[(3 * 16 + r) * 64 + lane];
+        const int row = acc_row(r, lane);
+        if (row >= M || col >= N) continue;
+        if (EPI == EPI_I32) {
+            reinterpret_cast<int *>(out)[(int64_t)row * ldo + col] = sum;
+        } else {
+            reinterpret_cast<float *>(out)[(int64_t)row * ldo + col] =
+                epilogue<EPI>(sum, aS[row], ws, has_bias, bb);
+        }
+    }
+}
+
+}  // namespace enchip

@@ -1,0 +1,211 @@
+"""ctypes binding of libenchip.so (the C ABI in include/enchip.h).
+
+This is the Python twin of what the Go leaf ``gpu/enchip`` binds with purego: it
+loads the in-tree ``libenchip.so`` and exposes each entry point one to one. It
+has no compute path of its own -- when the library is missing, or no device is
+present, calls raise; nothing here falls back to the CPU.
+
+torch is imported (when installed) before the library is loaded, so that the
+process has one HIP runtime: libenchip.so's ``libamdhip64.so.7`` dependency then
+resolves to the runtime torch already loaded, and device pointers from torch
+tensors are valid in both.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libenchip.so")
+
+OK, ERR_NO_DEVICE, ERR_ARG, ERR_HIP, ERR_OOM, ERR_HANDLE = range(6)
+ACT_NONE, ACT_GELU = 0, 1
+ABI_VERSION = 1
+
+# Every symbol include/enchip.h declares, with (restype, argtypes).
+_vp, _i64, _int = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+_SIGNATURES = {
+    "enchip_abi_version": (_int, []),
+    "enchip_open": (_int, [_int, ctypes.POINTER(_vp)]),
+    "enchip_close": (_int, [_vp]),
+    "enchip_last_error": (ctypes.c_char_p, [_vp]),
+    "enchip_device_info": (_int, [_vp, ctypes.POINTER(_int), ctypes.POINTER(_int), ctypes.c_char_p, _int]),
+    "enchip_quant_rows": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "enchip_weight_register": (_int, [_vp, _vp, _vp, _i64, _i64, ctypes.POINTER(ctypes.c_uint64)]),
+    "enchip_weight_release": (_int, [_vp, ctypes.c_uint64]),
+    "enchip_weight_shape": (_int, [_vp, ctypes.c_uint64, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
+    "enchip_w8a8_linear": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _vp, _int, _vp, _vp]),
+    "enchip_w8a8_batch": (_int, [_vp, _vp, _i64, _i64, _vp, _int]),
+    "enchip_quant_rows_dev": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "enchip_w8a8_pre_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _i64, _vp, _vp, _int, _vp, _vp]),
+    "enchip_w8a8_linear_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _vp, _int, _vp, _vp]),
+    "enchip_set_small_m": (_int, [_vp, _i64]),
+}
+SYMBOLS = tuple(_SIGNATURES)
+
+
+class EnchipOp(ctypes.Structure):
+    """``enchip_op`` of include/enchip.h."""
+    _fields_ = [("w", ctypes.c_uint64), ("bias", _vp), ("act", _int), ("dst", _vp)]
+
+
+class EnchipError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"enchip error {code}: {msg}")
+        self.code = code
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libenchip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise FileNotFoundError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+    try:  # share torch's HIP runtime when torch is present (see module docstring)
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.enchip_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"libenchip ABI {lib.enchip_abi_version()} != binding ABI {ABI_VERSION}")
+    _lib = lib
+    return lib
+
+
+def _ptr(x: Optional[np.ndarray]):
+    return None if x is None else ctypes.c_void_p(x.ctypes.data)
+
+
+@dataclass(frozen=True)
+class Weight:
+    handle: int
+    N: int
+    K: int
+
+
+class Context:
+    """One enchip context (device + stream + registered weights)."""
+
+    def __init__(self, device: int = 0):
+        self._lib = load()
+        h = ctypes.c_void_p()
+        rc = self._lib.enchip_open(device, ctypes.byref(h))
+        if rc != OK:
+            raise EnchipError(rc, self._lib.enchip_last_error(None).decode())
+        self._h = h
+
+    # -- lifecycle ------------------------------------------------------------
+    def close(self) -> None:
+        if self._h:
+            self._lib.enchip_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc: int) -> None:
+        if rc != OK:
+            raise EnchipError(rc, self._lib.enchip_last_error(self._h).decode())
+
+    @property
+    def handle(self):
+        return self._h
+
+    # -- queries / knobs --------------------------------------------------------
+    def device_info(self) -> dict:
+        cus, clk = ctypes.c_int(), ctypes.c_int()
+        name = ctypes.create_string_buffer(64)
+        self._check(self._lib.enchip_device_info(self._h, ctypes.byref(cus), ctypes.byref(clk), name, 64))
+        return {"num_cus": cus.value, "clock_khz": clk.value, "arch": name.value.decode()}
+
+    def set_small_m(self, max_m: int) -> None:
+        self._check(self._lib.enchip_set_small_m(self._h, max_m))
+
+    # -- host-buffer entry points ----------------------------------------------
+    def quant_rows(self, a: np.ndarray):
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        M, K = a.shape
+        aq = np.empty((M, K), np.int8)
+        s = np.empty(max(M, 1), np.float32)
+        self._check(self._lib.enchip_quant_rows(self._h, _ptr(a), M, K, _ptr(aq), _ptr(s)))
+        return aq, s[:M]
+
+    def register_weight(self, wq: np.ndarray, wscale: np.ndarray) -> Weight:
+        wq = np.ascontiguousarray(wq, dtype=np.int8)
+        wscale = np.ascontiguousarray(wscale, dtype=np.float32)
+        N, K = wq.shape
+        if wscale.shape != (N,):
+            raise ValueError(f"wscale shape {wscale.shape} != ({N},)")
+        out = ctypes.c_uint64()
+        self._check(self._lib.enchip_weight_register(self._h, _ptr(wq), _ptr(wscale), N, K, ctypes.byref(out)))
+        return Weight(out.value, N, K)
+
+    def release_weight(self, w: Weight) -> None:
+        self._check(self._lib.enchip_weight_release(self._h, w.handle))
+
+    def weight_shape(self, w: Weight):
+        n, k = ctypes.c_int64(), ctypes.c_int64()
+        self._check(self._lib.enchip_weight_shape(self._h, w.handle, ctypes.byref(n), ctypes.byref(k)))
+        return n.value, k.value
+
+    def linear(self, w: Weight, a: np.ndarray, bias: Optional[np.ndarray] = None, act: int = ACT_NONE,
+               want_acc: bool = False):
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        M = a.shape[0]
+        if a.shape != (M, w.K):
+            raise ValueError(f"a shape {a.shape} != (M, {w.K})")
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        dst = np.empty((M, w.N), np.float32)
+        acc = np.empty((M, w.N), np.int32) if want_acc else None
+        self._check(self._lib.enchip_w8a8_linear(self._h, w.handle, _ptr(a), M, _ptr(b), act, _ptr(dst), _ptr(acc)))
+        return (dst, acc) if want_acc else dst
+
+    def batch(self, a: np.ndarray, ops: Sequence[tuple]):
+        """ops: sequence of (Weight, bias-or-None, act). Returns one dst per op."""
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        M, K = a.shape
+        keep, arr = [], (EnchipOp * max(len(ops), 1))()
+        outs = []
+        for i, (w, bias, act) in enumerate(ops):
+            b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+            d = np.empty((M, w.N), np.float32)
+            keep.append(b)
+            outs.append(d)
+            arr[i] = EnchipOp(w.handle, None if b is None else b.ctypes.data, act, d.ctypes.data)
+        self._check(self._lib.enchip_w8a8_batch(self._h, _ptr(a), M, K, ctypes.cast(arr, ctypes.c_void_p), len(ops)))
+        return outs
+
+    # -- device-resident entry points (raw device pointers as ints) ------------
+    def quant_rows_dev(self, d_a: int, M: int, K: int, d_aq: int, d_ascale: int, stream: int = 0,
+                       ldq: Optional[int] = None) -> None:
+        self._check(self._lib.enchip_quant_rows_dev(self._h, d_a, M, K, d_aq, K if ldq is None else ldq,
+                                                    d_ascale, stream or None))
+
+    def pre_dev(self, w: Weight, d_aq: int, ldq: int, M: int, d_ascale: int, d_bias: int, act: int, d_dst: int,
+                stream: int = 0) -> None:
+        self._check(self._lib.enchip_w8a8_pre_dev(self._h, w.handle, d_aq, ldq, M, d_ascale, d_bias or None, act,
+                                                  d_dst, stream or None))
+
+    def linear_dev(self, w: Weight, d_a: int, M: int, d_bias: int, act: int, d_dst: int, stream: int = 0) -> None:
+        self._check(self._lib.enchip_w8a8_linear_dev(self._h, w.handle, d_a, M, d_bias or None, act, d_dst,
+                                                     stream or None))

@@ -1,0 +1,281 @@
+"""bench.py -- W8A8 encode throughput on one MI355X (BERT-base, batch 64 x seq 512).
+
+A step is one pass of the hot path over one batch: every W8A8 linear of a
+12-layer BERT-base forward at M = 64*512 = 32768 tokens, in encoder/bert.go:343-368
+order -- fused QKV (768->2304, bias), attention output (768->768, bias), FFN up
+(768->3072, bias + exact GELU), FFN down (3072->768, bias) -- each as
+per-token int8 quantization + int8 MFMA GEMM with the fused dequant epilogue.
+Inputs are synthetic and already resident in HBM when the timed region starts:
+the layer inputs are seeded N(0,1) activations (the FFN-down input is the FFN-up
+output, as in the model); weights are random N(0,0.02) f32 quantized per output
+channel. Attention, softmax and LayerNorm are not part of the step: at the
+reference seam they run on the host (encoder/backend.go:8-18), outside the W8A8
+path.
+
+Prints ONE JSON line on stdout (progress goes to stderr).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "W8A8 encode seqs/sec (BERT-base b64×s512) + int8 GEMM TOPS as % of peak"
+PEAK_INT8_OPS = 5.0e15  # MI355X dense int8 MFMA (no sparsity)
+PEAK_HBM_BPS = 8.0e12  # MI355X HBM3E
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def host_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(layer_w, cfg, seconds: float):
+    """The reference's AVX2 W8A8 CPU path (oracle/cpu_baseline.c) on a bounded
+    sample: one sequence (512 tokens) through one layer's four linears, repeated
+    for about `seconds`, scaled to seqs/s of the 12-layer stack."""
+    import numpy as np
+
+    import oracle
+    from aikit_amd import workloads
+
+    workers = host_threads()
+    g = workloads.rng(99)
+    M = cfg.seq
+    inputs = {name: g.standard_normal((M, K), dtype=np.float32) for name, K, _, _ in cfg.linears()}
+    bufs = {name: np.empty(M * N, np.float32) for name, _, N, _ in cfg.linears()}
+    aq = np.empty(M * cfg.ffn, np.int8)
+    asc = np.empty(M, np.float32)
+
+    def one_layer():
+        for name, K, N, act in cfg.linears():
+            wq, ws, b, _ = layer_w[name]
+            x = bufs["ffn_up"].reshape(M, cfg.ffn) if name == "ffn_down" else inputs[name]
+            oracle.cpu_w8a8_linear(x, wq, ws, b, act, M, K, N, workers, dst=bufs[name], aq=aq, ascales=asc)
+
+    one_layer()  # warm-up
+    rounds, t0 = 0, time.perf_counter()
+    while True:
+        one_layer()
+        rounds += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or rounds >= 10000:
+            break
+    per_layer = el / rounds
+    seqs_per_s = 1.0 / (per_layer * cfg.layers)
+    macs = sum(M * K * N for _, K, N, _ in cfg.linears())
+    return {
+        "value": seqs_per_s,
+        "unit": "seqs/s",
+        "cores": workers,
+        "kind": "port",
+        "sample": (f"1 sequence (512 tokens) through one BERT-base layer's 4 W8A8 linears "
+                   f"(QKV, O, FFN-up+GELU, FFN-down), {rounds} repetitions in {el:.1f} s, scaled x{cfg.layers} "
+                   f"layers; C restatement of aikit's Go AVX2 W8A8 path (oracle/cpu_baseline.c), "
+                   f"{workers} threads on {cpu_model()}"),
+        "gmac_per_s": macs * rounds / el / 1e9,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length (0 = skip)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (the W8A8 path is not sharded across GPUs; "
+              "see DESIGN.md for how it would shard). Use --gpus 1.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from aikit_amd import enchip, workloads
+
+    cfg = workloads.BERT_BASE
+    M = cfg.tokens
+    log(f"torch {torch.__version__}, device {torch.cuda.get_device_name(0)}")
+    ctx = enchip.Context(0)
+    info = ctx.device_info()
+    log(f"enchip device {info}")
+    stream = torch.cuda.Stream()
+    sptr = stream.cuda_stream
+
+    # ---- weights: 12 layers x 4 linears, random N(0,0.02) quantized per channel
+    g = workloads.rng(2024)
+    layers = []
+    layer0_host = None
+    t0 = time.perf_counter()
+    for li in range(cfg.layers):
+        lw = workloads.encoder_layer_weights(g, cfg)
+        if li == 0:
+            layer0_host = lw
+        entry = {}
+        for name, (wq, ws, b, act) in lw.items():
+            h = ctx.register_weight(wq, ws)
+            entry[name] = (h, torch.from_numpy(b).cuda(), act)
+        layers.append(entry)
+    log(f"registered {cfg.layers * 4} weights in {time.perf_counter() - t0:.1f}s")
+
+    # ---- activations resident in HBM
+    with torch.cuda.stream(stream):
+        gen = torch.Generator(device="cuda").manual_seed(7)
+        x_in = {n: torch.randn((M, K), generator=gen, device="cuda", dtype=torch.float32)
+                for n, K, _, _ in cfg.linears() if n != "ffn_down"}
+        outs = {n: torch.empty((M, N), device="cuda", dtype=torch.float32) for n, _, N, _ in cfg.linears()}
+        kmax = max(K for _, K, _, _ in cfg.linears())
+        aq = torch.empty((M, kmax), device="cuda", dtype=torch.int8)
+        asc = torch.empty(M, device="cuda", dtype=torch.float32)
+    torch.cuda.synchronize()
+    lin = cfg.linears()
+
+    def run_step(evs=None):
+        for li in range(cfg.layers):
+            for j, (name, K, N, act) in enumerate(lin):
+                h, b, _ = layers[li][name]
+                x = outs["ffn_up"] if name == "ffn_down" else x_in[name]
+                if evs is not None:
+                    evs[li][j][0].record(stream)
+                ctx.quant_rows_dev(x.data_ptr(), M, K, aq.data_ptr(), asc.data_ptr(), sptr, ldq=K)
+                if evs is not None:
+                    evs[li][j][1].record(stream)
+                ctx.pre_dev(h, aq.data_ptr(), K, M, asc.data_ptr(), b.data_ptr(), act, outs[name].data_ptr(), sptr)
+                if evs is not None:
+                    evs[li][j][2].record(stream)
+
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            run_step()
+    torch.cuda.synchronize()
+    log(f"warmup {args.warmup} steps done")
+
+    events = [[[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in lin] for _ in range(cfg.layers)]
+              for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    with torch.cuda.stream(stream):
+        for s in range(args.steps):
+            run_step(events[s])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    ms_per_step = elapsed * 1e3 / args.steps
+    seqs_per_s = cfg.batch * args.steps / elapsed
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {seqs_per_s:.1f} seqs/s")
+
+    # ---- per-kernel durations from the events of the timed region
+    per = {name: {"quant_ms": [], "gemm_ms": []} for name, _, _, _ in lin}
+    for s in range(args.steps):
+        for li in range(cfg.layers):
+            for j, (name, _, _, _) in enumerate(lin):
+                e0, e1, e2 = events[s][li][j]
+                per[name]["quant_ms"].append(e0.elapsed_time(e1))
+                per[name]["gemm_ms"].append(e1.elapsed_time(e2))
+    kernels = {}
+    tot_ops = tot_gemm_s = 0.0
+    groups = {}  # kernel instantiation -> [ops, seconds, launches, bytes]
+    for name, K, N, act in lin:
+        gq = float(np.mean(per[name]["gemm_ms"])) * 1e-3
+        qq = float(np.mean(per[name]["quant_ms"])) * 1e-3
+        ops = 2.0 * M * N * K
+        gbytes = M * K + N * K + 4 * N + 4 * N + 4 * M + 4 * M * N
+        qbytes = 4 * M * K + M * K + 4 * M
+        kernels[name] = {
+            "M": M, "K": K, "N": N, "act": "gelu" if act else "none",
+            "gemm_us": gq * 1e6, "gemm_tops": ops / gq / 1e12, "gemm_frac_int8_peak": ops / gq / PEAK_INT8_OPS,
+            "gemm_alg_gbps": gbytes / gq / 1e9,
+            "quant_us": qq * 1e6, "quant_gbps": qbytes / qq / 1e9, "quant_frac_hbm": qbytes / qq / PEAK_HBM_BPS,
+        }
+        tot_ops += ops * cfg.layers
+        tot_gemm_s += gq * cfg.layers
+        kname = f"gemm_w8a8<256,128,{'EPI_F32_GELU' if act else 'EPI_F32'}>"
+        grp = groups.setdefault(kname, [0.0, 0.0, 0, 0.0])
+        grp[0] += ops * cfg.layers
+        grp[1] += gq * cfg.layers
+        grp[2] += cfg.layers
+        grp[3] += gbytes * cfg.layers
+    dom = max(groups, key=lambda k: groups[k][1])
+    d_ops, d_s, d_n, d_bytes = groups[dom]
+    achieved = d_ops / d_s
+    roofline = {
+        "kernel": dom,
+        "bound": "mfma",
+        "achieved": achieved / 1e12,
+        "peak": PEAK_INT8_OPS / 1e12,
+        "unit": "TFLOP/s",
+        "frac": achieved / PEAK_INT8_OPS,
+        "traffic": None,
+        "ops": "int8 multiply-adds x2, algorithmic 2*M*N*K per launch",
+        "launches_per_step": d_n,
+        "avg_launch_us": d_s / d_n * 1e6,
+        "alg_bytes_per_launch": d_bytes / d_n,
+        "alg_hbm_frac": (d_bytes / d_s) / PEAK_HBM_BPS,
+    }
+    result = {
+        "metric": METRIC,
+        "value": seqs_per_s,
+        "unit": "seqs/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": ("bert-base b64xs512 W8A8 linear stack: 12 layers x {QKV 768->2304 +bias, "
+                         "O 768->768 +bias, FFN-up 768->3072 +bias+GELU, FFN-down 3072->768 +bias}, "
+                         "per-token int8 quant + int8 MFMA GEMM + fused dequant epilogue per linear; "
+                         "activations resident in HBM; attention/softmax/LayerNorm not in the step"),
+            "model": "bert-base (random-init weights, per-channel int8)",
+            "global_batch": cfg.batch,
+            "seq_len": cfg.seq,
+            "tokens_per_step": M,
+            "parallelism": "single GPU",
+            "seeds": {"weights": 2024, "activations": 7},
+        },
+        "gemm_tops": tot_ops / tot_gemm_s / 1e12,
+        "gemm_frac_int8_peak": tot_ops / tot_gemm_s / PEAK_INT8_OPS,
+        "int8_tops_per_step": tot_ops / 1e12,
+        "kernels": kernels,
+        "roofline": roofline,
+        "device": info,
+    }
+    if args.cpu_seconds > 0:
+        log(f"CPU baseline ({args.cpu_seconds:.0f}s sample, {host_threads()} threads)")
+        result["cpu_baseline"] = cpu_baseline(layer0_host, cfg, args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    ctx.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,166 @@
+/*
+ * enchip.h -- C ABI of libenchip.so, the MI355X (gfx950) W8A8 linear engine that
+ * aikit's encoder reaches through a "hip" backend.
+ *
+ * The Go leaf `gpu/enchip` binds these symbols with purego (dlopen, no cgo) and
+ * implements encoder.Backend / encoder.Q8Backend / W8A8Backend on top of them,
+ * registering with encoder.RegisterBackend("hip", ...) from init(). Plain C types
+ * only: no C++ or torch types cross this boundary.
+ *
+ * Conventions
+ *   - Every entry point returns an int status: ENCHIP_OK (0) means handled; any
+ *     other value means the call did nothing useful and the caller must fall back
+ *     to its CPU path (the reference seam's "decline", encoder/backend_use.go:77-80).
+ *     enchip_last_error() then describes the failure.
+ *   - Matrices are row-major. a[M,K] f32 activations, wq[N,K] int8 weights in the
+ *     PyTorch [out,in] layout, wscale[N], dst[M,N] f32, bias[N] (nullable).
+ *   - Host pointers are borrowed for the duration of the call only.
+ *   - A context owns all device memory it allocates; enchip_close frees it.
+ *   - Host-pointer entry points are serialised by a per-context mutex and are safe
+ *     to call from several threads (encoder.EncodeBatch's worker goroutines,
+ *     encoder/model.go:214). The *_dev entry points share the context's device
+ *     scratch: calls on one context must be issued on one stream at a time.
+ *
+ * Numerics (bit-exact against aikit's Go linalg path, default amd64 build):
+ *   codes   = quantizeRowInt8Core (linalg/quant.go:43-71), activations' zero row -> scale 0
+ *   acc     = exact int32 dot                      (linalg/quant.go:150-156)
+ *   y       = float32(acc) * aScale[m] * wScale[n] (linalg/quant.go:295), +0 when aScale[m]==0
+ *   y      += bias[n]                              (encoder/linalg.go:130-140)
+ *   y       = GELUF32(y) when act == ENCHIP_ACT_GELU (linalg/exp.go:260-263)
+ */
+#ifndef ENCHIP_H
+#define ENCHIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ENCHIP_ABI_VERSION 1
+
+typedef struct enchip_ctx enchip_ctx;
+typedef uint64_t enchip_weight; /* opaque handle; 0 is never a valid handle */
+
+enum enchip_status {
+    ENCHIP_OK = 0,
+    ENCHIP_ERR_NO_DEVICE = 1, /* no HIP device, or the device index is out of range */
+    ENCHIP_ERR_ARG = 2,       /* invalid argument (null pointer, bad shape, K mismatch) */
+    ENCHIP_ERR_HIP = 3,       /* a HIP runtime call failed */
+    ENCHIP_ERR_OOM = 4,       /* device allocation failed */
+    ENCHIP_ERR_HANDLE = 5     /* unknown or released weight handle */
+};
+
+enum enchip_act {
+    ENCHIP_ACT_NONE = 0,
+    ENCHIP_ACT_GELU = 1 /* exact-erf GELU, linalg.GELUF32 */
+};
+
+/* Returns ENCHIP_ABI_VERSION. Lets a binding check it loaded the library it was
+ * written against before calling anything else. No reference counterpart. */
+int enchip_abi_version(void);
+
+/* Opens device `device` and creates a context with its own HIP stream.
+ * Replaces enccuda.New -> gpu.CreateSystemDefaultDevice -> dev.NewViT
+ * (gpu/enccuda/backend.go:97-101; gpu/cuda.go:87-100; gpu/cuda_vit.go:174-208):
+ * device bring-up, kernel load and queue creation.
+ * On failure *out is NULL and enchip_last_error(NULL) says why. */
+int enchip_open(int device, enchip_ctx **out);
+
+/* Frees every device buffer and weight the context owns. Idempotent on NULL.
+ * Replaces Backend.Close (encoder/backend.go:26-27; gpu/enccuda/backend.go). */
+int enchip_close(enchip_ctx *ctx);
+
+/* Last error message of this context (or, for ctx == NULL, of the last failed
+ * enchip_open on this thread). Never NULL. Diagnostics only. */
+const char *enchip_last_error(const enchip_ctx *ctx);
+
+/* Device facts used for roofline reporting: compute-unit count, peak engine clock
+ * in kHz, and the gfx architecture name (e.g. "gfx950"). name_len includes the NUL.
+ * Replaces the device queries behind gpu/roofline_test.go:57-140. */
+int enchip_device_info(enchip_ctx *ctx, int *num_cus, int *clock_khz, char *name,
+                       int name_len);
+
+/* Per-row dynamic symmetric int8 quantization of a[M,K] into aq[M,K] and
+ * ascale[M], on the device, host buffers in and out. Replaces
+ * linalg.QuantizeActivationsInto (linalg/quant.go:206-213; all-zero row ->
+ * scale 0) and the CUDA quant_rows kernel (gpu/vit.cu:49-83). */
+int enchip_quant_rows(enchip_ctx *ctx, const float *a, int64_t M, int64_t K,
+                      int8_t *aq, float *ascale);
+
+/* Uploads an int8 weight matrix wq[N,K] with per-output-channel scales wscale[N]
+ * once, pre-swizzled into the MFMA operand layout, and returns a handle. The
+ * context keeps its own copy: the caller may free wq/wscale afterwards. Replaces
+ * the (ptr,len)-keyed weight residency of gpu/enccuda/backend.go:204-244 for
+ * linalg.WeightMat{w8a8: true} (linalg/weightmat.go:61-64,117-118). */
+int enchip_weight_register(enchip_ctx *ctx, const int8_t *wq, const float *wscale,
+                           int64_t N, int64_t K, enchip_weight *out);
+
+/* Releases a registered weight's device memory. */
+int enchip_weight_release(enchip_ctx *ctx, enchip_weight w);
+
+/* Shape of a registered weight. */
+int enchip_weight_shape(enchip_ctx *ctx, enchip_weight w, int64_t *N, int64_t *K);
+
+/* One W8A8 linear on host buffers, synchronous:
+ *   dst[M,N] = act(W8A8(a[M,K], w) + bias)
+ * i.e. linalg.MatmulBTW8A8Into (linalg/quant.go:192-234) followed by addBias
+ * (encoder/linalg.go:130-140) and, for ENCHIP_ACT_GELU, gelu
+ * (encoder/bert.go:397-413). bias may be NULL. When acc_debug is non-NULL the
+ * int32 accumulators [M,N] are also written to it (parity testing).
+ * This is the body of the new opt-in W8A8Backend.MatmulBTW8A8 capability; the
+ * weight-only Q8Backend.MatmulBTQ8 contract (encoder/backend_use.go:59-83) is NOT
+ * served by it. */
+int enchip_w8a8_linear(enchip_ctx *ctx, enchip_weight w, const float *a, int64_t M,
+                       const float *bias, int act, float *dst, int32_t *acc_debug);
+
+/* The shared-activation batch: one quantization of a[M,K], then nops linears, each
+ * with its own weight, bias, activation and dst[M, N_i]. Numerically identical to
+ * calling enchip_w8a8_linear once per op. Replaces linalg.MatmulBTW8A8Batch /
+ * W8A8Op (linalg/quant.go:303-370): BERT's Q,K,V projections share one quant. */
+typedef struct enchip_op {
+    enchip_weight w;
+    const float *bias; /* nullable */
+    int act;
+    float *dst; /* [M, N of w] */
+} enchip_op;
+int enchip_w8a8_batch(enchip_ctx *ctx, const float *a, int64_t M, int64_t K,
+                      const enchip_op *ops, int nops);
+
+/* ---- device-resident entry points (pointers are device memory) ----------------
+ * stream is a hipStream_t (NULL = the context's own stream). They enqueue work and
+ * return without synchronising. No reference counterpart: the reference seam
+ * passes host slices per call (encoder/backend.go:19-28); these are the resident
+ * form the seam's planned residency widening needs (docs/task-native-gpu.md:418-427). */
+
+/* Device form of enchip_quant_rows: d_a[M,K] row-major f32 in; codes out at row
+ * pitch ldq >= K (columns [K,ldq) are written as zero), d_ascale[M].
+ * linalg.QuantizeActivationsInto (linalg/quant.go:206-213). With ldq a multiple of
+ * 64 the result feeds enchip_w8a8_pre_dev directly. */
+int enchip_quant_rows_dev(enchip_ctx *ctx, const float *d_a, int64_t M, int64_t K,
+                          int8_t *d_aq, int64_t ldq, float *d_ascale, void *stream);
+
+/* GEMM + fused epilogue on ALREADY quantized activations: d_aq[M][ldq] int8 with
+ * ldq a multiple of 64, ldq >= K and columns [K,ldq) zero (as enchip_quant_rows_dev
+ * writes them), d_ascale[M]. d_dst[M,N] = act(W8A8 + bias).
+ * linalg.MatmulBTW8A8Pre (linalg/quant.go:215-234): quantize once, reuse across
+ * weights. Bit-identical to enchip_w8a8_linear_dev on the same activations. */
+int enchip_w8a8_pre_dev(enchip_ctx *ctx, enchip_weight w, const int8_t *d_aq,
+                        int64_t ldq, int64_t M, const float *d_ascale,
+                        const float *d_bias, int act, float *d_dst, void *stream);
+
+/* Device form of enchip_w8a8_linear. d_bias may be NULL. */
+int enchip_w8a8_linear_dev(enchip_ctx *ctx, enchip_weight w, const float *d_a,
+                           int64_t M, const float *d_bias, int act, float *d_dst,
+                           void *stream);
+
+/* Rows at or below which the small-M (HBM-bound, split-K) kernel runs instead of
+ * the tiled MFMA GEMM. Both produce identical bits; this only selects the kernel.
+ * Mirrors the reference's dispatch knobs (linalg.SetParallelThreshold,
+ * linalg/linalg.go:58-74). Default 32. */
+int enchip_set_small_m(enchip_ctx *ctx, int64_t max_m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ENCHIP_H */

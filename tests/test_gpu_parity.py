@@ -1,0 +1,265 @@
+"""GPU parity: libenchip.so on the MI355X against the CPU oracle, through the C ABI.
+
+The bar: quantized activations and int32 accumulators
+bit-exact; dequantized f32 outputs within 1e-5 max relative error per GEMM. The
+epilogue restates the reference's float32 operation order, so the f32 outputs
+are also asserted bit-identical, which is stronger.
+
+Mirrors the reference's device tests: TestCUDA_vitQuantRows (byte-exact incl. the
+zero row, gpu/cuda_vit_test.go:154-226), TestCUDA_vitGEMMs (exact int reference,
+:228-310), TestCUDA_gemmTiledMatchesUntiled (bit-identical across shapes,
+:720-800), TestW8A8Batch_bitIdenticalToPerOp and TestW8A8Reblock_matchesPerRow
+(linalg/batch_test.go:13-66,102-135).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from aikit_amd import enchip, workloads
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "w8a8_golden.npz")
+REL_TOL = 1e-5  # north_star: dequantized f32 outputs, max relative error per GEMM
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def bits(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+def assert_f32_parity(got, want, what):
+    """Bit-identical (NaN payloads aside), and the north-star 1e-5 max rel error."""
+    assert got.shape == want.shape, what
+    nan = np.isnan(want)
+    assert (np.isnan(got) == nan).all(), f"{what}: NaN mismatch"
+    g, w = got[~nan], want[~nan]
+    denom = np.maximum(np.abs(w), np.finfo(np.float32).tiny)
+    rel = float(np.max(np.abs(g.astype(np.float64) - w) / denom)) if g.size else 0.0
+    assert rel <= REL_TOL, f"{what}: max rel err {rel:.3g} > {REL_TOL}"
+    mism = np.flatnonzero(bits(g) != bits(w))
+    assert mism.size == 0, f"{what}: {mism.size} elements differ in bits (first at {mism[:5]})"
+
+
+# ------------------------------------------------------------------ quantization
+def test_quant_rows_golden(ctx):
+    d = np.load(GOLDEN, allow_pickle=False)
+    names, off, rows = d["quant_names"], d["quant_offsets"], d["quant_rows"]
+    for i, name in enumerate(names):
+        r = rows[off[i]:off[i + 1]][None, :]
+        say(f"quant golden {name} K={r.shape[1]}")
+        q, s = ctx.quant_rows(r)
+        assert (q[0] == d["quant_codes_act"][off[i]:off[i + 1]]).all(), name
+        assert bits(s) [0] == bits(d["quant_scales_act"][i:i + 1])[0], name
+
+
+@pytest.mark.parametrize("K", [1, 3, 4, 64, 97, 384, 768, 1000, 1024, 1536, 3072, 4096, 4100, 5000])
+def test_quant_rows_matches_oracle(ctx, K):
+    # gpu/cuda_vit_test.go:154-226 shape family, plus the vector/scalar kernel edges.
+    g = workloads.rng(100 + K)
+    M = 37
+    a = workloads.activations(g, M, K)
+    a[5] = 0
+    a[7] *= np.float32(1e-3)
+    a[9, : min(K, 4)] = [127, -2.5, 0.5, 1.5][: min(K, 4)]
+    say(f"quant M={M} K={K}")
+    q, s = ctx.quant_rows(a)
+    wq, ws = oracle.quantize_activations(a, M, K)
+    assert (q == wq).all()
+    assert (bits(s) == bits(ws)).all()
+    assert s[5] == 0 and (q[5] == 0).all()
+
+
+def test_quant_rows_dev_matches_host(ctx):
+    import torch
+
+    g = workloads.rng(7)
+    M, K = 1000, 768
+    a = workloads.activations(g, M, K)
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        da = torch.from_numpy(a).cuda()
+        dq = torch.empty((M, K), dtype=torch.int8, device="cuda")
+        ds = torch.empty(M, dtype=torch.float32, device="cuda")
+        say("quant_rows_dev M=1000 K=768")
+        ctx.quant_rows_dev(da.data_ptr(), M, K, dq.data_ptr(), ds.data_ptr(), st.cuda_stream)
+    torch.cuda.synchronize()
+    wq, ws = oracle.quantize_activations(a, M, K)
+    assert (dq.cpu().numpy() == wq).all()
+    assert (bits(ds.cpu().numpy()) == bits(ws)).all()
+
+
+# ------------------------------------------------------------------ GEMM + epilogue
+def _linear_case(ctx, M, K, N, act, with_bias, seed, small_m=32, zero_rows=(0,)):
+    g = workloads.rng(seed)
+    a = workloads.activations(g, M, K)
+    for r in zero_rows:
+        if r < M:
+            a[r] = 0
+    wq, ws = workloads.int8_weights(g, N, K)
+    b = workloads.bias(g, N) if with_bias else None
+    w = ctx.register_weight(wq, ws)
+    try:
+        ctx.set_small_m(small_m)
+        dst, acc = ctx.linear(w, a, bias=b, act=act, want_acc=True)
+    finally:
+        ctx.set_small_m(32)
+        ctx.release_weight(w)
+    return a, wq, ws, b, dst, acc
+
+
+REF_SHAPES = [(1, 1, 1), (16, 16, 16), (17, 47, 33), (64, 129, 96), (129, 1152, 65),  # gpu/cuda_vit_test.go:720-800
+              (1, 16, 8), (16, 32, 32), (17, 65, 33),  # gpu/cuda_vit_test.go:233 (M,K,N)
+              (33, 768, 300), (257, 200, 513), (300, 3072, 768), (1000, 96, 1000)]
+
+
+@pytest.mark.parametrize("M,K,N", REF_SHAPES)
+@pytest.mark.parametrize("act,with_bias", [(0, False), (1, True)])
+def test_linear_matches_oracle(ctx, M, K, N, act, with_bias):
+    say(f"linear M={M} K={K} N={N} act={act} bias={with_bias}")
+    a, wq, ws, b, dst, acc = _linear_case(ctx, M, K, N, act, with_bias, seed=M * 7 + K * 3 + N)
+    aq, a_s = oracle.quantize_activations(a, M, K)
+    want_acc = (aq.astype(np.int64) @ wq.astype(np.int64).T).astype(np.int32)
+    assert np.array_equal(acc, want_acc), "int32 accumulators differ"
+    want = oracle.w8a8_linear(a, wq, ws, b, act, M, K, N)
+    assert_f32_parity(dst, want, f"linear {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("M", [1, 2, 5, 16, 31, 32])
+@pytest.mark.parametrize("K,N", [(768, 768), (768, 3072), (100, 50)])
+def test_small_m_kernel_matches_gemm_kernel(ctx, M, K, N):
+    # Kernel choice is numerically inert (cf. TestParallelWidth_bitIdentical,
+    # linalg/width_test.go:13): the small-M path and the tiled GEMM give the same bits.
+    say(f"small-M vs GEMM M={M} K={K} N={N}")
+    _, _, _, _, d1, acc1 = _linear_case(ctx, M, K, N, 1, True, seed=M + K + N, small_m=32)
+    a, wq, ws, b, d2, acc2 = _linear_case(ctx, M, K, N, 1, True, seed=M + K + N, small_m=0)
+    assert np.array_equal(acc1, acc2)
+    assert np.array_equal(bits(d1), bits(d2))
+    assert_f32_parity(d1, oracle.w8a8_linear(a, wq, ws, b, 1, M, K, N), "small-M")
+
+
+def test_batch_bit_identical_to_per_op(ctx):
+    # linalg/batch_test.go:13-66: a shared-activation batch equals one call per op.
+    g = workloads.rng(21)
+    M, K = 300, 768
+    a = workloads.activations(g, M, K)
+    ws_ = [workloads.int8_weights(g, N, K) for N in (768, 768, 768, 3072)]
+    bs = [workloads.bias(g, N) for N in (768, 768, 768, 3072)]
+    handles = [ctx.register_weight(wq, s) for wq, s in ws_]
+    try:
+        say("batch of 4 ops")
+        outs = ctx.batch(a, [(handles[0], bs[0], 0), (handles[1], None, 0), (handles[2], bs[2], 0),
+                             (handles[3], bs[3], 1)])
+        for i, (h, b, act) in enumerate([(handles[0], bs[0], 0), (handles[1], None, 0), (handles[2], bs[2], 0),
+                                         (handles[3], bs[3], 1)]):
+            single = ctx.linear(h, a, bias=b, act=act)
+            assert np.array_equal(bits(outs[i]), bits(single)), f"op {i}"
+    finally:
+        for h in handles:
+            ctx.release_weight(h)
+
+
+def test_row_invariance(ctx):
+    # linalg/batch_test.go:102-135: a row's output does not depend on the other rows.
+    g = workloads.rng(22)
+    M, K, N = 777, 768, 1024
+    a = workloads.activations(g, M, K)
+    wq, ws = workloads.int8_weights(g, N, K)
+    b = workloads.bias(g, N)
+    w = ctx.register_weight(wq, ws)
+    try:
+        say("row invariance")
+        full = ctx.linear(w, a, bias=b, act=1)
+        for lo, hi in [(0, 1), (5, 37), (300, 777)]:
+            part = ctx.linear(w, a[lo:hi], bias=b, act=1)
+            assert np.array_equal(bits(part), bits(full[lo:hi]))
+    finally:
+        ctx.release_weight(w)
+
+
+def test_linear_dev_matches_host(ctx):
+    import torch
+
+    g = workloads.rng(23)
+    M, K, N = 2048, 768, 2304
+    a = workloads.activations(g, M, K)
+    wq, ws = workloads.int8_weights(g, N, K)
+    b = workloads.bias(g, N)
+    w = ctx.register_weight(wq, ws)
+    try:
+        host = ctx.linear(w, a, bias=b, act=1)
+        st = torch.cuda.Stream()
+        with torch.cuda.stream(st):
+            da, db = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+            dd = torch.empty((M, N), dtype=torch.float32, device="cuda")
+            say("linear_dev 2048x768x2304")
+            ctx.linear_dev(w, da.data_ptr(), M, db.data_ptr(), 1, dd.data_ptr(), st.cuda_stream)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(dd.cpu().numpy()), bits(host))
+    finally:
+        ctx.release_weight(w)
+
+
+def test_golden_linears(ctx):
+    d = np.load(GOLDEN, allow_pickle=False)
+    for i in range(3):
+        a, wq, ws = d[f"lin{i}_a"], d[f"lin{i}_wq"], d[f"lin{i}_ws"]
+        b = d[f"lin{i}_bias"]
+        b = b if b.size else None
+        w = ctx.register_weight(wq, ws)
+        try:
+            say(f"golden linear {i}")
+            got = ctx.linear(w, a, bias=b, act=int(d[f"lin{i}_act"]))
+        finally:
+            ctx.release_weight(w)
+        assert np.array_equal(bits(got), bits(d[f"lin{i}_dst"]))
+
+
+# ------------------------------------------------------------------ BASELINE configs at full size
+def _full_config(ctx, workers, M, K, N, act, seed, sample_rows=None):
+    g = workloads.rng(seed)
+    a = workloads.activations(g, M, K)
+    a[1] = 0
+    wq, ws = workloads.int8_weights(g, N, K)
+    b = workloads.bias(g, N)
+    w = ctx.register_weight(wq, ws)
+    try:
+        say(f"full config M={M} K={K} N={N} act={act}")
+        dst = ctx.linear(w, a, bias=b, act=act)
+    finally:
+        ctx.release_weight(w)
+    rows = np.arange(M) if sample_rows is None else sample_rows
+    want = oracle.cpu_w8a8_linear(a[rows], wq, ws, b, act, len(rows), K, N, workers=workers)
+    assert_f32_parity(dst[rows], want, f"config {M}x{K}x{N}")
+
+
+def test_config2_isolated_linear(ctx, workers):
+    c = workloads.LINEAR_CFG2
+    _full_config(ctx, workers, c["M"], c["K"], c["N"], c["act"], seed=2)
+
+
+@pytest.mark.parametrize("N", [768, 3072])
+def test_config3_small_m(ctx, workers, N):
+    _full_config(ctx, workers, 16, 768, N, 0, seed=3)
+
+
+@pytest.mark.parametrize("name,K,N,act", workloads.BERT_BASE.linears())
+def test_config4_bert_base_linears(ctx, workers, name, K, N, act):
+    # Full M = 64*512 rows; every row is checked.
+    _full_config(ctx, workers, workloads.BERT_BASE.tokens, K, N, act, seed=40 + N + K)
+
+
+@pytest.mark.parametrize("name,K,N,act", workloads.XLMR_LARGE_CE.linears())
+def test_config5_xlmr_linears(ctx, workers, name, K, N, act):
+    # M = 128*512 = 65536 rows computed on the device; 1024 rows (the first 512
+    # and 512 random) are checked -- each output row depends only on its own
+    # input row (row invariance, tested above).
+    M = workloads.XLMR_LARGE_CE.tokens
+    g = np.random.Generator(np.random.PCG64(5))
+    rows = np.concatenate([np.arange(512), np.sort(g.choice(np.arange(512, M), 512, replace=False))])
+    _full_config(ctx, workers, M, K, N, act, seed=50 + N + K, sample_rows=rows)

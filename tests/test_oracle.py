@@ -1,0 +1,302 @@
+"""Pins the CPU oracle (oracle/) to things other than itself.
+
+Each check is chosen so that a plausible mistake in the restatement (a dropped
+polynomial term, half-to-even instead of half-away rounding, the wrong zero-row
+convention, a reassociated rescale) fails:
+
+* the reference's own test vectors (encoder/quant_test.go:165-201,
+  gpu/cuda_vit_test.go:154-310, linalg/quant_test.go:234-262);
+* the accuracy figures the reference quotes for its own transcendental kernels,
+  reproduced on the same dense sweeps (linalg/exp.go:22-23,184-188,246-252;
+  linalg/exp_test.go:17-58,326-366,559-589);
+* exact integer arithmetic in numpy int64, closed forms, invariants;
+* the committed golden vectors (tests/golden/w8a8_golden.npz), themselves
+  checked here against the same independent facts.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+from scipy.special import erf
+
+import oracle
+from aikit_amd import workloads
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "w8a8_golden.npz")
+ULP = 2.0 ** -23
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+# ------------------------------------------------------------------ quantizer
+def test_quant_reference_extreme_row():
+    # encoder/quant_test.go:187-201: [1,-1,0,0] -> scale float32(1/127), codes +-127.
+    q, s = oracle.quantize_row(np.array([1, -1, 0, 0], np.float32), 1.0)
+    assert s == np.float32(1.0 / 127.0)
+    assert q.tolist() == [127, -127, 0, 0]
+
+
+def test_quant_zero_row_conventions():
+    # weights (QuantizeRowInt8): scale 1 (encoder/quant_test.go:165-185);
+    # activations (quantizeRowInt8): scale 0 (gpu/cuda_vit_test.go:220-222).
+    z = np.zeros(8, np.float32)
+    assert oracle.quantize_row(z, 1.0)[1] == 1.0
+    assert oracle.quantize_row(z, 0.0)[1] == 0.0
+    q, s = oracle.quantize_rows_weights(np.zeros((2, 5), np.float32), 2, 5)
+    assert (q == 0).all() and (s == 1).all()
+    q, s = oracle.quantize_activations(np.zeros((2, 5), np.float32), 2, 5)
+    assert (q == 0).all() and (s == 0).all()
+
+
+def test_quant_ties_round_half_away_from_zero():
+    # maxAbs = 127 -> s = 1, inv = 1, so v*inv = v exactly: every .5 is a tie.
+    # Go's math.Round rounds half away from zero; half-to-even would give 0,2,2,-0,-2.
+    row = np.array([127, 0.5, 1.5, 2.5, -0.5, -2.5, 126.5, -126.5], np.float32)
+    q, s = oracle.quantize_row(row, 0.0)
+    assert s == 1.0
+    assert q.tolist() == [127, 1, 2, 3, -1, -3, 127, -127]
+
+
+def test_quant_nan_inf_and_subnormal():
+    q, s = oracle.quantize_row(np.array([np.nan, 1.0, -2.0], np.float32), 0.0)
+    assert s == np.float32(2) / np.float32(127)  # NaN ignored by `v > maxAbs`
+    assert q.tolist() == [0, 64, -127]  # 1*63.5 = 63.5 -> 64 (away from zero)
+    q, s = oracle.quantize_row(np.array([np.inf, 1.0], np.float32), 0.0)
+    assert np.isinf(s) and q.tolist() == [0, 0]  # inv = 0 -> Inf*0 = NaN -> 0 on amd64
+    q, s = oracle.quantize_row(np.array([1e-40, -1e-40], np.float32), 0.0)
+    assert s > 0 and q.tolist() == [127, -127]  # subnormal maxAbs is not flushed
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_quant_invariants(seed):
+    g = np.random.Generator(np.random.PCG64(seed))
+    a = (g.standard_normal((64, 300)) * g.uniform(0.01, 100)).astype(np.float32)
+    q, s = oracle.quantize_activations(a, 64, 300)
+    maxabs = np.abs(a).max(axis=1)
+    assert (s == (maxabs / np.float32(127)).astype(np.float32)).all()
+    # the max element maps to +-127; |q| <= 127; sign preserved; error <= half a step
+    assert (np.abs(q).max(axis=1) == 127).all()
+    assert (np.sign(q) * np.sign(a) >= 0).all()
+    err = np.abs(a.astype(np.float64) - q.astype(np.float64) * s[:, None].astype(np.float64))
+    assert (err <= 0.5 * s[:, None] * (1 + 1e-5)).all()
+    # scaling by a power of two scales s exactly and leaves the codes unchanged
+    q2, s2 = oracle.quantize_activations(a * np.float32(8), 64, 300)
+    assert (q2 == q).all() and (s2 == s * 8).all()
+
+
+def test_quant_brute_force_small():
+    # Every float32 code computed by exhaustive search over k in [-127,127]:
+    # the code is the integer nearest to v*inv (an f32 product), ties away from zero.
+    g = np.random.Generator(np.random.PCG64(7))
+    for _ in range(200):
+        n = int(g.integers(1, 9))
+        row = (g.standard_normal(n) * 3).astype(np.float32)
+        q, s = oracle.quantize_row(row, 0.0)
+        inv = np.float32(1) / s
+        for v, c in zip(row, q):
+            x = float(np.float32(v * inv))
+            ks = np.arange(-127, 128)
+            d = np.abs(ks - x)
+            best = ks[d == d.min()]
+            want = best.max() if x > 0 else best.min()  # tie -> away from zero
+            assert c == want, (row, v, x, c, want)
+
+
+def test_workloads_quantize_weights_matches_oracle():
+    g = np.random.Generator(np.random.PCG64(11))
+    w = (g.standard_normal((50, 77)) * 0.02).astype(np.float32)
+    w[3] = 0
+    w[4, :5] = [0.5, -0.5, 1.5, -2.5, 127.0]
+    q1, s1 = workloads.quantize_weights(w)
+    q2, s2 = oracle.quantize_rows_weights(w, 50, 77)
+    assert (q1 == q2).all() and (s1 == s2).all()
+
+
+# ------------------------------------------------------------------ int8 dot
+def test_dot_lengths_and_extremes():
+    # linalg/quant_test.go:234-262: lengths straddling the 64/16 loops, +-127 extremes.
+    g = np.random.Generator(np.random.PCG64(8))
+    for n in [0, 1, 7, 15, 16, 17, 31, 47, 63, 64, 65, 80, 127, 128, 129, 191, 192, 2048, 2049]:
+        a = g.integers(-127, 128, n, dtype=np.int8)
+        b = g.integers(-127, 128, n, dtype=np.int8)
+        want = int(np.dot(a.astype(np.int64), b.astype(np.int64)))
+        assert oracle.dot_i8(a, b) == want
+        assert oracle.cpu_dot_i8(a, b) == want  # the AVX2 restatement
+    for n in [16, 2048]:
+        a = np.full(n, -127, np.int8)
+        b = np.full(n, 127, np.int8)
+        assert oracle.dot_i8(a, b) == oracle.cpu_dot_i8(a, b) == -127 * 127 * n
+
+
+# ------------------------------------------------------------------ rescale
+def test_rescale_order_and_zero_row():
+    # linalg/quant.go:291-295: +0 for aScale == 0, else float32(acc)*aS*bS left to right.
+    g = np.random.Generator(np.random.PCG64(9))
+    M, K, N = 33, 129, 47
+    A = g.integers(-127, 128, (M, K), dtype=np.int8)
+    B = g.integers(-127, 128, (N, K), dtype=np.int8)
+    a_s = g.uniform(1e-4, 1e-1, M).astype(np.float32)
+    a_s[5] = 0
+    b_s = (g.standard_normal(N) * 1e-2).astype(np.float32)
+    dst = oracle.w8a8_span(A, a_s, B, b_s, M, K, N)
+    acc = A.astype(np.int64) @ B.astype(np.int64).T
+    want = (acc.astype(np.float32) * a_s[:, None]).astype(np.float32) * b_s[None, :]
+    want[5] = 0
+    assert np.array_equal(dst.view(np.uint32), want.astype(np.float32).view(np.uint32))
+    # the other association differs somewhere: the test can tell them apart
+    other = acc.astype(np.float32) * (a_s[:, None] * b_s[None, :]).astype(np.float32)
+    other[5] = 0
+    assert not np.array_equal(dst, other)
+
+
+def test_cpu_baseline_bit_identical_to_oracle(workers):
+    g = np.random.Generator(np.random.PCG64(12))
+    for M, K, N, act in [(64, 768, 512, 1), (300, 100, 77, 0), (1, 2049, 3, 1)]:
+        a = workloads.activations(g, M, K)
+        wq, ws = workloads.int8_weights(g, N, K)
+        b = workloads.bias(g, N)
+        want = oracle.w8a8_linear(a, wq, ws, b, act, M, K, N)
+        got = oracle.cpu_w8a8_linear(a, wq, ws, b, act, M, K, N, workers=max(2, workers))
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ------------------------------------------------------------------ transcendental kernels
+def test_erf_gelu_accuracy_matches_reference_quotes():
+    # linalg/exp_test.go:326-366 sweep: 4,000,001 points over [-8,8]. The reference
+    # quotes max |ErfF32 - erf| = 1.92e-07 (linalg/exp.go:186-188), GELU abs
+    # 4.67e-07 and 1.41 ULP relative on x >= 0.1 (linalg/exp.go:187-188,251-252).
+    i = np.arange(4_000_001, dtype=np.float64)
+    x = (-8 + 16 * i / 4_000_000).astype(np.float32)
+    xf = x.astype(np.float64)
+    e = np.abs(oracle.erf_vec(x).astype(np.float64) - erf(xf)).max()
+    assert f"{e:.3g}" == "1.92e-07"
+    want = 0.5 * xf * (1 + erf(xf * 0.7071067811865476))
+    ab = np.abs(oracle.gelu(x).astype(np.float64) - want)
+    assert f"{ab.max():.3g}" == "4.67e-07"
+    m = x >= 0.1
+    rel = (ab[m] / np.abs(want[m])).max() / ULP
+    assert f"{rel:.2f}" == "1.41"
+
+
+def test_exp_accuracy_dense_sweep():
+    # linalg/exp_test.go:47-49 dense sweep; the contract is <= 1 ULP (measured
+    # 0.68 ULP over the dense+random sweep, linalg/exp.go:22-23), subnormals flushed.
+    i = np.arange(2_000_000, dtype=np.float64)
+    x = (-103.9 + 192.6 * i / 2_000_000).astype(np.float32)
+    got = oracle.exp_vec(x).astype(np.float64)
+    w = np.exp(x.astype(np.float64))
+    ok = np.isfinite(w) & (w >= 1.1754944e-38)
+    rel = np.abs((got[ok] - w[ok]) / w[ok])
+    assert rel.max() <= 0.68 * ULP
+    assert (got[(w < 1.1754944e-38)] == 0).all()
+    assert oracle.exp_f32(0.0) == 1.0 and math.isinf(oracle.exp_f32(89.0)) and oracle.exp_f32(-88.0) == 0.0
+
+
+def test_tanh_accuracy():
+    # linalg/exp_test.go:559-589: <= 2 ULP over [-20,20]; exact special values.
+    i = np.arange(4_000_001, dtype=np.float64)
+    x = (-20 + 40 * i / 4_000_000).astype(np.float32)
+    w = np.tanh(x.astype(np.float64))
+    t = oracle.tanh(x).astype(np.float64)
+    nz = w != 0
+    assert (np.abs((t[nz] - w[nz]) / w[nz])).max() <= 2 * ULP
+    assert oracle.tanh(np.array([0, 20, -20, 10, -10], np.float32)).tolist() == [0, 1, -1, 1, -1]
+
+
+def test_gelu_special_values():
+    y = oracle.gelu(np.array([0.0, 10.0, -10.0, 100.0, -100.0], np.float32))
+    assert y.tolist() == [0.0, 10.0, -0.0, 100.0, -0.0]
+    assert np.signbit(y[2]) and np.signbit(y[4])
+
+
+# ------------------------------------------------------------------ encoder glue
+def test_layer_norm_pool_l2_closed_forms():
+    g = np.random.Generator(np.random.PCG64(13))
+    L, D = 7, 384
+    x = g.standard_normal((L, D)).astype(np.float32) * 3 + 1
+    w = g.standard_normal(D).astype(np.float32)
+    b = g.standard_normal(D).astype(np.float32)
+    y = oracle.layer_norm(x, w, b, L, D, 1e-12)
+    xd = x.astype(np.float64)
+    mu = xd.mean(axis=1, keepdims=True)
+    var = ((xd - mu) ** 2).mean(axis=1, keepdims=True)
+    want = (xd - mu) / np.sqrt(var + 1e-12) * w + b
+    assert np.allclose(y, want, rtol=1e-6, atol=1e-6)
+    p = oracle.pool_mean(x, L, D)
+    assert np.allclose(p, xd.mean(axis=0), rtol=1e-6, atol=1e-7)
+    v = oracle.l2_normalize(p)
+    assert abs(np.linalg.norm(v.astype(np.float64)) - 1) < 1e-6
+    assert (oracle.l2_normalize(np.zeros(4, np.float32)) == 0).all()  # embed/pool.go:27-32
+    assert (oracle.pool_mean(np.zeros((0, 3), np.float32), 0, 3) == 0).all()  # encoder/pooling.go:86-88
+
+
+def test_softmax_rows_sum_to_one_and_uniform_fallback():
+    g = np.random.Generator(np.random.PCG64(14))
+    r = g.standard_normal(129).astype(np.float32) * 4
+    s = oracle.softmax_row_scaled(r, np.float32(0.125))
+    assert abs(s.astype(np.float64).sum() - 1) < 1e-6
+    want = np.exp((r * np.float32(0.125)).astype(np.float64) - (r * np.float32(0.125)).max())
+    assert np.allclose(s, want / want.sum(), rtol=2e-6, atol=1e-9)
+
+
+# ------------------------------------------------------------------ golden vectors
+def test_golden_quant(golden):
+    names, off, rows = golden["quant_names"], golden["quant_offsets"], golden["quant_rows"]
+    for i, name in enumerate(names):
+        r = rows[off[i]:off[i + 1]]
+        for zero, codes_key, scales_key in [(0.0, "quant_codes_act", "quant_scales_act"),
+                                            (1.0, "quant_codes_w", "quant_scales_w")]:
+            q, s = oracle.quantize_row(r, zero)
+            assert (q == golden[codes_key][off[i]:off[i + 1]]).all(), name
+            assert np.array_equal(np.float32(s), golden[scales_key][i]) or (np.isnan(s) and np.isnan(golden[scales_key][i])), name
+    # independent facts about the fixture itself
+    i = list(names).index("ref_extreme")
+    assert golden["quant_scales_w"][i] == np.float32(1.0 / 127.0)
+    i = list(names).index("vit_row5")
+    assert golden["quant_scales_act"][i] == 0 and golden["quant_scales_w"][i] == 1
+
+
+def test_golden_gemm(golden):
+    for i in range(3):
+        A, B = golden[f"gemm{i}_A"], golden[f"gemm{i}_B"]
+        acc = golden[f"gemm{i}_acc"]
+        assert np.array_equal(acc, (A.astype(np.int64) @ B.astype(np.int64).T).astype(np.int32))
+        M, K = A.shape
+        N = B.shape[0]
+        assert np.array_equal(oracle.acc_i32(A, B, M, K, N), acc)
+        want = (acc.astype(np.float32) * golden[f"gemm{i}_as"][:, None]).astype(np.float32) * golden[f"gemm{i}_bs"][None, :]
+        assert np.array_equal(golden[f"gemm{i}_dst"], want.astype(np.float32))
+
+
+def test_golden_linear(golden):
+    for i in range(3):
+        a, wq, ws = golden[f"lin{i}_a"], golden[f"lin{i}_wq"], golden[f"lin{i}_ws"]
+        b = golden[f"lin{i}_bias"]
+        b = b if b.size else None
+        act = int(golden[f"lin{i}_act"])
+        M, K = a.shape
+        N = wq.shape[0]
+        got = oracle.w8a8_linear(a, wq, ws, b, act, M, K, N)
+        assert np.array_equal(got.view(np.uint32), golden[f"lin{i}_dst"].view(np.uint32))
+        # independent: integer accumulators from numpy, rescale, bias, and GELU vs
+        # erf in float64 within the reference's 1e-6 absolute GELU contract.
+        aq, a_s = oracle.quantize_activations(a, M, K)
+        acc = aq.astype(np.int64) @ wq.astype(np.int64).T
+        y = (acc.astype(np.float32) * a_s[:, None]).astype(np.float32) * ws[None, :]
+        y[a_s == 0] = 0
+        if b is not None:
+            y = (y + b[None, :]).astype(np.float32)
+        if act == 1:
+            yd = y.astype(np.float64)
+            y = 0.5 * yd * (1 + erf(yd / math.sqrt(2)))
+        assert np.abs(got - y).max() <= 1e-6
+
+
+def test_golden_gelu(golden):
+    assert np.array_equal(oracle.gelu(golden["gelu_x"]).view(np.uint32), golden["gelu_y"].view(np.uint32))
+    xd = golden["gelu_x"].astype(np.float64)
+    assert np.abs(golden["gelu_y"] - 0.5 * xd * (1 + erf(xd / math.sqrt(2)))).max() <= 1e-6

@@ -16,6 +16,7 @@
 
 #include "enchip.h"
 #include "kernels.h"
+#include "probes.h"
 
 namespace {
 
@@ -130,12 +131,20 @@ int launch_quant(enchip_ctx *c, const float *d_a, int64_t M, int64_t K, int8_t *
     return check_launch(c, "quant_rows");
 }
 
-template <int BM, int BN, int EPI>
+template <int BM, int BN, int EPI, int MINB>
 void launch_gemm_t(const Weight &w, const int8_t *aq, int64_t lda, const float *as, const float *bias,
                    void *out, int64_t ldo, int64_t M, hipStream_t s) {
     const int tilesM = (int)((M + BM - 1) / BM), tilesN = (int)((w.N + BN - 1) / BN);
-    hipLaunchKernelGGL((enchip::gemm_w8a8<BM, BN, EPI>), dim3((unsigned)(tilesM * tilesN)), dim3(256), 0,
+    hipLaunchKernelGGL((enchip::gemm_w8a8<BM, BN, EPI, MINB>), dim3((unsigned)(tilesM * tilesN)), dim3(256), 0,
                        s, aq, lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp, tilesN);
+}
+
+// Tile choice: 128x256 tiles (2 blocks per CU) when they give every CU at least two
+// blocks; otherwise 128x128 tiles (3 blocks per CU) to fill the chip. Measured on
+// MI355X: 128x256 is fastest for BERT-base's M=32768 shapes, 128x128 for M=4096.
+bool use_wide_tile(const enchip_ctx *c, const Weight &w, int64_t M) {
+    const int64_t t256 = ((M + 127) / 128) * ((w.N + 255) / 256);
+    return t256 >= 2 * (int64_t)c->num_cus;
 }
 
 template <int EPI>
@@ -146,14 +155,10 @@ void launch_gemm_epi(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t l
                            lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp);
         return;
     }
-    // Largest tile that still gives every CU at least one block.
-    auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((w.N + bn - 1) / bn); };
-    if (tiles(256, 128) >= c->num_cus)
-        launch_gemm_t<256, 128, EPI>(w, aq, lda, as, bias, out, ldo, M, s);
-    else if (tiles(128, 128) >= c->num_cus)
-        launch_gemm_t<128, 128, EPI>(w, aq, lda, as, bias, out, ldo, M, s);
+    if (use_wide_tile(c, w, M))
+        launch_gemm_t<128, 256, EPI, 2>(w, aq, lda, as, bias, out, ldo, M, s);
     else
-        launch_gemm_t<128, 64, EPI>(w, aq, lda, as, bias, out, ldo, M, s);
+        launch_gemm_t<128, 128, EPI, 3>(w, aq, lda, as, bias, out, ldo, M, s);
 }
 
 int launch_gemm(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, const float *as,
@@ -265,6 +270,84 @@ int enchip_device_info(enchip_ctx *ctx, int *num_cus, int *clock_khz, char *name
         name[name_len - 1] = 0;
     }
     return ENCHIP_OK;
+}
+
+int enchip_gemm_kernel_name(enchip_ctx *ctx, enchip_weight h, int64_t M, int act, char *buf, int len) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    Weight *w;
+    int rc = find_weight(ctx, h, &w);
+    if (rc) return rc;
+    if (!buf || len <= 0) return fail(ctx, ENCHIP_ERR_ARG, "gemm_kernel_name: bad buffer");
+    const int epi = act_code(act);
+    char name[96];
+    if (M <= ctx->small_m)
+        snprintf(name, sizeof name, "enchip::gemv_w8a8<%d>", epi);
+    else if (use_wide_tile(ctx, *w, M))
+        snprintf(name, sizeof name, "enchip::gemm_w8a8<128, 256, %d, 2>", epi);
+    else
+        snprintf(name, sizeof name, "enchip::gemm_w8a8<128, 128, %d, 3>", epi);
+    std::strncpy(buf, name, (size_t)len - 1);
+    buf[len - 1] = 0;
+    return ENCHIP_OK;
+}
+
+int enchip_probe_ceilings(enchip_ctx *ctx, enchip_ceilings *out) {
+    if (!ctx || !out) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    const int64_t bytes = (int64_t)1 << 30;
+    void *buf = nullptr;
+    int *sink = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t e = hipMalloc(&buf, (size_t)bytes);
+    if (e != hipSuccess) return fail(ctx, ENCHIP_ERR_OOM, "probe: hipMalloc(1 GiB): %s", hipGetErrorString(e));
+    int rc = ENCHIP_OK;
+    auto best_us = [&](auto launch, float *best) -> hipError_t {
+        hipError_t err;
+        *best = 1e30f;
+        for (int rep = 0; rep < 6; ++rep) {
+            if ((err = hipEventRecord(e0, ctx->stream)) != hipSuccess) return err;
+            launch();
+            if ((err = hipGetLastError()) != hipSuccess) return err;
+            if ((err = hipEventRecord(e1, ctx->stream)) != hipSuccess) return err;
+            if ((err = hipEventSynchronize(e1)) != hipSuccess) return err;
+            float ms = 0;
+            if ((err = hipEventElapsedTime(&ms, e0, e1)) != hipSuccess) return err;
+            if (rep > 0 && ms * 1e3f < *best) *best = ms * 1e3f;  // rep 0 is warm-up
+        }
+        return hipSuccess;
+    };
+    do {
+        if ((e = hipMalloc((void **)&sink, 1 << 20)) != hipSuccess) break;
+        if ((e = hipEventCreate(&e0)) != hipSuccess || (e = hipEventCreate(&e1)) != hipSuccess) break;
+        if ((e = hipMemsetAsync(buf, 0x11, (size_t)bytes, ctx->stream)) != hipSuccess) break;
+        const int64_t n16 = bytes / 16;
+        const unsigned grid = (unsigned)(ctx->num_cus * 8);
+        float us = 0;
+        if ((e = best_us([&] {
+                 hipLaunchKernelGGL(enchip::probe_stream_read, dim3(grid), dim3(256), 0, ctx->stream,
+                                    (const enchip::i32x4_p *)buf, n16, sink);
+             }, &us)) != hipSuccess) break;
+        out->hbm_read_gbps = (double)bytes / us / 1e3;
+        if ((e = best_us([&] {
+                 hipLaunchKernelGGL(enchip::probe_stream_write, dim3(grid), dim3(256), 0, ctx->stream,
+                                    (enchip::i32x4_p *)buf, n16);
+             }, &us)) != hipSuccess) break;
+        out->hbm_write_gbps = (double)bytes / us / 1e3;
+        const int iters = 2000;
+        const unsigned mgrid = (unsigned)(ctx->num_cus * 2);
+        if ((e = best_us([&] {
+                 hipLaunchKernelGGL(enchip::probe_mfma_i8, dim3(mgrid), dim3(256), 0, ctx->stream, sink, iters);
+             }, &us)) != hipSuccess) break;
+        out->mfma_i8_tops = (double)mgrid * 4 * iters * 8 * 65536.0 / us / 1e6;
+    } while (0);
+    if (e != hipSuccess) rc = fail(ctx, ENCHIP_ERR_HIP, "probe: %s", hipGetErrorString(e));
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (sink) (void)hipFree(sink);
+    (void)hipFree(buf);
+    return rc;
 }
 
 int enchip_set_small_m(enchip_ctx *ctx, int64_t max_m) {

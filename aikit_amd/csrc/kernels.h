@@ -156,13 +156,6 @@ __device__ __forceinline__ int acc_row(int r, int lane) {
     return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
 }
 
-// XOR swizzle of the four 16-byte chunks of a 64-byte LDS row of A: any 16
-// consecutive rows read at one logical chunk hit 16 distinct 16-byte bank groups
-// (so do any 8-row aligned groups on a 32-bank LDS).
-__device__ __forceinline__ int a_swz(int r) {
-    return (((r >> 2) ^ (r >> 1)) & 1) | ((((r >> 3) ^ (r >> 1)) & 1) << 1);
-}
-
 // Map the hardware's round-robin XCD dispatch (block b runs on XCD b % 8) to a
 // contiguous range of logical tiles per XCD, so tiles that share an A row-block
 // run on the same XCD and share its L2.
@@ -173,29 +166,75 @@ __device__ __forceinline__ int xcd_logical_tile(int pid, int nblocks) {
 }
 
 // ----------------------------------------------------------------------------
-// Tiled GEMM: block tile BM x BN, BK = 64, 4 waves in a 2x2 grid, each wave a
-// (BM/2) x (BN/2) tile of 32x32 MFMA accumulators. A and W stages are staged
-// through LDS, double-buffered: the global loads of stage k+1 are issued before
-// the MFMAs of stage k.
-template <int BM, int BN, int EPI>
-__global__ __launch_bounds__(256, 2) void gemm_w8a8(
+// Tiled GEMM. Block tile BM x BN, K stage of 64, 4 waves in a 2x2 grid, each wave a
+// (BM/2) x (BN/2) tile of 32x32x32 i8 MFMA accumulators.
+//
+// LDS holds each stage as 1 KiB "fragments" in MFMA operand order (lane l's 16 bytes
+// at l*16): A fragment (rb, s) = rows rb*32.., k 32*s..; W fragment (nb, s) likewise.
+// Every ds_read_b128 is 64 lanes x 16 contiguous bytes, so fragment reads are free of
+// bank conflicts with no swizzle. W arrives already in this order (pre-swizzled at
+// registration); A is row-major in HBM and each lane fetches its 16 bytes from row
+// (lane & 31), k offset 16*(lane >> 5).
+//
+// Pipeline: stage k+2 in flight to VGPRs, stage k+1 in the other LDS buffer, stage k
+// computed; the fragments of the second k-step of a stage are read while the MFMAs
+// of the first run, and the next stage's first fragments while the second runs.
+template <int BM, int BN, int EPI, int MINB>
+__global__ __launch_bounds__(256, MINB) void gemm_w8a8(
     const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ Wf,
     const float *__restrict__ aS, const float *__restrict__ wS, const float *__restrict__ bias,
     void *__restrict__ out, int64_t ldo, int M, int N, int Kp, int tilesN) {
     constexpr int WTM = BM / 2, WTN = BN / 2;
     constexpr int TM = WTM / 32, TN = WTN / 32;
-    constexpr int A_STAGE = BM * 64, B_STAGE = BN * 64;
-    constexpr int A_CH = BM * 4 / 256;  // 16-byte chunks per thread per stage
-    constexpr int B_CH = BN * 4 / 256;
-    static_assert(TM >= 1 && TN >= 1 && A_CH >= 1 && B_CH >= 1, "tile too small");
-
-    __shared__ __attribute__((aligned(16))) int8_t smem[2 * (A_STAGE + B_STAGE)];
+    constexpr int CA = BM / 16, CB = BN / 16, C = CA + CB;  // 1 KiB chunks per stage
+    constexpr int LPW = C / 4;                               // chunks each wave moves
+    static_assert(C % 4 == 0 && TM >= 1 && TN >= 1, "tile shape");
+    constexpr int STAGE = C * 1024;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[2 * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int logical = xcd_logical_tile(blockIdx.x, gridDim.x);
     const int m0 = (logical / tilesN) * BM, n0 = (logical % tilesN) * BN;
     const int nk = Kp >> 6, nk32 = Kp >> 5;
+
+    // Source of this wave's chunks at k = 0; chunk c < CA is A (rb = c/2, s = c%2).
+    const int8_t *src[LPW];
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+        const int c = wave + 4 * i;
+        if (c < CA) {
+            const int rb = c >> 1, s = c & 1;
+            const int gr = min(m0 + rb * 32 + (lane & 31), M - 1);  // rows past M re-read M-1, never stored
+            src[i] = A + (int64_t)gr * lda + 32 * s + 16 * (lane >> 5);
+        } else {
+            const int cb = c - CA, nb = cb >> 1, s = cb & 1;
+            src[i] = Wf + ((int64_t)((n0 >> 5) + nb) * nk32 + s) * 1024 + lane * 16;
+        }
+    }
+    i32x4 R[LPW];
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) {
+            const int c = wave + 4 * i;
+            const int64_t koff = (c < CA) ? (int64_t)kt * 64 : (int64_t)kt * 2048;
+            R[i] = *reinterpret_cast<const i32x4 *>(src[i] + koff);
+        }
+    };
+    auto swrite = [&](int slot) {
+        int8_t *base = smem + slot * STAGE + lane * 16;
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) *reinterpret_cast<i32x4 *>(base + (wave + 4 * i) * 1024) = R[i];
+    };
+    const int aoff = (wm * WTM >> 5) * 2048 + lane * 16;
+    const int boff = CA * 1024 + (wn * WTN >> 5) * 2048 + lane * 16;
+    auto read_frags = [&](int slot, int s, i32x4 *af, i32x4 *bf) {
+        const int8_t *base = smem + slot * STAGE + s * 1024;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const i32x4 *>(base + aoff + i * 2048);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const i32x4 *>(base + boff + j * 2048);
+    };
 
     i32x16 acc[TM][TN];
 #pragma unroll
@@ -205,69 +244,31 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-    // Global -> register staging of one K stage.
-    i32x4 ra[A_CH], rb[B_CH];
-    auto load_stage = [&](int kt) {
-        const int k0 = kt * 64;
-#pragma unroll
-        for (int i = 0; i < A_CH; ++i) {
-            const int c = tid + 256 * i, r = c >> 2, qc = c & 3;
-            const int gr = min(m0 + r, M - 1);  // rows past M re-read row M-1; never stored
-            ra[i] = *reinterpret_cast<const i32x4 *>(A + (int64_t)gr * lda + k0 + qc * 16);
-        }
-#pragma unroll
-        for (int i = 0; i < B_CH; ++i) {
-            const int c = tid + 256 * i, f = c >> 6, l = c & 63;
-            const int nb = (n0 >> 5) + (f >> 1), kb = (k0 >> 5) + (f & 1);
-            rb[i] = *reinterpret_cast<const i32x4 *>(Wf + ((int64_t)nb * nk32 + kb) * 1024 + l * 16);
-        }
-    };
-    auto store_stage = [&](int buf) {
-        int8_t *As = smem + buf * (A_STAGE + B_STAGE);
-        int8_t *Bs = As + A_STAGE;
-#pragma unroll
-        for (int i = 0; i < A_CH; ++i) {
-            const int c = tid + 256 * i, r = c >> 2, qc = c & 3;
-            *reinterpret_cast<i32x4 *>(As + r * 64 + ((qc ^ a_swz(r)) << 4)) = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < B_CH; ++i) {
-            const int c = tid + 256 * i;
-            *reinterpret_cast<i32x4 *>(Bs + c * 16) = rb[i];
-        }
-    };
-
-    load_stage(0);
-    store_stage(0);
+    gload(0);
+    swrite(0);
+    if (nk > 1) gload(1);
     __syncthreads();
-
+    i32x4 a0[TM], b0[TN], a1[TM], b1[TN];
+    read_frags(0, 0, a0, b0);
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
-        if (kt + 1 < nk) load_stage(kt + 1);
-        const int8_t *As = smem + cur * (A_STAGE + B_STAGE);
-        const int8_t *Bs = As + A_STAGE;
+        read_frags(cur, 1, a1, b1);
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            i32x4 af[TM], bf[TN];
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                const int rr = wm * WTM + i * 32 + (lane & 31);
-                const int qc = 2 * s + (lane >> 5);
-                af[i] = *reinterpret_cast<const i32x4 *>(As + rr * 64 + ((qc ^ a_swz(rr)) << 4));
-            }
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int f = ((wn * WTN >> 5) + j) * 2 + s;
-                bf[j] = *reinterpret_cast<const i32x4 *>(Bs + f * 1024 + lane * 16);
-            }
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0[i], b0[j], acc[i][j], 0, 0, 0);
+        if (kt + 1 < nk) {
+            swrite(cur ^ 1);
+            if (kt + 2 < nk) gload(kt + 2);
+            __syncthreads();
+            read_frags(cur ^ 1, 0, a0, b0);
         }
-        if (kt + 1 < nk) store_stage(cur ^ 1);
-        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1[i], b1[j], acc[i][j], 0, 0, 0);
     }
 
     // Epilogue straight from the accumulators: for a fixed register, lanes 0-31

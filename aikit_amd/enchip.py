@@ -42,6 +42,8 @@ _SIGNATURES = {
     "enchip_quant_rows_dev": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
     "enchip_w8a8_pre_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _i64, _vp, _vp, _int, _vp, _vp]),
     "enchip_w8a8_linear_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _vp, _int, _vp, _vp]),
+    "enchip_gemm_kernel_name": (_int, [_vp, ctypes.c_uint64, _i64, _int, ctypes.c_char_p, _int]),
+    "enchip_probe_ceilings": (_int, [_vp, _vp]),
     "enchip_set_small_m": (_int, [_vp, _i64]),
 }
 SYMBOLS = tuple(_SIGNATURES)
@@ -50,6 +52,12 @@ SYMBOLS = tuple(_SIGNATURES)
 class EnchipOp(ctypes.Structure):
     """``enchip_op`` of include/enchip.h."""
     _fields_ = [("w", ctypes.c_uint64), ("bias", _vp), ("act", _int), ("dst", _vp)]
+
+
+class EnchipCeilings(ctypes.Structure):
+    """``enchip_ceilings`` of include/enchip.h."""
+    _fields_ = [("hbm_read_gbps", ctypes.c_double), ("hbm_write_gbps", ctypes.c_double),
+                ("mfma_i8_tops", ctypes.c_double)]
 
 
 class EnchipError(RuntimeError):
@@ -137,6 +145,17 @@ class Context:
         name = ctypes.create_string_buffer(64)
         self._check(self._lib.enchip_device_info(self._h, ctypes.byref(cus), ctypes.byref(clk), name, 64))
         return {"num_cus": cus.value, "clock_khz": clk.value, "arch": name.value.decode()}
+
+    def gemm_kernel_name(self, w: Weight, M: int, act: int) -> str:
+        buf = ctypes.create_string_buffer(128)
+        self._check(self._lib.enchip_gemm_kernel_name(self._h, w.handle, M, act, buf, 128))
+        return buf.value.decode()
+
+    def probe_ceilings(self) -> dict:
+        c = EnchipCeilings()
+        self._check(self._lib.enchip_probe_ceilings(self._h, ctypes.byref(c)))
+        return {"hbm_read_gbps": c.hbm_read_gbps, "hbm_write_gbps": c.hbm_write_gbps,
+                "mfma_i8_tops": c.mfma_i8_tops}
 
     def set_small_m(self, max_m: int) -> None:
         self._check(self._lib.enchip_set_small_m(self._h, max_m))

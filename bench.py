@@ -125,6 +125,8 @@ def main() -> int:
     log(f"enchip device {info}")
     stream = torch.cuda.Stream()
     sptr = stream.cuda_stream
+    ceilings = ctx.probe_ceilings()
+    log(f"measured ceilings {ceilings}")
 
     # ---- weights: 12 layers x 4 linears, random N(0,0.02) quantized per channel
     g = workloads.rng(2024)
@@ -212,7 +214,7 @@ def main() -> int:
         }
         tot_ops += ops * cfg.layers
         tot_gemm_s += gq * cfg.layers
-        kname = f"gemm_w8a8<256,128,{'EPI_F32_GELU' if act else 'EPI_F32'}>"
+        kname = ctx.gemm_kernel_name(layers[0][name][0], M, act)
         grp = groups.setdefault(kname, [0.0, 0.0, 0, 0.0])
         grp[0] += ops * cfg.layers
         grp[1] += gq * cfg.layers
@@ -234,6 +236,7 @@ def main() -> int:
         "avg_launch_us": d_s / d_n * 1e6,
         "alg_bytes_per_launch": d_bytes / d_n,
         "alg_hbm_frac": (d_bytes / d_s) / PEAK_HBM_BPS,
+        "frac_of_measured_mfma_peak": achieved / (ceilings["mfma_i8_tops"] * 1e12),
     }
     result = {
         "metric": METRIC,
@@ -265,6 +268,7 @@ def main() -> int:
         "int8_tops_per_step": tot_ops / 1e12,
         "kernels": kernels,
         "roofline": roofline,
+        "measured_ceilings": ceilings,
         "device": info,
     }
     if args.cpu_seconds > 0:

@@ -154,6 +154,25 @@ int enchip_w8a8_linear_dev(enchip_ctx *ctx, enchip_weight w, const float *d_a,
                            int64_t M, const float *d_bias, int act, float *d_dst,
                            void *stream);
 
+/* Name of the GEMM kernel instantiation a linear on weight w with M rows and
+ * activation act launches (as it appears in rocprofv3 traces), written to buf
+ * (NUL-terminated, truncated to len). Diagnostics for attributing profiles to
+ * calls; no reference counterpart. */
+int enchip_gemm_kernel_name(enchip_ctx *ctx, enchip_weight w, int64_t M, int act,
+                            char *buf, int len);
+
+/* Measured device ceilings (best of 5): HBM streaming read and write over a 1 GiB
+ * buffer (past the 256 MiB MALL), and the dense int8 MFMA rate
+ * (v_mfma_i32_32x32x32_i8, 8 independent chains per wave, 2 blocks per CU).
+ * Replaces gpu/roofline.cu's stream_read / imad_peak / dp4a_peak probes and
+ * TestDeviceCeilings (gpu/roofline_test.go:57-140). Allocates and frees 1 GiB. */
+typedef struct enchip_ceilings {
+    double hbm_read_gbps;
+    double hbm_write_gbps;
+    double mfma_i8_tops;
+} enchip_ceilings;
+int enchip_probe_ceilings(enchip_ctx *ctx, enchip_ceilings *out);
+
 /* Rows at or below which the small-M (HBM-bound, split-K) kernel runs instead of
  * the tiled MFMA GEMM. Both produce identical bits; this only selects the kernel.
  * Mirrors the reference's dispatch knobs (linalg.SetParallelThreshold,

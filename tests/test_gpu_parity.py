@@ -263,3 +263,49 @@ def test_config5_xlmr_linears(ctx, workers, name, K, N, act):
     g = np.random.Generator(np.random.PCG64(5))
     rows = np.concatenate([np.arange(512), np.sort(g.choice(np.arange(512, M), 512, replace=False))])
     _full_config(ctx, workers, M, K, N, act, seed=50 + N + K, sample_rows=rows)
+
+
+def test_device_ceilings_coherent(ctx):
+    # gpu/roofline_test.go:57-140 asserts the probes are coherent, not that the
+    # device is fast: each ceiling is positive and below the nameplate with margin.
+    say("roofline probes")
+    c = ctx.probe_ceilings()
+    print(f"[ceilings] {c}", flush=True)
+    assert 1000 < c["hbm_read_gbps"] < 12000
+    assert 1000 < c["hbm_write_gbps"] < 12000
+    assert 500 < c["mfma_i8_tops"] < 6000
+
+
+def test_pre_quantized_matches_linear(ctx):
+    # linalg/quant.go:215-234 MatmulBTW8A8Pre: quantize once (QuantizeActivationsInto)
+    # and reuse the codes across weights; bit-identical to the fused call.
+    import torch
+
+    g = workloads.rng(24)
+    M, K = 1500, 768
+    a = workloads.activations(g, M, K)
+    a[3] = 0
+    wts = [workloads.int8_weights(g, N, K) for N in (2304, 768)]
+    bs = [workloads.bias(g, N) for N in (2304, 768)]
+    hs = [ctx.register_weight(wq, s) for wq, s in wts]
+    try:
+        st = torch.cuda.Stream()
+        with torch.cuda.stream(st):
+            da = torch.from_numpy(a).cuda()
+            ldq = 768
+            dq = torch.empty((M, ldq), dtype=torch.int8, device="cuda")
+            ds = torch.empty(M, dtype=torch.float32, device="cuda")
+            say("quant_rows_dev + pre_dev")
+            ctx.quant_rows_dev(da.data_ptr(), M, K, dq.data_ptr(), ds.data_ptr(), st.cuda_stream, ldq=ldq)
+            outs = []
+            for h, b, act in zip(hs, bs, (0, 1)):
+                db = torch.from_numpy(b).cuda()
+                dd = torch.empty((M, h.N), dtype=torch.float32, device="cuda")
+                ctx.pre_dev(h, dq.data_ptr(), ldq, M, ds.data_ptr(), db.data_ptr(), act, dd.data_ptr(), st.cuda_stream)
+                outs.append((dd, db))
+        torch.cuda.synchronize()
+        for (dd, _), h, b, act in zip(outs, hs, bs, (0, 1)):
+            assert np.array_equal(bits(dd.cpu().numpy()), bits(ctx.linear(h, a, bias=b, act=act)))
+    finally:
+        for h in hs:
+            ctx.release_weight(h)

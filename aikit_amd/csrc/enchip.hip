@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "enchip.h"
+#include "gemm_persistent.h"
 #include "kernels.h"
 #include "probes.h"
 
@@ -139,12 +140,27 @@ void launch_gemm_t(const Weight &w, const int8_t *aq, int64_t lda, const float *
                        s, aq, lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp, tilesN);
 }
 
-// Tile choice: 128x256 tiles (2 blocks per CU) when they give every CU at least two
-// blocks; otherwise 128x128 tiles (3 blocks per CU) to fill the chip. Measured on
-// MI355X: 128x256 is fastest for BERT-base's M=32768 shapes, 128x128 for M=4096.
+// Tile choice for gemm_w8a8 (the general kernel): 128x256 tiles (2 blocks per CU)
+// when they give every CU at least two blocks, otherwise 128x128 tiles (3 blocks per
+// CU) to fill the chip.
 bool use_wide_tile(const enchip_ctx *c, const Weight &w, int64_t M) {
     const int64_t t256 = ((M + 127) / 128) * ((w.N + 255) / 256);
     return t256 >= 2 * (int64_t)c->num_cus;
+}
+
+// gemm_w8a8_pt's preconditions (gemm_persistent.h): an even number of 64-deep K
+// stages, 16-byte aligned A rows, 32-bit byte offsets into A and the weights, and
+// 16-byte row-major output stores (N and the output pitch multiples of 4).
+bool use_persistent(const Weight &w, const void *aq, int64_t lda, const void *out, int64_t ldo, int64_t M) {
+    const int64_t lim = (int64_t)1 << 31;
+    return (w.Kp % (enchip::PT_BK * enchip::PT_PW)) == 0 && (lda % 16) == 0 && ((uintptr_t)aq % 16) == 0 &&
+           (M - 1) * lda + w.Kp < lim && w.Np * w.Kp < lim && (w.N % 4) == 0 && (ldo % 4) == 0 &&
+           ((uintptr_t)out % 16) == 0;
+}
+
+int persistent_grid(const enchip_ctx *c, int64_t tiles) {
+    const int64_t full = std::max<int64_t>(8, (2 * (int64_t)c->num_cus) / 8 * 8);
+    return (int)std::min<int64_t>(full, (tiles + 7) / 8 * 8);
 }
 
 template <int EPI>
@@ -153,6 +169,15 @@ void launch_gemm_epi(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t l
     if (M <= c->small_m) {
         hipLaunchKernelGGL((enchip::gemv_w8a8<EPI>), dim3((unsigned)((w.N + 31) / 32)), dim3(256), 0, s, aq,
                            lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp);
+        return;
+    }
+    if (use_persistent(w, aq, lda, out, ldo, M)) {
+        using namespace enchip;
+        const int tilesM = (int)((M + PT_BM - 1) / PT_BM), tilesN = (int)((w.N + PT_BN - 1) / PT_BN);
+        const int64_t tiles = (int64_t)tilesM * tilesN;
+        hipLaunchKernelGGL((gemm_w8a8_pt<PT_BM, PT_BN, PT_BK, PT_PW, EPI>), dim3(persistent_grid(c, tiles)), dim3(256),
+                           0, s, aq, lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp, tilesN,
+                           (int)tiles);
         return;
     }
     if (use_wide_tile(c, w, M))
@@ -283,6 +308,9 @@ int enchip_gemm_kernel_name(enchip_ctx *ctx, enchip_weight h, int64_t M, int act
     char name[96];
     if (M <= ctx->small_m)
         snprintf(name, sizeof name, "enchip::gemv_w8a8<%d>", epi);
+    else if (use_persistent(*w, nullptr, w->Kp, nullptr, w->N, M))
+        snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d>", enchip::PT_BM, enchip::PT_BN,
+                 enchip::PT_BK, enchip::PT_PW, epi);
     else if (use_wide_tile(ctx, *w, M))
         snprintf(name, sizeof name, "enchip::gemm_w8a8<128, 256, %d, 2>", epi);
     else

@@ -1,0 +1,247 @@
+// gemm_persistent.h -- the persistent W8A8 GEMM used for M > small-M on gfx950.
+//
+// One workgroup per half CU (2 per CU), each walking a list of 128 x 256 output tiles.
+//
+// Main loop (per 64-deep K stage, 4 waves side by side along N, each 128 x 64):
+//   * W fragments go HBM -> registers directly. The weights are pre-swizzled
+//     fragment-major, so each load is 64 lanes x 16 contiguous bytes. Each wave owns its
+//     64 output channels, so nothing is shared and nothing passes through LDS.
+//   * A (row-major int8 activations) is staged through two LDS slots as 1 KiB
+//     fragments in MFMA operand order. All 4 waves read all of it.
+//   * One ring of PW stages carries both operands. Its refill loads are unconditional
+//     and wrap into the next tile's first stages, so:
+//       - the compiler's wait counts stay exact;
+//       - the next tile's data is in flight during the epilogue.
+//   * All LDS fragment reads of a stage are issued before its MFMAs
+//     (sched_group_barrier), so no MFMA waits on a just-issued LDS read.
+//
+// Epilogue (per tile, no VMEM loads):
+//   * The tile's aS / wS / bias are loaded once per ring group as inline-asm loads, so
+//     the compiler can neither hoist nor sink them. An explicit wait at the tile end
+//     covers them; they are older than the last group's PW * 6 ring loads.
+//   * They are staged in LDS.
+//   * Each wave transposes its accumulators through a private LDS scratch and writes
+//     16-byte row-major stores: 32 stores per wave per tile instead of 128 dword
+//     stores interleaved with loads.
+//
+// Numerics are those of gemm_w8a8 (kernels.h): the int32 dot is exact, and the epilogue
+// rounds in the reference's order, so the two kernels give identical bits.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernels.h"
+
+#pragma clang fp contract(off)
+
+namespace enchip {
+
+// Tile geometry of the persistent kernel (the host checks its preconditions).
+constexpr int PT_BM = 128, PT_BN = 256, PT_BK = 64, PT_PW = 2;
+
+template <int BM, int BN, int BK, int PW, int EPI>
+__global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
+    const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ Wf,
+    const float *__restrict__ aS, const float *__restrict__ wS, const float *__restrict__ bias,
+    void *__restrict__ out, int64_t ldo, int M, int N, int Kp, int tilesN, int numTiles) {
+    constexpr int WN = BN / 4;
+    constexpr int TM = BM / 32, TN = WN / 32;
+    constexpr int KB = BK / 32;
+    constexpr int FA = TM * KB;  // A fragments per stage
+    static_assert(FA % 4 == 0, "A fragments per stage must split over 4 waves");
+    static_assert(BN == 256 && BM <= 256 && (BM & (BM - 1)) == 0, "constant staging: 256 threads cover BN");
+    constexpr int FAW = FA / 4;  // A fragments each wave moves per stage
+    constexpr int STAGE = FA * 1024;
+    constexpr int RING_LOADS = FAW + KB * TN;  // VMEM loads per ring stage per lane
+    constexpr int SP = WN + 8;    // transpose scratch pitch in ints (4*SP = 32 mod 64 banks)
+    constexpr int C4 = WN / 4;    // 4-column groups per scratch row
+    constexpr int RPL = 64 / C4;  // scratch rows covered by one pass of the wave
+    __shared__ __attribute__((aligned(1024))) int8_t smem[2 * STAGE];
+    __shared__ __attribute__((aligned(16))) int s_tr[4][32 * SP];
+    __shared__ __attribute__((aligned(16))) float s_as[BM];
+    __shared__ __attribute__((aligned(16))) float s_ws[BN];
+    __shared__ __attribute__((aligned(16))) float s_b[BN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nk = Kp / BK, nk32 = Kp >> 5;
+    // Block b runs on XCD b % 8. Each XCD walks a contiguous range of tiles, so the
+    // tiles it holds at once share A row-blocks in its L2.
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per_xcd = gridDim.x >> 3;
+    const int q = numTiles >> 3, r = numTiles & 7;
+    const int xbeg = xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q;
+    const int xcnt = q + (xcd < r ? 1 : 0);
+    const int ntiles = slot < xcnt ? (xcnt - slot + per_xcd - 1) / per_xcd : 0;
+    if (ntiles == 0) return;
+    auto tile_id = [&](int i) { return xbeg + slot + i * per_xcd; };
+    const uint32_t ldau = (uint32_t)lda;
+    const bool has_bias = bias != nullptr;
+
+    // 32-bit byte offsets (host guarantees M*lda and Np*Kp fit).
+    uint32_t aoff_c[FAW], aoff_x[FAW];  // this lane's A rows: current / next tile
+    uint32_t woff_c, woff_x;
+    uint32_t acol[FAW];
+#pragma unroll
+    for (int i = 0; i < FAW; ++i) {
+        const int f = wave + 4 * i, kb = f % KB;
+        acol[i] = kb * 32 + 16 * (lane >> 5);
+    }
+    auto tile_offs = [&](int tile, uint32_t *aoff, uint32_t &woff) {
+        const int m0 = (tile / tilesN) * BM, n0 = (tile % tilesN) * BN;
+#pragma unroll
+        for (int i = 0; i < FAW; ++i) {
+            const int f = wave + 4 * i, rb = f / KB;
+            // rows past M re-read row M-1 and are never stored
+            aoff[i] = (uint32_t)min(m0 + rb * 32 + (lane & 31), M - 1) * ldau + acol[i];
+        }
+        woff = (uint32_t)(n0 / 32 + wave * TN) * (uint32_t)nk32 * 1024u + lane * 16;
+    };
+
+    i32x4 wreg[PW][KB][TN];
+    i32x4 areg[PW][FAW];
+    // Stage ls of the current tile, or stage ls - nk of the next one (a select, not a
+    // branch).
+    auto load_stage = [&](int ring, int ls) {
+        const bool nx = ls >= nk;
+        const uint32_t t = nx ? ls - nk : ls;
+        const uint32_t wo = nx ? woff_x : woff_c;
+#pragma unroll
+        for (int i = 0; i < FAW; ++i) {
+            const uint32_t ao = (nx ? aoff_x[i] : aoff_c[i]) + t * BK;
+            areg[ring][i] = *reinterpret_cast<const i32x4 *>(A + ao);
+        }
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                wreg[ring][kb][j] = *reinterpret_cast<const i32x4 *>(Wf + (wo + ((uint32_t)j * nk32 + t * KB + kb) * 1024u));
+    };
+    auto awrite = [&](int ls, int ring) {
+#pragma unroll
+        for (int i = 0; i < FAW; ++i)
+            *reinterpret_cast<i32x4 *>(smem + ls * STAGE + (wave + 4 * i) * 1024 + lane * 16) = areg[ring][i];
+    };
+
+    i32x16 acc[TM][TN];
+    tile_offs(tile_id(0), aoff_c, woff_c);
+    tile_offs(tile_id(ntiles > 1 ? 1 : 0), aoff_x, woff_x);
+#pragma unroll
+    for (int p = 0; p < PW; ++p) load_stage(p, p);  // nk >= PW
+    awrite(0, 0);
+    __syncthreads();
+
+    // Position of tile row R in s_as: the 8 rows a lane needs per 32-row chunk
+    // ((lane >> 4) + 4k, k = 0..7) are contiguous.
+    const int as_slot = (tid & ~31) + (tid & 3) * 8 + ((tid & 31) >> 2);
+    int g = 0;  // stages consumed so far: LDS slot parity across tiles
+    for (int it = 0; it < ntiles; ++it) {
+        const int tile = tile_id(it);
+        const int m0 = (tile / tilesN) * BM, n0 = (tile % tilesN) * BN;
+        float c_as = 0.f, c_ws = 0.f, c_b = 0.f;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int rr = 0; rr < 16; ++rr) acc[i][j][rr] = 0;
+        for (int t0 = 0; t0 < nk; t0 += PW) {
+            {
+                const float *pa = aS + min(m0 + (tid & (BM - 1)), M - 1);
+                const float *pw = wS + min(n0 + tid, N - 1);
+                const float *pb = (has_bias ? bias : wS) + min(n0 + tid, N - 1);
+                asm volatile("global_load_dword %0, %1, off" : "=v"(c_as) : "v"(pa) : "memory");
+                asm volatile("global_load_dword %0, %1, off" : "=v"(c_ws) : "v"(pw) : "memory");
+                asm volatile("global_load_dword %0, %1, off" : "=v"(c_b) : "v"(pb) : "memory");
+            }
+#pragma unroll
+            for (int p = 0; p < PW; ++p) {
+                const int t = t0 + p;
+                const int8_t *base = smem + ((g + t) & 1) * STAGE + lane * 16;
+                i32x4 af[KB][TM];
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+                        af[kb][i] = *reinterpret_cast<const i32x4 *>(base + (i * KB + kb) * 1024);
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < TN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[kb][i], wreg[p][kb][j], acc[i][j], 0, 0, 0);
+                awrite((g + t + 1) & 1, (p + 1) % PW);  // A of the next stage, maybe the next tile's
+                load_stage(p, t + PW);                   // refill this ring slot
+                // LDS reads first, then MFMAs with the LDS writes and VMEM loads interleaved
+                __builtin_amdgcn_sched_group_barrier(0x100, FA, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x200, FAW, 0);
+#pragma unroll
+                for (int u = 0; u < RING_LOADS; ++u) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, TM * TN * KB - 2 - RING_LOADS, 0);
+                __syncthreads();
+            }
+        }
+        g += nk;
+#pragma unroll
+        for (int i = 0; i < FAW; ++i) aoff_c[i] = aoff_x[i];
+        woff_c = woff_x;
+        tile_offs(tile_id(it + 2 < ntiles ? it + 2 : ntiles - 1), aoff_x, woff_x);
+
+        // ---- epilogue: constants to LDS (their loads are older than the last group's
+        // PW * RING_LOADS ring loads), then transpose + 16-byte stores per wave
+        asm volatile("s_waitcnt vmcnt(%3)" : "+v"(c_as), "+v"(c_ws), "+v"(c_b) : "n"(PW * RING_LOADS) : "memory");
+        if (!has_bias) c_b = 0.0f;
+        if (tid < BM) s_as[as_slot] = c_as;
+        s_ws[tid] = c_ws;
+        s_b[tid] = c_b;
+        __syncthreads();
+        const int c4 = lane % C4, rsub = lane / C4;
+        const int lcol = wave * WN + 4 * c4;  // tile column of this lane's first output
+        const int col = n0 + lcol;
+        const float4 ws4 = *reinterpret_cast<const float4 *>(&s_ws[lcol]);
+        const float4 b4 = *reinterpret_cast<const float4 *>(&s_b[lcol]);
+        const float wsv[4] = {ws4.x, ws4.y, ws4.z, ws4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+        int *scr = s_tr[wave];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int rr = 0; rr < 16; ++rr) scr[acc_row(rr, lane) * SP + j * 32 + (lane & 31)] = acc[i][j][rr];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const float4 a4a = *reinterpret_cast<const float4 *>(&s_as[i * 32 + rsub * 8]);
+            const float4 a4b = *reinterpret_cast<const float4 *>(&s_as[i * 32 + rsub * 8 + 4]);
+            const float asv[8] = {a4a.x, a4a.y, a4a.z, a4a.w, a4b.x, a4b.y, a4b.z, a4b.w};
+#pragma unroll
+            for (int k = 0; k < 32 / RPL; ++k) {
+                const int rl = rsub + RPL * k;  // row within the 32-row chunk
+                const int4 v = *reinterpret_cast<const int4 *>(&scr[rl * SP + 4 * c4]);
+                const int row = m0 + i * 32 + rl;
+                // N % 4 == 0 (host check): a lane's 4 columns are all in or all out
+                if (row < M && col < N) {
+                    if (EPI == EPI_I32) {
+                        *reinterpret_cast<int4 *>(reinterpret_cast<int *>(out) + (int64_t)row * ldo + col) = v;
+                    } else {
+                        const int vv[4] = {v.x, v.y, v.z, v.w};
+                        float y[4];
+#pragma unroll
+                        for (int qq = 0; qq < 4; ++qq) y[qq] = epilogue<EPI>(vv[qq], asv[k], wsv[qq], has_bias, bv[qq]);
+                        *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + (int64_t)row * ldo + col) =
+                            make_float4(y[0], y[1], y[2], y[3]);
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    }
+}
+
+}  // namespace enchip

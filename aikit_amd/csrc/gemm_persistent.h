@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
         // ---- epilogue: constants to LDS (their loads are older than the last group's
         // PW * RING_LOADS ring loads), then transpose + 16-byte stores per wave
         asm volatile("s_waitcnt vmcnt(%3)" : "+v"(c_as), "+v"(c_ws), "+v"(c_b) : "n"(PW * RING_LOADS) : "memory");
-        if (!has_bias) c_b = 0.0f;
+        if (!has_bias) c_b = kNoBias;
         if (tid < BM) s_as[as_slot] = c_as;
         s_ws[tid] = c_ws;
         s_b[tid] = c_b;
@@ -218,22 +218,67 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
             const float4 a4a = *reinterpret_cast<const float4 *>(&s_as[i * 32 + rsub * 8]);
             const float4 a4b = *reinterpret_cast<const float4 *>(&s_as[i * 32 + rsub * 8 + 4]);
             const float asv[8] = {a4a.x, a4a.y, a4a.z, a4a.w, a4b.x, a4b.y, a4b.z, a4b.w};
+            if (EPI == EPI_F32_GELU) {
+                // Pass 1: dequantize and apply GELU's series / sign branches to all 32
+                // of this lane's values, in place in the scratch; remember which need
+                // the erf tail (1 <= |u| <= 4) and leave their dequantized value there.
+                uint32_t tail_mask = 0;
 #pragma unroll
-            for (int k = 0; k < 32 / RPL; ++k) {
-                const int rl = rsub + RPL * k;  // row within the 32-row chunk
-                const int4 v = *reinterpret_cast<const int4 *>(&scr[rl * SP + 4 * c4]);
-                const int row = m0 + i * 32 + rl;
-                // N % 4 == 0 (host check): a lane's 4 columns are all in or all out
-                if (row < M && col < N) {
-                    if (EPI == EPI_I32) {
-                        *reinterpret_cast<int4 *>(reinterpret_cast<int *>(out) + (int64_t)row * ldo + col) = v;
-                    } else {
-                        const int vv[4] = {v.x, v.y, v.z, v.w};
-                        float y[4];
+                for (int k = 0; k < 32 / RPL; ++k) {
+                    int4 *cell = reinterpret_cast<int4 *>(&scr[(rsub + RPL * k) * SP + 4 * c4]);
+                    const int4 v = *cell;
+                    const int vv[4] = {v.x, v.y, v.z, v.w};
+                    float o4[4];
 #pragma unroll
-                        for (int qq = 0; qq < 4; ++qq) y[qq] = epilogue<EPI>(vv[qq], asv[k], wsv[qq], has_bias, bv[qq]);
-                        *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + (int64_t)row * ldo + col) =
-                            make_float4(y[0], y[1], y[2], y[3]);
+                    for (int qq = 0; qq < 4; ++qq) {
+                        const float y = dequant(vv[qq], asv[k], wsv[qq], bv[qq]);
+                        bool tail;
+                        const float gy = gelu_f32_no_tail(y, tail);
+                        o4[qq] = tail ? y : gy;
+                        tail_mask |= (uint32_t)tail << (4 * k + qq);
+                    }
+                    *cell = make_int4(__float_as_int(o4[0]), __float_as_int(o4[1]), __float_as_int(o4[2]),
+                                      __float_as_int(o4[3]));
+                }
+                // Pass 2: the tail values, one per lane per round, so the wavefront runs
+                // the tail code max-popcount times instead of once per mixed instruction.
+                for (;;) {
+                    const bool pending = tail_mask != 0u;
+                    if (__builtin_amdgcn_ballot_w64(pending) == 0) break;
+                    if (pending) {
+                        const int b = __builtin_ctz(tail_mask);
+                        tail_mask &= tail_mask - 1u;
+                        int *cell = &scr[(rsub + RPL * (b >> 2)) * SP + 4 * c4 + (b & 3)];
+                        *cell = __float_as_int(gelu_f32(__int_as_float(*cell)));
+                    }
+                }
+                // Pass 3: 16-byte stores of the finished values.
+#pragma unroll
+                for (int k = 0; k < 32 / RPL; ++k) {
+                    const int rl = rsub + RPL * k;
+                    const int4 v = *reinterpret_cast<const int4 *>(&scr[rl * SP + 4 * c4]);
+                    const int row = m0 + i * 32 + rl;
+                    if (row < M && col < N)
+                        *reinterpret_cast<int4 *>(reinterpret_cast<float *>(out) + (int64_t)row * ldo + col) = v;
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 32 / RPL; ++k) {
+                    const int rl = rsub + RPL * k;  // row within the 32-row chunk
+                    const int4 v = *reinterpret_cast<const int4 *>(&scr[rl * SP + 4 * c4]);
+                    const int row = m0 + i * 32 + rl;
+                    // N % 4 == 0 (host check): a lane's 4 columns are all in or all out
+                    if (row < M && col < N) {
+                        if (EPI == EPI_I32) {
+                            *reinterpret_cast<int4 *>(reinterpret_cast<int *>(out) + (int64_t)row * ldo + col) = v;
+                        } else {
+                            const int vv[4] = {v.x, v.y, v.z, v.w};
+                            float y[4];
+#pragma unroll
+                            for (int qq = 0; qq < 4; ++qq) y[qq] = dequant(vv[qq], asv[k], wsv[qq], bv[qq]);
+                            *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + (int64_t)row * ldo + col) =
+                                make_float4(y[0], y[1], y[2], y[3]);
+                        }
                     }
                 }
             }

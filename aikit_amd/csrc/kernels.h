@@ -142,11 +142,19 @@ __global__ __launch_bounds__(256) void quant_rows_scalar(const float *__restrict
 // ----------------------------------------------------------------------------
 // Epilogue of one output element (linalg/quant.go:291-295, encoder/linalg.go:130-140,
 // linalg/exp.go:260-263): float32(acc)*aS*wS left to right, +0 for an all-zero
-// activation row, then the bias as a separate rounding, then GELU.
+// activation row, then the bias as a separate rounding, then GELU. Callers without a
+// bias pass b = -0.0f: y + (-0.0f) == y bit for bit for every y (-0 stays -0, NaN
+// stays NaN), so the add needs no per-element select.
+constexpr float kNoBias = -0.0f;
+
+__device__ __forceinline__ float dequant(int acc, float as, float ws, float b) {
+    const float y = (as == 0.0f) ? 0.0f : (float)acc * as * ws;
+    return y + b;
+}
+
 template <int EPI>
-__device__ __forceinline__ float epilogue(int acc, float as, float ws, bool has_bias, float b) {
-    float y = (as == 0.0f) ? 0.0f : (float)acc * as * ws;
-    if (has_bias) y = y + b;
+__device__ __forceinline__ float epilogue(int acc, float as, float ws, float b) {
+    float y = dequant(acc, as, ws, b);
     if (EPI == EPI_F32_GELU) y = gelu_f32(y);
     return y;
 }
@@ -280,7 +288,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_w8a8(
     for (int j = 0; j < TN; ++j) {
         cols[j] = n0 + wn * WTN + j * 32 + (lane & 31);
         ws[j] = cols[j] < N ? wS[cols[j]] : 0.0f;
-        bb[j] = (has_bias && cols[j] < N) ? bias[cols[j]] : 0.0f;
+        bb[j] = (has_bias && cols[j] < N) ? bias[cols[j]] : kNoBias;
     }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -298,7 +306,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_w8a8(
                 float *o = reinterpret_cast<float *>(out) + (int64_t)row * ldo;
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    if (cols[j] < N) o[cols[j]] = epilogue<EPI>(acc[i][j][r], as, ws[j], has_bias, bb[j]);
+                    if (cols[j] < N) o[cols[j]] = epilogue<EPI>(acc[i][j][r], as, ws[j], bb[j]);
             }
         }
     }
@@ -334,9 +342,8 @@ __global__ __launch_bounds__(256) void gemv_w8a8(
     __syncthreads();
 
     const int col = nb * 32 + (lane & 31);
-    const bool has_bias = bias != nullptr;
     const float ws = col < N ? wS[col] : 0.0f;
-    const float bb = (has_bias && col < N) ? bias[col] : 0.0f;
+    const float bb = (bias != nullptr && col < N) ? bias[col] : kNoBias;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
         const int r = wave * 4 + rr;
@@ -348,7 +355,7 @@ __global__ __launch_bounds__(256) void gemv_w8a8(
             reinterpret_cast<int *>(out)[(int64_t)row * ldo + col] = sum;
         } else {
             reinterpret_cast<float *>(out)[(int64_t)row * ldo + col] =
-                epilogue<EPI>(sum, aS[row], ws, has_bias, bb);
+                epilogue<EPI>(sum, aS[row], ws, bb);
         }
     }
 }

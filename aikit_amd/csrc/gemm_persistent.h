@@ -40,6 +40,14 @@ namespace enchip {
 // Tile geometry of the persistent kernel (the host checks its preconditions).
 constexpr int PT_BM = 128, PT_BN = 256, PT_BK = 64, PT_PW = 2;
 
+// 16-byte nontemporal store of 4 output words. The f32 outputs are written once and
+// not read by this kernel; a normal store would let them evict the A row-blocks and
+// weights the XCD's other tiles are still reading from L2.
+__device__ __forceinline__ void store_nt(void *p, int4 v) {
+    const i32x4 t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<i32x4 *>(p));
+}
+
 template <int BM, int BN, int BK, int PW, int EPI>
 __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
     const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ Wf,
@@ -259,7 +267,7 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
                     const int4 v = *reinterpret_cast<const int4 *>(&scr[rl * SP + 4 * c4]);
                     const int row = m0 + i * 32 + rl;
                     if (row < M && col < N)
-                        *reinterpret_cast<int4 *>(reinterpret_cast<float *>(out) + (int64_t)row * ldo + col) = v;
+                        store_nt(reinterpret_cast<float *>(out) + (int64_t)row * ldo + col, v);
                 }
             } else {
 #pragma unroll
@@ -270,14 +278,15 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
                     // N % 4 == 0 (host check): a lane's 4 columns are all in or all out
                     if (row < M && col < N) {
                         if (EPI == EPI_I32) {
-                            *reinterpret_cast<int4 *>(reinterpret_cast<int *>(out) + (int64_t)row * ldo + col) = v;
+                            store_nt(reinterpret_cast<int *>(out) + (int64_t)row * ldo + col, v);
                         } else {
                             const int vv[4] = {v.x, v.y, v.z, v.w};
-                            float y[4];
-#pragma unroll
-                            for (int qq = 0; qq < 4; ++qq) y[qq] = dequant(vv[qq], asv[k], wsv[qq], bv[qq]);
-                            *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + (int64_t)row * ldo + col) =
-                                make_float4(y[0], y[1], y[2], y[3]);
+                            int4 y;
+                            y.x = __float_as_int(dequant(vv[0], asv[k], wsv[0], bv[0]));
+                            y.y = __float_as_int(dequant(vv[1], asv[k], wsv[1], bv[1]));
+                            y.z = __float_as_int(dequant(vv[2], asv[k], wsv[2], bv[2]));
+                            y.w = __float_as_int(dequant(vv[3], asv[k], wsv[3], bv[3]));
+                            store_nt(reinterpret_cast<float *>(out) + (int64_t)row * ldo + col, y);
                         }
                     }
                 }

@@ -31,6 +31,31 @@ PEAK_INT8_OPS = 5.0e15  # MI355X dense int8 MFMA (no sparsity)
 PEAK_HBM_BPS = 8.0e12  # MI355X HBM3E
 
 
+TRAFFIC_PROFILE = "profiles/bert_base_b64s512_hbm_traffic.md"
+
+
+def quant_kernel_name(K: int) -> str:
+    """Name of the quantize kernel enchip launches for rows of K floats (aligned
+    buffers): quant_rows_vec<ceil(K/256)> up to K = 4096."""
+    return f"enchip::quant_rows_vec<{(K + 255) // 256}>" if 0 < K <= 4096 and K % 4 == 0 else "enchip::quant_rows_scalar"
+
+
+def measured_traffic() -> dict:
+    """HBM bytes per launch for each linear and its quantizer, as measured by the two
+    rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) recorded in TRAFFIC_PROFILE. The
+    numbers are calibrated per counter against a 1 GiB copy kernel; that file gives the
+    commands and the calibration. Empty when the file is absent."""
+    path = os.path.join(ROOT, TRAFFIC_PROFILE)
+    out = {}
+    try:
+        lines = open(path).read().split("traffic_bytes_per_launch", 1)[1].split("```", 1)[0].split()
+    except (OSError, IndexError):
+        return out
+    for k, v in zip(lines[0::2], lines[1::2]):
+        out[k] = int(v)
+    return out
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -198,45 +223,51 @@ def main() -> int:
                 per[name]["quant_ms"].append(e0.elapsed_time(e1))
                 per[name]["gemm_ms"].append(e1.elapsed_time(e2))
     kernels = {}
+    units = []  # (key, kernel name, seconds per launch, algorithmic ops, algorithmic bytes)
     tot_ops = tot_gemm_s = 0.0
-    groups = {}  # kernel instantiation -> [ops, seconds, launches, bytes]
     for name, K, N, act in lin:
         gq = float(np.mean(per[name]["gemm_ms"])) * 1e-3
         qq = float(np.mean(per[name]["quant_ms"])) * 1e-3
         ops = 2.0 * M * N * K
-        gbytes = M * K + N * K + 4 * N + 4 * N + 4 * M + 4 * M * N
+        gbytes = M * K + N * K + 4 * M + 8 * N + 4 * M * N  # A, W, aS, wS + bias, f32 out
         qbytes = 4 * M * K + M * K + 4 * M
         kernels[name] = {
             "M": M, "K": K, "N": N, "act": "gelu" if act else "none",
+            "gemm_kernel": ctx.gemm_kernel_name(layers[0][name][0], M, act),
             "gemm_us": gq * 1e6, "gemm_tops": ops / gq / 1e12, "gemm_frac_int8_peak": ops / gq / PEAK_INT8_OPS,
-            "gemm_alg_gbps": gbytes / gq / 1e9,
+            "gemm_alg_gbps": gbytes / gq / 1e9, "gemm_frac_hbm": gbytes / gq / PEAK_HBM_BPS,
             "quant_us": qq * 1e6, "quant_gbps": qbytes / qq / 1e9, "quant_frac_hbm": qbytes / qq / PEAK_HBM_BPS,
         }
         tot_ops += ops * cfg.layers
         tot_gemm_s += gq * cfg.layers
-        kname = ctx.gemm_kernel_name(layers[0][name][0], M, act)
-        grp = groups.setdefault(kname, [0.0, 0.0, 0, 0.0])
-        grp[0] += ops * cfg.layers
-        grp[1] += gq * cfg.layers
-        grp[2] += cfg.layers
-        grp[3] += gbytes * cfg.layers
-    dom = max(groups, key=lambda k: groups[k][1])
-    d_ops, d_s, d_n, d_bytes = groups[dom]
-    achieved = d_ops / d_s
+        units.append((name, kernels[name]["gemm_kernel"], gq, ops, gbytes))
+        units.append(("quant_" + name, quant_kernel_name(K), qq, 0.0, qbytes))
+    # The dominant unit is the (kernel, shape) pair with the most time per step. Its
+    # bound is the roofline's: MFMA when its arithmetic intensity reaches the ridge
+    # point (peak ops / peak bytes), HBM below it.
+    key, kname, t, ops, nbytes = max(units, key=lambda u: u[2])
+    ridge = PEAK_INT8_OPS / PEAK_HBM_BPS
+    traffic = measured_traffic().get(key)
+    if ops > 0 and ops / nbytes >= ridge:
+        roof = {"bound": "mfma", "achieved": ops / t / 1e12, "peak": PEAK_INT8_OPS / 1e12, "unit": "TFLOP/s",
+                "frac": ops / t / PEAK_INT8_OPS}
+    else:
+        roof = {"bound": "hbm", "achieved": nbytes / t / 1e9, "peak": PEAK_HBM_BPS / 1e9, "unit": "GB/s",
+                "frac": nbytes / t / PEAK_HBM_BPS}
     roofline = {
-        "kernel": dom,
-        "bound": "mfma",
-        "achieved": achieved / 1e12,
-        "peak": PEAK_INT8_OPS / 1e12,
-        "unit": "TFLOP/s",
-        "frac": achieved / PEAK_INT8_OPS,
-        "traffic": None,
-        "ops": "int8 multiply-adds x2, algorithmic 2*M*N*K per launch",
-        "launches_per_step": d_n,
-        "avg_launch_us": d_s / d_n * 1e6,
-        "alg_bytes_per_launch": d_bytes / d_n,
-        "alg_hbm_frac": (d_bytes / d_s) / PEAK_HBM_BPS,
-        "frac_of_measured_mfma_peak": achieved / (ceilings["mfma_i8_tops"] * 1e12),
+        **roof,
+        "traffic": traffic,
+        "kernel": kname,
+        "shape": key,
+        "launches_per_step": cfg.layers,
+        "avg_launch_us": t * 1e6,
+        "alg_bytes_per_launch": nbytes,
+        "alg_ops_per_launch": ops,
+        "arithmetic_intensity": (ops / nbytes) if ops else 0.0,
+        "ridge_op_per_byte": ridge,
+        "int8_frac_of_peak": ops / t / PEAK_INT8_OPS,
+        "frac_of_measured_mfma_peak": ops / t / (ceilings["mfma_i8_tops"] * 1e12),
+        "traffic_source": TRAFFIC_PROFILE if traffic is not None else None,
     }
     result = {
         "metric": METRIC,

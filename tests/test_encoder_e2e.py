@@ -1,0 +1,128 @@
+"""End-to-end W8A8 encoder forward: pooled embeddings from the device linears vs the
+CPU reference composition ("final pooled embeddings must
+reach cosine >= 0.9999").
+
+The forward follows encoder/bert.go:300-368 operation for operation:
+  1. embeddings word + position (+ token type 0), then LayerNorm (eps 1e-12);
+  2. per layer:
+     - Q, K, V = h W + b;
+     - per-head scaled-dot-product attention (encoder/attention.go:81-130);
+     - O projection + bias, residual, LayerNorm;
+     - FFN-up + bias, then GELU;
+     - FFN-down + bias, residual, LayerNorm;
+  3. mean pooling (encoder/pooling.go:84-105) and L2Normalize (embed/pool.go:22-38).
+
+Each `s.mm(W) + addBias (+ gelu)` is one W8A8 linear: per-token int8 activations and
+per-channel int8 weights, the composition SURVEY.md describes for configs 1/4/5
+(vision/encoder.go:234-255 is the in-tree precedent). Q, K and V share one
+quantization of h and run as a single N = 3D linear (linalg.MatmulBTW8A8Batch,
+bit-identical to per-op).
+
+The two arms differ only in who computes the linears:
+  * reference: oracle.cpu_w8a8_linear, the C restatement of aikit's Go path;
+  * device: libenchip.so on the GPU, through the C ABI.
+The glue (attention, LayerNorm, pooling) is the oracle's in both arms, so any difference
+in the embeddings comes from the linears.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from aikit_amd import enchip, workloads
+
+pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.9999  # north_star
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def model_weights(cfg, seed, max_pos=512, type_vocab=2):
+    g = workloads.rng(seed)
+    D = cfg.hidden
+    w = {
+        "word": (g.standard_normal((cfg.vocab, D)) * 0.02).astype(np.float32),
+        "pos": (g.standard_normal((max_pos, D)) * 0.02).astype(np.float32),
+        "type": (g.standard_normal((type_vocab, D)) * 0.02).astype(np.float32),
+        "emb_ln": ((1 + g.standard_normal(D) * 0.02).astype(np.float32), (g.standard_normal(D) * 0.02).astype(np.float32)),
+        "layers": [],
+    }
+    for _ in range(cfg.layers):
+        lw = workloads.encoder_layer_weights(g, cfg)
+        lw["attn_ln"] = ((1 + g.standard_normal(D) * 0.02).astype(np.float32), (g.standard_normal(D) * 0.02).astype(np.float32))
+        lw["out_ln"] = ((1 + g.standard_normal(D) * 0.02).astype(np.float32), (g.standard_normal(D) * 0.02).astype(np.float32))
+        w["layers"].append(lw)
+    return w
+
+
+def encode(ids, w, cfg, linear):
+    """bert.go forward + mean pool + L2 for one sequence. linear(x, li, name) returns
+    act(W8A8(x, W_name) + b_name) as an f32 [M, N] array."""
+    L, D = len(ids), cfg.hidden
+    eps = 1e-12
+    h = np.empty((L, D), np.float32)
+    for i, t in enumerate(ids):
+        row = (w["word"][t] + w["pos"][i]).astype(np.float32)
+        h[i] = (row + w["type"][0]).astype(np.float32)
+    h = oracle.layer_norm(h, *w["emb_ln"], L, D, eps)
+    for li in range(cfg.layers):
+        qkv = linear(h, li, "qkv")
+        Q = np.ascontiguousarray(qkv[:, :D])
+        K = np.ascontiguousarray(qkv[:, D:2 * D])
+        V = np.ascontiguousarray(qkv[:, 2 * D:])
+        ctx = oracle.attention(Q, K, V, L, D, cfg.heads)
+        out = linear(ctx, li, "o")
+        h = oracle.layer_norm((h + out).astype(np.float32), *w["layers"][li]["attn_ln"], L, D, eps)
+        inter = linear(h, li, "ffn_up")
+        ffn = linear(inter, li, "ffn_down")
+        h = oracle.layer_norm((h + ffn).astype(np.float32), *w["layers"][li]["out_ln"], L, D, eps)
+    return oracle.l2_normalize(oracle.pool_mean(h, L, D))
+
+
+def run_both(ctx, workers, cfg, seqs, seed):
+    w = model_weights(cfg, seed)
+    handles = [{n: ctx.register_weight(v[0], v[1]) for n, v in lw.items() if n in ("qkv", "o", "ffn_up", "ffn_down")}
+               for lw in w["layers"]]
+    try:
+        def ref_linear(x, li, name):
+            wq, ws, b, act = w["layers"][li][name]
+            M, K = x.shape
+            return oracle.cpu_w8a8_linear(x, wq, ws, b, act, M, K, wq.shape[0], workers=workers).reshape(M, -1)
+
+        def dev_linear(x, li, name):
+            _, _, b, act = w["layers"][li][name]
+            return ctx.linear(handles[li][name], np.ascontiguousarray(x), bias=b, act=act)
+
+        for s, ids in enumerate(seqs):
+            say(f"{cfg.name} sequence {s} (L={len(ids)})")
+            ref = encode(ids, w, cfg, ref_linear)
+            dev = encode(ids, w, cfg, dev_linear)
+            cos = float(np.dot(ref.astype(np.float64), dev.astype(np.float64)) /
+                        (np.linalg.norm(ref.astype(np.float64)) * np.linalg.norm(dev.astype(np.float64))))
+            assert cos >= COS_MIN, f"{cfg.name} seq {s}: cosine {cos}"
+            # the linears are bit-exact, so the whole forward is too
+            assert np.array_equal(ref.view(np.uint32), dev.view(np.uint32)), f"{cfg.name} seq {s}: embeddings differ in bits"
+    finally:
+        for hs in handles:
+            for h in hs.values():
+                ctx.release_weight(h)
+
+
+def test_config1_minilm_l6_embeddings(ctx, workers):
+    # MiniLM-L6 shape, batch 8 x seq 128, ids uniform in [1000, 30000)
+    cfg = workloads.MINILM_L6
+    g = workloads.rng(11)
+    seqs = [g.integers(1000, 30000, size=cfg.seq) for _ in range(cfg.batch)]
+    run_both(ctx, workers, cfg, seqs, seed=101)
+
+
+def test_config4_bert_base_embedding(ctx, workers):
+    # BASELINE config 4 shape at full sequence length, one sequence (each sequence's
+    # forward is independent of the others in the batch; the full b64 linears are
+    # checked row by row in test_gpu_parity.py)
+    cfg = workloads.BERT_BASE
+    g = workloads.rng(12)
+    seqs = [g.integers(1000, 30000, size=cfg.seq)]
+    run_both(ctx, workers, cfg, seqs, seed=102)

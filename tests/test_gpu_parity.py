@@ -34,13 +34,17 @@ def bits(x):
 
 
 def assert_f32_parity(got, want, what):
-    """Bit-identical (NaN payloads aside), and the north-star 1e-5 max rel error."""
+    """Bit-identical (NaN payloads aside), and the north-star 1e-5 max rel error over
+    the finite values (infinities must match exactly)."""
     assert got.shape == want.shape, what
     nan = np.isnan(want)
     assert (np.isnan(got) == nan).all(), f"{what}: NaN mismatch"
     g, w = got[~nan], want[~nan]
-    denom = np.maximum(np.abs(w), np.finfo(np.float32).tiny)
-    rel = float(np.max(np.abs(g.astype(np.float64) - w) / denom)) if g.size else 0.0
+    fin = np.isfinite(w)
+    assert (g[~fin] == w[~fin]).all(), f"{what}: infinity mismatch"
+    gf, wf = g[fin], w[fin]
+    denom = np.maximum(np.abs(wf), np.finfo(np.float32).tiny)
+    rel = float(np.max(np.abs(gf.astype(np.float64) - wf) / denom)) if gf.size else 0.0
     assert rel <= REL_TOL, f"{what}: max rel err {rel:.3g} > {REL_TOL}"
     mism = np.flatnonzero(bits(g) != bits(w))
     assert mism.size == 0, f"{what}: {mism.size} elements differ in bits (first at {mism[:5]})"
@@ -309,3 +313,81 @@ def test_pre_quantized_matches_linear(ctx):
     finally:
         for h in hs:
             ctx.release_weight(h)
+
+
+# ------------------------------------------------------------------ epilogue branches and dispatch
+# (M, N) pairs that route to each GEMM kernel: M <= 32 runs gemv_w8a8; otherwise
+# gemm_w8a8_pt when N % 4 == 0 (and the K stages are even), gemm_w8a8 when not.
+KERNEL_ROUTES = [(8, 1024, "gemv"), (20, 1001, "gemv"), (300, 1024, "gemm_w8a8_pt"), (300, 1001, "gemm_w8a8<")]
+
+
+def _gelu_spread_scales(a, wq, target_std=3.0):
+    """Per-channel weight scales that put the pre-GELU values of every column at
+    std ~target_std, so ErfF32's three branches (|u| < 1, 1 <= |u| <= 4, |u| > 4,
+    u = x / sqrt(2)) all occur many times."""
+    M, K = a.shape
+    aq, a_s = oracle.quantize_activations(a, M, K)
+    y0 = (aq.astype(np.float64) @ wq.astype(np.float64).T) * a_s[:, None]
+    sd = np.maximum(y0.std(axis=0), 1e-6)
+    return (target_std / sd).astype(np.float32)
+
+
+@pytest.mark.parametrize("M,N,route", KERNEL_ROUTES)
+def test_gelu_every_branch(ctx, M, N, route):
+    g = workloads.rng(31 + M + N)
+    K = 768
+    a = workloads.activations(g, M, K)
+    a[M // 2] = 0  # an all-zero row (scale 0 -> +0 before bias)
+    wq, _ = workloads.int8_weights(g, N, K)
+    ws = _gelu_spread_scales(a, wq)
+    b = workloads.bias(g, N)
+    w = ctx.register_weight(wq, ws)
+    try:
+        assert route in ctx.gemm_kernel_name(w, M, enchip.ACT_GELU)
+        say(f"GELU branches M={M} N={N} via {route}")
+        got = ctx.linear(w, a, bias=b, act=enchip.ACT_GELU)
+    finally:
+        ctx.release_weight(w)
+    # the inputs exercise every branch (checked on the oracle's pre-GELU values)
+    u = np.abs(oracle.w8a8_linear(a, wq, ws, b, 0, M, K, N).astype(np.float64)) / np.sqrt(2.0)
+    n = u.size
+    assert (u < 1).sum() > 0.05 * n and ((u >= 1) & (u <= 4)).sum() > 0.05 * n and (u > 4).sum() > 0.01 * n
+    assert_f32_parity(got, oracle.w8a8_linear(a, wq, ws, b, 1, M, K, N), f"GELU {route}")
+
+
+@pytest.mark.parametrize("M,N,route", KERNEL_ROUTES)
+@pytest.mark.parametrize("act", [0, 1])
+def test_special_weight_scales(ctx, M, N, route, act):
+    # Scales the quantizer never produces but the ABI accepts: inf, NaN, negative,
+    # zero, subnormal, huge. With zero activation rows these reach the reference's
+    # "+0 when aScale == 0" rule (linalg/quant.go:291-293) with every sign of wS.
+    g = workloads.rng(41 + M + N + act)
+    K = 768
+    a = workloads.activations(g, M, K)
+    a[0] = 0
+    a[M - 1] = 0
+    wq, ws = workloads.int8_weights(g, N, K)
+    special = np.array([np.inf, -np.inf, np.nan, -1e-3, 0.0, -0.0, 1e-40, 3e38, -3e38], np.float32)
+    ws[:special.size] = special
+    ws[N - special.size:] = special
+    b = workloads.bias(g, N)
+    w = ctx.register_weight(wq, ws)
+    try:
+        say(f"special scales M={M} N={N} act={act} via {route}")
+        got = ctx.linear(w, a, bias=b, act=act)
+    finally:
+        ctx.release_weight(w)
+    assert_f32_parity(got, oracle.w8a8_linear(a, wq, ws, b, act, M, K, N), f"special scales {route}")
+
+
+def test_kernel_name_matches_dispatch(ctx):
+    g = workloads.rng(51)
+    for M, N, route in KERNEL_ROUTES:
+        wq, ws = workloads.int8_weights(g, N, 768)
+        w = ctx.register_weight(wq, ws)
+        try:
+            for act in (0, 1):
+                name = ctx.gemm_kernel_name(w, M, act)
+                assert route in name, (M, N, name)
+        finally:
+            ctx.release_weight(w)

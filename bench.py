@@ -125,12 +125,91 @@ def cpu_baseline(layer_w, cfg, seconds: float):
     }
 
 
+def other_configs(ctx, torch, stream, ceilings):
+    """BASELINE configs 2 and 3, timed with HIP events on the launch stream.
+
+    * config 2: the isolated W8A8 linear (M=4096, K=768 -> N=3072, bias + GELU), as
+      quantize + GEMM per call. Judged on int8 TOPS.
+    * config 3: the small-M GEMV (M=16, K=768 -> N=768 and N=3072). Each call reads a
+      different registered copy of the weights, and the copies total > 2x the 256 MB
+      MALL, so every call streams its weights from HBM. Judged on HBM GB/s over the
+      algorithmic bytes N*K + M*K + 4M + 8N + 4MN.
+    """
+    import numpy as np
+
+    from aikit_amd import workloads
+
+    out = {}
+    c2 = workloads.LINEAR_CFG2
+    M, K, N = c2["M"], c2["K"], c2["N"]
+    g = workloads.rng(2)
+    wq, ws = workloads.int8_weights(g, N, K)
+    h = ctx.register_weight(wq, ws)
+    with torch.cuda.stream(stream):
+        a = torch.from_numpy(workloads.activations(g, M, K)).cuda()
+        b = torch.from_numpy(workloads.bias(g, N)).cuda()
+        dst = torch.empty((M, N), device="cuda", dtype=torch.float32)
+    torch.cuda.synchronize()
+    sp = stream.cuda_stream
+    for _ in range(5):
+        ctx.linear_dev(h, a.data_ptr(), M, b.data_ptr(), c2["act"], dst.data_ptr(), sp)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 50
+    e0.record(stream)
+    for _ in range(reps):
+        ctx.linear_dev(h, a.data_ptr(), M, b.data_ptr(), c2["act"], dst.data_ptr(), sp)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / reps
+    ops = 2.0 * M * N * K
+    out["config2_isolated_linear"] = {
+        "M": M, "K": K, "N": N, "act": "gelu", "us_per_call": t * 1e6, "int8_tops": ops / t / 1e12,
+        "frac_int8_peak": ops / t / PEAK_INT8_OPS, "kernel": ctx.gemm_kernel_name(h, M, c2["act"]),
+        "note": "quantize + GEMM + fused epilogue per call, activations resident in HBM"}
+    ctx.release_weight(h)
+
+    for c3 in workloads.GEMV_CFG3:
+        M, K, N = c3["M"], c3["K"], c3["N"]
+        g = workloads.rng(3)
+        wq, ws = workloads.int8_weights(g, N, K)
+        copies = max(2, int(np.ceil(600e6 / (N * K))))  # > 2 x 256 MB MALL of distinct weights
+        hs = [ctx.register_weight(wq, ws) for _ in range(copies)]
+        with torch.cuda.stream(stream):
+            a = torch.from_numpy(workloads.activations(g, M, K)).cuda()
+            b = torch.from_numpy(workloads.bias(g, N)).cuda()
+            aq = torch.empty((M, K), device="cuda", dtype=torch.int8)
+            asc = torch.empty(M, device="cuda", dtype=torch.float32)
+            dst = torch.empty((M, N), device="cuda", dtype=torch.float32)
+        torch.cuda.synchronize()
+        ctx.quant_rows_dev(a.data_ptr(), M, K, aq.data_ptr(), asc.data_ptr(), sp, ldq=K)
+        for hh in hs[:8]:
+            ctx.pre_dev(hh, aq.data_ptr(), K, M, asc.data_ptr(), b.data_ptr(), c3["act"], dst.data_ptr(), sp)
+        e0.record(stream)
+        for hh in hs:
+            ctx.pre_dev(hh, aq.data_ptr(), K, M, asc.data_ptr(), b.data_ptr(), c3["act"], dst.data_ptr(), sp)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / len(hs)
+        nbytes = N * K + M * K + 4 * M + 8 * N + 4 * M * N
+        out[f"config3_gemv_n{N}"] = {
+            "M": M, "K": K, "N": N, "us_per_call": t * 1e6, "hbm_gbps": nbytes / t / 1e9,
+            "frac_hbm_peak": nbytes / t / PEAK_HBM_BPS,
+            "frac_measured_read_ceiling": nbytes / t / 1e9 / ceilings["hbm_read_gbps"],
+            "weight_copies": len(hs), "weight_set_mb": len(hs) * N * K / 1e6,
+            "kernel": ctx.gemm_kernel_name(hs[0], M, c3["act"]),
+            "note": "GEMM on pre-quantized activations (enchip_w8a8_pre_dev), one distinct weight copy per call"}
+        for hh in hs:
+            ctx.release_weight(hh)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length (0 = skip)")
+    ap.add_argument("--no-other-configs", action="store_true", help="skip the config 2 / config 3 measurements")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the W8A8 path is not sharded across GPUs; "
@@ -302,6 +381,9 @@ def main() -> int:
         "measured_ceilings": ceilings,
         "device": info,
     }
+    if not args.no_other_configs:
+        log("configs 2 and 3 (isolated linear, small-M GEMV over a rotating > 2x MALL weight set)")
+        result["other_configs"] = other_configs(ctx, torch, stream, ceilings)
     if args.cpu_seconds > 0:
         log(f"CPU baseline ({args.cpu_seconds:.0f}s sample, {host_threads()} threads)")
         result["cpu_baseline"] = cpu_baseline(layer0_host, cfg, args.cpu_seconds)

@@ -56,6 +56,48 @@ def measured_traffic() -> dict:
     return out
 
 
+class HipEvents:
+    """Timing events recorded on a raw HIP stream (the one the enchip kernels are
+    launched on), through libamdhip64, the runtime torch has already loaded.
+    torch.cuda.Event records only on torch's current stream."""
+
+    def __init__(self):
+        import ctypes
+
+        self.ct = ctypes
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventRecordWithFlags.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.events = []
+
+    def create(self):
+        ev = self.ct.c_void_p()
+        rc = self.lib.hipEventCreate(self.ct.byref(ev))
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreate: {rc}")
+        self.events.append(ev)
+        return ev
+
+    def record(self, ev, stream_ptr: int):
+        rc = self.lib.hipEventRecordWithFlags(ev, self.ct.c_void_p(stream_ptr), 0)
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecordWithFlags: {rc}")
+
+    def elapsed_ms(self, e0, e1) -> float:
+        ms = self.ct.c_float()
+        rc = self.lib.hipEventElapsedTime(self.ct.byref(ms), e0, e1)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime: {rc}")
+        return ms.value
+
+    def close(self):
+        for ev in self.events:
+            self.lib.hipEventDestroy(ev)
+        self.events = []
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -210,6 +252,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length (0 = skip)")
     ap.add_argument("--no-other-configs", action="store_true", help="skip the config 2 / config 3 measurements")
+    ap.add_argument("--graph", type=int, default=0,
+                    help="1: replay each timed step as a captured HIP graph; 0 (default): eager launches. "
+                         "Measured equal on MI355X (launch overhead hides behind the kernels)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the W8A8 path is not sharded across GPUs; "
@@ -260,19 +305,21 @@ def main() -> int:
     torch.cuda.synchronize()
     lin = cfg.linears()
 
+    hev = HipEvents()
+
     def run_step(evs=None):
         for li in range(cfg.layers):
             for j, (name, K, N, act) in enumerate(lin):
                 h, b, _ = layers[li][name]
                 x = outs["ffn_up"] if name == "ffn_down" else x_in[name]
                 if evs is not None:
-                    evs[li][j][0].record(stream)
+                    hev.record(evs[li][j][0], sptr)
                 ctx.quant_rows_dev(x.data_ptr(), M, K, aq.data_ptr(), asc.data_ptr(), sptr, ldq=K)
                 if evs is not None:
-                    evs[li][j][1].record(stream)
+                    hev.record(evs[li][j][1], sptr)
                 ctx.pre_dev(h, aq.data_ptr(), K, M, asc.data_ptr(), b.data_ptr(), act, outs[name].data_ptr(), sptr)
                 if evs is not None:
-                    evs[li][j][2].record(stream)
+                    hev.record(evs[li][j][2], sptr)
 
     with torch.cuda.stream(stream):
         for _ in range(args.warmup):
@@ -280,18 +327,49 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"warmup {args.warmup} steps done")
 
-    events = [[[[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in lin] for _ in range(cfg.layers)]
-              for _ in range(args.steps)]
+    # Timed region 1 (value): K steps with nothing between the kernels. With --graph 1
+    # each step is replayed as a captured HIP graph: the same 96 kernels with the same
+    # arguments, without per-launch host overhead between them.
+    graphs = None
+    if args.graph:
+        try:
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=stream):
+                run_step()
+            gr.replay()  # untimed check replay
+            torch.cuda.synchronize()
+            graphs = gr
+        except Exception as exc:  # capture unsupported: time eager launches instead
+            log(f"graph capture failed ({exc}); timing eager launches")
+            graphs = None
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     with torch.cuda.stream(stream):
         for s in range(args.steps):
-            run_step(events[s])
+            if graphs is not None:
+                graphs.replay()
+            else:
+                run_step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
     ms_per_step = elapsed * 1e3 / args.steps
     seqs_per_s = cfg.batch * args.steps / elapsed
-    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {seqs_per_s:.1f} seqs/s")
+    launch_mode = "HIP graph per step" if graphs is not None else "eager"
+    log(f"timed {args.steps} steps ({launch_mode}): {ms_per_step:.3f} ms/step, {seqs_per_s:.1f} seqs/s")
+
+    # Timed region 2 (kernel durations): K eager steps of the same kernels with HIP
+    # events recorded on the launch stream around every launch (events cannot be read
+    # back from inside a replayed graph on this runtime).
+    events = [[[[hev.create() for _ in range(3)] for _ in lin] for _ in range(cfg.layers)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t_ev = time.perf_counter()
+    with torch.cuda.stream(stream):
+        for s in range(args.steps):
+            run_step(events[s])
+    torch.cuda.synchronize()
+    ev_elapsed = time.perf_counter() - t_ev
+    log(f"timed {args.steps} eager steps with per-kernel events: {ev_elapsed * 1e3 / args.steps:.3f} ms/step")
 
     # ---- per-kernel durations from the events of the timed region
     per = {name: {"quant_ms": [], "gemm_ms": []} for name, _, _, _ in lin}
@@ -299,8 +377,8 @@ def main() -> int:
         for li in range(cfg.layers):
             for j, (name, _, _, _) in enumerate(lin):
                 e0, e1, e2 = events[s][li][j]
-                per[name]["quant_ms"].append(e0.elapsed_time(e1))
-                per[name]["gemm_ms"].append(e1.elapsed_time(e2))
+                per[name]["quant_ms"].append(hev.elapsed_ms(e0, e1))
+                per[name]["gemm_ms"].append(hev.elapsed_ms(e1, e2))
     kernels = {}
     units = []  # (key, kernel name, seconds per launch, algorithmic ops, algorithmic bytes)
     tot_ops = tot_gemm_s = 0.0
@@ -347,6 +425,9 @@ def main() -> int:
         "int8_frac_of_peak": ops / t / PEAK_INT8_OPS,
         "frac_of_measured_mfma_peak": ops / t / (ceilings["mfma_i8_tops"] * 1e12),
         "traffic_source": TRAFFIC_PROFILE if traffic is not None else None,
+        "timing": "HIP events around each launch on the launch stream, over a second K-step timed region of "
+                  "the same kernels; value's region has no events between launches (144 event records per "
+                  "step cost ~0.5 ms)",
     }
     result = {
         "metric": METRIC,
@@ -372,6 +453,7 @@ def main() -> int:
             "tokens_per_step": M,
             "parallelism": "single GPU",
             "seeds": {"weights": 2024, "activations": 7},
+            "launch": launch_mode,
         },
         "gemm_tops": tot_ops / tot_gemm_s / 1e12,
         "gemm_frac_int8_peak": tot_ops / tot_gemm_s / PEAK_INT8_OPS,
@@ -389,6 +471,8 @@ def main() -> int:
         result["cpu_baseline"] = cpu_baseline(layer0_host, cfg, args.cpu_seconds)
     else:
         result["cpu_baseline"] = None
+    graphs = None
+    hev.close()
     ctx.close()
     print(json.dumps(result), flush=True)
     return 0

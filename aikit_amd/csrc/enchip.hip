@@ -108,26 +108,36 @@ int check_launch(enchip_ctx *c, const char *what) {
     return ENCHIP_OK;
 }
 
-// Quantizes d_a[M,K] into q[M][ldq] (zero-padded to ldq) and scale[M].
+// Quantizes d_a[M,K] into q (zero-padded to ldq) and scale[M]: row-major q[M][ldq], or
+// fragment-major (kernels.h frag_off) when frag.
 int launch_quant(enchip_ctx *c, const float *d_a, int64_t M, int64_t K, int8_t *q, int64_t ldq,
-                 float *scale, hipStream_t s) {
+                 float *scale, hipStream_t s, bool frag = false) {
     if (M == 0) return ENCHIP_OK;
-    const dim3 grid((unsigned)((M + 3) / 4)), block(256);
     const bool vec = (K % 4 == 0) && (ldq % 4 == 0) && ((uintptr_t)d_a % 16 == 0) &&
-                     ((uintptr_t)q % 4 == 0) && K > 0 && K <= 256 * 16;
+                     ((uintptr_t)q % (frag ? 16 : 4) == 0) && K > 0 && (frag ? ldq : K) <= 256 * 16;
     if (vec) {
-        const int ch = (int)((K + 255) / 256);
+        const int ch = (int)(((frag ? ldq : K) + 255) / 256);
         const int k = (int)K;
+        const dim3 grid((unsigned)(frag ? (M + 7) / 8 : (M + 3) / 4)), block(frag ? 512 : 256);
         switch (ch) {
-#define QCASE(N) \
-    case N: hipLaunchKernelGGL(enchip::quant_rows_vec<N>, grid, block, 0, s, d_a, q, ldq, scale, M, k); break;
+#define QCASE(N)                                                                                           \
+    case N:                                                                                                \
+        if (frag)                                                                                          \
+            hipLaunchKernelGGL(enchip::quant_rows_frag<N>, grid, block, 0, s, d_a, q, ldq, scale, M, k);   \
+        else                                                                                               \
+            hipLaunchKernelGGL(enchip::quant_rows_vec<N>, grid, block, 0, s, d_a, q, ldq, scale, M, k);    \
+        break;
             QCASE(1) QCASE(2) QCASE(3) QCASE(4) QCASE(5) QCASE(6) QCASE(7) QCASE(8)
             QCASE(9) QCASE(10) QCASE(11) QCASE(12) QCASE(13) QCASE(14) QCASE(15) QCASE(16)
 #undef QCASE
             default: return fail(c, ENCHIP_ERR_ARG, "quant: bad chunk count %d", ch);
         }
     } else {
-        hipLaunchKernelGGL(enchip::quant_rows_scalar, grid, block, 0, s, d_a, q, ldq, scale, M, K);
+        const dim3 grid((unsigned)((M + 3) / 4)), block(256);
+        if (frag)
+            hipLaunchKernelGGL(enchip::quant_rows_scalar<true>, grid, block, 0, s, d_a, q, ldq, scale, M, K);
+        else
+            hipLaunchKernelGGL(enchip::quant_rows_scalar<false>, grid, block, 0, s, d_a, q, ldq, scale, M, K);
     }
     return check_launch(c, "quant_rows");
 }
@@ -148,14 +158,29 @@ bool use_wide_tile(const enchip_ctx *c, const Weight &w, int64_t M) {
     return t256 >= 2 * (int64_t)c->num_cus;
 }
 
-// gemm_w8a8_pt's preconditions (gemm_persistent.h): an even number of 64-deep K
-// stages, 16-byte aligned A rows, 32-bit byte offsets into A and the weights, and
-// 16-byte row-major output stores (N and the output pitch multiples of 4).
-bool use_persistent(const Weight &w, const void *aq, int64_t lda, const void *out, int64_t ldo, int64_t M) {
+// Ring depth of gemm_w8a8_pt: 2 stages, so the 64-deep K stages must be even (0 = not
+// usable). A 3-stage ring speeds up the bare main loop by 2-9% on MI355X, but with the
+// epilogue its register pressure spills and the whole kernel is no faster.
+int pt_ring(const Weight &w) {
+    return (w.Kp / enchip::PT_BK) % enchip::PT_PW == 0 ? enchip::PT_PW : 0;
+}
+
+// gemm_w8a8_pt's preconditions (gemm_persistent.h): a usable ring depth, 16-byte
+// aligned A, 32-bit byte offsets into A and the weights, and 16-byte row-major output
+// stores (N and the output pitch multiples of 4). Fragment-major A (af) has pitch Kp
+// and is read up to the next multiple of PT_BM rows.
+bool use_persistent(const Weight &w, const void *aq, int64_t lda, const void *out, int64_t ldo, int64_t M,
+                    bool af) {
     const int64_t lim = (int64_t)1 << 31;
-    return (w.Kp % (enchip::PT_BK * enchip::PT_PW)) == 0 && (lda % 16) == 0 && ((uintptr_t)aq % 16) == 0 &&
-           (M - 1) * lda + w.Kp < lim && w.Np * w.Kp < lim && (w.N % 4) == 0 && (ldo % 4) == 0 &&
-           ((uintptr_t)out % 16) == 0;
+    const int64_t a_end = af ? round_up(M, enchip::PT_BM) * w.Kp : (M - 1) * lda + w.Kp;
+    return pt_ring(w) != 0 && (lda % 16) == 0 && (!af || lda == w.Kp) && ((uintptr_t)aq % 16) == 0 &&
+           a_end < lim && w.Np * w.Kp < lim && (w.N % 4) == 0 && (ldo % 4) == 0 && ((uintptr_t)out % 16) == 0;
+}
+
+// True when a GEMM on activations this library quantizes itself (into the context
+// scratch, pitch Kp) runs gemm_w8a8_pt, which then takes them fragment-major.
+bool route_af(const enchip_ctx *c, const Weight &w, int64_t M, const void *out, int64_t ldo) {
+    return M > c->small_m && use_persistent(w, nullptr, w.Kp, out, ldo, M, true);
 }
 
 int persistent_grid(const enchip_ctx *c, int64_t tiles) {
@@ -163,21 +188,29 @@ int persistent_grid(const enchip_ctx *c, int64_t tiles) {
     return (int)std::min<int64_t>(full, (tiles + 7) / 8 * 8);
 }
 
+template <int PW, int EPI, bool AF>
+void launch_pt(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, const float *as, const float *bias,
+               void *out, int64_t ldo, int64_t M, hipStream_t s) {
+    using namespace enchip;
+    const int tilesM = (int)((M + PT_BM - 1) / PT_BM), tilesN = (int)((w.N + PT_BN - 1) / PT_BN);
+    const int64_t tiles = (int64_t)tilesM * tilesN;
+    hipLaunchKernelGGL((gemm_w8a8_pt<PT_BM, PT_BN, PT_BK, PW, EPI, AF>), dim3(persistent_grid(c, tiles)), dim3(256),
+                       0, s, aq, lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp, tilesN,
+                       (int)tiles);
+}
+
+// af: aq is fragment-major (the caller checked route_af); otherwise row-major at pitch lda.
 template <int EPI>
 void launch_gemm_epi(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, const float *as,
-                     const float *bias, void *out, int64_t ldo, int64_t M, hipStream_t s) {
+                     const float *bias, void *out, int64_t ldo, int64_t M, hipStream_t s, bool af) {
+    if (af || (M > c->small_m && use_persistent(w, aq, lda, out, ldo, M, false))) {
+        if (af) launch_pt<enchip::PT_PW, EPI, true>(c, w, aq, lda, as, bias, out, ldo, M, s);
+        else launch_pt<enchip::PT_PW, EPI, false>(c, w, aq, lda, as, bias, out, ldo, M, s);
+        return;
+    }
     if (M <= c->small_m) {
         hipLaunchKernelGGL((enchip::gemv_w8a8<EPI>), dim3((unsigned)((w.N + 31) / 32)), dim3(256), 0, s, aq,
                            lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp);
-        return;
-    }
-    if (use_persistent(w, aq, lda, out, ldo, M)) {
-        using namespace enchip;
-        const int tilesM = (int)((M + PT_BM - 1) / PT_BM), tilesN = (int)((w.N + PT_BN - 1) / PT_BN);
-        const int64_t tiles = (int64_t)tilesM * tilesN;
-        hipLaunchKernelGGL((gemm_w8a8_pt<PT_BM, PT_BN, PT_BK, PT_PW, EPI>), dim3(persistent_grid(c, tiles)), dim3(256),
-                           0, s, aq, lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp, tilesN,
-                           (int)tiles);
         return;
     }
     if (use_wide_tile(c, w, M))
@@ -187,13 +220,13 @@ void launch_gemm_epi(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t l
 }
 
 int launch_gemm(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, const float *as,
-                const float *bias, int epi, void *out, int64_t ldo, int64_t M, hipStream_t s) {
+                const float *bias, int epi, void *out, int64_t ldo, int64_t M, hipStream_t s, bool af = false) {
     if (M == 0) return ENCHIP_OK;
     switch (epi) {
-        case enchip::EPI_I32: launch_gemm_epi<enchip::EPI_I32>(c, w, aq, lda, as, bias, out, ldo, M, s); break;
-        case enchip::EPI_F32: launch_gemm_epi<enchip::EPI_F32>(c, w, aq, lda, as, bias, out, ldo, M, s); break;
+        case enchip::EPI_I32: launch_gemm_epi<enchip::EPI_I32>(c, w, aq, lda, as, bias, out, ldo, M, s, af); break;
+        case enchip::EPI_F32: launch_gemm_epi<enchip::EPI_F32>(c, w, aq, lda, as, bias, out, ldo, M, s, af); break;
         case enchip::EPI_F32_GELU:
-            launch_gemm_epi<enchip::EPI_F32_GELU>(c, w, aq, lda, as, bias, out, ldo, M, s);
+            launch_gemm_epi<enchip::EPI_F32_GELU>(c, w, aq, lda, as, bias, out, ldo, M, s, af);
             break;
         default: return fail(c, ENCHIP_ERR_ARG, "bad epilogue %d", epi);
     }
@@ -306,11 +339,14 @@ int enchip_gemm_kernel_name(enchip_ctx *ctx, enchip_weight h, int64_t M, int act
     if (!buf || len <= 0) return fail(ctx, ENCHIP_ERR_ARG, "gemm_kernel_name: bad buffer");
     const int epi = act_code(act);
     char name[96];
-    if (M <= ctx->small_m)
+    if (route_af(ctx, *w, M, nullptr, w->N))
+        snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, true>", enchip::PT_BM, enchip::PT_BN,
+                 enchip::PT_BK, pt_ring(*w), epi);
+    else if (M <= ctx->small_m)
         snprintf(name, sizeof name, "enchip::gemv_w8a8<%d>", epi);
-    else if (use_persistent(*w, nullptr, w->Kp, nullptr, w->N, M))
-        snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d>", enchip::PT_BM, enchip::PT_BN,
-                 enchip::PT_BK, enchip::PT_PW, epi);
+    else if (use_persistent(*w, nullptr, w->Kp, nullptr, w->N, M, false))
+        snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, false>", enchip::PT_BM, enchip::PT_BN,
+                 enchip::PT_BK, pt_ring(*w), epi);
     else if (use_wide_tile(ctx, *w, M))
         snprintf(name, sizeof name, "enchip::gemm_w8a8<128, 256, %d, 2>", epi);
     else
@@ -418,6 +454,55 @@ int enchip_w8a8_pre_dev(enchip_ctx *ctx, enchip_weight h, const int8_t *d_aq, in
     return launch_gemm(ctx, *w, d_aq, ldq, d_ascale, d_bias, act_code(act), d_dst, w->N, M, s);
 }
 
+int enchip_frag_route(enchip_ctx *ctx, enchip_weight h, int64_t M, int64_t *ldq) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    Weight *w;
+    int rc = find_weight(ctx, h, &w);
+    if (rc) return 0;
+    if (ldq) *ldq = w->Kp;
+    return (M > 0 && M <= ((int64_t)1 << 30) && route_af(ctx, *w, M, nullptr, w->N)) ? 1 : 0;
+}
+
+int enchip_quant_rows_frag_dev(enchip_ctx *ctx, const float *d_a, int64_t M, int64_t K, int8_t *d_aq, int64_t ldq,
+                               float *d_ascale, void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (M < 0 || K < 0 || K > kMaxK || ldq < K || ldq % 64 != 0 || ldq < 64)
+        return fail(ctx, ENCHIP_ERR_ARG, "quant_frag: bad shape M=%lld K=%lld ldq=%lld (ldq a multiple of 64 >= K)",
+                    (long long)M, (long long)K, (long long)ldq);
+    if (M == 0) return ENCHIP_OK;
+    if ((K > 0 && !d_a) || !d_aq || !d_ascale) return fail(ctx, ENCHIP_ERR_ARG, "quant_frag: null pointer");
+    if ((uintptr_t)d_aq % 16 != 0) return fail(ctx, ENCHIP_ERR_ARG, "quant_frag: d_aq must be 16-byte aligned");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    return launch_quant(ctx, d_a, M, K, d_aq, ldq, d_ascale, s, true);
+}
+
+int enchip_w8a8_pre_frag_dev(enchip_ctx *ctx, enchip_weight h, const int8_t *d_aq, int64_t ldq, int64_t M,
+                             const float *d_ascale, const float *d_bias, int act, float *d_dst, void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    Weight *w;
+    int rc = find_weight(ctx, h, &w);
+    if (rc) return rc;
+    if (M < 0 || M > ((int64_t)1 << 30)) return fail(ctx, ENCHIP_ERR_ARG, "pre_frag: bad M=%lld", (long long)M);
+    if (ldq != w->Kp)
+        return fail(ctx, ENCHIP_ERR_ARG, "pre_frag: ldq=%lld must equal the padded K %lld", (long long)ldq, (long long)w->Kp);
+    if (act != ENCHIP_ACT_NONE && act != ENCHIP_ACT_GELU) return fail(ctx, ENCHIP_ERR_ARG, "pre_frag: bad act %d", act);
+    if (M == 0) return ENCHIP_OK;
+    if (!d_aq || !d_ascale || !d_dst) return fail(ctx, ENCHIP_ERR_ARG, "pre_frag: null pointer");
+    if ((uintptr_t)d_aq % 16 != 0) return fail(ctx, ENCHIP_ERR_ARG, "pre_frag: d_aq must be 16-byte aligned");
+    if (!route_af(ctx, *w, M, d_dst, w->N))
+        return fail(ctx, ENCHIP_ERR_ARG,
+                    "pre_frag: M=%lld N=%lld has no fragment-major GEMM route (needs M > %lld, N %% 4 == 0, a "
+                    "16-byte aligned d_dst); use enchip_w8a8_pre_dev",
+                    (long long)M, (long long)w->N, (long long)ctx->small_m);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    return launch_gemm(ctx, *w, d_aq, ldq, d_ascale, d_bias, act_code(act), d_dst, w->N, M, s, true);
+}
+
 int enchip_quant_rows(enchip_ctx *ctx, const float *a, int64_t M, int64_t K, int8_t *aq, float *ascale) {
     if (!ctx) return ENCHIP_ERR_ARG;
     std::lock_guard<std::mutex> g(ctx->mu);
@@ -523,8 +608,9 @@ int enchip_w8a8_linear_dev(enchip_ctx *ctx, enchip_weight h, const float *d_a, i
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     if ((rc = ensure_act_scratch(ctx, M, w->Kp))) return rc;
-    if ((rc = launch_quant(ctx, d_a, M, w->K, ctx->d_aq, w->Kp, ctx->d_as, s))) return rc;
-    return launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, d_bias, act_code(act), d_dst, w->N, M, s);
+    const bool af = route_af(ctx, *w, M, d_dst, w->N);
+    if ((rc = launch_quant(ctx, d_a, M, w->K, ctx->d_aq, w->Kp, ctx->d_as, s, af))) return rc;
+    return launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, d_bias, act_code(act), d_dst, w->N, M, s, af);
 }
 
 int enchip_w8a8_linear(enchip_ctx *ctx, enchip_weight h, const float *a, int64_t M, const float *bias, int act,
@@ -549,12 +635,13 @@ int enchip_w8a8_linear(enchip_ctx *ctx, enchip_weight h, const float *a, int64_t
     hipStream_t s = ctx->stream;
     if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
     if (bias) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_bias, bias, (size_t)N * sizeof(float), hipMemcpyHostToDevice, s));
-    if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, w->Kp, ctx->d_as, s))) return rc;
+    const bool af = route_af(ctx, *w, M, ctx->d_dst, N) && (!acc_debug || route_af(ctx, *w, M, ctx->d_acc, N));
+    if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, w->Kp, ctx->d_as, s, af))) return rc;
     if ((rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, bias ? ctx->d_bias : nullptr, act_code(act),
-                          ctx->d_dst, N, M, s)))
+                          ctx->d_dst, N, M, s, af)))
         return rc;
     if (acc_debug &&
-        (rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, nullptr, enchip::EPI_I32, ctx->d_acc, N, M, s)))
+        (rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, nullptr, enchip::EPI_I32, ctx->d_acc, N, M, s, af)))
         return rc;
     HIP_TRY(ctx, hipMemcpyAsync(dst, ctx->d_dst, out_bytes, hipMemcpyDeviceToHost, s));
     if (acc_debug) HIP_TRY(ctx, hipMemcpyAsync(acc_debug, ctx->d_acc, out_bytes, hipMemcpyDeviceToHost, s));
@@ -589,13 +676,16 @@ int enchip_w8a8_batch(enchip_ctx *ctx, const float *a, int64_t M, int64_t K, con
     if ((rc = ensure_act_scratch(ctx, M, Kp))) return rc;
     hipStream_t s = ctx->stream;
     if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
-    if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, Kp, ctx->d_as, s))) return rc;
+    // one quantization serves every op, so its layout must suit all of them
+    bool af = true;
+    for (int i = 0; i < nops; ++i) af = af && route_af(ctx, *ws[(size_t)i], M, ctx->d_dst, ws[(size_t)i]->N);
+    if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, Kp, ctx->d_as, s, af))) return rc;
     for (int i = 0; i < nops; ++i) {
         const Weight &w = *ws[(size_t)i];
         if (ops[i].bias)
             HIP_TRY(ctx, hipMemcpyAsync(ctx->d_bias, ops[i].bias, (size_t)w.N * sizeof(float), hipMemcpyHostToDevice, s));
         if ((rc = launch_gemm(ctx, w, ctx->d_aq, Kp, ctx->d_as, ops[i].bias ? ctx->d_bias : nullptr,
-                              act_code(ops[i].act), ctx->d_dst, w.N, M, s)))
+                              act_code(ops[i].act), ctx->d_dst, w.N, M, s, af)))
             return rc;
         HIP_TRY(ctx, hipMemcpyAsync(ops[i].dst, ctx->d_dst, (size_t)(M * w.N) * sizeof(float), hipMemcpyDeviceToHost, s));
         // The next op reuses d_bias / d_dst: wait for this op's download.

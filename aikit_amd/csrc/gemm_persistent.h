@@ -6,9 +6,13 @@
 //   * W fragments go HBM -> registers directly. The weights are pre-swizzled
 //     fragment-major, so each load is 64 lanes x 16 contiguous bytes. Each wave owns its
 //     64 output channels, so nothing is shared and nothing passes through LDS.
-//   * A (row-major int8 activations) is staged through two LDS slots as 1 KiB
-//     fragments in MFMA operand order. All 4 waves read all of it.
-//   * One ring of PW stages carries both operands. Its refill loads are unconditional
+//   * A is staged through two LDS slots as 1 KiB fragments in MFMA operand order, and
+//     all 4 waves read all of it. With AF the activations are already fragment-major
+//     (quant_rows_*<FRAG>): each load is 64 lanes x 16 contiguous bytes, like the
+//     weights'. Without AF they are row-major int8 at pitch lda, and each load gathers
+//     32 rows x 32 bytes (measured 15-25% slower main loop on MI355X).
+//   * One ring of PW stages (the loads for stage t + PW are issued during stage t)
+//     carries both operands. Its refill loads are unconditional
 //     and wrap into the next tile's first stages, so:
 //       - the compiler's wait counts stay exact;
 //       - the next tile's data is in flight during the epilogue.
@@ -37,7 +41,8 @@
 
 namespace enchip {
 
-// Tile geometry of the persistent kernel (the host checks its preconditions).
+// Tile geometry and ring depth of the persistent kernel (the host checks its
+// preconditions).
 constexpr int PT_BM = 128, PT_BN = 256, PT_BK = 64, PT_PW = 2;
 
 // 16-byte nontemporal store of 4 output words. The f32 outputs are written once and
@@ -48,7 +53,7 @@ __device__ __forceinline__ void store_nt(void *p, int4 v) {
     __builtin_nontemporal_store(t, reinterpret_cast<i32x4 *>(p));
 }
 
-template <int BM, int BN, int BK, int PW, int EPI>
+template <int BM, int BN, int BK, int PW, int EPI, bool AF>
 __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
     const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ Wf,
     const float *__restrict__ aS, const float *__restrict__ wS, const float *__restrict__ bias,
@@ -88,19 +93,24 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
     // 32-bit byte offsets (host guarantees M*lda and Np*Kp fit).
     uint32_t aoff_c[FAW], aoff_x[FAW];  // this lane's A rows: current / next tile
     uint32_t woff_c, woff_x;
-    uint32_t acol[FAW];
+    uint32_t acol[FAW];  // this lane's offset within its A row-block (per stage 0)
 #pragma unroll
     for (int i = 0; i < FAW; ++i) {
         const int f = wave + 4 * i, kb = f % KB;
-        acol[i] = kb * 32 + 16 * (lane >> 5);
+        acol[i] = AF ? (uint32_t)(kb * 1024 + lane * 16) : (uint32_t)(kb * 32 + 16 * (lane >> 5));
     }
+    constexpr uint32_t ASTEP = AF ? KB * 1024 : BK;  // A bytes per K stage along a row-block
     auto tile_offs = [&](int tile, uint32_t *aoff, uint32_t &woff) {
         const int m0 = (tile / tilesN) * BM, n0 = (tile % tilesN) * BN;
 #pragma unroll
         for (int i = 0; i < FAW; ++i) {
             const int f = wave + 4 * i, rb = f / KB;
-            // rows past M re-read row M-1 and are never stored
-            aoff[i] = (uint32_t)min(m0 + rb * 32 + (lane & 31), M - 1) * ldau + acol[i];
+            // rows past M are never stored: row-major A re-reads row M-1, fragment-major
+            // A reads the buffer's padding rows (allocated up to a multiple of BM)
+            if (AF)
+                aoff[i] = (uint32_t)((m0 / 32 + rb) * nk32) * 1024u + acol[i];
+            else
+                aoff[i] = (uint32_t)min(m0 + rb * 32 + (lane & 31), M - 1) * ldau + acol[i];
         }
         woff = (uint32_t)(n0 / 32 + wave * TN) * (uint32_t)nk32 * 1024u + lane * 16;
     };
@@ -115,7 +125,7 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
         const uint32_t wo = nx ? woff_x : woff_c;
 #pragma unroll
         for (int i = 0; i < FAW; ++i) {
-            const uint32_t ao = (nx ? aoff_x[i] : aoff_c[i]) + t * BK;
+            const uint32_t ao = (nx ? aoff_x[i] : aoff_c[i]) + t * ASTEP;
             areg[ring][i] = *reinterpret_cast<const i32x4 *>(A + ao);
         }
 #pragma unroll

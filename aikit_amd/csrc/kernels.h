@@ -8,7 +8,9 @@
 //   activations (f32, caller)   a[M][K] row-major
 //   quantized activations       aq[M][lda] int8 row-major, lda a multiple of 64 >= K,
 //                               columns [K,lda) zero (the GEMMs read rows past M as
-//                               row M-1 and never store them)
+//                               row M-1 and never store them); or, for the persistent
+//                               GEMM, fragment-major like the weights (frag_off), rows
+//                               past M read but never stored
 //   activation scales           as[Mp] f32
 //   weights (pre-swizzled once) wf[Np/32][Kp/32][64 lanes][16 B] int8 -- one 1 KiB
 //                               "fragment" per 32 output channels x 32 k; lane l holds
@@ -67,12 +69,52 @@ __device__ __forceinline__ float wave_absmax(float m) {
     return m;
 }
 
+// Byte offset of code (row, k) in the fragment-major activation layout
+// [Mp/32][ldq/32][64 lanes][16 B]: one 1 KiB fragment per 32 rows x 32 k, lane l
+// holding row 32*rb + l%32, k 32*kb + 16*(l/32) .. +16 -- the A-operand layout of
+// v_mfma_i32_32x32x32_i8, the same as the weights'. The persistent GEMM loads a
+// fragment as 64 lanes x 16 contiguous bytes (8 full cache lines per instruction);
+// a row-major A tile touches 32 lines per instruction and uses 32 B of each.
+__device__ __forceinline__ int64_t frag_off(int64_t row, int64_t k, int64_t nk32) {
+    return (((row >> 5) * nk32 + (k >> 5)) << 10) + ((((row & 31) + ((k >> 4) & 1) * 32)) << 4) + (k & 15);
+}
+
 // One wavefront per row, 4 rows per 256-thread block. Each lane holds CH float4 of
 // the row in registers (K <= 256*CH, K % 4 == 0, rows 16-byte aligned), so the
 // row is read from HBM exactly once. The reads are nontemporal: the f32 rows are
 // read once, and caching them only evicts the codes the GEMM reads next (measured
-// 1.3-1.6x faster on MI355X). Codes are written as packed 32-bit words; columns
-// [K, ldq) are zero-filled.
+// 1.3-1.6x faster on MI355X).
+template <int CH>
+__device__ __forceinline__ float load_row(const float *__restrict__ a, int64_t row, int K, int lane, float4 (&v)[CH]) {
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(a + row * (int64_t)K);
+    const int K4 = K >> 2;
+    // Unconditional loads (lanes past the row re-read its last float4 and zero it), so
+    // all CH are in flight at once; behind a per-chunk branch the compiler waits for
+    // each load before issuing the next.
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int k4 = lane + 64 * c;
+        const f32x4 t = __builtin_nontemporal_load(src + min(k4, K4 - 1));
+        v[c] = k4 < K4 ? make_float4(t.x, t.y, t.z, t.w) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        m = absmax_step(m, v[c].x);
+        m = absmax_step(m, v[c].y);
+        m = absmax_step(m, v[c].z);
+        m = absmax_step(m, v[c].w);
+    }
+    return wave_absmax(m);
+}
+
+__device__ __forceinline__ int pack_codes(float4 v, float inv) {
+    const int c0 = quant_code(v.x, inv), c1 = quant_code(v.y, inv);
+    const int c2 = quant_code(v.z, inv), c3 = quant_code(v.w, inv);
+    return (c0 & 0xff) | ((c1 & 0xff) << 8) | ((c2 & 0xff) << 16) | ((int)((unsigned)c3 << 24));
+}
+
+// Row-major codes q[M][ldq], written as packed 32-bit words; columns [K, ldq) zero.
 template <int CH>
 __global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ a,
                                                       int8_t *__restrict__ q, int64_t ldq,
@@ -81,27 +123,10 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ 
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= M) return;
-    const f32x4 *src = reinterpret_cast<const f32x4 *>(a + row * (int64_t)K);
-    const int K4 = K >> 2;
     float4 v[CH];
-    float m = 0.0f;
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        const int k4 = lane + 64 * c;
-        if (k4 < K4) {
-            const f32x4 t = __builtin_nontemporal_load(src + k4);
-            v[c] = make_float4(t.x, t.y, t.z, t.w);
-        } else {
-            v[c] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        m = absmax_step(m, v[c].x);
-        m = absmax_step(m, v[c].y);
-        m = absmax_step(m, v[c].z);
-        m = absmax_step(m, v[c].w);
-    }
-    m = wave_absmax(m);
+    const float m = load_row<CH>(a, row, K, lane, v);
     int *dst = reinterpret_cast<int *>(q + row * ldq);
-    const int ldq4 = (int)(ldq >> 2);
+    const int K4 = K >> 2, ldq4 = (int)(ldq >> 2);
     if (m == 0.0f) {
         for (int k4 = lane; k4 < ldq4; k4 += 64) dst[k4] = 0;
         if (lane == 0) scale[row] = 0.0f;
@@ -112,17 +137,61 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ 
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int k4 = lane + 64 * c;
-        if (k4 < K4) {
-            const int c0 = quant_code(v[c].x, inv), c1 = quant_code(v[c].y, inv);
-            const int c2 = quant_code(v[c].z, inv), c3 = quant_code(v[c].w, inv);
-            dst[k4] = (c0 & 0xff) | ((c1 & 0xff) << 8) | ((c2 & 0xff) << 16) | ((int)((unsigned)c3 << 24));
-        }
+        if (k4 < K4) dst[k4] = pack_codes(v[c], inv);
     }
     for (int k4 = K4 + lane; k4 < ldq4; k4 += 64) dst[k4] = 0;
     if (lane == 0) scale[row] = s;
 }
 
-// Any K and alignment: one wavefront per row, two passes over the row.
+// Fragment-major codes (frag_off; ldq a multiple of 64, ldq <= 256*CH). Rows 8t..8t+7
+// of a 32-row block fill one 128-byte line of each 1 KiB fragment (16 bytes each), so a
+// single row's codes land in 16-byte pieces of ldq/16 different lines. Here a 512-thread
+// block quantizes 8 such rows (one wavefront each, as quant_rows_vec), gathers their
+// codes in LDS in line order, and then writes whole lines with 16-byte stores.
+template <int CH>
+__global__ __launch_bounds__(512) void quant_rows_frag(const float *__restrict__ a,
+                                                       int8_t *__restrict__ q, int64_t ldq,
+                                                       float *__restrict__ scale, int64_t M,
+                                                       int K) {
+    constexpr int CP = 144;  // LDS bytes per 16-code chunk: 8 rows x 16 B + 16 B against bank conflicts
+    __shared__ __attribute__((aligned(16))) int8_t lds[16 * CH * CP];
+    const int lane = threadIdx.x & 63, rr = threadIdx.x >> 6;
+    const int64_t r0 = (int64_t)blockIdx.x * 8, row = r0 + rr;
+    const int K4 = K >> 2, ldq4 = (int)(ldq >> 2);
+    // the 32-bit word of codes 4*k4 .. 4*k4+3 of this wave's row
+    auto word = [&](int k4) -> int * { return reinterpret_cast<int *>(lds + (k4 >> 2) * CP + rr * 16 + (k4 & 3) * 4); };
+    if (row < M) {
+        float4 v[CH];
+        const float m = load_row<CH>(a, row, K, lane, v);
+        if (m == 0.0f) {
+            for (int k4 = lane; k4 < ldq4; k4 += 64) *word(k4) = 0;
+            if (lane == 0) scale[row] = 0.0f;
+        } else {
+            const float s = m / 127.0f;
+            const float inv = 1.0f / s;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int k4 = lane + 64 * c;
+                if (k4 < K4) *word(k4) = pack_codes(v[c], inv);
+            }
+            for (int k4 = K4 + lane; k4 < ldq4; k4 += 64) *word(k4) = 0;
+            if (lane == 0) scale[row] = s;
+        }
+    }
+    __syncthreads();
+    // piece p = (chunk p / 8, row p % 8): 8 consecutive threads write one whole line
+    const int64_t nk32 = ldq >> 5;
+    for (int p = threadIdx.x; p < 2 * ldq4; p += 512) {
+        const int c = p >> 3, r2 = p & 7;
+        if (r0 + r2 < M)
+            *reinterpret_cast<int4 *>(q + frag_off(r0 + r2, 16 * (int64_t)c, nk32)) =
+                *reinterpret_cast<const int4 *>(lds + c * CP + r2 * 16);
+    }
+}
+
+// Any K and alignment: one wavefront per row, two passes over the row. FRAG as in
+// quant_rows_vec.
+template <bool FRAG>
 __global__ __launch_bounds__(256) void quant_rows_scalar(const float *__restrict__ a,
                                                          int8_t *__restrict__ q, int64_t ldq,
                                                          float *__restrict__ scale, int64_t M,
@@ -131,19 +200,20 @@ __global__ __launch_bounds__(256) void quant_rows_scalar(const float *__restrict
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= M) return;
     const float *src = a + row * K;
-    int8_t *dst = q + row * ldq;
+    const int64_t nk32 = ldq >> 5;
+    auto dst = [&](int64_t k) -> int8_t & { return q[FRAG ? frag_off(row, k, nk32) : row * ldq + k]; };
     float m = 0.0f;
     for (int64_t k = lane; k < K; k += 64) m = absmax_step(m, src[k]);
     m = wave_absmax(m);
     if (m == 0.0f) {
-        for (int64_t k = lane; k < ldq; k += 64) dst[k] = 0;
+        for (int64_t k = lane; k < ldq; k += 64) dst(k) = 0;
         if (lane == 0) scale[row] = 0.0f;
         return;
     }
     const float s = m / 127.0f;
     const float inv = 1.0f / s;
-    for (int64_t k = lane; k < K; k += 64) dst[k] = (int8_t)quant_code(src[k], inv);
-    for (int64_t k = K + lane; k < ldq; k += 64) dst[k] = 0;
+    for (int64_t k = lane; k < K; k += 64) dst(k) = (int8_t)quant_code(src[k], inv);
+    for (int64_t k = K + lane; k < ldq; k += 64) dst(k) = 0;
     if (lane == 0) scale[row] = s;
 }
 

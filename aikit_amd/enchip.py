@@ -42,6 +42,9 @@ _SIGNATURES = {
     "enchip_quant_rows_dev": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
     "enchip_w8a8_pre_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _i64, _vp, _vp, _int, _vp, _vp]),
     "enchip_w8a8_linear_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _vp, _int, _vp, _vp]),
+    "enchip_quant_rows_frag_dev": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "enchip_w8a8_pre_frag_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _i64, _vp, _vp, _int, _vp, _vp]),
+    "enchip_frag_route": (_int, [_vp, ctypes.c_uint64, _i64, ctypes.POINTER(_i64)]),
     "enchip_gemm_kernel_name": (_int, [_vp, ctypes.c_uint64, _i64, _int, ctypes.c_char_p, _int]),
     "enchip_probe_ceilings": (_int, [_vp, _vp]),
     "enchip_set_small_m": (_int, [_vp, _i64]),
@@ -224,6 +227,22 @@ class Context:
                 stream: int = 0) -> None:
         self._check(self._lib.enchip_w8a8_pre_dev(self._h, w.handle, d_aq, ldq, M, d_ascale, d_bias or None, act,
                                                   d_dst, stream or None))
+
+    def frag_route(self, w: Weight, M: int):
+        """(ok, ldq): whether a linear on w with M rows takes fragment-major codes, and the
+        pitch (padded K) the frag entry points take."""
+        ldq = _i64(0)
+        ok = self._lib.enchip_frag_route(self._h, w.handle, M, ctypes.byref(ldq))
+        return bool(ok == 1), int(ldq.value)
+
+    def quant_rows_frag_dev(self, d_a: int, M: int, K: int, d_aq: int, ldq: int, d_ascale: int,
+                            stream: int = 0) -> None:
+        self._check(self._lib.enchip_quant_rows_frag_dev(self._h, d_a, M, K, d_aq, ldq, d_ascale, stream or None))
+
+    def pre_frag_dev(self, w: Weight, d_aq: int, ldq: int, M: int, d_ascale: int, d_bias: int, act: int, d_dst: int,
+                     stream: int = 0) -> None:
+        self._check(self._lib.enchip_w8a8_pre_frag_dev(self._h, w.handle, d_aq, ldq, M, d_ascale, d_bias or None, act,
+                                                       d_dst, stream or None))
 
     def linear_dev(self, w: Weight, d_a: int, M: int, d_bias: int, act: int, d_dst: int, stream: int = 0) -> None:
         self._check(self._lib.enchip_w8a8_linear_dev(self._h, w.handle, d_a, M, d_bias or None, act, d_dst,

@@ -34,10 +34,15 @@ PEAK_HBM_BPS = 8.0e12  # MI355X HBM3E
 TRAFFIC_PROFILE = "profiles/bert_base_b64s512_hbm_traffic.md"
 
 
-def quant_kernel_name(K: int) -> str:
+def quant_kernel_name(K: int, frag: bool) -> str:
     """Name of the quantize kernel enchip launches for rows of K floats (aligned
-    buffers): quant_rows_vec<ceil(K/256)> up to K = 4096."""
-    return f"enchip::quant_rows_vec<{(K + 255) // 256}>" if 0 < K <= 4096 and K % 4 == 0 else "enchip::quant_rows_scalar"
+    buffers, pitch K padded to 64): quant_rows_frag<ceil(Kp/256)> for fragment-major
+    codes (the persistent GEMM's), quant_rows_vec<ceil(K/256)> for row-major, up to
+    4096."""
+    Kp = (K + 63) // 64 * 64
+    if frag:
+        return f"enchip::quant_rows_frag<{(Kp + 255) // 256}>" if 0 < Kp <= 4096 and K % 4 == 0 else "enchip::quant_rows_scalar<true>"
+    return f"enchip::quant_rows_vec<{(K + 255) // 256}>" if 0 < K <= 4096 and K % 4 == 0 else "enchip::quant_rows_scalar<false>"
 
 
 def measured_traffic() -> dict:
@@ -300,10 +305,20 @@ def main() -> int:
                 for n, K, _, _ in cfg.linears() if n != "ffn_down"}
         outs = {n: torch.empty((M, N), device="cuda", dtype=torch.float32) for n, _, N, _ in cfg.linears()}
         kmax = max(K for _, K, _, _ in cfg.linears())
-        aq = torch.empty((M, kmax), device="cuda", dtype=torch.int8)
+        # codes in the fragment-major layout the persistent GEMM reads (rows padded to 128)
+        aq = torch.empty(((M + 127) // 128 * 128) * kmax, device="cuda", dtype=torch.int8)
         asc = torch.empty(M, device="cuda", dtype=torch.float32)
     torch.cuda.synchronize()
     lin = cfg.linears()
+    # every linear of the stack takes fragment-major codes (enchip_frag_route), so a step
+    # is exactly the kernels enchip_w8a8_linear_dev launches, with a seam between the
+    # quantizer and the GEMM for the per-kernel events
+    ldqs = {}
+    for name, K, N, act in lin:
+        ok, ldq = ctx.frag_route(layers[0][name][0], M)
+        if not ok:
+            raise SystemExit(f"bench: {name} has no fragment-major route")
+        ldqs[name] = ldq
 
     hev = HipEvents()
 
@@ -314,10 +329,11 @@ def main() -> int:
                 x = outs["ffn_up"] if name == "ffn_down" else x_in[name]
                 if evs is not None:
                     hev.record(evs[li][j][0], sptr)
-                ctx.quant_rows_dev(x.data_ptr(), M, K, aq.data_ptr(), asc.data_ptr(), sptr, ldq=K)
+                ctx.quant_rows_frag_dev(x.data_ptr(), M, K, aq.data_ptr(), ldqs[name], asc.data_ptr(), sptr)
                 if evs is not None:
                     hev.record(evs[li][j][1], sptr)
-                ctx.pre_dev(h, aq.data_ptr(), K, M, asc.data_ptr(), b.data_ptr(), act, outs[name].data_ptr(), sptr)
+                ctx.pre_frag_dev(h, aq.data_ptr(), ldqs[name], M, asc.data_ptr(), b.data_ptr(), act,
+                                 outs[name].data_ptr(), sptr)
                 if evs is not None:
                     hev.record(evs[li][j][2], sptr)
 
@@ -398,7 +414,7 @@ def main() -> int:
         tot_ops += ops * cfg.layers
         tot_gemm_s += gq * cfg.layers
         units.append((name, kernels[name]["gemm_kernel"], gq, ops, gbytes))
-        units.append(("quant_" + name, quant_kernel_name(K), qq, 0.0, qbytes))
+        units.append(("quant_" + name, quant_kernel_name(K, kernels[name]["gemm_kernel"].endswith("true>")), qq, 0.0, qbytes))
     # The dominant unit is the (kernel, shape) pair with the most time per step. Its
     # bound is the roofline's: MFMA when its arithmetic intensity reaches the ridge
     # point (peak ops / peak bytes), HBM below it.

@@ -149,10 +149,37 @@ int enchip_w8a8_pre_dev(enchip_ctx *ctx, enchip_weight w, const int8_t *d_aq,
                         int64_t ldq, int64_t M, const float *d_ascale,
                         const float *d_bias, int act, float *d_dst, void *stream);
 
-/* Device form of enchip_w8a8_linear. d_bias may be NULL. */
+/* Device form of enchip_w8a8_linear. d_bias may be NULL. When
+ * enchip_frag_route(ctx, w, M) is 1 it runs exactly the kernels of
+ * enchip_quant_rows_frag_dev + enchip_w8a8_pre_frag_dev. */
 int enchip_w8a8_linear_dev(enchip_ctx *ctx, enchip_weight w, const float *d_a,
                            int64_t M, const float *d_bias, int act, float *d_dst,
                            void *stream);
+
+/* Fragment-major twins of enchip_quant_rows_dev / enchip_w8a8_pre_dev (the same
+ * reference interfaces, linalg/quant.go:206-234, with a device-native code layout).
+ * The codes are laid out as the weights are: byte (r, k) of the M x ldq code matrix at
+ *   ((r/32)*(ldq/32) + k/32)*1024 + ((r%32) + 32*((k/16)%2))*16 + k%16,
+ * i.e. one 1 KiB block per 32 rows x 32 k in the operand order of
+ * v_mfma_i32_32x32x32_i8, so the persistent GEMM loads 16 contiguous bytes per lane.
+ * ldq must equal the weight's padded K (K rounded up to 64; enchip_frag_route checks
+ * it is usable) and d_aq must hold roundup(M, 128) * ldq bytes: rows past M are read
+ * by the GEMM but never stored, so their content is irrelevant. */
+int enchip_quant_rows_frag_dev(enchip_ctx *ctx, const float *d_a, int64_t M, int64_t K,
+                               int8_t *d_aq, int64_t ldq, float *d_ascale, void *stream);
+
+/* GEMM + fused epilogue on fragment-major codes from enchip_quant_rows_frag_dev.
+ * Returns ENCHIP_ERR_ARG unless enchip_frag_route(ctx, w, M) is 1. Bit-identical to
+ * enchip_w8a8_pre_dev / enchip_w8a8_linear_dev on the same activations. */
+int enchip_w8a8_pre_frag_dev(enchip_ctx *ctx, enchip_weight w, const int8_t *d_aq,
+                             int64_t ldq, int64_t M, const float *d_ascale,
+                             const float *d_bias, int act, float *d_dst, void *stream);
+
+/* 1 when a linear on weight w with M rows runs the persistent GEMM on fragment-major
+ * codes (M above the small-M limit, N % 4 == 0, an even number of 64-deep K stages,
+ * 32-bit offsets), else 0; the padded K (the ldq the frag entry points take) goes to
+ * *ldq when ldq is not NULL. No reference counterpart: it exposes a dispatch choice. */
+int enchip_frag_route(enchip_ctx *ctx, enchip_weight w, int64_t M, int64_t *ldq);
 
 /* Name of the GEMM kernel instantiation a linear on weight w with M rows and
  * activation act launches (as it appears in rocprofv3 traces), written to buf

@@ -280,26 +280,30 @@ def test_device_ceilings_coherent(ctx):
     assert 500 < c["mfma_i8_tops"] < 6000
 
 
-def test_pre_quantized_matches_linear(ctx):
+@pytest.mark.parametrize("M,K", [(1500, 768), (300, 1024), (77, 1536)])
+def test_pre_quantized_matches_linear(ctx, M, K):
     # linalg/quant.go:215-234 MatmulBTW8A8Pre: quantize once (QuantizeActivationsInto)
-    # and reuse the codes across weights; bit-identical to the fused call.
+    # and reuse the codes across weights; bit-identical to the fused call. pre_dev takes
+    # row-major codes (the persistent kernel without AF), the fused call quantizes
+    # fragment-major.
     import torch
 
-    g = workloads.rng(24)
-    M, K = 1500, 768
+    g = workloads.rng(24 + K)
     a = workloads.activations(g, M, K)
     a[3] = 0
     wts = [workloads.int8_weights(g, N, K) for N in (2304, 768)]
     bs = [workloads.bias(g, N) for N in (2304, 768)]
     hs = [ctx.register_weight(wq, s) for wq, s in wts]
     try:
+        for h in hs:
+            assert ctx.gemm_kernel_name(h, M, 0).endswith(", true>")
         st = torch.cuda.Stream()
         with torch.cuda.stream(st):
             da = torch.from_numpy(a).cuda()
-            ldq = 768
+            ldq = K
             dq = torch.empty((M, ldq), dtype=torch.int8, device="cuda")
             ds = torch.empty(M, dtype=torch.float32, device="cuda")
-            say("quant_rows_dev + pre_dev")
+            say(f"quant_rows_dev + pre_dev M={M} K={K}")
             ctx.quant_rows_dev(da.data_ptr(), M, K, dq.data_ptr(), ds.data_ptr(), st.cuda_stream, ldq=ldq)
             outs = []
             for h, b, act in zip(hs, bs, (0, 1)):
@@ -316,9 +320,11 @@ def test_pre_quantized_matches_linear(ctx):
 
 
 # ------------------------------------------------------------------ epilogue branches and dispatch
-# (M, N) pairs that route to each GEMM kernel: M <= 32 runs gemv_w8a8; otherwise
-# gemm_w8a8_pt when N % 4 == 0 (and the K stages are even), gemm_w8a8 when not.
-KERNEL_ROUTES = [(8, 1024, "gemv"), (20, 1001, "gemv"), (300, 1024, "gemm_w8a8_pt"), (300, 1001, "gemm_w8a8<")]
+# (M, N) pairs that route to each GEMM kernel (K = 768): M <= 32 runs gemv_w8a8;
+# otherwise gemm_w8a8_pt (fragment-major activations) when N % 4 == 0, gemm_w8a8 when
+# not.
+KERNEL_ROUTES = [(8, 1024, "gemv"), (20, 1001, "gemv"), (300, 1024, "gemm_w8a8_pt<128, 256, 64, 2,"),
+                 (300, 1001, "gemm_w8a8<")]
 
 
 def _gelu_spread_scales(a, wq, target_std=3.0):
@@ -391,3 +397,84 @@ def test_kernel_name_matches_dispatch(ctx):
                 assert route in name, (M, N, name)
         finally:
             ctx.release_weight(w)
+
+
+# ------------------------------------------------------------------ fragment-major codes
+def frag_to_rows(buf, M, ldq):
+    """Row-major [M][ldq] view of codes in the documented fragment-major layout:
+    byte (r, k) at ((r/32)*(ldq/32) + k/32)*1024 + ((r%32) + 32*((k/16)%2))*16 + k%16."""
+    r = np.arange(M)[:, None]
+    k = np.arange(ldq)[None, :]
+    off = ((r // 32) * (ldq // 32) + k // 32) * 1024 + ((r % 32) + 32 * ((k // 16) % 2)) * 16 + k % 16
+    return buf[off]
+
+
+@pytest.mark.parametrize("M,K,N,act", [(1500, 768, 2304, 0), (300, 3072, 768, 1), (129, 200, 64, 1), (33, 768, 3072, 1)])
+def test_frag_twins_match_linear(ctx, M, K, N, act):
+    # enchip_quant_rows_frag_dev + enchip_w8a8_pre_frag_dev: codes byte-exact against the
+    # oracle under the documented layout (zero K padding), outputs bit-identical to the
+    # fused linear and to the row-major pre_dev path.
+    import torch
+
+    g = workloads.rng(61 + M + K + N)
+    a = workloads.activations(g, M, K)
+    a[M // 3] = 0
+    wq, ws = workloads.int8_weights(g, N, K)
+    b = workloads.bias(g, N)
+    w = ctx.register_weight(wq, ws)
+    try:
+        ok, ldq = ctx.frag_route(w, M)
+        assert ok and ldq == (K + 63) // 64 * 64
+        st = torch.cuda.Stream()
+        with torch.cuda.stream(st):
+            da = torch.from_numpy(a).cuda()
+            db = torch.from_numpy(b).cuda()
+            Mp = (M + 127) // 128 * 128
+            dq = torch.full((Mp * ldq,), 99, dtype=torch.int8, device="cuda")  # padding rows: any content
+            ds = torch.empty(M, dtype=torch.float32, device="cuda")
+            dd = torch.empty((M, N), dtype=torch.float32, device="cuda")
+            say(f"frag twins M={M} K={K} N={N} act={act}")
+            ctx.quant_rows_frag_dev(da.data_ptr(), M, K, dq.data_ptr(), ldq, ds.data_ptr(), st.cuda_stream)
+            ctx.pre_frag_dev(w, dq.data_ptr(), ldq, M, ds.data_ptr(), db.data_ptr(), act, dd.data_ptr(), st.cuda_stream)
+        torch.cuda.synchronize()
+        want_q, want_s = oracle.quantize_activations(a, M, K)
+        codes = frag_to_rows(dq.cpu().numpy(), M, ldq)
+        assert np.array_equal(codes[:, :K], want_q), "codes differ"
+        assert (codes[:, K:] == 0).all(), "K padding not zero"
+        assert np.array_equal(bits(ds.cpu().numpy()), bits(want_s))
+        got = dd.cpu().numpy()
+        assert np.array_equal(bits(got), bits(ctx.linear(w, a, bias=b, act=act)))
+        assert_f32_parity(got, oracle.w8a8_linear(a, wq, ws, b, act, M, K, N), "frag twins")
+    finally:
+        ctx.release_weight(w)
+
+
+def test_frag_route_rejects_other_shapes(ctx):
+    import torch
+
+    g = workloads.rng(71)
+    for M, N, why in [(16, 768, "small M"), (300, 1001, "N % 4")]:
+        wq, ws = workloads.int8_weights(g, N, 768)
+        w = ctx.register_weight(wq, ws)
+        try:
+            ok, ldq = ctx.frag_route(w, M)
+            assert not ok and ldq == 768, why
+            dq = torch.zeros(((M + 127) // 128 * 128) * ldq, dtype=torch.int8, device="cuda")
+            ds = torch.ones(M, dtype=torch.float32, device="cuda")
+            dd = torch.empty((M, N), dtype=torch.float32, device="cuda")
+            with pytest.raises(enchip.EnchipError):
+                ctx.pre_frag_dev(w, dq.data_ptr(), ldq, M, ds.data_ptr(), 0, 0, dd.data_ptr())
+        finally:
+            ctx.release_weight(w)
+    # a pitch other than the padded K is refused
+    wq, ws = workloads.int8_weights(g, 768, 768)
+    w = ctx.register_weight(wq, ws)
+    try:
+        dq = torch.zeros(512 * 1024, dtype=torch.int8, device="cuda")
+        ds = torch.ones(300, dtype=torch.float32, device="cuda")
+        dd = torch.empty((300, 768), dtype=torch.float32, device="cuda")
+        with pytest.raises(enchip.EnchipError):
+            ctx.pre_frag_dev(w, dq.data_ptr(), 1024, 300, ds.data_ptr(), 0, 0, dd.data_ptr())
+    finally:
+        ctx.release_weight(w)
+    torch.cuda.synchronize()

@@ -70,6 +70,7 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
     constexpr int SP = WN + 8;    // transpose scratch pitch in ints (4*SP = 32 mod 64 banks)
     constexpr int C4 = WN / 4;    // 4-column groups per scratch row
     constexpr int RPL = 64 / C4;  // scratch rows covered by one pass of the wave
+    constexpr int KR = 32 / RPL;  // passes per 32-row chunk
     __shared__ __attribute__((aligned(1024))) int8_t smem[2 * STAGE];
     __shared__ __attribute__((aligned(16))) int s_tr[4][32 * SP];
     __shared__ __attribute__((aligned(16))) float s_as[BM];
@@ -218,6 +219,7 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
         s_b[tid] = c_b;
         __syncthreads();
         const int c4 = lane % C4, rsub = lane / C4;
+        const bool full = m0 + BM <= M && n0 + BN <= N;  // whole tile in range
         const int lcol = wave * WN + 4 * c4;  // tile column of this lane's first output
         const int col = n0 + lcol;
         const float4 ws4 = *reinterpret_cast<const float4 *>(&s_ws[lcol]);
@@ -236,27 +238,31 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
             const float4 a4a = *reinterpret_cast<const float4 *>(&s_as[i * 32 + rsub * 8]);
             const float4 a4b = *reinterpret_cast<const float4 *>(&s_as[i * 32 + rsub * 8 + 4]);
             const float asv[8] = {a4a.x, a4a.y, a4a.z, a4a.w, a4b.x, a4b.y, a4b.z, a4b.w};
+            // This lane's 4 outputs of row rsub + RPL*k of the chunk are at p0 + k*step.
+            float *const p0 = reinterpret_cast<float *>(out) + (int64_t)(m0 + i * 32 + rsub) * ldo + col;
+            const int64_t step = (int64_t)RPL * ldo;
+            auto row_ok = [&](int k) { return m0 + i * 32 + rsub + RPL * k < M && col < N; };
+            int4 v[KR];
             if (EPI == EPI_F32_GELU) {
                 // Pass 1: dequantize and apply GELU's series / sign branches to all 32
                 // of this lane's values, in place in the scratch; remember which need
                 // the erf tail (1 <= |u| <= 4) and leave their dequantized value there.
                 uint32_t tail_mask = 0;
 #pragma unroll
-                for (int k = 0; k < 32 / RPL; ++k) {
-                    int4 *cell = reinterpret_cast<int4 *>(&scr[(rsub + RPL * k) * SP + 4 * c4]);
-                    const int4 v = *cell;
-                    const int vv[4] = {v.x, v.y, v.z, v.w};
-                    float o4[4];
+                for (int k = 0; k < KR; ++k) v[k] = *reinterpret_cast<const int4 *>(&scr[(rsub + RPL * k) * SP + 4 * c4]);
+#pragma unroll
+                for (int k = 0; k < KR; ++k) {
+                    const int vv[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+                    int o4[4];
 #pragma unroll
                     for (int qq = 0; qq < 4; ++qq) {
                         const float y = dequant(vv[qq], asv[k], wsv[qq], bv[qq]);
                         bool tail;
                         const float gy = gelu_f32_no_tail(y, tail);
-                        o4[qq] = tail ? y : gy;
+                        o4[qq] = __float_as_int(tail ? y : gy);
                         tail_mask |= (uint32_t)tail << (4 * k + qq);
                     }
-                    *cell = make_int4(__float_as_int(o4[0]), __float_as_int(o4[1]), __float_as_int(o4[2]),
-                                      __float_as_int(o4[3]));
+                    *reinterpret_cast<int4 *>(&scr[(rsub + RPL * k) * SP + 4 * c4]) = make_int4(o4[0], o4[1], o4[2], o4[3]);
                 }
                 // Pass 2: the tail values, one per lane per round, so the wavefront runs
                 // the tail code max-popcount times instead of once per mixed instruction.
@@ -272,34 +278,31 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
                 }
                 // Pass 3: 16-byte stores of the finished values.
 #pragma unroll
-                for (int k = 0; k < 32 / RPL; ++k) {
-                    const int rl = rsub + RPL * k;
-                    const int4 v = *reinterpret_cast<const int4 *>(&scr[rl * SP + 4 * c4]);
-                    const int row = m0 + i * 32 + rl;
-                    if (row < M && col < N)
-                        store_nt(reinterpret_cast<float *>(out) + (int64_t)row * ldo + col, v);
-                }
+                for (int k = 0; k < KR; ++k) v[k] = *reinterpret_cast<const int4 *>(&scr[(rsub + RPL * k) * SP + 4 * c4]);
             } else {
+                // all of the chunk's LDS reads first, then the arithmetic
 #pragma unroll
-                for (int k = 0; k < 32 / RPL; ++k) {
-                    const int rl = rsub + RPL * k;  // row within the 32-row chunk
-                    const int4 v = *reinterpret_cast<const int4 *>(&scr[rl * SP + 4 * c4]);
-                    const int row = m0 + i * 32 + rl;
-                    // N % 4 == 0 (host check): a lane's 4 columns are all in or all out
-                    if (row < M && col < N) {
-                        if (EPI == EPI_I32) {
-                            store_nt(reinterpret_cast<int *>(out) + (int64_t)row * ldo + col, v);
-                        } else {
-                            const int vv[4] = {v.x, v.y, v.z, v.w};
-                            int4 y;
-                            y.x = __float_as_int(dequant(vv[0], asv[k], wsv[0], bv[0]));
-                            y.y = __float_as_int(dequant(vv[1], asv[k], wsv[1], bv[1]));
-                            y.z = __float_as_int(dequant(vv[2], asv[k], wsv[2], bv[2]));
-                            y.w = __float_as_int(dequant(vv[3], asv[k], wsv[3], bv[3]));
-                            store_nt(reinterpret_cast<float *>(out) + (int64_t)row * ldo + col, y);
-                        }
+                for (int k = 0; k < KR; ++k) v[k] = *reinterpret_cast<const int4 *>(&scr[(rsub + RPL * k) * SP + 4 * c4]);
+                if (EPI == EPI_F32) {
+#pragma unroll
+                    for (int k = 0; k < KR; ++k) {
+                        const int vv[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+                        v[k].x = __float_as_int(dequant(vv[0], asv[k], wsv[0], bv[0]));
+                        v[k].y = __float_as_int(dequant(vv[1], asv[k], wsv[1], bv[1]));
+                        v[k].z = __float_as_int(dequant(vv[2], asv[k], wsv[2], bv[2]));
+                        v[k].w = __float_as_int(dequant(vv[3], asv[k], wsv[3], bv[3]));
                     }
                 }
+            }
+            // N % 4 == 0 (host check): a lane's 4 columns are all in or all out. Whole
+            // tiles store without per-row checks.
+            if (full) {
+#pragma unroll
+                for (int k = 0; k < KR; ++k) store_nt(p0 + k * step, v[k]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < KR; ++k)
+                    if (row_ok(k)) store_nt(p0 + k * step, v[k]);
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();

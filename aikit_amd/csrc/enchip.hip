@@ -194,7 +194,7 @@ void launch_pt(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, co
     using namespace enchip;
     const int tilesM = (int)((M + PT_BM - 1) / PT_BM), tilesN = (int)((w.N + PT_BN - 1) / PT_BN);
     const int64_t tiles = (int64_t)tilesM * tilesN;
-    hipLaunchKernelGGL((gemm_w8a8_pt<PT_BM, PT_BN, PT_BK, PW, EPI, AF>), dim3(persistent_grid(c, tiles)), dim3(256),
+    hipLaunchKernelGGL((gemm_w8a8_pt<PT_BM, PT_BN, PT_BK, PW, EPI, AF, PT_NW>), dim3(persistent_grid(c, tiles)), dim3(64 * PT_NW),
                        0, s, aq, lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp, tilesN,
                        (int)tiles);
 }
@@ -340,13 +340,13 @@ int enchip_gemm_kernel_name(enchip_ctx *ctx, enchip_weight h, int64_t M, int act
     const int epi = act_code(act);
     char name[96];
     if (route_af(ctx, *w, M, nullptr, w->N))
-        snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, true>", enchip::PT_BM, enchip::PT_BN,
-                 enchip::PT_BK, pt_ring(*w), epi);
+        snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, true, %d>", enchip::PT_BM, enchip::PT_BN,
+                 enchip::PT_BK, pt_ring(*w), epi, enchip::PT_NW);
     else if (M <= ctx->small_m)
         snprintf(name, sizeof name, "enchip::gemv_w8a8<%d>", epi);
     else if (use_persistent(*w, nullptr, w->Kp, nullptr, w->N, M, false))
-        snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, false>", enchip::PT_BM, enchip::PT_BN,
-                 enchip::PT_BK, pt_ring(*w), epi);
+        snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, false, %d>", enchip::PT_BM, enchip::PT_BN,
+                 enchip::PT_BK, pt_ring(*w), epi, enchip::PT_NW);
     else if (use_wide_tile(ctx, *w, M))
         snprintf(name, sizeof name, "enchip::gemm_w8a8<128, 256, %d, 2>", epi);
     else

@@ -43,7 +43,7 @@ namespace enchip {
 
 // Tile geometry and ring depth of the persistent kernel (the host checks its
 // preconditions).
-constexpr int PT_BM = 128, PT_BN = 256, PT_BK = 64, PT_PW = 2;
+constexpr int PT_BM = 128, PT_BN = 256, PT_BK = 64, PT_PW = 2, PT_NW = 4;
 
 // 16-byte nontemporal store of 4 output words. The f32 outputs are written once and
 // not read by this kernel; a normal store would let them evict the A row-blocks and
@@ -53,26 +53,28 @@ __device__ __forceinline__ void store_nt(void *p, int4 v) {
     __builtin_nontemporal_store(t, reinterpret_cast<i32x4 *>(p));
 }
 
-template <int BM, int BN, int BK, int PW, int EPI, bool AF>
-__global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
+template <int BM, int BN, int BK, int PW, int EPI, bool AF, int NW>
+__global__ __launch_bounds__(64 * NW, NW / 2) void gemm_w8a8_pt(
     const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ Wf,
     const float *__restrict__ aS, const float *__restrict__ wS, const float *__restrict__ bias,
     void *__restrict__ out, int64_t ldo, int M, int N, int Kp, int tilesN, int numTiles) {
-    constexpr int WN = BN / 4;
+    constexpr int NT = 64 * NW;  // threads
+    constexpr int WN = BN / NW;  // output columns per wave
     constexpr int TM = BM / 32, TN = WN / 32;
     constexpr int KB = BK / 32;
     constexpr int FA = TM * KB;  // A fragments per stage
-    static_assert(FA % 4 == 0, "A fragments per stage must split over 4 waves");
-    static_assert(BN == 256 && BM <= 256 && (BM & (BM - 1)) == 0, "constant staging: 256 threads cover BN");
-    constexpr int FAW = FA / 4;  // A fragments each wave moves per stage
+    static_assert(FA % NW == 0 && TN >= 1, "A fragments per stage must split over the waves");
+    static_assert(NT >= BN && NT >= BM && (BM & (BM - 1)) == 0, "constant staging: one thread per row / column");
+    constexpr int FAW = FA / NW;  // A fragments each wave moves per stage
     constexpr int STAGE = FA * 1024;
     constexpr int RING_LOADS = FAW + KB * TN;  // VMEM loads per ring stage per lane
     constexpr int SP = WN + 8;    // transpose scratch pitch in ints (4*SP = 32 mod 64 banks)
     constexpr int C4 = WN / 4;    // 4-column groups per scratch row
     constexpr int RPL = 64 / C4;  // scratch rows covered by one pass of the wave
     constexpr int KR = 32 / RPL;  // passes per 32-row chunk
+    static_assert(KR % 4 == 0, "row scales are read as float4");
     __shared__ __attribute__((aligned(1024))) int8_t smem[2 * STAGE];
-    __shared__ __attribute__((aligned(16))) int s_tr[4][32 * SP];
+    __shared__ __attribute__((aligned(16))) int s_tr[NW][32 * SP];
     __shared__ __attribute__((aligned(16))) float s_as[BM];
     __shared__ __attribute__((aligned(16))) float s_ws[BN];
     __shared__ __attribute__((aligned(16))) float s_b[BN];
@@ -97,7 +99,7 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
     uint32_t acol[FAW];  // this lane's offset within its A row-block (per stage 0)
 #pragma unroll
     for (int i = 0; i < FAW; ++i) {
-        const int f = wave + 4 * i, kb = f % KB;
+        const int f = wave + NW * i, kb = f % KB;
         acol[i] = AF ? (uint32_t)(kb * 1024 + lane * 16) : (uint32_t)(kb * 32 + 16 * (lane >> 5));
     }
     constexpr uint32_t ASTEP = AF ? KB * 1024 : BK;  // A bytes per K stage along a row-block
@@ -105,7 +107,7 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
         const int m0 = (tile / tilesN) * BM, n0 = (tile % tilesN) * BN;
 #pragma unroll
         for (int i = 0; i < FAW; ++i) {
-            const int f = wave + 4 * i, rb = f / KB;
+            const int f = wave + NW * i, rb = f / KB;
             // rows past M are never stored: row-major A re-reads row M-1, fragment-major
             // A reads the buffer's padding rows (allocated up to a multiple of BM)
             if (AF)
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
     auto awrite = [&](int ls, int ring) {
 #pragma unroll
         for (int i = 0; i < FAW; ++i)
-            *reinterpret_cast<i32x4 *>(smem + ls * STAGE + (wave + 4 * i) * 1024 + lane * 16) = areg[ring][i];
+            *reinterpret_cast<i32x4 *>(smem + ls * STAGE + (wave + NW * i) * 1024 + lane * 16) = areg[ring][i];
     };
 
     i32x16 acc[TM][TN];
@@ -149,9 +151,9 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
     awrite(0, 0);
     __syncthreads();
 
-    // Position of tile row R in s_as: the 8 rows a lane needs per 32-row chunk
-    // ((lane >> 4) + 4k, k = 0..7) are contiguous.
-    const int as_slot = (tid & ~31) + (tid & 3) * 8 + ((tid & 31) >> 2);
+    // Position of tile row R in s_as: the KR rows a lane needs per 32-row chunk
+    // (rsub + RPL * k, k < KR) are contiguous.
+    const int as_slot = (tid & ~31) + (tid % RPL) * KR + ((tid & 31) / RPL);
     int g = 0;  // stages consumed so far: LDS slot parity across tiles
     for (int it = 0; it < ntiles; ++it) {
         const int tile = tile_id(it);
@@ -176,31 +178,49 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
             for (int p = 0; p < PW; ++p) {
                 const int t = t0 + p;
                 const int8_t *base = smem + ((g + t) & 1) * STAGE + lane * 16;
-                i32x4 af[KB][TM];
+                if constexpr (NW == 4) {
+                    i32x4 af[KB][TM];
 #pragma unroll
-                for (int kb = 0; kb < KB; ++kb)
+                    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-                    for (int i = 0; i < TM; ++i)
-                        af[kb][i] = *reinterpret_cast<const i32x4 *>(base + (i * KB + kb) * 1024);
+                        for (int i = 0; i < TM; ++i)
+                            af[kb][i] = *reinterpret_cast<const i32x4 *>(base + (i * KB + kb) * 1024);
 #pragma unroll
-                for (int kb = 0; kb < KB; ++kb)
+                    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-                    for (int i = 0; i < TM; ++i)
+                        for (int i = 0; i < TM; ++i)
 #pragma unroll
-                        for (int j = 0; j < TN; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[kb][i], wreg[p][kb][j], acc[i][j], 0, 0, 0);
-                awrite((g + t + 1) & 1, (p + 1) % PW);  // A of the next stage, maybe the next tile's
-                load_stage(p, t + PW);                   // refill this ring slot
-                // LDS reads first, then MFMAs with the LDS writes and VMEM loads interleaved
-                __builtin_amdgcn_sched_group_barrier(0x100, FA, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-                __builtin_amdgcn_sched_group_barrier(0x200, FAW, 0);
+                            for (int j = 0; j < TN; ++j)
+                                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[kb][i], wreg[p][kb][j], acc[i][j], 0, 0, 0);
+                    awrite((g + t + 1) & 1, (p + 1) % PW);  // A of the next stage, maybe the next tile's
+                    load_stage(p, t + PW);                   // refill this ring slot
+                    // LDS reads first, then MFMAs with the LDS writes and VMEM loads interleaved
+                    __builtin_amdgcn_sched_group_barrier(0x100, FA, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x200, FAW, 0);
 #pragma unroll
-                for (int u = 0; u < RING_LOADS; ++u) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                    for (int u = 0; u < RING_LOADS; ++u) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x008, TM * TN * KB - 2 - RING_LOADS, 0);
+                } else {
+                    // 4 waves per SIMD: registers for one K half-stage of A fragments at a
+                    // time; the other waves cover the LDS latency between the halves
+#pragma unroll
+                    for (int kb = 0; kb < KB; ++kb) {
+                        i32x4 af[TM];
+#pragma unroll
+                        for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const i32x4 *>(base + (i * KB + kb) * 1024);
+#pragma unroll
+                        for (int i = 0; i < TM; ++i)
+#pragma unroll
+                            for (int j = 0; j < TN; ++j)
+                                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], wreg[p][kb][j], acc[i][j], 0, 0, 0);
+                        if (kb == 0) awrite((g + t + 1) & 1, (p + 1) % PW);
+                    }
+                    load_stage(p, t + PW);  // after the last MFMA that reads this ring slot
                 }
-                __builtin_amdgcn_sched_group_barrier(0x008, TM * TN * KB - 2 - RING_LOADS, 0);
                 __syncthreads();
             }
         }
@@ -215,8 +235,10 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
         asm volatile("s_waitcnt vmcnt(%3)" : "+v"(c_as), "+v"(c_ws), "+v"(c_b) : "n"(PW * RING_LOADS) : "memory");
         if (!has_bias) c_b = kNoBias;
         if (tid < BM) s_as[as_slot] = c_as;
-        s_ws[tid] = c_ws;
-        s_b[tid] = c_b;
+        if (tid < BN) {
+            s_ws[tid] = c_ws;
+            s_b[tid] = c_b;
+        }
         __syncthreads();
         const int c4 = lane % C4, rsub = lane / C4;
         const bool full = m0 + BM <= M && n0 + BN <= N;  // whole tile in range
@@ -235,9 +257,12 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_pt(
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            const float4 a4a = *reinterpret_cast<const float4 *>(&s_as[i * 32 + rsub * 8]);
-            const float4 a4b = *reinterpret_cast<const float4 *>(&s_as[i * 32 + rsub * 8 + 4]);
-            const float asv[8] = {a4a.x, a4a.y, a4a.z, a4a.w, a4b.x, a4b.y, a4b.z, a4b.w};
+            float asv[KR];
+#pragma unroll
+            for (int k4 = 0; k4 < KR; k4 += 4) {
+                const float4 t = *reinterpret_cast<const float4 *>(&s_as[i * 32 + rsub * KR + k4]);
+                asv[k4] = t.x, asv[k4 + 1] = t.y, asv[k4 + 2] = t.z, asv[k4 + 3] = t.w;
+            }
             // This lane's 4 outputs of row rsub + RPL*k of the chunk are at p0 + k*step.
             float *const p0 = reinterpret_cast<float *>(out) + (int64_t)(m0 + i * 32 + rsub) * ldo + col;
             const int64_t step = (int64_t)RPL * ldo;

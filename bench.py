@@ -414,7 +414,7 @@ def main() -> int:
         tot_ops += ops * cfg.layers
         tot_gemm_s += gq * cfg.layers
         units.append((name, kernels[name]["gemm_kernel"], gq, ops, gbytes))
-        units.append(("quant_" + name, quant_kernel_name(K, kernels[name]["gemm_kernel"].endswith("true>")), qq, 0.0, qbytes))
+        units.append(("quant_" + name, quant_kernel_name(K, ", true, " in kernels[name]["gemm_kernel"]), qq, 0.0, qbytes))
     # The dominant unit is the (kernel, shape) pair with the most time per step. Its
     # bound is the roofline's: MFMA when its arithmetic intensity reaches the ridge
     # point (peak ops / peak bytes), HBM below it.

@@ -296,7 +296,7 @@ def test_pre_quantized_matches_linear(ctx, M, K):
     hs = [ctx.register_weight(wq, s) for wq, s in wts]
     try:
         for h in hs:
-            assert ctx.gemm_kernel_name(h, M, 0).endswith(", true>")
+            assert ", true, " in ctx.gemm_kernel_name(h, M, 0)
         st = torch.cuda.Stream()
         with torch.cuda.stream(st):
             da = torch.from_numpy(a).cuda()

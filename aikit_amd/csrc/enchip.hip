@@ -209,7 +209,7 @@ void launch_gemm_epi(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t l
         return;
     }
     if (M <= c->small_m) {
-        hipLaunchKernelGGL((enchip::gemv_w8a8<EPI>), dim3((unsigned)((w.N + 31) / 32)), dim3(256), 0, s, aq,
+        hipLaunchKernelGGL((enchip::gemv_w8a8<EPI>), dim3((unsigned)((w.N + 31) / 32)), dim3(64 * enchip::GV_WAVES), 0, s, aq,
                            lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp);
         return;
     }

@@ -393,14 +393,18 @@ __global__ __launch_bounds__(256, MINB) void gemm_w8a8(
 // ----------------------------------------------------------------------------
 // Small-M variant (M <= 32): HBM-bound on the weight stream, so every weight
 // byte is read once and the whole M tile (zero-padded to 32 rows) rides along in
-// the MFMA. One block per 32 output channels; its 4 waves split K and their int32
-// partial sums are added exactly through LDS.
+// the MFMA. One block per 32 output channels; its GV_WAVES waves split K, each
+// issuing all of its weight-fragment loads (up to GV_BATCH at a time) before its
+// MFMAs, so a call costs about one HBM round trip rather than one per fragment.
+// The int32 partial sums are added exactly through LDS.
+constexpr int GV_WAVES = 8, GV_BATCH = 8;
+
 template <int EPI>
-__global__ __launch_bounds__(256) void gemv_w8a8(
+__global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8a8(
     const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ Wf,
     const float *__restrict__ aS, const float *__restrict__ wS, const float *__restrict__ bias,
     void *__restrict__ out, int64_t ldo, int M, int N, int Kp) {
-    __shared__ int red[4 * 16 * 64];
+    __shared__ int red[GV_WAVES * 16 * 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nb = blockIdx.x, nk32 = Kp >> 5;
     const int8_t *arow = A + (int64_t)min(lane & 31, M - 1) * lda + (lane >> 5) * 16;
@@ -409,11 +413,19 @@ __global__ __launch_bounds__(256) void gemv_w8a8(
     i32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0;
-#pragma unroll 4
-    for (int kk = wave; kk < nk32; kk += 4) {
-        const i32x4 a = *reinterpret_cast<const i32x4 *>(arow + kk * 32);
-        const i32x4 b = *reinterpret_cast<const i32x4 *>(wfr + (int64_t)kk * 1024);
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc, 0, 0, 0);
+    for (int k0 = wave; k0 < nk32; k0 += GV_WAVES * GV_BATCH) {
+        // this wave's fragments k0, k0 + GV_WAVES, ...: loads first (clamped to the last
+        // fragment, whose extra copies are skipped below), then the MFMAs
+        i32x4 a[GV_BATCH], b[GV_BATCH];
+#pragma unroll
+        for (int u = 0; u < GV_BATCH; ++u) {
+            const int kk = min(k0 + u * GV_WAVES, nk32 - 1);
+            a[u] = *reinterpret_cast<const i32x4 *>(arow + kk * 32);
+            b[u] = *reinterpret_cast<const i32x4 *>(wfr + (int64_t)kk * 1024);
+        }
+#pragma unroll
+        for (int u = 0; u < GV_BATCH; ++u)
+            if (k0 + u * GV_WAVES < nk32) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[u], b[u], acc, 0, 0, 0);
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
@@ -423,10 +435,11 @@ __global__ __launch_bounds__(256) void gemv_w8a8(
     const float ws = col < N ? wS[col] : 0.0f;
     const float bb = (bias != nullptr && col < N) ? bias[col] : kNoBias;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-        const int r = wave * 4 + rr;
-        const int sum = red[(0 * 16 + r) * 64 + lane] + red[(1 * 16 + r) * 64 + lane] +
-                        red[(2 * 16 + r) * 64 + lane] + red[(3 * 16 + r) * 64 + lane];
+    for (int rr = 0; rr < 16 / GV_WAVES; ++rr) {
+        const int r = wave * (16 / GV_WAVES) + rr;
+        int sum = 0;
+#pragma unroll
+        for (int w = 0; w < GV_WAVES; ++w) sum += red[(w * 16 + r) * 64 + lane];
         const int row = acc_row(r, lane);
         if (row >= M || col >= N) continue;
         if (EPI == EPI_I32) {

@@ -118,14 +118,18 @@ int launch_quant(enchip_ctx *c, const float *d_a, int64_t M, int64_t K, int8_t *
     if (vec) {
         const int ch = (int)(((frag ? ldq : K) + 255) / 256);
         const int k = (int)K;
-        const dim3 grid((unsigned)(frag ? (M + 7) / 8 : (M + 3) / 4)), block(frag ? 512 : 256);
+        // fragment-major: 8 rows per block, 2 per wavefront for rows up to 1536 floats
+        const int rpw = ch <= 6 ? 2 : 1;
+        const dim3 grid((unsigned)(frag ? (M + 7) / 8 : (M + 3) / 4)), block(frag ? 512 / rpw : 256);
         switch (ch) {
-#define QCASE(N)                                                                                           \
-    case N:                                                                                                \
-        if (frag)                                                                                          \
-            hipLaunchKernelGGL(enchip::quant_rows_frag<N>, grid, block, 0, s, d_a, q, ldq, scale, M, k);   \
-        else                                                                                               \
-            hipLaunchKernelGGL(enchip::quant_rows_vec<N>, grid, block, 0, s, d_a, q, ldq, scale, M, k);    \
+#define QCASE(N)                                                                                                  \
+    case N:                                                                                                       \
+        if (frag && rpw == 2)                                                                                     \
+            hipLaunchKernelGGL((enchip::quant_rows_frag<N, 2>), grid, block, 0, s, d_a, q, ldq, scale, M, k);     \
+        else if (frag)                                                                                            \
+            hipLaunchKernelGGL((enchip::quant_rows_frag<N, 1>), grid, block, 0, s, d_a, q, ldq, scale, M, k);     \
+        else                                                                                                      \
+            hipLaunchKernelGGL(enchip::quant_rows_vec<N>, grid, block, 0, s, d_a, q, ldq, scale, M, k);           \
         break;
             QCASE(1) QCASE(2) QCASE(3) QCASE(4) QCASE(5) QCASE(6) QCASE(7) QCASE(8)
             QCASE(9) QCASE(10) QCASE(11) QCASE(12) QCASE(13) QCASE(14) QCASE(15) QCASE(16)

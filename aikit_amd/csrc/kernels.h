@@ -85,7 +85,7 @@ __device__ __forceinline__ int64_t frag_off(int64_t row, int64_t k, int64_t nk32
 // read once, and caching them only evicts the codes the GEMM reads next (measured
 // 1.3-1.6x faster on MI355X).
 template <int CH>
-__device__ __forceinline__ float load_row(const float *__restrict__ a, int64_t row, int K, int lane, float4 (&v)[CH]) {
+__device__ __forceinline__ void load_row_raw(const float *__restrict__ a, int64_t row, int K, int lane, float4 (&v)[CH]) {
     const f32x4 *src = reinterpret_cast<const f32x4 *>(a + row * (int64_t)K);
     const int K4 = K >> 2;
     // Unconditional loads (lanes past the row re-read its last float4 and zero it), so
@@ -97,6 +97,10 @@ __device__ __forceinline__ float load_row(const float *__restrict__ a, int64_t r
         const f32x4 t = __builtin_nontemporal_load(src + min(k4, K4 - 1));
         v[c] = k4 < K4 ? make_float4(t.x, t.y, t.z, t.w) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+}
+
+template <int CH>
+__device__ __forceinline__ float row_absmax(const float4 (&v)[CH]) {
     float m = 0.0f;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -106,6 +110,12 @@ __device__ __forceinline__ float load_row(const float *__restrict__ a, int64_t r
         m = absmax_step(m, v[c].w);
     }
     return wave_absmax(m);
+}
+
+template <int CH>
+__device__ __forceinline__ float load_row(const float *__restrict__ a, int64_t row, int K, int lane, float4 (&v)[CH]) {
+    load_row_raw<CH>(a, row, K, lane, v);
+    return row_absmax<CH>(v);
 }
 
 __device__ __forceinline__ int pack_codes(float4 v, float inv) {
@@ -145,26 +155,34 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ 
 
 // Fragment-major codes (frag_off; ldq a multiple of 64, ldq <= 256*CH). Rows 8t..8t+7
 // of a 32-row block fill one 128-byte line of each 1 KiB fragment (16 bytes each), so a
-// single row's codes land in 16-byte pieces of ldq/16 different lines. Here a 512-thread
-// block quantizes 8 such rows (one wavefront each, as quant_rows_vec), gathers their
-// codes in LDS in line order, and then writes whole lines with 16-byte stores.
-template <int CH>
-__global__ __launch_bounds__(512) void quant_rows_frag(const float *__restrict__ a,
-                                                       int8_t *__restrict__ q, int64_t ldq,
-                                                       float *__restrict__ scale, int64_t M,
-                                                       int K) {
+// single row's codes land in 16-byte pieces of ldq/16 different lines. Here a block
+// quantizes 8 such rows, RPW per wavefront (all of a wavefront's row loads in flight at
+// once, so short rows still keep enough bytes in flight), gathers their codes in LDS in
+// line order, and then writes whole lines with 16-byte stores.
+template <int CH, int RPW>
+__global__ __launch_bounds__(512 / RPW) void quant_rows_frag(const float *__restrict__ a,
+                                                             int8_t *__restrict__ q, int64_t ldq,
+                                                             float *__restrict__ scale, int64_t M,
+                                                             int K) {
+    constexpr int NT = 512 / RPW;
     constexpr int CP = 144;  // LDS bytes per 16-code chunk: 8 rows x 16 B + 16 B against bank conflicts
     __shared__ __attribute__((aligned(16))) int8_t lds[16 * CH * CP];
-    const int lane = threadIdx.x & 63, rr = threadIdx.x >> 6;
-    const int64_t r0 = (int64_t)blockIdx.x * 8, row = r0 + rr;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t r0 = (int64_t)blockIdx.x * 8;
     const int K4 = K >> 2, ldq4 = (int)(ldq >> 2);
-    // the 32-bit word of codes 4*k4 .. 4*k4+3 of this wave's row
-    auto word = [&](int k4) -> int * { return reinterpret_cast<int *>(lds + (k4 >> 2) * CP + rr * 16 + (k4 & 3) * 4); };
-    if (row < M) {
-        float4 v[CH];
-        const float m = load_row<CH>(a, row, K, lane, v);
+    // the 32-bit word of codes 4*k4 .. 4*k4+3 of block row rr
+    auto word = [&](int rr, int k4) -> int * { return reinterpret_cast<int *>(lds + (k4 >> 2) * CP + rr * 16 + (k4 & 3) * 4); };
+    float4 v[RPW][CH];
+#pragma unroll
+    for (int u = 0; u < RPW; ++u) load_row_raw<CH>(a, min(r0 + wave * RPW + u, M - 1), K, lane, v[u]);
+#pragma unroll
+    for (int u = 0; u < RPW; ++u) {
+        const int rr = wave * RPW + u;
+        const int64_t row = r0 + rr;
+        if (row >= M) continue;
+        const float m = row_absmax<CH>(v[u]);
         if (m == 0.0f) {
-            for (int k4 = lane; k4 < ldq4; k4 += 64) *word(k4) = 0;
+            for (int k4 = lane; k4 < ldq4; k4 += 64) *word(rr, k4) = 0;
             if (lane == 0) scale[row] = 0.0f;
         } else {
             const float s = m / 127.0f;
@@ -172,16 +190,16 @@ __global__ __launch_bounds__(512) void quant_rows_frag(const float *__restrict__
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
                 const int k4 = lane + 64 * c;
-                if (k4 < K4) *word(k4) = pack_codes(v[c], inv);
+                if (k4 < K4) *word(rr, k4) = pack_codes(v[u][c], inv);
             }
-            for (int k4 = K4 + lane; k4 < ldq4; k4 += 64) *word(k4) = 0;
+            for (int k4 = K4 + lane; k4 < ldq4; k4 += 64) *word(rr, k4) = 0;
             if (lane == 0) scale[row] = s;
         }
     }
     __syncthreads();
     // piece p = (chunk p / 8, row p % 8): 8 consecutive threads write one whole line
     const int64_t nk32 = ldq >> 5;
-    for (int p = threadIdx.x; p < 2 * ldq4; p += 512) {
+    for (int p = threadIdx.x; p < 2 * ldq4; p += NT) {
         const int c = p >> 3, r2 = p & 7;
         if (r0 + r2 < M)
             *reinterpret_cast<int4 *>(q + frag_off(r0 + r2, 16 * (int64_t)c, nk32)) =

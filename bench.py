@@ -36,12 +36,13 @@ TRAFFIC_PROFILE = "profiles/bert_base_b64s512_hbm_traffic.md"
 
 def quant_kernel_name(K: int, frag: bool) -> str:
     """Name of the quantize kernel enchip launches for rows of K floats (aligned
-    buffers, pitch K padded to 64): quant_rows_frag<ceil(Kp/256)> for fragment-major
+    buffers, pitch K padded to 64): quant_rows_frag<ceil(Kp/256), rows per wave> for fragment-major
     codes (the persistent GEMM's), quant_rows_vec<ceil(K/256)> for row-major, up to
     4096."""
     Kp = (K + 63) // 64 * 64
     if frag:
-        return f"enchip::quant_rows_frag<{(Kp + 255) // 256}>" if 0 < Kp <= 4096 and K % 4 == 0 else "enchip::quant_rows_scalar<true>"
+        ch = (Kp + 255) // 256
+        return f"enchip::quant_rows_frag<{ch}, {2 if ch <= 6 else 1}>" if 0 < Kp <= 4096 and K % 4 == 0 else "enchip::quant_rows_scalar<true>"
     return f"enchip::quant_rows_vec<{(K + 255) // 256}>" if 0 < K <= 4096 and K % 4 == 0 else "enchip::quant_rows_scalar<false>"
 
 

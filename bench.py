@@ -174,7 +174,8 @@ def cpu_baseline(layer_w, cfg, seconds: float):
 
 
 def other_configs(ctx, torch, stream, ceilings):
-    """BASELINE configs 2 and 3, timed with HIP events on the launch stream.
+    """BASELINE configs 2 and 3, and ann.FlatI8 scoring, timed with HIP events on the
+    launch stream.
 
     * config 2: the isolated W8A8 linear (M=4096, K=768 -> N=3072, bias + GELU), as
       quantize + GEMM per call. Judged on int8 TOPS.
@@ -182,6 +183,9 @@ def other_configs(ctx, torch, stream, ceilings):
       different registered copy of the weights, and the copies total > 2x the 256 MB
       MALL, so every call streams its weights from HBM. Judged on HBM GB/s over the
       algorithmic bytes N*K + M*K + 4M + 8N + 4MN.
+    * ann.FlatI8 scoring: M in {1, 16, 256} queries against a 2^20 x 384 int8 index
+      (403 MB, larger than the MALL), bias-free W8A8 scores. Judged on HBM GB/s over
+      N*K + M*K + 4M + 4N + 4MN.
     """
     import numpy as np
 
@@ -248,6 +252,44 @@ def other_configs(ctx, torch, stream, ceilings):
             "note": "GEMM on pre-quantized activations (enchip_w8a8_pre_dev), one distinct weight copy per call"}
         for hh in hs:
             ctx.release_weight(hh)
+
+    # ann.FlatI8 scoring (SURVEY next row): an int8 index of N rows x dim registered as a
+    # weight (ann.Backend.NewI8Index), M queries scored as a bias-free W8A8 linear
+    # (I8Index.Score / I8BatchIndex.ScoreBatch). The 403 MB index exceeds the 256 MB
+    # MALL, so every call streams it from HBM.
+    N, K = 1 << 20, 384
+    g = workloads.rng(5)
+    codes = g.integers(-127, 128, size=(N, K), dtype=np.int8)
+    rscale = g.uniform(1e-3, 1e-2, size=N).astype(np.float32)
+    hidx = ctx.register_weight(codes, rscale)
+    del codes
+    for M in (1, 16, 256):
+        with torch.cuda.stream(stream):
+            a = torch.from_numpy(workloads.activations(g, M, K)).cuda()
+            aq = torch.empty((M, K), device="cuda", dtype=torch.int8)
+            asc = torch.empty(M, device="cuda", dtype=torch.float32)
+            dst = torch.empty((M, N), device="cuda", dtype=torch.float32)
+        torch.cuda.synchronize()
+        ctx.quant_rows_dev(a.data_ptr(), M, K, aq.data_ptr(), asc.data_ptr(), sp, ldq=K)
+        for _ in range(3):
+            ctx.pre_dev(hidx, aq.data_ptr(), K, M, asc.data_ptr(), 0, 0, dst.data_ptr(), sp)
+        reps = 20
+        e0.record(stream)
+        for _ in range(reps):
+            ctx.pre_dev(hidx, aq.data_ptr(), K, M, asc.data_ptr(), 0, 0, dst.data_ptr(), sp)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / reps
+        nbytes = N * K + M * K + 4 * M + 4 * N + 4 * M * N
+        out[f"ann_flat_i8_m{M}"] = {
+            "M": M, "K": K, "N": N, "us_per_call": t * 1e6, "hbm_gbps": nbytes / t / 1e9,
+            "frac_hbm_peak": nbytes / t / PEAK_HBM_BPS,
+            "frac_measured_read_ceiling": nbytes / t / 1e9 / ceilings["hbm_read_gbps"],
+            "int8_tops": 2.0 * M * N * K / t / 1e12, "kernel": ctx.gemm_kernel_name(hidx, M, 0),
+            "note": "M queries against a 2^20 x 384 int8 index (403 MB > MALL), pre-quantized queries, "
+                    "bias-free W8A8 scores (enchip_w8a8_pre_dev); bytes = index + queries + scales + M*N f32 scores"}
+        del a, aq, asc, dst
+    ctx.release_weight(hidx)
     return out
 
 
@@ -481,7 +523,7 @@ def main() -> int:
         "device": info,
     }
     if not args.no_other_configs:
-        log("configs 2 and 3 (isolated linear, small-M GEMV over a rotating > 2x MALL weight set)")
+        log("configs 2 and 3 (isolated linear, small-M GEMV over a rotating > 2x MALL weight set), ann.FlatI8 scoring")
         result["other_configs"] = other_configs(ctx, torch, stream, ceilings)
     if args.cpu_seconds > 0:
         log(f"CPU baseline ({args.cpu_seconds:.0f}s sample, {host_threads()} threads)")

@@ -478,3 +478,22 @@ def test_frag_route_rejects_other_shapes(ctx):
     finally:
         ctx.release_weight(w)
     torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------ ann.FlatI8 scoring
+@pytest.mark.parametrize("M,N,K", [(1, 5000, 384), (16, 4099, 384), (40, 3000, 768)])
+def test_ann_flat_i8_scores(ctx, M, N, K):
+    # ann.Backend (ann/backend.go:16-60): NewI8Index = a registered weight (int8 codes +
+    # per-row scales), I8Index.Score / I8BatchIndex.ScoreBatch = the bias-free W8A8
+    # linear, "the same W8A8 value linalg.MatmulBTW8A8 computes on the CPU".
+    g = workloads.rng(81 + M + N)
+    q = workloads.activations(g, M, K)
+    codes = g.integers(-127, 128, size=(N, K), dtype=np.int8)
+    scales = g.uniform(1e-3, 1e-2, size=N).astype(np.float32)
+    w = ctx.register_weight(codes, scales)
+    try:
+        say(f"ann scores M={M} N={N} K={K} via {ctx.gemm_kernel_name(w, M, 0)}")
+        got = ctx.linear(w, q)
+    finally:
+        ctx.release_weight(w)
+    assert_f32_parity(got, oracle.w8a8_linear(q, codes, scales, None, 0, M, K, N), "ann scores")

@@ -187,6 +187,17 @@ bool route_af(const enchip_ctx *c, const Weight &w, int64_t M, const void *out, 
     return M > c->small_m && use_persistent(w, nullptr, w.Kp, out, ldo, M, true);
 }
 
+// Small-M kernel choice: gemv_w8a8_wide (one wavefront per 32-channel group, whole K)
+// once there are enough groups to spread over the SIMDs, else gemv_w8a8 (one workgroup
+// per group, K split over its waves). Measured crossover on MI355X (M=1..16): with
+// K <= 1024 the wide kernel is 1.5x faster from 4 groups per CU (N=32768, K=384..768);
+// with K=3072 it loses at 2 groups per CU (each wave then walks 96 fragments in series)
+// and wins by 1.3x from 8 per CU.
+bool gemv_wide(const enchip_ctx *c, const Weight &w) {
+    const int64_t groups = (w.N + 31) / 32, cus = c->num_cus;
+    return groups >= 8 * cus || (groups >= 4 * cus && w.Kp <= 1024);
+}
+
 int persistent_grid(const enchip_ctx *c, int64_t tiles) {
     const int64_t full = std::max<int64_t>(8, (2 * (int64_t)c->num_cus) / 8 * 8);
     return (int)std::min<int64_t>(full, (tiles + 7) / 8 * 8);
@@ -213,8 +224,14 @@ void launch_gemm_epi(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t l
         return;
     }
     if (M <= c->small_m) {
-        hipLaunchKernelGGL((enchip::gemv_w8a8<EPI>), dim3((unsigned)((w.N + 31) / 32)), dim3(64 * enchip::GV_WAVES), 0, s, aq,
-                           lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp);
+        if (gemv_wide(c, w))
+            hipLaunchKernelGGL((enchip::gemv_w8a8_wide<EPI>),
+                               dim3((unsigned)((w.N + 32 * enchip::GVW_WAVES - 1) / (32 * enchip::GVW_WAVES))),
+                               dim3(64 * enchip::GVW_WAVES), 0, s, aq, lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M,
+                               (int)w.N, (int)w.Kp);
+        else
+            hipLaunchKernelGGL((enchip::gemv_w8a8<EPI>), dim3((unsigned)((w.N + 31) / 32)), dim3(64 * enchip::GV_WAVES), 0,
+                               s, aq, lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp);
         return;
     }
     if (use_wide_tile(c, w, M))
@@ -346,6 +363,8 @@ int enchip_gemm_kernel_name(enchip_ctx *ctx, enchip_weight h, int64_t M, int act
     if (route_af(ctx, *w, M, nullptr, w->N))
         snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, true, %d>", enchip::PT_BM, enchip::PT_BN,
                  enchip::PT_BK, pt_ring(*w), epi, enchip::PT_NW);
+    else if (M <= ctx->small_m && gemv_wide(ctx, *w))
+        snprintf(name, sizeof name, "enchip::gemv_w8a8_wide<%d>", epi);
     else if (M <= ctx->small_m)
         snprintf(name, sizeof name, "enchip::gemv_w8a8<%d>", epi);
     else if (use_persistent(*w, nullptr, w->Kp, nullptr, w->N, M, false))

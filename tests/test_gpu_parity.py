@@ -134,6 +134,25 @@ def test_linear_matches_oracle(ctx, M, K, N, act, with_bias):
     assert_f32_parity(dst, want, f"linear {M}x{K}x{N}")
 
 
+@pytest.mark.parametrize("M,K,N", [(1, 384, 131104), (7, 100, 140001), (32, 200, 131200), (3, 768, 40000)])
+@pytest.mark.parametrize("act,with_bias", [(0, False), (1, True)])
+def test_wide_small_m_kernel_matches_oracle(ctx, M, K, N, act, with_bias):
+    # N wide enough (>= 8 32-channel groups per CU, or >= 4 with K <= 1024, on MI355X) for the
+    # one-wavefront-per-group small-M kernel; ragged N and K below one 12-fragment batch.
+    g = workloads.rng(M * 11 + K + N)
+    wq, ws = workloads.int8_weights(g, 64, K)
+    w = ctx.register_weight(np.resize(wq, (N, K)), np.resize(ws, N))
+    name = ctx.gemm_kernel_name(w, M, act)
+    ctx.release_weight(w)
+    say(f"wide small-M linear M={M} K={K} N={N} act={act} via {name}")
+    assert name.startswith("enchip::gemv_w8a8_wide<"), name
+    a, wq, ws, b, dst, acc = _linear_case(ctx, M, K, N, act, with_bias, seed=M * 13 + K + N)
+    aq, _ = oracle.quantize_activations(a, M, K)
+    want_acc = (aq.astype(np.int64) @ wq.astype(np.int64).T).astype(np.int32)
+    assert np.array_equal(acc, want_acc), "int32 accumulators differ"
+    assert_f32_parity(dst, oracle.w8a8_linear(a, wq, ws, b, act, M, K, N), f"wide linear {M}x{K}x{N}")
+
+
 @pytest.mark.parametrize("M", [1, 2, 5, 16, 31, 32])
 @pytest.mark.parametrize("K,N", [(768, 768), (768, 3072), (100, 50)])
 def test_small_m_kernel_matches_gemm_kernel(ctx, M, K, N):

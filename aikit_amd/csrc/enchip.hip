@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "enchip.h"
+#include "gemm_f32.h"
 #include "gemm_persistent.h"
 #include "kernels.h"
 #include "probes.h"
@@ -60,6 +61,8 @@ struct enchip_ctx {
     size_t bias_cap = 0;
     int32_t *d_acc = nullptr;
     size_t acc_cap = 0;
+    float *d_fb = nullptr;  // enchip_matmul_bt_f32's b operand
+    size_t fb_cap = 0;
 };
 
 namespace {
@@ -331,7 +334,7 @@ int enchip_close(enchip_ctx *ctx) {
             (void)hipFree(kv.second.d_s);
         }
         ctx->weights.clear();
-        void *bufs[] = {ctx->d_aq, ctx->d_as, ctx->d_a, ctx->d_dst, ctx->d_bias, ctx->d_acc};
+        void *bufs[] = {ctx->d_aq, ctx->d_as, ctx->d_a, ctx->d_dst, ctx->d_bias, ctx->d_acc, ctx->d_fb};
         for (void *p : bufs)
             if (p) (void)hipFree(p);
         if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -718,3 +721,117 @@ int enchip_w8a8_batch(enchip_ctx *ctx, const float *a, int64_t M, int64_t K, con
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------- f32 MatmulBT
+
+namespace {
+
+// Enqueues C = A . B^T for count1 x count2 problems (gemm_f32.h), after the caller
+// checked the arguments. Batches beyond the 65535 grid rows run as several launches.
+int launch_matmul_f32(enchip_ctx *c, const float *A, int64_t lda, const float *B, int64_t ldb, bool bkn, float *C,
+                      int64_t ldc, int64_t M, int64_t K, int64_t N, const enchip_f32_batch &b1,
+                      const enchip_f32_batch &b2, hipStream_t s) {
+    using namespace enchip;
+    if (M == 0 || N == 0 || b1.count == 0 || b2.count == 0) return ENCHIP_OK;
+    const F32Strides s1{b1.stride_a, b1.stride_b, b1.stride_c}, s2{b2.stride_a, b2.stride_b, b2.stride_c};
+    auto al4 = [](int64_t v) { return v % 4 == 0; };
+    const bool vec = K % 4 == 0 && al4(lda) && al4(s1.a) && al4(s2.a) && (uintptr_t)A % 16 == 0 &&
+                     (bkn || (al4(ldb) && al4(s1.b) && al4(s2.b) && (uintptr_t)B % 16 == 0));
+    const bool km = K % F32_KB != 0;
+    const int wm = N <= 64 ? 4 : (M <= 64 ? 1 : 2), wn = 4 / wm;
+    const int tilesM = (int)((M + 64 * wm - 1) / (64 * wm)), tilesN = (int)((N + 64 * wn - 1) / (64 * wn));
+    constexpr int64_t kGrid = 65535;
+    for (int64_t z0 = 0; z0 < b2.count; z0 += kGrid)
+        for (int64_t y0 = 0; y0 < b1.count; y0 += kGrid) {
+            const unsigned ny = (unsigned)std::min(kGrid, b1.count - y0), nz = (unsigned)std::min(kGrid, b2.count - z0);
+            const float *a = A + y0 * s1.a + z0 * s2.a, *b = B + y0 * s1.b + z0 * s2.b;
+            float *cz = C + y0 * s1.c + z0 * s2.c;
+            if (K == 0) {
+                hipLaunchKernelGGL(fill_zero_f32, dim3((unsigned)((M * N + 255) / 256), ny, nz), dim3(256), 0, s, cz,
+                                   ldc, s1.c, s2.c, (int)M, (int)N);
+                continue;
+            }
+            const dim3 grid((unsigned)(tilesM * tilesN), ny, nz), block(256);
+#define F32_CALL(WM, WN, BKN, VEC, KM)                                                                          \
+    hipLaunchKernelGGL((gemm_f32_bt<WM, WN, BKN, VEC, KM>), grid, block, 0, s, a, lda, b, ldb, cz, ldc, s1, s2,   \
+                       (int)M, (int)N, (int)K, tilesN)
+#define F32_KM(WM, WN, BKN, VEC)                                                                               \
+    do {                                                                                                       \
+        if (km) F32_CALL(WM, WN, BKN, VEC, true);                                                              \
+        else F32_CALL(WM, WN, BKN, VEC, false);                                                                \
+    } while (0)
+#define F32_LAUNCH(WM, WN)                                                                                     \
+    do {                                                                                                       \
+        if (bkn && vec) F32_KM(WM, WN, true, true);                                                            \
+        else if (bkn) F32_KM(WM, WN, true, false);                                                             \
+        else if (vec) F32_KM(WM, WN, false, true);                                                             \
+        else F32_KM(WM, WN, false, false);                                                                     \
+    } while (0)
+            if (wm == 4) F32_LAUNCH(4, 1);
+            else if (wm == 1) F32_LAUNCH(1, 4);
+            else F32_LAUNCH(2, 2);
+#undef F32_CALL
+#undef F32_KM
+#undef F32_LAUNCH
+        }
+    return check_launch(c, "gemm_f32_bt");
+}
+
+constexpr int64_t kMaxDimF32 = (int64_t)1 << 30;  // M, N, K; and M*N below 2^36 elements
+
+}  // namespace
+
+int enchip_matmul_bt_f32(enchip_ctx *ctx, const float *a, const float *b, float *dst, int64_t M, int64_t K, int64_t N) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (M < 0 || K < 0 || N < 0 || M > kMaxDimF32 || K > kMaxDimF32 || N > kMaxDimF32 || M * N > ((int64_t)1 << 36))
+        return fail(ctx, ENCHIP_ERR_ARG, "matmul_bt_f32: bad shape M=%lld K=%lld N=%lld", (long long)M, (long long)K,
+                    (long long)N);
+    if (M == 0 || N == 0) return ENCHIP_OK;
+    if (!dst || (K > 0 && (!a || !b))) return fail(ctx, ENCHIP_ERR_ARG, "matmul_bt_f32: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    int rc;
+    const size_t out_bytes = (size_t)(M * N) * sizeof(float);
+    if ((rc = ensure(ctx, &ctx->d_a, &ctx->a_cap, std::max<size_t>((size_t)(M * K) * sizeof(float), 16)))) return rc;
+    if ((rc = ensure(ctx, &ctx->d_fb, &ctx->fb_cap, std::max<size_t>((size_t)(N * K) * sizeof(float), 16)))) return rc;
+    if ((rc = ensure(ctx, &ctx->d_dst, &ctx->dst_cap, out_bytes))) return rc;
+    hipStream_t s = ctx->stream;
+    // operands are uploaded on every call: their contents are never cached (attention
+    // rewrites pooled scratch in place between calls, gpu/enccuda/backend_test.go:88-130)
+    if (K > 0) {
+        HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
+        HIP_TRY(ctx, hipMemcpyAsync(ctx->d_fb, b, (size_t)(N * K) * sizeof(float), hipMemcpyHostToDevice, s));
+    }
+    const enchip_f32_batch one{1, 0, 0, 0};
+    if ((rc = launch_matmul_f32(ctx, ctx->d_a, K, ctx->d_fb, K, false, ctx->d_dst, N, M, K, N, one, one, s))) return rc;
+    HIP_TRY(ctx, hipMemcpyAsync(dst, ctx->d_dst, out_bytes, hipMemcpyDeviceToHost, s));
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    return ENCHIP_OK;
+}
+
+int enchip_matmul_bt_f32_dev(enchip_ctx *ctx, const float *d_a, int64_t lda, const float *d_b, int64_t ldb,
+                             int b_layout, float *d_c, int64_t ldc, int64_t M, int64_t K, int64_t N,
+                             const enchip_f32_batch *inner, const enchip_f32_batch *outer, void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (b_layout != ENCHIP_B_NK && b_layout != ENCHIP_B_KN)
+        return fail(ctx, ENCHIP_ERR_ARG, "matmul_bt_f32_dev: bad b_layout %d", b_layout);
+    const bool bkn = b_layout == ENCHIP_B_KN;
+    const enchip_f32_batch one{1, 0, 0, 0};
+    const enchip_f32_batch b1 = inner ? *inner : one, b2 = outer ? *outer : one;
+    if (M < 0 || K < 0 || N < 0 || M > kMaxDimF32 || K > kMaxDimF32 || N > kMaxDimF32 ||
+        M * N > ((int64_t)1 << 36) || b1.count < 0 || b2.count < 0 || b1.count > kMaxDimF32 || b2.count > kMaxDimF32)
+        return fail(ctx, ENCHIP_ERR_ARG, "matmul_bt_f32_dev: bad shape M=%lld K=%lld N=%lld batch %lld x %lld",
+                    (long long)M, (long long)K, (long long)N, (long long)b1.count, (long long)b2.count);
+    if (M == 0 || N == 0 || b1.count == 0 || b2.count == 0) return ENCHIP_OK;
+    if (lda < K || ldb < (bkn ? N : K) || ldc < N)
+        return fail(ctx, ENCHIP_ERR_ARG, "matmul_bt_f32_dev: pitches lda=%lld ldb=%lld ldc=%lld must cover a row (K=%lld, N=%lld)",
+                    (long long)lda, (long long)ldb, (long long)ldc, (long long)K, (long long)N);
+    for (const enchip_f32_batch *b : {&b1, &b2})
+        if (b->stride_a < 0 || b->stride_b < 0 || b->stride_c < 0)
+            return fail(ctx, ENCHIP_ERR_ARG, "matmul_bt_f32_dev: batch strides must be >= 0");
+    if (!d_c || (K > 0 && (!d_a || !d_b))) return fail(ctx, ENCHIP_ERR_ARG, "matmul_bt_f32_dev: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    return launch_matmul_f32(ctx, d_a, lda, d_b, ldb, bkn, d_c, ldc, M, K, N, b1, b2, s);
+}

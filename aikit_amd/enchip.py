@@ -23,6 +23,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libenchip.s
 
 OK, ERR_NO_DEVICE, ERR_ARG, ERR_HIP, ERR_OOM, ERR_HANDLE = range(6)
 ACT_NONE, ACT_GELU = 0, 1
+B_NK, B_KN = 0, 1  # enchip_matmul_bt_f32_dev b layouts: b[N,K] rows, b[K,N] rows
 ABI_VERSION = 1
 
 # Every symbol include/enchip.h declares, with (restype, argtypes).
@@ -43,6 +44,9 @@ _SIGNATURES = {
     "enchip_w8a8_pre_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _i64, _vp, _vp, _int, _vp, _vp]),
     "enchip_w8a8_linear_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _vp, _int, _vp, _vp]),
     "enchip_quant_rows_frag_dev": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "enchip_matmul_bt_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64]),
+    "enchip_matmul_bt_f32_dev": (_int, [_vp, _vp, _i64, _vp, _i64, _int, _vp, _i64, _i64, _i64, _i64, _vp, _vp,
+                                        _vp]),
     "enchip_w8a8_pre_frag_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _i64, _vp, _vp, _int, _vp, _vp]),
     "enchip_frag_route": (_int, [_vp, ctypes.c_uint64, _i64, ctypes.POINTER(_i64)]),
     "enchip_gemm_kernel_name": (_int, [_vp, ctypes.c_uint64, _i64, _int, ctypes.c_char_p, _int]),
@@ -92,6 +96,12 @@ def load() -> ctypes.CDLL:
         raise RuntimeError(f"libenchip ABI {lib.enchip_abi_version()} != binding ABI {ABI_VERSION}")
     _lib = lib
     return lib
+
+
+class F32Batch(ctypes.Structure):
+    """enchip_f32_batch: one batching level of enchip_matmul_bt_f32_dev."""
+    _fields_ = [("count", ctypes.c_int64), ("stride_a", ctypes.c_int64), ("stride_b", ctypes.c_int64),
+                ("stride_c", ctypes.c_int64)]
 
 
 def _ptr(x: Optional[np.ndarray]):
@@ -238,6 +248,27 @@ class Context:
     def quant_rows_frag_dev(self, d_a: int, M: int, K: int, d_aq: int, ldq: int, d_ascale: int,
                             stream: int = 0) -> None:
         self._check(self._lib.enchip_quant_rows_frag_dev(self._h, d_a, M, K, d_aq, ldq, d_ascale, stream or None))
+
+    def matmul_bt_f32(self, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+        """encoder.Backend.MatmulBT (encoder/backend.go:19-28): f32 a[M,K] . b[N,K]^T on the device."""
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        if a.ndim != 2 or b.ndim != 2 or a.shape[1] != b.shape[1]:
+            raise ValueError(f"matmul_bt_f32: a {a.shape} and b {b.shape} must be [M,K] and [N,K]")
+        M, K = a.shape
+        N = b.shape[0]
+        dst = np.empty((M, N), np.float32)
+        self._check(self._lib.enchip_matmul_bt_f32(self._h, _ptr(a), _ptr(b), _ptr(dst), M, K, N))
+        return dst
+
+    def matmul_bt_f32_dev(self, d_a: int, lda: int, d_b: int, ldb: int, b_layout: int, d_c: int, ldc: int,
+                          M: int, K: int, N: int, inner: Optional[tuple] = None, outer: Optional[tuple] = None,
+                          stream: int = 0) -> None:
+        """Batched device MatmulBT; inner / outer are (count, stride_a, stride_b, stride_c) in
+        floats, None for one problem."""
+        lv = [None if t is None else ctypes.byref(F32Batch(*t)) for t in (inner, outer)]
+        self._check(self._lib.enchip_matmul_bt_f32_dev(self._h, d_a or None, lda, d_b or None, ldb, b_layout,
+                                                       d_c or None, ldc, M, K, N, lv[0], lv[1], stream or None))
 
     def pre_frag_dev(self, w: Weight, d_aq: int, ldq: int, M: int, d_ascale: int, d_bias: int, act: int, d_dst: int,
                      stream: int = 0) -> None:

@@ -29,6 +29,7 @@ if ROOT not in sys.path:
 METRIC = "W8A8 encode seqs/sec (BERT-base b64×s512) + int8 GEMM TOPS as % of peak"
 PEAK_INT8_OPS = 5.0e15  # MI355X dense int8 MFMA (no sparsity)
 PEAK_HBM_BPS = 8.0e12  # MI355X HBM3E
+PEAK_FP32_FLOPS = 157.3e12  # MI355X dense fp32 MFMA
 
 
 TRAFFIC_PROFILE = "profiles/bert_base_b64s512_hbm_traffic.md"
@@ -314,6 +315,53 @@ def other_configs(ctx, torch, stream, ceilings):
                     "bias-free W8A8 scores (enchip_w8a8_pre_dev); bytes = index + queries + scales + M*N f32 scores"}
         del a, aq, asc, dst
     ctx.release_weight(hidx)
+
+    # f32 attention products of one config-4 layer (encoder/attention.go:108,111) on the
+    # device MatmulBT: QK^T and scores . V for all 64 sequences x 12 heads, each one
+    # launch with the heads read in place from the fused [tokens, 3D] QKV rows.
+    from aikit_amd.enchip import B_KN, B_NK
+
+    S, L, H, hd = 64, 512, 12, 64
+    D = H * hd
+    with torch.cuda.stream(stream):
+        qkv = torch.randn((S * L, 3 * D), device="cuda", generator=torch.Generator(device="cuda").manual_seed(9))
+        scores = torch.empty((S, H, L, L), device="cuda")
+        ctxv = torch.empty((S * L, D), device="cuda")
+    torch.cuda.synchronize()
+    base = qkv.data_ptr()
+
+    def qk():
+        ctx.matmul_bt_f32_dev(base, 3 * D, base + D * 4, 3 * D, B_NK, scores.data_ptr(), L, L, hd, L,
+                              inner=(H, hd, hd, L * L), outer=(S, L * 3 * D, L * 3 * D, H * L * L), stream=sp)
+
+    def pv():
+        ctx.matmul_bt_f32_dev(scores.data_ptr(), L, base + 2 * D * 4, 3 * D, B_KN, ctxv.data_ptr(), D, L, L, hd,
+                              inner=(H, L * L, hd, hd), outer=(S, H * L * L, L * 3 * D, L * D), stream=sp)
+
+    flops = 2.0 * S * H * L * L * hd
+    att = {}
+    for name, fn, nbytes in (("qk", qk, 2 * S * L * D * 4 + S * H * L * L * 4),
+                             ("pv", pv, S * H * L * L * 4 + 2 * S * L * D * 4)):
+        for _ in range(3):
+            fn()
+        reps = 10
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / reps
+        att[f"{name}_us"] = t * 1e6
+        att[f"{name}_tflops"] = flops / t / 1e12
+        att[f"{name}_frac_fp32_mfma_peak"] = flops / t / PEAK_FP32_FLOPS
+        att[f"{name}_hbm_gbps"] = nbytes / t / 1e9
+    att.update({"S": S, "L": L, "heads": H, "head_dim": hd, "gflop_per_product": flops / 1e9,
+                "kernels": "enchip::gemm_f32_bt<2, 2, false, true> (QK^T), enchip::gemm_f32_bt<4, 1, true, true> (PV)",
+                "note": "one config-4 layer's attention products in f32 (v_mfma_f32_32x32x2_f32), all 768 "
+                        "(sequence, head) problems per launch, operands resident; bytes = operands read once + "
+                        "output written once; softmax not included"})
+    out["attention_f32_cfg4_layer"] = att
+    del qkv, scores, ctxv
     return out
 
 

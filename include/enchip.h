@@ -56,6 +56,12 @@ enum enchip_act {
     ENCHIP_ACT_GELU = 1 /* exact-erf GELU, linalg.GELUF32 */
 };
 
+/* Layout of the b operand of enchip_matmul_bt_f32_dev. */
+enum enchip_b_layout {
+    ENCHIP_B_NK = 0, /* b[N, K] rows, pitch ldb: MatmulBT's own b (dst = a . b^T) */
+    ENCHIP_B_KN = 1  /* b[K, N] rows, pitch ldb: dst = a . b, e.g. V for scores . V */
+};
+
 /* Returns ENCHIP_ABI_VERSION. Lets a binding check it loaded the library it was
  * written against before calling anything else. No reference counterpart. */
 int enchip_abi_version(void);
@@ -199,6 +205,43 @@ typedef struct enchip_ceilings {
     double mfma_i8_tops;
 } enchip_ceilings;
 int enchip_probe_ceilings(enchip_ctx *ctx, enchip_ceilings *out);
+
+/* f32 dst[M,N] = a[M,K] . b[N,K]^T on host buffers, all row-major: the device side of
+ * encoder.Backend.MatmulBT (encoder/backend.go:19-28; enccuda's MatmulBT,
+ * gpu/enccuda/backend.go:136-172). Synchronous. a and b are uploaded on every call
+ * (their contents are never cached: attention rewrites the same pooled buffers
+ * between calls), dst is downloaded before returning. Products and sums are f32 on
+ * the f32 MFMA in an order of its own; the contract is the reference's gate, worst
+ * |dst - float64 dot| / max(|float64 dot|, 1) <= 2e-4 (gpu/enccuda/backend_test.go:
+ * 47-86). K == 0 gives zeros. Which shapes are worth the round trip is the caller's
+ * choice (enccuda's minGPUFlops, gpu/enccuda/backend.go:48-75): this entry point
+ * always runs on the device. */
+int enchip_matmul_bt_f32(enchip_ctx *ctx, const float *a, const float *b, float *dst,
+                         int64_t M, int64_t K, int64_t N);
+
+/* One level of batching for enchip_matmul_bt_f32_dev: `count` problems, the next one's
+ * operands `stride_a` / `stride_b` / `stride_c` floats further on. */
+typedef struct enchip_f32_batch {
+    int64_t count;
+    int64_t stride_a, stride_b, stride_c;
+} enchip_f32_batch;
+
+/* Device form of enchip_matmul_bt_f32, batched over two levels and strided, enqueued on
+ * `stream` (NULL: the context stream). For problem (i, o), i < inner->count,
+ * o < outer->count (a NULL level is one problem):
+ *   C[m][n] = sum_k A[m][k] * B(n, k) with A = d_a + i*inner->stride_a + o*outer->stride_a
+ *   (pitch lda), C likewise from d_c (pitch ldc), B likewise from d_b with element (n, k)
+ *   at B[n*ldb + k] (ENCHIP_B_NK) or B[k*ldb + n] (ENCHIP_B_KN).
+ * Pitches and strides are in floats. One call covers every (head, sequence) of an
+ * attention layer with the heads read in place from the [tokens, 3D] QKV rows: QK^T is
+ * A = Q head (lda = 3D, inner stride hd, outer stride L*3D), B = K head (ENCHIP_B_NK);
+ * scores . V is A = scores, B = V head (ENCHIP_B_KN) -- the reference's qH / kH / vHT
+ * extraction (encoder/attention.go:95-111) without the copies. Same arithmetic and
+ * contract as enchip_matmul_bt_f32; M, N, K, counts <= 2^30 and M*N <= 2^36. */
+int enchip_matmul_bt_f32_dev(enchip_ctx *ctx, const float *d_a, int64_t lda, const float *d_b,
+                             int64_t ldb, int b_layout, float *d_c, int64_t ldc, int64_t M,
+                             int64_t K, int64_t N, const enchip_f32_batch *inner,
+                             const enchip_f32_batch *outer, void *stream);
 
 /* Rows at or below which the small-M (HBM-bound, split-K) kernel runs instead of
  * the tiled MFMA GEMM. Both produce identical bits; this only selects the kernel.

@@ -61,6 +61,8 @@ def lib() -> ctypes.CDLL:
             "orc_layer_norm": (None, [_f32p, _f32p, _f32p, _i64, _i64, ctypes.c_double]),
             "orc_softmax_row_scaled": (None, [_f32p, _i64, ctypes.c_float]),
             "orc_attention": (None, [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64]),
+            "orc_matmul_bt_f64": (None, [_f32p, _f32p, _i64, _i64, _i64,
+                                         np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")]),
             "orc_pool_mean": (None, [_f32p, _i64, _i64, _f32p]),
             "orc_l2_normalize": (None, [_f32p, _i64]),
             "cpub_dot_i8": (ctypes.c_int32, [_i8p, _i8p, _i64]),
@@ -209,6 +211,21 @@ def attention(Q, K, V, L, D, heads):
     lib().orc_attention(_c(Q, np.float32).reshape(-1), _c(K, np.float32).reshape(-1),
                         _c(V, np.float32).reshape(-1), ctx, L, D, heads)
     return ctx.reshape(L, D)
+
+
+def matmul_bt_f64(a, b, M: int, K: int, N: int):
+    """refMatmulBT (gpu/enccuda/backend_test.go:32-44): float64 a[M,K] . b[N,K]^T."""
+    dst = np.empty(max(M * N, 1), np.float64)
+    lib().orc_matmul_bt_f64(_c(a, np.float32).reshape(-1), _c(b, np.float32).reshape(-1), M, K, N, dst)
+    return dst[: M * N].reshape(M, N)
+
+
+def matmul_bt_worst_rel(got, ref) -> float:
+    """The f32 MatmulBT gate's statistic (gpu/enccuda/backend_test.go:71-80): the worst
+    |got - ref| / max(|ref|, 1) over all elements; the gate is <= 2e-4."""
+    ref = np.asarray(ref, np.float64)
+    den = np.maximum(np.abs(ref), 1.0)
+    return float(np.max(np.abs(np.asarray(got, np.float64) - ref) / den)) if ref.size else 0.0
 
 
 def pool_mean(seq, L, D):

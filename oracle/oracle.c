@@ -307,6 +307,18 @@ void orc_attention(const float *Q, const float *K, const float *V, float *ctx,
     free(scores);
 }
 
+/* gpu/enccuda/backend_test.go:32-44 refMatmulBT: the float64 ground truth of
+ * MatmulBT, dst[m][n] = sum_k (double)a[m][k] * (double)b[n][k], accumulated in k
+ * order. The gate every f32 MatmulBT backend is held to (backend_test.go:47-86). */
+void orc_matmul_bt_f64(const float *a, const float *b, int64_t M, int64_t K, int64_t N, double *dst) {
+    for (int64_t m = 0; m < M; m++)
+        for (int64_t n = 0; n < N; n++) {
+            double acc = 0;
+            for (int64_t k = 0; k < K; k++) acc += (double)a[m * K + k] * (double)b[n * K + k];
+            dst[m * N + n] = acc;
+        }
+}
+
 /* encoder/pooling.go:84-105 poolOne(mean). */
 void orc_pool_mean(const float *seq, int64_t L, int64_t D, float *out) {
     if (L == 0) {

@@ -80,6 +80,10 @@ void orc_layer_norm(float *x, const float *w, const float *b, int64_t L,
  * in place on one row. */
 void orc_softmax_row_scaled(float *row, int64_t n, float scale);
 
+/* gpu/enccuda/backend_test.go:32-44 refMatmulBT: float64 dst[M,N] = a[M,K] . b[N,K]^T,
+ * each dot accumulated in double in k order. */
+void orc_matmul_bt_f64(const float *a, const float *b, int64_t M, int64_t K, int64_t N, double *dst);
+
 /* encoder/attention.go:81-130 attentionCore for one sequence with mOut == L:
  * per-head softmax(Q Kᵀ * 1/sqrt(headDim)) V into ctx[L,D]. The f32 dots use
  * a plain sequential f32 sum (the reference's AVX2 dotF32 reduction order is not

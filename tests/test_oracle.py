@@ -300,3 +300,36 @@ def test_golden_gelu(golden):
     assert np.array_equal(oracle.gelu(golden["gelu_x"]).view(np.uint32), golden["gelu_y"].view(np.uint32))
     xd = golden["gelu_x"].astype(np.float64)
     assert np.abs(golden["gelu_y"] - 0.5 * xd * (1 + erf(xd / math.sqrt(2)))).max() <= 1e-6
+
+
+# ------------------------------------------------------------------ f32 MatmulBT ground truth
+def test_matmul_bt_f64_brute_force_and_integers():
+    # refMatmulBT (gpu/enccuda/backend_test.go:32-44) against a Python triple loop on a
+    # tiny case, and exactly against integer arithmetic where every product and partial
+    # sum is an integer below 2^53 (a transposed operand or a dropped term fails both).
+    g = np.random.default_rng(41)
+    M, K, N = 3, 5, 4
+    a = g.standard_normal((M, K)).astype(np.float32)
+    b = g.standard_normal((N, K)).astype(np.float32)
+    got = oracle.matmul_bt_f64(a, b, M, K, N)
+    for m in range(M):
+        for n in range(N):
+            s = 0.0
+            for k in range(K):
+                s += float(a[m, k]) * float(b[n, k])
+            assert got[m, n] == s
+    M, K, N = 7, 300, 9
+    ai = g.integers(-1000, 1001, size=(M, K))
+    bi = g.integers(-1000, 1001, size=(N, K))
+    got = oracle.matmul_bt_f64(ai.astype(np.float32), bi.astype(np.float32), M, K, N)
+    assert np.array_equal(got, (ai @ bi.T).astype(np.float64))
+    assert oracle.matmul_bt_f64(a[:, :0], b[:, :0], 3, 0, 4).tolist() == [[0.0] * 4] * 3
+
+
+def test_matmul_bt_worst_rel_statistic():
+    # backend_test.go:71-80: relative to |ref|, with |ref| < 1 measured absolutely.
+    ref = np.array([[1000.0, 0.5, -2.0]])
+    assert oracle.matmul_bt_worst_rel(ref, ref) == 0.0
+    assert oracle.matmul_bt_worst_rel([[1000.1, 0.5, -2.0]], ref) == pytest.approx(1e-4)
+    assert oracle.matmul_bt_worst_rel([[1000.0, 0.5003, -2.0]], ref) == pytest.approx(3e-4)
+    assert oracle.matmul_bt_worst_rel([[1000.0, 0.5, -2.002]], ref) == pytest.approx(1e-3)

@@ -738,6 +738,9 @@ int launch_matmul_f32(enchip_ctx *c, const float *A, int64_t lda, const float *B
     const bool vec = K % 4 == 0 && al4(lda) && al4(s1.a) && al4(s2.a) && (uintptr_t)A % 16 == 0 &&
                      (bkn || (al4(ldb) && al4(s1.b) && al4(s2.b) && (uintptr_t)B % 16 == 0));
     const bool km = K % F32_KB != 0;
+    // the LDS-staged kernel loads whole float4 of A rows and of B rows ([N,K]) or B k-rows ([K,N])
+    const bool lds = K % 4 == 0 && al4(lda) && al4(s1.a) && al4(s2.a) && (uintptr_t)A % 16 == 0 && al4(ldb) &&
+                     al4(s1.b) && al4(s2.b) && (uintptr_t)B % 16 == 0 && (!bkn || N % 4 == 0);
     const int wm = N <= 64 ? 4 : (M <= 64 ? 1 : 2), wn = 4 / wm;
     const int tilesM = (int)((M + 64 * wm - 1) / (64 * wm)), tilesN = (int)((N + 64 * wn - 1) / (64 * wn));
     constexpr int64_t kGrid = 65535;
@@ -752,6 +755,27 @@ int launch_matmul_f32(enchip_ctx *c, const float *A, int64_t lda, const float *B
                 continue;
             }
             const dim3 grid((unsigned)(tilesM * tilesN), ny, nz), block(256);
+            if (lds) {
+                if (wm == 4 && bkn)
+                    hipLaunchKernelGGL((gemm_f32_bt_lds<4, 1, true>), grid, block, 0, s, a, lda, b, ldb, cz, ldc, s1, s2,
+                                       (int)M, (int)N, (int)K, tilesN);
+                else if (wm == 4)
+                    hipLaunchKernelGGL((gemm_f32_bt_lds<4, 1, false>), grid, block, 0, s, a, lda, b, ldb, cz, ldc, s1,
+                                       s2, (int)M, (int)N, (int)K, tilesN);
+                else if (wm == 1 && bkn)
+                    hipLaunchKernelGGL((gemm_f32_bt_lds<1, 4, true>), grid, block, 0, s, a, lda, b, ldb, cz, ldc, s1, s2,
+                                       (int)M, (int)N, (int)K, tilesN);
+                else if (wm == 1)
+                    hipLaunchKernelGGL((gemm_f32_bt_lds<1, 4, false>), grid, block, 0, s, a, lda, b, ldb, cz, ldc, s1,
+                                       s2, (int)M, (int)N, (int)K, tilesN);
+                else if (bkn)
+                    hipLaunchKernelGGL((gemm_f32_bt_lds<2, 2, true>), grid, block, 0, s, a, lda, b, ldb, cz, ldc, s1, s2,
+                                       (int)M, (int)N, (int)K, tilesN);
+                else
+                    hipLaunchKernelGGL((gemm_f32_bt_lds<2, 2, false>), grid, block, 0, s, a, lda, b, ldb, cz, ldc, s1,
+                                       s2, (int)M, (int)N, (int)K, tilesN);
+                continue;
+            }
 #define F32_CALL(WM, WN, BKN, VEC, KM)                                                                          \
     hipLaunchKernelGGL((gemm_f32_bt<WM, WN, BKN, VEC, KM>), grid, block, 0, s, a, lda, b, ldb, cz, ldc, s1, s2,   \
                        (int)M, (int)N, (int)K, tilesN)

@@ -356,7 +356,7 @@ def other_configs(ctx, torch, stream, ceilings):
         att[f"{name}_frac_fp32_mfma_peak"] = flops / t / PEAK_FP32_FLOPS
         att[f"{name}_hbm_gbps"] = nbytes / t / 1e9
     att.update({"S": S, "L": L, "heads": H, "head_dim": hd, "gflop_per_product": flops / 1e9,
-                "kernels": "enchip::gemm_f32_bt<2, 2, false, true> (QK^T), enchip::gemm_f32_bt<4, 1, true, true> (PV)",
+                "kernels": "enchip::gemm_f32_bt_lds<2, 2, false> (QK^T), enchip::gemm_f32_bt_lds<4, 1, true> (PV)",
                 "note": "one config-4 layer's attention products in f32 (v_mfma_f32_32x32x2_f32), all 768 "
                         "(sequence, head) problems per launch, operands resident; bytes = operands read once + "
                         "output written once; softmax not included"})

@@ -1,0 +1,117 @@
+"""A BERT encoder forward resident on the device, composed from libenchip's entry points.
+
+It follows encoder/bert.go:324-368 layer for layer, with every activation kept in device
+memory between operations (the residency the reference names as the next step after the
+matmul seam, docs/task-native-gpu.md:418-427):
+
+  qkv   = W8A8(h, Wqkv) + b            enchip_w8a8_linear_dev (Q, K, V fused: one N = 3D
+                                        weight sharing one activation quantization,
+                                        linalg.MatmulBTW8A8Batch)
+  S     = Q_h . K_h^T                   enchip_matmul_bt_f32_dev, every (head, sequence) in
+                                        one launch, heads read in place from qkv
+  P     = softmax(S * 1/sqrt(hd))       enchip_softmax_rows_scaled_dev
+  ctx_h = P . V_h                       enchip_matmul_bt_f32_dev (V read as [K, N] rows)
+  out   = W8A8(ctx, Wo) + b             enchip_w8a8_linear_dev
+  h     = LN(h + out)                   enchip_residual_layer_norm_dev
+  inter = GELU(W8A8(h, Wi) + b)         enchip_w8a8_linear_dev (fused epilogue)
+  ffn   = W8A8(inter, Wd) + b           enchip_w8a8_linear_dev
+  h     = LN(h + ffn)                   enchip_residual_layer_norm_dev
+
+and pools with enchip_pool_mean_l2_dev (encoder/pooling.go:84-105, embed/pool.go:22-38).
+The embedding lookup and its LayerNorm (bert.go:299-323) stay with the caller: the input
+is the [S*L, D] f32 hidden state after them. Every sequence of a batch has the same L.
+
+This module holds no arithmetic of its own; torch provides device buffers and the stream.
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, List, Sequence, Tuple
+
+import numpy as np
+
+from . import enchip
+
+LN_EPS = 1e-12  # BERT's layer_norm_eps (encoder/bert.go)
+
+
+class DeviceBert:
+    """Weights registered once; forward() runs the layers on device tensors.
+
+    layers: per layer {"qkv"|"o"|"ffn_up"|"ffn_down": (wq int8 [N,K], ws f32 [N],
+    bias f32 [N], act), "attn_ln"|"out_ln": (gain f32 [D], shift f32 [D])}.
+    """
+
+    def __init__(self, ctx: enchip.Context, layers: Sequence[Dict], hidden: int, heads: int, ffn: int):
+        import torch
+
+        self.torch = torch
+        self.ctx, self.D, self.H, self.I = ctx, hidden, heads, ffn
+        self.hd = hidden // heads
+        if self.hd * heads != hidden:
+            raise ValueError(f"hidden {hidden} is not a multiple of heads {heads}")
+        self.handles: List[Dict[str, Tuple]] = []
+        dev = torch.device("cuda")
+        for lw in layers:
+            entry = {}
+            for name in ("qkv", "o", "ffn_up", "ffn_down"):
+                wq, ws, b, act = lw[name]
+                entry[name] = (ctx.register_weight(wq, ws), torch.from_numpy(np.ascontiguousarray(b)).to(dev), act)
+            for name in ("attn_ln", "out_ln"):
+                g, s = lw[name]
+                entry[name] = (torch.from_numpy(np.ascontiguousarray(g)).to(dev),
+                               torch.from_numpy(np.ascontiguousarray(s)).to(dev))
+            self.handles.append(entry)
+        self._bufs = {}
+
+    def close(self) -> None:
+        for entry in self.handles:
+            for name in ("qkv", "o", "ffn_up", "ffn_down"):
+                self.ctx.release_weight(entry[name][0])
+        self.handles = []
+        self._bufs = {}
+
+    def _buffers(self, S: int, L: int):
+        key = (S, L)
+        if key not in self._bufs:
+            t, M = self.torch, S * L
+            f = dict(device="cuda", dtype=t.float32)
+            self._bufs = {key: dict(qkv=t.empty((M, 3 * self.D), **f), scores=t.empty((S, self.H, L, L), **f),
+                                    ctx=t.empty((M, self.D), **f), out=t.empty((M, self.D), **f),
+                                    inter=t.empty((M, self.I), **f), ffn=t.empty((M, self.D), **f))}
+        return self._bufs[key]
+
+    def forward(self, h, S: int, L: int, stream: int = 0) -> None:
+        """Runs every layer on h ([S*L, D] f32 on the device), in place, on `stream`."""
+        c, D, H, hd, M = self.ctx, self.D, self.H, self.hd, S * L
+        if tuple(h.shape) != (M, D) or not h.is_contiguous():
+            raise ValueError(f"h must be a contiguous [{M}, {D}] tensor")
+        b = self._buffers(S, L)
+        qkv, scores, ctxv, out, inter, ffn = b["qkv"], b["scores"], b["ctx"], b["out"], b["inter"], b["ffn"]
+        q = qkv.data_ptr()
+        scale = float(np.float32(1.0 / math.sqrt(hd)))  # encoder/attention.go:86
+        for e in self.handles:
+            w, bias, act = e["qkv"]
+            c.linear_dev(w, h.data_ptr(), M, bias.data_ptr(), act, q, stream)
+            c.matmul_bt_f32_dev(q, 3 * D, q + D * 4, 3 * D, enchip.B_NK, scores.data_ptr(), L, L, hd, L,
+                                inner=(H, hd, hd, L * L), outer=(S, L * 3 * D, L * 3 * D, H * L * L), stream=stream)
+            c.softmax_rows_scaled_dev(scores.data_ptr(), L, S * H * L, L, scale, stream)
+            c.matmul_bt_f32_dev(scores.data_ptr(), L, q + 2 * D * 4, 3 * D, enchip.B_KN, ctxv.data_ptr(), D, L, L, hd,
+                                inner=(H, L * L, hd, hd), outer=(S, H * L * L, L * 3 * D, L * D), stream=stream)
+            w, bias, act = e["o"]
+            c.linear_dev(w, ctxv.data_ptr(), M, bias.data_ptr(), act, out.data_ptr(), stream)
+            g, s = e["attn_ln"]
+            c.residual_layer_norm_dev(h.data_ptr(), D, out.data_ptr(), D, M, D, g.data_ptr(), s.data_ptr(), LN_EPS,
+                                      stream)
+            w, bias, act = e["ffn_up"]
+            c.linear_dev(w, h.data_ptr(), M, bias.data_ptr(), act, inter.data_ptr(), stream)
+            w, bias, act = e["ffn_down"]
+            c.linear_dev(w, inter.data_ptr(), M, bias.data_ptr(), act, ffn.data_ptr(), stream)
+            g, s = e["out_ln"]
+            c.residual_layer_norm_dev(h.data_ptr(), D, ffn.data_ptr(), D, M, D, g.data_ptr(), s.data_ptr(), LN_EPS,
+                                      stream)
+
+    def embed(self, h, S: int, L: int, pooled, stream: int = 0) -> None:
+        """forward(), then mean pooling + L2 normalisation of each sequence into pooled [S, D]."""
+        self.forward(h, S, L, stream)
+        self.ctx.pool_mean_l2_dev(h.data_ptr(), self.D, S, L, self.D, pooled.data_ptr(), self.D, stream)

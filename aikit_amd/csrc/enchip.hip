@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "enchip.h"
+#include "encoder_ops.h"
 #include "gemm_f32.h"
 #include "gemm_persistent.h"
 #include "kernels.h"
@@ -858,4 +859,74 @@ int enchip_matmul_bt_f32_dev(enchip_ctx *ctx, const float *d_a, int64_t lda, con
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     return launch_matmul_f32(ctx, d_a, lda, d_b, ldb, bkn, d_c, ldc, M, K, N, b1, b2, s);
+}
+
+// ---------------------------------------------------------------------------- encoder row ops
+
+namespace {
+
+constexpr int64_t kMaxRowOp = 4096;  // softmax columns / LayerNorm width held in registers
+
+// Launches K<CPL> for rows of up to 64*CPL floats, CPL the smallest power of two that fits.
+#define ROWOP_DISPATCH(KERNEL, n, grid, s, ...)                                               \
+    do {                                                                                     \
+        if ((n) <= 64) hipLaunchKernelGGL((KERNEL<1>), grid, dim3(256), 0, s, __VA_ARGS__);    \
+        else if ((n) <= 128) hipLaunchKernelGGL((KERNEL<2>), grid, dim3(256), 0, s, __VA_ARGS__); \
+        else if ((n) <= 256) hipLaunchKernelGGL((KERNEL<4>), grid, dim3(256), 0, s, __VA_ARGS__); \
+        else if ((n) <= 512) hipLaunchKernelGGL((KERNEL<8>), grid, dim3(256), 0, s, __VA_ARGS__); \
+        else if ((n) <= 1024) hipLaunchKernelGGL((KERNEL<16>), grid, dim3(256), 0, s, __VA_ARGS__); \
+        else if ((n) <= 2048) hipLaunchKernelGGL((KERNEL<32>), grid, dim3(256), 0, s, __VA_ARGS__); \
+        else hipLaunchKernelGGL((KERNEL<64>), grid, dim3(256), 0, s, __VA_ARGS__);            \
+    } while (0)
+
+}  // namespace
+
+int enchip_softmax_rows_scaled_dev(enchip_ctx *ctx, float *d_x, int64_t ld, int64_t rows, int64_t cols, float scale,
+                                   void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (rows < 0 || cols < 0 || cols > kMaxRowOp || ld < cols || rows > ((int64_t)1 << 34))
+        return fail(ctx, ENCHIP_ERR_ARG, "softmax: bad shape rows=%lld cols=%lld ld=%lld (cols <= %lld)",
+                    (long long)rows, (long long)cols, (long long)ld, (long long)kMaxRowOp);
+    if (rows == 0 || cols == 0) return ENCHIP_OK;
+    if (!d_x) return fail(ctx, ENCHIP_ERR_ARG, "softmax: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    ROWOP_DISPATCH(enchip::softmax_rows_scaled, cols, grid, s, d_x, ld, rows, (int)cols, scale);
+    return check_launch(ctx, "softmax_rows_scaled");
+}
+
+int enchip_residual_layer_norm_dev(enchip_ctx *ctx, float *d_h, int64_t ldh, const float *d_y, int64_t ldy,
+                                   int64_t rows, int64_t D, const float *d_w, const float *d_b, double eps,
+                                   void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (rows < 0 || D < 0 || D > kMaxRowOp || ldh < D || (d_y && ldy < D) || rows > ((int64_t)1 << 34))
+        return fail(ctx, ENCHIP_ERR_ARG, "layer_norm: bad shape rows=%lld D=%lld ldh=%lld ldy=%lld (D <= %lld)",
+                    (long long)rows, (long long)D, (long long)ldh, (long long)ldy, (long long)kMaxRowOp);
+    if (rows == 0 || D == 0) return ENCHIP_OK;
+    if (!d_h || !d_w || !d_b) return fail(ctx, ENCHIP_ERR_ARG, "layer_norm: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    ROWOP_DISPATCH(enchip::residual_layer_norm, D, grid, s, d_h, ldh, d_y, ldy, rows, (int)D, d_w, d_b, eps);
+    return check_launch(ctx, "residual_layer_norm");
+}
+
+int enchip_pool_mean_l2_dev(enchip_ctx *ctx, const float *d_h, int64_t ldh, int64_t nseq, int64_t L, int64_t D,
+                            float *d_out, int64_t ldo, void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (nseq < 0 || L < 0 || D < 0 || D > enchip::kPoolMaxD || ldh < D || ldo < D || nseq > 0x7fffffff ||
+        L > 0x7fffffff)
+        return fail(ctx, ENCHIP_ERR_ARG, "pool: bad shape nseq=%lld L=%lld D=%lld (D <= %d)", (long long)nseq,
+                    (long long)L, (long long)D, enchip::kPoolMaxD);
+    if (nseq == 0 || D == 0) return ENCHIP_OK;
+    if (!d_out || (L > 0 && !d_h)) return fail(ctx, ENCHIP_ERR_ARG, "pool: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    hipLaunchKernelGGL(enchip::pool_mean_l2, dim3((unsigned)nseq), dim3(256), 0, s, d_h, ldh, (int)L, (int)D, d_out,
+                       ldo);
+    return check_launch(ctx, "pool_mean_l2");
 }

@@ -1,0 +1,161 @@
+// encoder_ops.h -- the f32 row operations between a BERT layer's linears, on the device:
+// the scaled softmax of attention scores, the residual add + LayerNorm, and mean pooling
+// with L2 normalisation. With the W8A8 linears and the f32 MatmulBT they let a whole
+// encoder layer stay resident on the device.
+//
+// Each restates the reference operation for operation (f32 where it is f32, float64
+// where it accumulates in float64, no contraction). Softmax and LayerNorm add their
+// float64 partial sums over a wavefront as a tree rather than left to right, so their
+// float64 sums can differ from the reference in the last bits, and an output in rare
+// cases by one f32 ulp. Pooling keeps the reference's summation order and is exact.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "gelu_f32.h"
+
+#pragma clang fp contract(off)
+
+namespace enchip {
+
+__device__ __forceinline__ double wave_sum_f64(double s) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    return s;
+}
+
+// linalg.SoftmaxRowScaledInto (linalg/exp.go:174-182 -> exp_scalar.go:84-89, 9-35), in
+// place on each of `rows` rows of `cols` floats (pitch ld); one wavefront per row, the
+// row held in registers (cols <= 64*CPL):
+//   v = x * scale (f32); maxV = the first v, raised by every later v > maxV (so a NaN
+//   first element makes maxV NaN, later NaNs are skipped); e = expF32Core(v - maxV);
+//   sum = sum of (double)e; sum == 0 -> every value 1/float32(cols); else
+//   x = e * float32(1 / sum).
+template <int CPL>
+__global__ __launch_bounds__(256) void softmax_rows_scaled(float *__restrict__ x, int64_t ld, int64_t rows, int cols,
+                                                           float scale) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float *p = x + row * ld;
+    float v[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = lane + 64 * j;
+        v[j] = c < cols ? p[c] * scale : -INFINITY;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) m = v[j] > m ? v[j] : m;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    const float first = __shfl(v[0], 0, 64);
+    if (first != first) m = first;  // the reference starts from element 0
+    double sum = 0.0;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = lane + 64 * j;
+        const float e = c < cols ? exp_f32_core(v[j] - m) : 0.0f;
+        v[j] = e;
+        sum += (double)e;
+    }
+    sum = wave_sum_f64(sum);
+    if (sum == 0.0) {
+        const float u = 1.0f / (float)cols;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = lane + 64 * j;
+            if (c < cols) p[c] = u;
+        }
+        return;
+    }
+    const float inv = (float)(1.0 / sum);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = lane + 64 * j;
+        if (c < cols) p[c] = v[j] * inv;
+    }
+}
+
+// h = layerNorm(h + y) per row (encoder/bert.go:352-353,363-367: the f32 residual add
+// `h[i] += y[i]`, then encoder/layernorm.go:18-38), y optional; one wavefront per row,
+// D <= 64*CPL:
+//   mean = sum((double)v) / D; variance = sum(((double)v - mean)^2) / D;
+//   invStd = 1 / sqrt(variance + eps); h = float32((((double)v - mean) * invStd) * w + b).
+template <int CPL>
+__global__ __launch_bounds__(256) void residual_layer_norm(float *__restrict__ h, int64_t ldh,
+                                                           const float *__restrict__ y, int64_t ldy, int64_t rows,
+                                                           int D, const float *__restrict__ w,
+                                                           const float *__restrict__ b, double eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float *p = h + row * ldh;
+    const float *q = y != nullptr ? y + row * ldy : nullptr;
+    float v[CPL];
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = lane + 64 * j;
+        v[j] = 0.0f;
+        if (c < D) {
+            v[j] = q != nullptr ? p[c] + q[c] : p[c];
+            s += (double)v[j];
+        }
+    }
+    const double mean = wave_sum_f64(s) / (double)D;
+    double sq = 0.0;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = lane + 64 * j;
+        if (c < D) {
+            const double d = (double)v[j] - mean;
+            sq += d * d;
+        }
+    }
+    const double variance = wave_sum_f64(sq) / (double)D;
+    const double inv_std = 1.0 / sqrt(variance + eps);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = lane + 64 * j;
+        if (c < D) p[c] = (float)((((double)v[j] - mean) * inv_std) * (double)w[c] + (double)b[c]);
+    }
+}
+
+// Mean pooling then L2 normalisation of each of nseq sequences of L rows
+// (encoder/pooling.go:84-105 poolOne(mean), embed/pool.go:22-38 L2Normalize), one
+// 256-thread block per sequence, in the reference's summation order: each column's
+// float64 sum runs over the rows in order (one thread per column), and the sum of
+// squares runs over the columns in order (one thread), so the result is exact.
+// D <= kPoolMaxD.
+constexpr int kPoolMaxD = 4096;
+
+__global__ __launch_bounds__(256) void pool_mean_l2(const float *__restrict__ h, int64_t ldh, int L, int D,
+                                                    float *__restrict__ out, int64_t ldo) {
+    __shared__ float pooled[kPoolMaxD];
+    __shared__ double norm_s;
+    const int64_t seq = blockIdx.x;
+    const float *base = h + seq * (int64_t)L * ldh;
+    for (int j = threadIdx.x; j < D; j += 256) {
+        double acc = 0.0;
+        for (int i = 0; i < L; ++i) acc += (double)base[(int64_t)i * ldh + j];
+        pooled[j] = L > 0 ? (float)(acc * (1.0 / (double)L)) : 0.0f;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double sq = 0.0;
+        for (int j = 0; j < D; ++j) sq += (double)pooled[j] * (double)pooled[j];
+        norm_s = sqrt(sq);
+    }
+    __syncthreads();
+    const double norm = norm_s;
+    float *o = out + seq * ldo;
+    for (int j = threadIdx.x; j < D; j += 256) o[j] = norm < 1e-12 ? 0.0f : (float)((double)pooled[j] / norm);
+}
+
+}  // namespace enchip

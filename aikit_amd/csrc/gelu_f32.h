@@ -13,18 +13,22 @@
 
 #include <hip/hip_runtime.h>
 
+#include <climits>
+
 #pragma clang fp contract(off)
 
 namespace enchip {
 
-// linalg/exp.go:81-117 expF32Core. Only reached from the erf tail, where the
-// argument is -x*x with x in [1,4], so k stays in [-24,-1] and the int32
-// conversion is exact.
+// linalg/exp.go:81-117 expF32Core, for the erf tail (argument -x*x, x in [1,4]) and
+// softmax (argument v - max <= 0, possibly -inf or NaN). k = int32(kf) follows Go's
+// amd64 conversion: a value outside the int32 range, or NaN, converts to INT32_MIN
+// (the hardware's saturating conversion would give INT32_MAX / 0 there), which then
+// takes the underflow branch and returns 0, as the reference does.
 __device__ __forceinline__ float exp_f32_core(float x) {
     float z = x * 1.4426950408889634f;
     float t = z + 12582912.0f;
     float kf = t - 12582912.0f;
-    int k = (int)kf;
+    const int k = (kf >= -2147483648.0f && kf < 2147483648.0f) ? (int)kf : INT_MIN;
     float r = x - kf * 0.693145751953125f - kf * 1.428606820309417e-06f;
     float p = 1.9875691500e-4f;
     p = p * r + 1.3981999507e-3f;
@@ -33,7 +37,7 @@ __device__ __forceinline__ float exp_f32_core(float x) {
     p = p * r + 1.6666665459e-1f;
     p = p * r + 5.0000001201e-1f;
     p = p * r * r + r + 1.0f;
-    int e = k + 127;
+    const int e = k + 127;  // k <= 2^31 - 128, so no overflow
     if (e <= 0) return 0.0f;
     if (e >= 255) return p * __uint_as_float((unsigned)(e - 1) << 23) * 2.0f;
     return p * __uint_as_float((unsigned)e << 23);

@@ -45,6 +45,10 @@ _SIGNATURES = {
     "enchip_w8a8_linear_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _vp, _int, _vp, _vp]),
     "enchip_quant_rows_frag_dev": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
     "enchip_matmul_bt_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64]),
+    "enchip_softmax_rows_scaled_dev": (_int, [_vp, _vp, _i64, _i64, _i64, ctypes.c_float, _vp]),
+    "enchip_residual_layer_norm_dev": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp, ctypes.c_double,
+                                              _vp]),
+    "enchip_pool_mean_l2_dev": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
     "enchip_matmul_bt_f32_dev": (_int, [_vp, _vp, _i64, _vp, _i64, _int, _vp, _i64, _i64, _i64, _i64, _vp, _vp,
                                         _vp]),
     "enchip_w8a8_pre_frag_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _i64, _vp, _vp, _int, _vp, _vp]),
@@ -269,6 +273,20 @@ class Context:
         lv = [None if t is None else ctypes.byref(F32Batch(*t)) for t in (inner, outer)]
         self._check(self._lib.enchip_matmul_bt_f32_dev(self._h, d_a or None, lda, d_b or None, ldb, b_layout,
                                                        d_c or None, ldc, M, K, N, lv[0], lv[1], stream or None))
+
+    def softmax_rows_scaled_dev(self, d_x: int, ld: int, rows: int, cols: int, scale: float, stream: int = 0) -> None:
+        self._check(self._lib.enchip_softmax_rows_scaled_dev(self._h, d_x or None, ld, rows, cols, scale,
+                                                             stream or None))
+
+    def residual_layer_norm_dev(self, d_h: int, ldh: int, d_y: int, ldy: int, rows: int, D: int, d_w: int, d_b: int,
+                                eps: float, stream: int = 0) -> None:
+        self._check(self._lib.enchip_residual_layer_norm_dev(self._h, d_h or None, ldh, d_y or None, ldy, rows, D,
+                                                             d_w or None, d_b or None, eps, stream or None))
+
+    def pool_mean_l2_dev(self, d_h: int, ldh: int, nseq: int, L: int, D: int, d_out: int, ldo: int,
+                         stream: int = 0) -> None:
+        self._check(self._lib.enchip_pool_mean_l2_dev(self._h, d_h or None, ldh, nseq, L, D, d_out or None, ldo,
+                                                      stream or None))
 
     def pre_frag_dev(self, w: Weight, d_aq: int, ldq: int, M: int, d_ascale: int, d_bias: int, act: int, d_dst: int,
                      stream: int = 0) -> None:

@@ -243,6 +243,32 @@ int enchip_matmul_bt_f32_dev(enchip_ctx *ctx, const float *d_a, int64_t lda, con
                              int64_t K, int64_t N, const enchip_f32_batch *inner,
                              const enchip_f32_batch *outer, void *stream);
 
+/* The f32 row operations between a BERT layer's linears, in place on device buffers,
+ * enqueued on `stream` (NULL: the context stream). Each restates the reference operation
+ * for operation; softmax and LayerNorm add their float64 partial sums as a tree across
+ * a wavefront, so their float64 sums may differ from the reference's left-to-right
+ * order in the last bits (an output, rarely, by one f32 ulp).
+ *
+ * Softmax of each of `rows` rows of `cols` floats (pitch ld), scaled first:
+ * linalg.SoftmaxRowScaledInto (linalg/exp.go:174-182, exp_scalar.go:9-35,84-89) as
+ * attention applies it to QK^T (encoder/attention.go:109). cols <= 4096. */
+int enchip_softmax_rows_scaled_dev(enchip_ctx *ctx, float *d_x, int64_t ld, int64_t rows,
+                                   int64_t cols, float scale, void *stream);
+
+/* h = layerNorm(h + y) per row: the f32 residual add of encoder/attention.go:123-127 and
+ * encoder/bert.go:363-365 (d_y may be NULL: no residual), then encoder/layernorm.go:18-38
+ * (float64 mean and variance, divisor D, gain d_w[D], shift d_b[D]). D <= 4096. */
+int enchip_residual_layer_norm_dev(enchip_ctx *ctx, float *d_h, int64_t ldh, const float *d_y,
+                                   int64_t ldy, int64_t rows, int64_t D, const float *d_w,
+                                   const float *d_b, double eps, void *stream);
+
+/* Mean pooling then L2 normalisation of nseq sequences of L rows each (rows
+ * z*L .. z*L+L-1 of d_h, pitch ldh) into d_out[nseq][ldo]: encoder/pooling.go:84-105
+ * poolOne(mean) and embed/pool.go:22-38 L2Normalize, in their summation order, so the
+ * result is exact. L == 0 gives zero vectors, as the reference does. D <= 4096. */
+int enchip_pool_mean_l2_dev(enchip_ctx *ctx, const float *d_h, int64_t ldh, int64_t nseq,
+                            int64_t L, int64_t D, float *d_out, int64_t ldo, void *stream);
+
 /* Rows at or below which the small-M (HBM-bound, split-K) kernel runs instead of
  * the tiled MFMA GEMM. Both produce identical bits; this only selects the kernel.
  * Mirrors the reference's dispatch knobs (linalg.SetParallelThreshold,

@@ -126,3 +126,55 @@ def test_config4_bert_base_embedding(ctx, workers):
     g = workloads.rng(12)
     seqs = [g.integers(1000, 30000, size=cfg.seq)]
     run_both(ctx, workers, cfg, seqs, seed=102)
+
+
+def embeddings_in(ids, w, cfg):
+    """bert.go:299-323 for one sequence: word + position + token type 0, then LayerNorm."""
+    L, D = len(ids), cfg.hidden
+    h = np.empty((L, D), np.float32)
+    for i, t in enumerate(ids):
+        row = (w["word"][t] + w["pos"][i]).astype(np.float32)
+        h[i] = (row + w["type"][0]).astype(np.float32)
+    return oracle.layer_norm(h, *w["emb_ln"], L, D, 1e-12)
+
+
+def test_config1_device_resident_forward(ctx, workers):
+    # The whole forward on the device (aikit_amd.bert_dev: W8A8 linears, f32 attention
+    # products, softmax, residual + LayerNorm, pooling), every activation resident,
+    # against the CPU reference composition of the same model. Attention and LayerNorm
+    # sum in a different order on the device, so the bar is the north star's cosine.
+    import torch
+
+    from aikit_amd.bert_dev import DeviceBert
+
+    cfg = workloads.MINILM_L6
+    g = workloads.rng(11)
+    seqs = [g.integers(1000, 30000, size=cfg.seq) for _ in range(cfg.batch)]
+    w = model_weights(cfg, seed=101)
+
+    def ref_linear(x, li, name):
+        wq, ws, b, act = w["layers"][li][name]
+        M, K = x.shape
+        return oracle.cpu_w8a8_linear(x, wq, ws, b, act, M, K, wq.shape[0], workers=workers).reshape(M, -1)
+
+    S, L, D = cfg.batch, cfg.seq, cfg.hidden
+    h0 = np.concatenate([embeddings_in(ids, w, cfg) for ids in seqs])
+    model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn)
+    try:
+        say(f"{cfg.name} device-resident forward, {S} sequences of {L}")
+        h = torch.from_numpy(h0).cuda()
+        pooled = torch.empty((S, D), device="cuda")
+        torch.cuda.synchronize()
+        model.embed(h, S, L, pooled)
+        torch.cuda.synchronize()
+        dev = pooled.cpu().numpy()
+    finally:
+        model.close()
+    worst = 1.0
+    for s, ids in enumerate(seqs):
+        ref = encode(ids, w, cfg, ref_linear)
+        cos = float(np.dot(ref.astype(np.float64), dev[s].astype(np.float64)) /
+                    (np.linalg.norm(ref.astype(np.float64)) * np.linalg.norm(dev[s].astype(np.float64))))
+        worst = min(worst, cos)
+        assert cos >= COS_MIN, f"{cfg.name} seq {s}: cosine {cos}"
+    say(f"  worst cosine {worst:.9f}")

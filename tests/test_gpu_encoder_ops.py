@@ -1,0 +1,142 @@
+"""GPU parity for the encoder row operations (softmax, residual + LayerNorm, mean pool +
+L2), through the C ABI, against the oracle's restatements of the reference
+(linalg/exp_scalar.go:9-35,84-89; encoder/layernorm.go:18-38; encoder/pooling.go:84-105;
+embed/pool.go:22-38).
+
+Pooling keeps the reference's summation order and must match bit for bit. Softmax and
+LayerNorm add their float64 partial sums as a tree, so a result may differ from the
+oracle by one f32 ulp where the float64 sum lands differently; the tests allow exactly
+that (and require NaN patterns and special rows to match exactly).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from aikit_amd import workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def ordered(x):
+    """float32 -> int64 keys whose differences count ulps across the sign boundary."""
+    i = np.ascontiguousarray(x, np.float32).view(np.int32).astype(np.int64)
+    return np.where(i < 0, -(i & 0x7FFFFFFF), i)
+
+
+def assert_ulps(got, want, max_ulps, what):
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    nan = np.isnan(want)
+    assert (np.isnan(got) == nan).all(), f"{what}: NaN pattern differs"
+    d = np.abs(ordered(got[~nan]) - ordered(want[~nan]))
+    assert d.size == 0 or d.max() <= max_ulps, f"{what}: {int(d.max())} ulps apart (allowed {max_ulps})"
+    return int((d > 0).sum())
+
+
+def _dev(torch, x):
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+@pytest.mark.parametrize("cols", [1, 7, 64, 77, 128, 512, 1000, 4096])
+def test_softmax_rows_scaled_matches_oracle(ctx, cols):
+    import torch
+
+    g = workloads.rng(300 + cols)
+    rows = 67
+    x = (g.standard_normal((rows, cols)) * 6).astype(np.float32)
+    if cols > 3:
+        x[1, 0] = np.nan            # NaN first: maxV NaN, every e 0 -> uniform row
+        x[2, 2] = np.nan            # later NaN: skipped by the max; expF32Core(NaN) is 0 (Go's int32 conversion)
+        x[3, :] = -np.inf           # all -inf: v - maxV is NaN -> e 0 -> uniform
+        x[4, 0] = -np.inf           # -inf first, then finite values
+        x[5, :] = 0                 # all equal
+        x[6, 1] = 200.0             # one dominant value, the rest underflow to 0
+    scale = np.float32(0.125)
+    say(f"softmax rows={rows} cols={cols}")
+    d = _dev(torch, x)
+    torch.cuda.synchronize()
+    ctx.softmax_rows_scaled_dev(d.data_ptr(), cols, rows, cols, float(scale))
+    torch.cuda.synchronize()
+    got = d.cpu().numpy()
+    want = np.stack([oracle.softmax_row_scaled(r, scale) for r in x])
+    n = assert_ulps(got, want, 1, f"softmax cols={cols}")
+    say(f"  {n} of {got.size} values one ulp apart")
+    if cols > 3:
+        for r in (1, 3, 5):  # uniform rows and the all-equal row: sums of integers, exact in any order
+            assert np.array_equal(got[r], want[r]), f"special row {r}"
+
+
+def test_softmax_pitched_rows(ctx):
+    # ld > cols: only the first cols of each row are touched.
+    import torch
+
+    g = workloads.rng(310)
+    rows, cols, ld = 40, 300, 320
+    x = g.standard_normal((rows, ld)).astype(np.float32)
+    d = _dev(torch, x)
+    torch.cuda.synchronize()
+    ctx.softmax_rows_scaled_dev(d.data_ptr(), ld, rows, cols, 0.5)
+    torch.cuda.synchronize()
+    got = d.cpu().numpy()
+    assert np.array_equal(got[:, cols:], x[:, cols:])
+    want = np.stack([oracle.softmax_row_scaled(r[:cols], np.float32(0.5)) for r in x])
+    assert_ulps(got[:, :cols], want, 1, "pitched softmax")
+
+
+@pytest.mark.parametrize("D,with_res", [(384, True), (768, True), (768, False), (1024, True), (100, True),
+                                        (4096, True)])
+def test_residual_layer_norm_matches_oracle(ctx, D, with_res):
+    import torch
+
+    g = workloads.rng(400 + D)
+    rows = 130
+    h = (g.standard_normal((rows, D)) * 3 + 0.5).astype(np.float32)
+    y = g.standard_normal((rows, D)).astype(np.float32)
+    h[7] = 1.25  # constant row: variance 0, output = shift
+    w = (1 + g.standard_normal(D) * 0.1).astype(np.float32)
+    b = (g.standard_normal(D) * 0.1).astype(np.float32)
+    say(f"layer norm rows={rows} D={D} residual={with_res}")
+    dh, dy, dw, db = (_dev(torch, v) for v in (h, y, w, b))
+    torch.cuda.synchronize()
+    ctx.residual_layer_norm_dev(dh.data_ptr(), D, dy.data_ptr() if with_res else 0, D, rows, D, dw.data_ptr(),
+                                db.data_ptr(), 1e-12)
+    torch.cuda.synchronize()
+    x = (h + y).astype(np.float32) if with_res else h  # the f32 residual add, element by element
+    want = oracle.layer_norm(x, w, b, rows, D, 1e-12)
+    n = assert_ulps(dh.cpu().numpy(), want, 1, f"layer norm D={D}")
+    say(f"  {n} of {rows * D} values one ulp apart")
+
+
+@pytest.mark.parametrize("S,L,D", [(3, 128, 384), (2, 512, 768), (1, 1, 5), (4, 77, 1024)])
+def test_pool_mean_l2_bit_exact(ctx, S, L, D):
+    import torch
+
+    g = workloads.rng(500 + S * L + D)
+    h = g.standard_normal((S * L, D)).astype(np.float32)
+    say(f"pool S={S} L={L} D={D}")
+    dh = _dev(torch, h)
+    out = torch.empty((S, D), device="cuda")
+    torch.cuda.synchronize()
+    ctx.pool_mean_l2_dev(dh.data_ptr(), D, S, L, D, out.data_ptr(), D)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for s in range(S):
+        want = oracle.l2_normalize(oracle.pool_mean(h[s * L:(s + 1) * L], L, D))
+        assert np.array_equal(got[s].view(np.uint32), want.view(np.uint32)), f"sequence {s}"
+
+
+def test_pool_zero_and_empty_sequences(ctx):
+    import torch
+
+    D = 64
+    h = np.zeros((4, D), np.float32)
+    dh = _dev(torch, h)
+    out = torch.full((2, D), 7.0, device="cuda")
+    torch.cuda.synchronize()
+    ctx.pool_mean_l2_dev(dh.data_ptr(), D, 2, 2, D, out.data_ptr(), D)  # all-zero rows: norm < 1e-12 -> zeros
+    ctx.pool_mean_l2_dev(dh.data_ptr(), D, 1, 0, D, out.data_ptr(), D)  # L = 0: the zero vector
+    torch.cuda.synchronize()
+    assert not out.cpu().numpy().any()

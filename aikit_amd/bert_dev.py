@@ -7,10 +7,12 @@ matmul seam, docs/task-native-gpu.md:418-427):
   qkv   = W8A8(h, Wqkv) + b            enchip_w8a8_linear_dev (Q, K, V fused: one N = 3D
                                         weight sharing one activation quantization,
                                         linalg.MatmulBTW8A8Batch)
-  S     = Q_h . K_h^T                   enchip_matmul_bt_f32_dev, every (head, sequence) in
-                                        one launch, heads read in place from qkv
-  P     = softmax(S * 1/sqrt(hd))       enchip_softmax_rows_scaled_dev
-  ctx_h = P . V_h                       enchip_matmul_bt_f32_dev (V read as [K, N] rows)
+  ctx_h = softmax(Q_h.K_h^T/sqrt(hd)).V_h
+                                        enchip_attention_f32_dev: every (head, sequence) in
+                                        one launch, heads read in place from qkv, scores
+                                        kept on chip (head_dim 32/64, L <= 512); otherwise
+                                        enchip_matmul_bt_f32_dev, enchip_softmax_rows_scaled_dev,
+                                        enchip_matmul_bt_f32_dev through an [S, H, L, L] buffer
   out   = W8A8(ctx, Wo) + b             enchip_w8a8_linear_dev
   h     = LN(h + out)                   enchip_residual_layer_norm_dev
   inter = GELU(W8A8(h, Wi) + b)         enchip_w8a8_linear_dev (fused epilogue)
@@ -42,9 +44,11 @@ class DeviceBert:
     bias f32 [N], act), "attn_ln"|"out_ln": (gain f32 [D], shift f32 [D])}.
     """
 
-    def __init__(self, ctx: enchip.Context, layers: Sequence[Dict], hidden: int, heads: int, ffn: int):
+    def __init__(self, ctx: enchip.Context, layers: Sequence[Dict], hidden: int, heads: int, ffn: int,
+                 fused: bool = True):
         import torch
 
+        self.fused = fused
         self.torch = torch
         self.ctx, self.D, self.H, self.I = ctx, hidden, heads, ffn
         self.hd = hidden // heads
@@ -71,12 +75,16 @@ class DeviceBert:
         self.handles = []
         self._bufs = {}
 
+    def fused_attention(self, L: int) -> bool:
+        return self.hd in (32, 64) and L <= 512 and self.fused
+
     def _buffers(self, S: int, L: int):
         key = (S, L)
         if key not in self._bufs:
             t, M = self.torch, S * L
             f = dict(device="cuda", dtype=t.float32)
-            self._bufs = {key: dict(qkv=t.empty((M, 3 * self.D), **f), scores=t.empty((S, self.H, L, L), **f),
+            sc = (1,) if self.fused_attention(L) else (S, self.H, L, L)
+            self._bufs = {key: dict(qkv=t.empty((M, 3 * self.D), **f), scores=t.empty(sc, **f),
                                     ctx=t.empty((M, self.D), **f), out=t.empty((M, self.D), **f),
                                     inter=t.empty((M, self.I), **f), ffn=t.empty((M, self.D), **f))}
         return self._bufs[key]
@@ -93,11 +101,16 @@ class DeviceBert:
         for e in self.handles:
             w, bias, act = e["qkv"]
             c.linear_dev(w, h.data_ptr(), M, bias.data_ptr(), act, q, stream)
-            c.matmul_bt_f32_dev(q, 3 * D, q + D * 4, 3 * D, enchip.B_NK, scores.data_ptr(), L, L, hd, L,
-                                inner=(H, hd, hd, L * L), outer=(S, L * 3 * D, L * 3 * D, H * L * L), stream=stream)
-            c.softmax_rows_scaled_dev(scores.data_ptr(), L, S * H * L, L, scale, stream)
-            c.matmul_bt_f32_dev(scores.data_ptr(), L, q + 2 * D * 4, 3 * D, enchip.B_KN, ctxv.data_ptr(), D, L, L, hd,
-                                inner=(H, L * L, hd, hd), outer=(S, H * L * L, L * 3 * D, L * D), stream=stream)
+            if self.fused_attention(L):
+                c.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, ctxv.data_ptr(), D, S, L, H, hd, scale, stream)
+            else:
+                c.matmul_bt_f32_dev(q, 3 * D, q + D * 4, 3 * D, enchip.B_NK, scores.data_ptr(), L, L, hd, L,
+                                    inner=(H, hd, hd, L * L), outer=(S, L * 3 * D, L * 3 * D, H * L * L),
+                                    stream=stream)
+                c.softmax_rows_scaled_dev(scores.data_ptr(), L, S * H * L, L, scale, stream)
+                c.matmul_bt_f32_dev(scores.data_ptr(), L, q + 2 * D * 4, 3 * D, enchip.B_KN, ctxv.data_ptr(), D, L, L,
+                                    hd, inner=(H, L * L, hd, hd), outer=(S, H * L * L, L * 3 * D, L * D),
+                                    stream=stream)
             w, bias, act = e["o"]
             c.linear_dev(w, ctxv.data_ptr(), M, bias.data_ptr(), act, out.data_ptr(), stream)
             g, s = e["attn_ln"]

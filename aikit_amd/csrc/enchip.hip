@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "enchip.h"
+#include "attention_f32.h"
 #include "encoder_ops.h"
 #include "gemm_f32.h"
 #include "gemm_persistent.h"
@@ -929,4 +930,41 @@ int enchip_pool_mean_l2_dev(enchip_ctx *ctx, const float *d_h, int64_t ldh, int6
     hipLaunchKernelGGL(enchip::pool_mean_l2, dim3((unsigned)nseq), dim3(256), 0, s, d_h, ldh, (int)L, (int)D, d_out,
                        ldo);
     return check_launch(ctx, "pool_mean_l2");
+}
+
+int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k, const float *d_v, int64_t ld,
+                             float *d_out, int64_t ldo, int64_t nseq, int64_t L, int64_t heads, int64_t head_dim,
+                             float scale, void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (head_dim != 32 && head_dim != 64)
+        return fail(ctx, ENCHIP_ERR_ARG, "attention: head_dim must be 32 or 64, got %lld", (long long)head_dim);
+    if (nseq < 0 || L < 0 || L > enchip::ATT_MAX_L || heads < 0 || heads > 65535 || ld < heads * head_dim ||
+        ldo < heads * head_dim || ld % 4 != 0 || nseq * L > ((int64_t)1 << 31))
+        return fail(ctx, ENCHIP_ERR_ARG,
+                    "attention: bad shape nseq=%lld L=%lld (<= %d) heads=%lld ld=%lld ldo=%lld (ld a multiple of 4 "
+                    "covering heads*head_dim)",
+                    (long long)nseq, (long long)L, enchip::ATT_MAX_L, (long long)heads, (long long)ld, (long long)ldo);
+    if (nseq == 0 || L == 0 || heads == 0) return ENCHIP_OK;
+    if (!d_q || !d_k || !d_v || !d_out) return fail(ctx, ENCHIP_ERR_ARG, "attention: null pointer");
+    if ((uintptr_t)d_q % 16 || (uintptr_t)d_k % 16 || (uintptr_t)d_v % 16)
+        return fail(ctx, ENCHIP_ERR_ARG, "attention: q, k and v must be 16-byte aligned");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    const size_t lds = (size_t)enchip::att_lds_floats((int)L) * sizeof(float);
+    const void *fn = head_dim == 64 ? reinterpret_cast<const void *>(&enchip::attention_f32<64>)
+                                    : reinterpret_cast<const void *>(&enchip::attention_f32<32>);
+    HIP_TRY(ctx, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    for (int64_t z0 = 0; z0 < nseq; z0 += 65535) {
+        const unsigned nz = (unsigned)std::min<int64_t>(65535, nseq - z0);
+        const dim3 grid((unsigned)((L + enchip::ATT_QT - 1) / enchip::ATT_QT), (unsigned)heads, nz);
+        const int64_t off = z0 * L;
+        if (head_dim == 64)
+            hipLaunchKernelGGL(enchip::attention_f32<64>, grid, dim3(64 * enchip::ATT_WAVES), lds, s, d_q + off * ld,
+                               d_k + off * ld, d_v + off * ld, ld, d_out + off * ldo, ldo, (int)L, scale);
+        else
+            hipLaunchKernelGGL(enchip::attention_f32<32>, grid, dim3(64 * enchip::ATT_WAVES), lds, s, d_q + off * ld,
+                               d_k + off * ld, d_v + off * ld, ld, d_out + off * ldo, ldo, (int)L, scale);
+    }
+    return check_launch(ctx, "attention_f32");
 }

@@ -49,6 +49,8 @@ _SIGNATURES = {
     "enchip_residual_layer_norm_dev": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp, ctypes.c_double,
                                               _vp]),
     "enchip_pool_mean_l2_dev": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
+    "enchip_attention_f32_dev": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
+                                        _vp]),
     "enchip_matmul_bt_f32_dev": (_int, [_vp, _vp, _i64, _vp, _i64, _int, _vp, _i64, _i64, _i64, _i64, _vp, _vp,
                                         _vp]),
     "enchip_w8a8_pre_frag_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _i64, _vp, _vp, _int, _vp, _vp]),
@@ -282,6 +284,12 @@ class Context:
                                 eps: float, stream: int = 0) -> None:
         self._check(self._lib.enchip_residual_layer_norm_dev(self._h, d_h or None, ldh, d_y or None, ldy, rows, D,
                                                              d_w or None, d_b or None, eps, stream or None))
+
+    def attention_f32_dev(self, d_q: int, d_k: int, d_v: int, ld: int, d_out: int, ldo: int, nseq: int, L: int,
+                          heads: int, head_dim: int, scale: float, stream: int = 0) -> None:
+        self._check(self._lib.enchip_attention_f32_dev(self._h, d_q or None, d_k or None, d_v or None, ld,
+                                                       d_out or None, ldo, nseq, L, heads, head_dim, scale,
+                                                       stream or None))
 
     def pool_mean_l2_dev(self, d_h: int, ldh: int, nseq: int, L: int, D: int, d_out: int, ldo: int,
                          stream: int = 0) -> None:

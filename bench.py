@@ -355,11 +355,24 @@ def other_configs(ctx, torch, stream, ceilings):
         att[f"{name}_tflops"] = flops / t / 1e12
         att[f"{name}_frac_fp32_mfma_peak"] = flops / t / PEAK_FP32_FLOPS
         att[f"{name}_hbm_gbps"] = nbytes / t / 1e9
+    # the fused form: both products and the softmax in one launch, scores kept on chip
+    for _ in range(3):
+        ctx.attention_f32_dev(base, base + D * 4, base + 2 * D * 4, 3 * D, ctxv.data_ptr(), D, S, L, H, hd, 0.125, sp)
+    e0.record(stream)
+    for _ in range(10):
+        ctx.attention_f32_dev(base, base + D * 4, base + 2 * D * 4, 3 * D, ctxv.data_ptr(), D, S, L, H, hd, 0.125, sp)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / 10
+    att["fused_us"] = t * 1e6
+    att["fused_tflops"] = 2 * flops / t / 1e12
+    att["fused_frac_fp32_mfma_peak"] = 2 * flops / t / PEAK_FP32_FLOPS
     att.update({"S": S, "L": L, "heads": H, "head_dim": hd, "gflop_per_product": flops / 1e9,
-                "kernels": "enchip::gemm_f32_bt_lds<2, 2, false> (QK^T), enchip::gemm_f32_bt_lds<4, 1, true> (PV)",
+                "kernels": "enchip::gemm_f32_bt_lds<2, 2, false> (QK^T), enchip::gemm_f32_bt_lds<4, 1, true> (PV), "
+                           "enchip::attention_f32<64> (fused: QK^T, softmax, PV with the scores in LDS)",
                 "note": "one config-4 layer's attention products in f32 (v_mfma_f32_32x32x2_f32), all 768 "
                         "(sequence, head) problems per launch, operands resident; bytes = operands read once + "
-                        "output written once; softmax not included"})
+                        "output written once; softmax not included in qk/pv, included in fused"})
     out["attention_f32_cfg4_layer"] = att
     del qkv, scores, ctxv
     return out

@@ -269,6 +269,22 @@ int enchip_residual_layer_norm_dev(enchip_ctx *ctx, float *d_h, int64_t ldh, con
 int enchip_pool_mean_l2_dev(enchip_ctx *ctx, const float *d_h, int64_t ldh, int64_t nseq,
                             int64_t L, int64_t D, float *d_out, int64_t ldo, void *stream);
 
+/* Scaled dot-product attention on device buffers, every head of nseq sequences of L
+ * tokens in one call: encoder/attention.go:81-121 attentionCore (mOut = L) up to the
+ * context, ctx = softmaxRowScaled(Q_h . K_h^T, scale) . V_h per head, written into
+ * d_out's head columns. Row i of sequence z, head h of Q starts at
+ * d_q + (z*L + i)*ld + h*head_dim (likewise K, V; all three share the pitch, as in the
+ * fused [tokens, 3D] QKV rows) and the context at d_out + (z*L + i)*ldo + h*head_dim.
+ * The score tile of 32 queries stays in on-chip memory (never written to device
+ * memory); its softmax follows enchip_softmax_rows_scaled_dev, its products the f32
+ * MFMA, and the result agrees with enchip_matmul_bt_f32_dev + softmax + matmul within
+ * the f32 MatmulBT gate (summation order differs). head_dim 32 or 64; L <= 512; ld a
+ * multiple of 4; q, k, v 16-byte aligned. */
+int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k,
+                             const float *d_v, int64_t ld, float *d_out, int64_t ldo,
+                             int64_t nseq, int64_t L, int64_t heads, int64_t head_dim,
+                             float scale, void *stream);
+
 /* Rows at or below which the small-M (HBM-bound, split-K) kernel runs instead of
  * the tiled MFMA GEMM. Both produce identical bits; this only selects the kernel.
  * Mirrors the reference's dispatch knobs (linalg.SetParallelThreshold,

@@ -138,7 +138,8 @@ def embeddings_in(ids, w, cfg):
     return oracle.layer_norm(h, *w["emb_ln"], L, D, 1e-12)
 
 
-def test_config1_device_resident_forward(ctx, workers):
+@pytest.mark.parametrize("fused", [True, False])
+def test_config1_device_resident_forward(ctx, workers, fused):
     # The whole forward on the device (aikit_amd.bert_dev: W8A8 linears, f32 attention
     # products, softmax, residual + LayerNorm, pooling), every activation resident,
     # against the CPU reference composition of the same model. Attention and LayerNorm
@@ -159,9 +160,9 @@ def test_config1_device_resident_forward(ctx, workers):
 
     S, L, D = cfg.batch, cfg.seq, cfg.hidden
     h0 = np.concatenate([embeddings_in(ids, w, cfg) for ids in seqs])
-    model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn)
+    model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn, fused=fused)
     try:
-        say(f"{cfg.name} device-resident forward, {S} sequences of {L}")
+        say(f"{cfg.name} device-resident forward, {S} sequences of {L}, fused attention {fused}")
         h = torch.from_numpy(h0).cuda()
         pooled = torch.empty((S, D), device="cuda")
         torch.cuda.synchronize()

@@ -140,3 +140,70 @@ def test_pool_zero_and_empty_sequences(ctx):
     ctx.pool_mean_l2_dev(dh.data_ptr(), D, 1, 0, D, out.data_ptr(), D)  # L = 0: the zero vector
     torch.cuda.synchronize()
     assert not out.cpu().numpy().any()
+
+
+# ------------------------------------------------------------------ fused attention
+def _attention_f64(qkv, S, L, H, hd, scale):
+    """float64 ground truth of attentionCore's context (encoder/attention.go:95-116)."""
+    D = H * hd
+    out = np.empty((S, L, D), np.float64)
+    for s in range(S):
+        x = qkv[s].astype(np.float64)
+        for h in range(H):
+            Q, K, V = (x[:, o + h * hd:o + (h + 1) * hd] for o in (0, D, 2 * D))
+            sc = (Q @ K.T) * float(scale)
+            e = np.exp(sc - sc.max(axis=1, keepdims=True))
+            out[s, :, h * hd:(h + 1) * hd] = (e / e.sum(axis=1, keepdims=True)) @ V
+    return out
+
+
+@pytest.mark.parametrize("S,L,H,hd", [(2, 128, 12, 64), (1, 512, 4, 64), (3, 77, 6, 32), (2, 40, 2, 64),
+                                      (1, 1, 3, 64), (2, 512, 2, 32)])
+def test_fused_attention_matches_f64_and_unfused(ctx, S, L, H, hd):
+    # Gate: the f32 MatmulBT statistic (gpu/enccuda/backend_test.go:71-81) against a
+    # float64 attention, for the fused kernel and for the unfused chain (two batched
+    # MatmulBT calls around the softmax), and between the two.
+    import torch
+
+    from aikit_amd import enchip
+
+    D = H * hd
+    g = workloads.rng(700 + S * L + H + hd)
+    qkv = g.standard_normal((S, L, 3 * D)).astype(np.float32)
+    scale = np.float32(1.0 / np.sqrt(hd))
+    say(f"fused attention S={S} L={L} H={H} hd={hd}")
+    dq = torch.from_numpy(qkv).cuda()
+    fused = torch.full((S * L, D), np.nan, device="cuda")
+    unfused = torch.full((S * L, D), np.nan, device="cuda")
+    scores = torch.empty((S, H, L, L), device="cuda")
+    torch.cuda.synchronize()
+    q = dq.data_ptr()
+    ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, fused.data_ptr(), D, S, L, H, hd, float(scale))
+    ctx.matmul_bt_f32_dev(q, 3 * D, q + D * 4, 3 * D, enchip.B_NK, scores.data_ptr(), L, L, hd, L,
+                          inner=(H, hd, hd, L * L), outer=(S, L * 3 * D, L * 3 * D, H * L * L))
+    ctx.softmax_rows_scaled_dev(scores.data_ptr(), L, S * H * L, L, float(scale))
+    ctx.matmul_bt_f32_dev(scores.data_ptr(), L, q + 2 * D * 4, 3 * D, enchip.B_KN, unfused.data_ptr(), D, L, L, hd,
+                          inner=(H, L * L, hd, hd), outer=(S, H * L * L, L * 3 * D, L * D))
+    torch.cuda.synchronize()
+    f, u = fused.cpu().numpy().reshape(S, L, D), unfused.cpu().numpy().reshape(S, L, D)
+    want = _attention_f64(qkv, S, L, H, hd, scale)
+    wf, wu, fu = (oracle.matmul_bt_worst_rel(a, b) for a, b in ((f, want), (u, want), (f, u)))
+    say(f"  worst rel: fused {wf:.3g}, unfused {wu:.3g}, fused vs unfused {fu:.3g}")
+    assert wf <= 2e-4 and wu <= 2e-4 and fu <= 2e-4
+    # and the CPU restatement of the reference's attention for the first sequence
+    ref = oracle.attention(qkv[0, :, :D], qkv[0, :, D:2 * D], qkv[0, :, 2 * D:], L, D, H)
+    assert oracle.matmul_bt_worst_rel(f[0], ref) <= 2e-4
+
+
+def test_fused_attention_rejects_unsupported(ctx):
+    import torch
+
+    from aikit_amd import enchip
+
+    d = torch.zeros(4096, device="cuda")
+    p = d.data_ptr()
+    with pytest.raises(enchip.EnchipError):  # head_dim 48
+        ctx.attention_f32_dev(p, p, p, 48, p, 48, 1, 8, 1, 48, 0.1)
+    with pytest.raises(enchip.EnchipError):  # L above 512
+        ctx.attention_f32_dev(p, p, p, 64, p, 64, 1, 513, 1, 64, 0.1)
+    torch.cuda.synchronize()

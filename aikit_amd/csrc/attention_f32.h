@@ -25,6 +25,7 @@
 
 #include "encoder_ops.h"
 #include "gemm_f32.h"
+#include "kernels.h"
 
 #pragma clang fp contract(off)
 
@@ -56,13 +57,17 @@ __device__ __forceinline__ void load8(const float *p, float *d) {
     d[4] = b.x; d[5] = b.y; d[6] = b.z; d[7] = b.w;
 }
 
-// HD: head dimension (32 or 64). Grid (ceil(L/32), heads, sequences), 512 threads,
-// att_lds_floats(L) floats of dynamic LDS. Row i of sequence z, head h starts at
-// q/k/v + (z*L + i)*ld + h*HD (16-byte aligned), out + (z*L + i)*ldo + h*HD.
+// HD: head dimension (32 or 64). A 1-D grid of ceil(L/32) * heads * sequences
+// workgroups of 512 threads, att_lds_floats(L) floats of dynamic LDS. Workgroups are
+// mapped XCD-aware (xcd_logical_tile): the query tiles of one (head, sequence) run on one
+// XCD, so its K and V (256 KB at L = 512) are fetched into one L2 (measured neutral at
+// BERT-base shapes, where K and V stay in the 256 MB MALL either way).
+// Row i of sequence z, head h starts at q/k/v + (z*L + i)*ld + h*HD (16-byte aligned),
+// out + (z*L + i)*ldo + h*HD.
 template <int HD>
 __global__ __launch_bounds__(64 * ATT_WAVES, 4) void attention_f32(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t ld,
-    float *__restrict__ out, int64_t ldo, int L, float scale) {
+    float *__restrict__ out, int64_t ldo, int L, int heads, float scale) {
     static_assert(HD == 32 || HD == 64, "head dimension");
     constexpr int NOT = HD / 32;                     // 32-column output tiles of the context
     constexpr int G = ATT_WAVES / NOT;               // key groups in step 3
@@ -72,9 +77,10 @@ __global__ __launch_bounds__(64 * ATT_WAVES, 4) void attention_f32(
     extern __shared__ __attribute__((aligned(16))) float sc[];
     const int P = att_pitch(L);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 31, hf = lane >> 5;
-    const int q0 = blockIdx.x * ATT_QT, head = blockIdx.y;
-    const int64_t row0 = (int64_t)blockIdx.z * L;
-    const int nkt = (L + 31) / 32;
+    const int nkt = (L + 31) / 32, nqt = (L + ATT_QT - 1) / ATT_QT;
+    const int logical = xcd_logical_tile(blockIdx.x, gridDim.x);
+    const int q0 = (logical % nqt) * ATT_QT, head = (logical / nqt) % heads;
+    const int64_t row0 = (int64_t)(logical / nqt / heads) * L;
 
     // ---- 1. S = Q K^T * scale into LDS. In MFMA step s of 16-deep block b, lane half hf
     // supplies head-dim index 16b + 8hf + s of both operands; rows past L re-read row L-1.

@@ -955,16 +955,19 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
     const void *fn = head_dim == 64 ? reinterpret_cast<const void *>(&enchip::attention_f32<64>)
                                     : reinterpret_cast<const void *>(&enchip::attention_f32<32>);
     HIP_TRY(ctx, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    for (int64_t z0 = 0; z0 < nseq; z0 += 65535) {
-        const unsigned nz = (unsigned)std::min<int64_t>(65535, nseq - z0);
-        const dim3 grid((unsigned)((L + enchip::ATT_QT - 1) / enchip::ATT_QT), (unsigned)heads, nz);
+    // one launch per chunk of sequences whose workgroup count fits a 32-bit grid
+    const int64_t per_seq = ((L + enchip::ATT_QT - 1) / enchip::ATT_QT) * heads;
+    const int64_t chunk = std::max<int64_t>(1, ((int64_t)1 << 30) / per_seq);
+    for (int64_t z0 = 0; z0 < nseq; z0 += chunk) {
+        const int64_t nz = std::min<int64_t>(chunk, nseq - z0);
+        const dim3 grid((unsigned)(per_seq * nz));
         const int64_t off = z0 * L;
         if (head_dim == 64)
             hipLaunchKernelGGL(enchip::attention_f32<64>, grid, dim3(64 * enchip::ATT_WAVES), lds, s, d_q + off * ld,
-                               d_k + off * ld, d_v + off * ld, ld, d_out + off * ldo, ldo, (int)L, scale);
+                               d_k + off * ld, d_v + off * ld, ld, d_out + off * ldo, ldo, (int)L, (int)heads, scale);
         else
             hipLaunchKernelGGL(enchip::attention_f32<32>, grid, dim3(64 * enchip::ATT_WAVES), lds, s, d_q + off * ld,
-                               d_k + off * ld, d_v + off * ld, ld, d_out + off * ldo, ldo, (int)L, scale);
+                               d_k + off * ld, d_v + off * ld, ld, d_out + off * ldo, ldo, (int)L, (int)heads, scale);
     }
     return check_launch(ctx, "attention_f32");
 }

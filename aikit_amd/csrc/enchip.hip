@@ -919,16 +919,16 @@ int enchip_pool_mean_l2_dev(enchip_ctx *ctx, const float *d_h, int64_t ldh, int6
                             float *d_out, int64_t ldo, void *stream) {
     if (!ctx) return ENCHIP_ERR_ARG;
     std::lock_guard<std::mutex> g(ctx->mu);
-    if (nseq < 0 || L < 0 || D < 0 || D > enchip::kPoolMaxD || ldh < D || ldo < D || nseq > 0x7fffffff ||
-        L > 0x7fffffff)
-        return fail(ctx, ENCHIP_ERR_ARG, "pool: bad shape nseq=%lld L=%lld D=%lld (D <= %d)", (long long)nseq,
-                    (long long)L, (long long)D, enchip::kPoolMaxD);
+    if (nseq < 0 || L < 0 || D < 0 || D > 4096 || ldh < D || ldo < D || nseq > 65535 || L > 0x7fffffff)
+        return fail(ctx, ENCHIP_ERR_ARG, "pool: bad shape nseq=%lld L=%lld D=%lld (D <= 4096, nseq <= 65535)",
+                    (long long)nseq, (long long)L, (long long)D);
     if (nseq == 0 || D == 0) return ENCHIP_OK;
     if (!d_out || (L > 0 && !d_h)) return fail(ctx, ENCHIP_ERR_ARG, "pool: null pointer");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    hipLaunchKernelGGL(enchip::pool_mean_l2, dim3((unsigned)nseq), dim3(256), 0, s, d_h, ldh, (int)L, (int)D, d_out,
-                       ldo);
+    hipLaunchKernelGGL(enchip::pool_mean_cols, dim3((unsigned)((D + 255) / 256), (unsigned)nseq), dim3(256), 0, s, d_h,
+                       ldh, (int)L, (int)D, d_out, ldo);
+    hipLaunchKernelGGL(enchip::l2_normalize_rows, dim3((unsigned)nseq), dim3(256), 0, s, d_out, ldo, (int)D);
     return check_launch(ctx, "pool_mean_l2");
 }
 

@@ -128,34 +128,33 @@ __global__ __launch_bounds__(256) void residual_layer_norm(float *__restrict__ h
 }
 
 // Mean pooling then L2 normalisation of each of nseq sequences of L rows
-// (encoder/pooling.go:84-105 poolOne(mean), embed/pool.go:22-38 L2Normalize), one
-// 256-thread block per sequence, in the reference's summation order: each column's
-// float64 sum runs over the rows in order (one thread per column), and the sum of
-// squares runs over the columns in order (one thread), so the result is exact.
-// D <= kPoolMaxD.
-constexpr int kPoolMaxD = 4096;
+// (encoder/pooling.go:84-105 poolOne(mean), embed/pool.go:22-38 L2Normalize) in the
+// reference's summation order, so the result is exact:
+//   pool_mean_cols: one thread per (sequence, column); the column's float64 sum runs over
+//     the rows in order; out = float32(sum * (1/L)). Grid (ceil(D/256), nseq).
+//   l2_normalize_rows: one block per sequence; one thread adds the squares over the
+//     columns in order, then out = float32(out / norm), or 0 when norm < 1e-12.
+__global__ __launch_bounds__(256) void pool_mean_cols(const float *__restrict__ h, int64_t ldh, int L, int D,
+                                                      float *__restrict__ out, int64_t ldo) {
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= D) return;
+    const float *col = h + (int64_t)blockIdx.y * L * ldh + j;
+    double acc = 0.0;
+    for (int i = 0; i < L; ++i) acc += (double)col[(int64_t)i * ldh];
+    out[blockIdx.y * ldo + j] = L > 0 ? (float)(acc * (1.0 / (double)L)) : 0.0f;
+}
 
-__global__ __launch_bounds__(256) void pool_mean_l2(const float *__restrict__ h, int64_t ldh, int L, int D,
-                                                    float *__restrict__ out, int64_t ldo) {
-    __shared__ float pooled[kPoolMaxD];
+__global__ __launch_bounds__(256) void l2_normalize_rows(float *__restrict__ out, int64_t ldo, int D) {
     __shared__ double norm_s;
-    const int64_t seq = blockIdx.x;
-    const float *base = h + seq * (int64_t)L * ldh;
-    for (int j = threadIdx.x; j < D; j += 256) {
-        double acc = 0.0;
-        for (int i = 0; i < L; ++i) acc += (double)base[(int64_t)i * ldh + j];
-        pooled[j] = L > 0 ? (float)(acc * (1.0 / (double)L)) : 0.0f;
-    }
-    __syncthreads();
+    float *o = out + blockIdx.x * ldo;
     if (threadIdx.x == 0) {
         double sq = 0.0;
-        for (int j = 0; j < D; ++j) sq += (double)pooled[j] * (double)pooled[j];
+        for (int j = 0; j < D; ++j) sq += (double)o[j] * (double)o[j];
         norm_s = sqrt(sq);
     }
     __syncthreads();
     const double norm = norm_s;
-    float *o = out + seq * ldo;
-    for (int j = threadIdx.x; j < D; j += 256) o[j] = norm < 1e-12 ? 0.0f : (float)((double)pooled[j] / norm);
+    for (int j = threadIdx.x; j < D; j += 256) o[j] = norm < 1e-12 ? 0.0f : (float)((double)o[j] / norm);
 }
 
 }  // namespace enchip

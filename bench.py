@@ -434,6 +434,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length (0 = skip)")
     ap.add_argument("--no-other-configs", action="store_true", help="skip the config 2 / config 3 measurements")
+    ap.add_argument("--forward-only", action="store_true",
+                    help="only time the config-4 forward resident on the device and print its figures (a profiling "
+                         "mode: its kernels are then the only ones in a trace)")
     ap.add_argument("--graph", type=int, default=0,
                     help="1: replay each timed step as a captured HIP graph; 0 (default): eager launches. "
                          "Measured equal on MI355X (launch overhead hides behind the kernels)")
@@ -458,6 +461,14 @@ def main() -> int:
     sptr = stream.cuda_stream
     ceilings = ctx.probe_ceilings()
     log(f"measured ceilings {ceilings}")
+
+    if args.forward_only:
+        g = workloads.rng(2024)
+        host = [workloads.encoder_layer_weights(g, cfg) for _ in range(cfg.layers)]
+        fwd = device_forward(ctx, torch, stream, host, cfg, reps=max(1, args.steps))
+        ctx.close()
+        print(json.dumps({"encode_device_cfg4": fwd}), flush=True)
+        return 0
 
     # ---- weights: 12 layers x 4 linears, random N(0,0.02) quantized per channel
     g = workloads.rng(2024)

@@ -265,7 +265,8 @@ int enchip_residual_layer_norm_dev(enchip_ctx *ctx, float *d_h, int64_t ldh, con
 /* Mean pooling then L2 normalisation of nseq sequences of L rows each (rows
  * z*L .. z*L+L-1 of d_h, pitch ldh) into d_out[nseq][ldo]: encoder/pooling.go:84-105
  * poolOne(mean) and embed/pool.go:22-38 L2Normalize, in their summation order, so the
- * result is exact. L == 0 gives zero vectors, as the reference does. D <= 4096. */
+ * result is exact. L == 0 gives zero vectors, as the reference does. D <= 4096,
+ * nseq <= 65535. */
 int enchip_pool_mean_l2_dev(enchip_ctx *ctx, const float *d_h, int64_t ldh, int64_t nseq,
                             int64_t L, int64_t D, float *d_out, int64_t ldo, void *stream);
 

@@ -551,6 +551,82 @@ int enchip_quant_rows(enchip_ctx *ctx, const float *a, int64_t M, int64_t K, int
     return ENCHIP_OK;
 }
 
+namespace {
+
+// Copies a fragment-major image (Np * Kp bytes) and the N scales to the device and
+// records the weight under a new handle.
+int upload_weight(enchip_ctx *ctx, Weight w, const int8_t *image, const float *wscale, enchip_weight *out) {
+    int rc;
+    size_t wcap = 0, scap = 0;
+    const size_t bytes = (size_t)(w.Np * w.Kp);
+    if ((rc = ensure(ctx, &w.d_w, &wcap, bytes))) return rc;
+    if ((rc = ensure(ctx, &w.d_s, &scap, (size_t)w.N * sizeof(float)))) {
+        (void)hipFree(w.d_w);
+        return rc;
+    }
+    hipError_t e1 = hipMemcpy(w.d_w, image, bytes, hipMemcpyHostToDevice);
+    hipError_t e2 = hipMemcpy(w.d_s, wscale, (size_t)w.N * sizeof(float), hipMemcpyHostToDevice);
+    if (e1 != hipSuccess || e2 != hipSuccess) {
+        (void)hipFree(w.d_w);
+        (void)hipFree(w.d_s);
+        return fail(ctx, ENCHIP_ERR_HIP, "weight upload: %s", hipGetErrorString(e1 != hipSuccess ? e1 : e2));
+    }
+    const uint64_t h = ctx->next_handle++;
+    ctx->weights[h] = w;
+    *out = h;
+    return ENCHIP_OK;
+}
+
+Weight weight_shape(int64_t N, int64_t K) {
+    Weight w;
+    w.N = N;
+    w.K = K;
+    w.Np = round_up(N, kColPad);
+    w.Kp = round_up(std::max<int64_t>(K, 1), 64);
+    return w;
+}
+
+}  // namespace
+
+int64_t enchip_weight_image_bytes(int64_t N, int64_t K) {
+    if (N <= 0 || K < 0 || K > kMaxK || N > (int64_t)1 << 30) return -1;
+    const Weight w = weight_shape(N, K);
+    return w.Np * w.Kp;
+}
+
+int enchip_weight_register_image(enchip_ctx *ctx, const int8_t *image, int64_t image_bytes, const float *wscale,
+                                 int64_t N, int64_t K, enchip_weight *out) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (!out) return fail(ctx, ENCHIP_ERR_ARG, "weight_register_image: out is NULL");
+    *out = 0;
+    const int64_t want = enchip_weight_image_bytes(N, K);
+    if (want < 0) return fail(ctx, ENCHIP_ERR_ARG, "weight_register_image: bad shape N=%lld K=%lld", (long long)N,
+                              (long long)K);
+    if (image_bytes != want)
+        return fail(ctx, ENCHIP_ERR_ARG, "weight_register_image: image is %lld bytes, N=%lld K=%lld needs %lld",
+                    (long long)image_bytes, (long long)N, (long long)K, (long long)want);
+    if (!image || !wscale) return fail(ctx, ENCHIP_ERR_ARG, "weight_register_image: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    return upload_weight(ctx, weight_shape(N, K), image, wscale, out);
+}
+
+int enchip_weight_export(enchip_ctx *ctx, enchip_weight h, int8_t *image, int64_t image_bytes, float *wscale) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    Weight *w;
+    int rc = find_weight(ctx, h, &w);
+    if (rc) return rc;
+    if (image_bytes != w->Np * w->Kp)
+        return fail(ctx, ENCHIP_ERR_ARG, "weight_export: buffer is %lld bytes, the image is %lld",
+                    (long long)image_bytes, (long long)(w->Np * w->Kp));
+    if (!image) return fail(ctx, ENCHIP_ERR_ARG, "weight_export: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    HIP_TRY(ctx, hipMemcpy(image, w->d_w, (size_t)image_bytes, hipMemcpyDeviceToHost));
+    if (wscale) HIP_TRY(ctx, hipMemcpy(wscale, w->d_s, (size_t)w->N * sizeof(float), hipMemcpyDeviceToHost));
+    return ENCHIP_OK;
+}
+
 int enchip_weight_register(enchip_ctx *ctx, const int8_t *wq, const float *wscale, int64_t N, int64_t K,
                            enchip_weight *out) {
     if (!ctx) return ENCHIP_ERR_ARG;
@@ -561,11 +637,7 @@ int enchip_weight_register(enchip_ctx *ctx, const int8_t *wq, const float *wscal
         return fail(ctx, ENCHIP_ERR_ARG, "weight_register: bad shape N=%lld K=%lld", (long long)N, (long long)K);
     if ((K > 0 && !wq) || !wscale) return fail(ctx, ENCHIP_ERR_ARG, "weight_register: null pointer");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
-    Weight w;
-    w.N = N;
-    w.K = K;
-    w.Np = round_up(N, kColPad);
-    w.Kp = round_up(std::max<int64_t>(K, 1), 64);
+    const Weight w = weight_shape(N, K);
     // Pre-swizzle on the host into the fragment-major MFMA operand layout.
     const int64_t nk32 = w.Kp / 32;
     std::vector<int8_t> frag((size_t)(w.Np * w.Kp), 0);
@@ -577,24 +649,7 @@ int enchip_weight_register(enchip_ctx *ctx, const int8_t *wq, const float *wscal
             frag[(size_t)((nb * nk32 + kb) * 1024 + (nl + 32 * kh) * 16 + j)] = src[k];
         }
     }
-    int rc;
-    size_t wcap = 0, scap = 0;
-    if ((rc = ensure(ctx, &w.d_w, &wcap, frag.size()))) return rc;
-    if ((rc = ensure(ctx, &w.d_s, &scap, (size_t)N * sizeof(float)))) {
-        (void)hipFree(w.d_w);
-        return rc;
-    }
-    hipError_t e1 = hipMemcpy(w.d_w, frag.data(), frag.size(), hipMemcpyHostToDevice);
-    hipError_t e2 = hipMemcpy(w.d_s, wscale, (size_t)N * sizeof(float), hipMemcpyHostToDevice);
-    if (e1 != hipSuccess || e2 != hipSuccess) {
-        (void)hipFree(w.d_w);
-        (void)hipFree(w.d_s);
-        return fail(ctx, ENCHIP_ERR_HIP, "weight upload: %s", hipGetErrorString(e1 != hipSuccess ? e1 : e2));
-    }
-    const uint64_t h = ctx->next_handle++;
-    ctx->weights[h] = w;
-    *out = h;
-    return ENCHIP_OK;
+    return upload_weight(ctx, w, frag.data(), wscale, out);
 }
 
 int enchip_weight_release(enchip_ctx *ctx, enchip_weight h) {

@@ -45,6 +45,9 @@ _SIGNATURES = {
     "enchip_w8a8_linear_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _vp, _int, _vp, _vp]),
     "enchip_quant_rows_frag_dev": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
     "enchip_matmul_bt_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64]),
+    "enchip_weight_image_bytes": (_i64, [_i64, _i64]),
+    "enchip_weight_export": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _vp]),
+    "enchip_weight_register_image": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, ctypes.POINTER(ctypes.c_uint64)]),
     "enchip_softmax_rows_scaled_dev": (_int, [_vp, _vp, _i64, _i64, _i64, ctypes.c_float, _vp]),
     "enchip_residual_layer_norm_dev": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp, ctypes.c_double,
                                               _vp]),
@@ -200,6 +203,28 @@ class Context:
 
     def release_weight(self, w: Weight) -> None:
         self._check(self._lib.enchip_weight_release(self._h, w.handle))
+
+    def weight_image_bytes(self, N: int, K: int) -> int:
+        """Bytes of the fragment-major image of an N x K weight (-1: shape refused)."""
+        return int(self._lib.enchip_weight_image_bytes(N, K))
+
+    def export_weight(self, w: Weight):
+        """(image int8 [bytes], scales f32 [N]): the device's pre-swizzled copy of w."""
+        image = np.empty(self.weight_image_bytes(w.N, w.K), np.int8)
+        scales = np.empty(w.N, np.float32)
+        self._check(self._lib.enchip_weight_export(self._h, w.handle, _ptr(image), image.size, _ptr(scales)))
+        return image, scales
+
+    def register_weight_image(self, image: np.ndarray, wscale: np.ndarray, N: int, K: int) -> Weight:
+        """Registers a pre-swizzled image (export_weight / weight_cache.frag_image) as is."""
+        image = np.ascontiguousarray(image, dtype=np.int8).reshape(-1)
+        wscale = np.ascontiguousarray(wscale, dtype=np.float32)
+        if wscale.shape != (N,):
+            raise ValueError(f"wscale shape {wscale.shape} != ({N},)")
+        out = ctypes.c_uint64()
+        self._check(self._lib.enchip_weight_register_image(self._h, _ptr(image), image.size, _ptr(wscale), N, K,
+                                                           ctypes.byref(out)))
+        return Weight(out.value, N, K)
 
     def weight_shape(self, w: Weight):
         n, k = ctypes.c_int64(), ctypes.c_int64()

@@ -378,6 +378,29 @@ def other_configs(ctx, torch, stream, ceilings):
     return out
 
 
+def weight_registration(ctx, layers_host):
+    """Registering the 48 BERT-base weights from int8 codes (host swizzle + upload) against
+    from pre-swizzled images (upload only; aikit_amd.weight_cache), wall time."""
+    from aikit_amd import weight_cache
+
+    ws = [(wq, s) for lw in layers_host for (wq, s, _, _) in lw.values()]
+    images = [(weight_cache.frag_image(wq), s, wq.shape) for wq, s in ws]
+    t0 = time.perf_counter()
+    hs = [ctx.register_weight(wq, s) for wq, s in ws]
+    t_codes = time.perf_counter() - t0
+    for h in hs:
+        ctx.release_weight(h)
+    t0 = time.perf_counter()
+    hs = [ctx.register_weight_image(img, s, N, K) for img, s, (N, K) in images]
+    t_images = time.perf_counter() - t0
+    for h in hs:
+        ctx.release_weight(h)
+    return {"weights": len(ws), "bytes": int(sum(img.size for img, _, _ in images)), "from_codes_s": t_codes,
+            "from_images_s": t_images,
+            "note": "enchip_weight_register (host swizzle + upload) vs enchip_weight_register_image (upload of a "
+                    "pre-swizzled image, as loaded from a mapped weight_cache file)"}
+
+
 def device_forward(ctx, torch, stream, layers_host, cfg, reps: int = 3):
     """The whole config-4 forward resident on the device (aikit_amd.bert_dev: per layer the
     fused-QKV / O / FFN W8A8 linears, the f32 attention products, softmax, two residual +
@@ -669,6 +692,7 @@ def main() -> int:
     if not args.no_other_configs:
         log("configs 2 and 3 (isolated linear, small-M GEMV over a rotating > 2x MALL weight set), ann.FlatI8 scoring")
         result["other_configs"] = other_configs(ctx, torch, stream, ceilings)
+        result["other_configs"]["weight_registration_cfg4"] = weight_registration(ctx, layers_host)
         log("config 4 forward resident on the device (linears, attention, LayerNorm, pooling)")
         result["other_configs"]["encode_device_cfg4"] = device_forward(ctx, torch, stream, layers_host, cfg)
         log(f"  {result['other_configs']['encode_device_cfg4']['seqs_per_s']:.1f} seqs/s end to end")

@@ -105,6 +105,25 @@ int enchip_weight_register(enchip_ctx *ctx, const int8_t *wq, const float *wscal
 /* Releases a registered weight's device memory. */
 int enchip_weight_release(enchip_ctx *ctx, enchip_weight w);
 
+/* Pre-swizzled weight images: the device's fragment-major layout of an N x K int8
+ * weight, byte (n, k) at ((n/32)*(Kp/32) + k/32)*1024 + ((n%32) + 32*((k/16)%2))*16 + k%16
+ * with Np = N rounded up to 256 and Kp = K rounded up to 64 (padding zero), so a model
+ * converted once can be registered straight from a memory-mapped file without the
+ * per-byte host swizzle: the device side of loading pre-quantized int8 weights from a
+ * mapping (linalg.WrapInt8 / WeightMat.MappedSpan, linalg/weightmat.go:81-88,215-231;
+ * embed.OpenSafetensorsMmap, embed/safetensors.go:290-305).
+ *
+ * enchip_weight_image_bytes: Np * Kp, or -1 for a shape enchip_weight_register refuses.
+ * enchip_weight_export: copies weight w's image (image_bytes must be exactly its size)
+ * and, when wscale is not NULL, its N scales back to the host.
+ * enchip_weight_register_image: registers an image (and N scales) as
+ * enchip_weight_register would have built it; refuses an image of the wrong size. */
+int64_t enchip_weight_image_bytes(int64_t N, int64_t K);
+int enchip_weight_export(enchip_ctx *ctx, enchip_weight w, int8_t *image, int64_t image_bytes,
+                         float *wscale);
+int enchip_weight_register_image(enchip_ctx *ctx, const int8_t *image, int64_t image_bytes,
+                                 const float *wscale, int64_t N, int64_t K, enchip_weight *out);
+
 /* Shape of a registered weight. */
 int enchip_weight_shape(enchip_ctx *ctx, enchip_weight w, int64_t *N, int64_t *K);
 

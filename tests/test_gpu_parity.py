@@ -516,3 +516,37 @@ def test_ann_flat_i8_scores(ctx, M, N, K):
     finally:
         ctx.release_weight(w)
     assert_f32_parity(got, oracle.w8a8_linear(q, codes, scales, None, 0, M, K, N), "ann scores")
+
+
+# ------------------------------------------------------------------ pre-swizzled weight images
+def test_weight_image_export_and_register(ctx, tmp_path):
+    # enchip_weight_export gives the image weight_cache.frag_image builds on the host;
+    # registering that image (directly, or from a memory-mapped safetensors file) gives a
+    # weight whose linears are bit-identical to the normally registered one.
+    from aikit_amd import weight_cache
+
+    g = workloads.rng(91)
+    M, K, N = 300, 200, 520
+    a = workloads.activations(g, M, K)
+    wq, ws = workloads.int8_weights(g, N, K)
+    b = workloads.bias(g, N)
+    w0 = ctx.register_weight(wq, ws)
+    w1 = w2 = None
+    try:
+        image, scales = ctx.export_weight(w0)
+        assert image.size == ctx.weight_image_bytes(N, K)
+        assert np.array_equal(image, weight_cache.frag_image(wq))
+        assert np.array_equal(bits(scales), bits(ws))
+        w1 = ctx.register_weight_image(weight_cache.frag_image(wq), ws, N, K)
+        path = str(tmp_path / "w.safetensors")
+        weight_cache.save(path, {"w": (wq, ws)})
+        w2 = weight_cache.load(ctx, path)["w"]
+        want = ctx.linear(w0, a, bias=b, act=1)
+        for w in (w1, w2):
+            assert np.array_equal(bits(ctx.linear(w, a, bias=b, act=1)), bits(want))
+        with pytest.raises(enchip.EnchipError):
+            ctx.register_weight_image(image[:-1], ws, N, K)
+    finally:
+        for w in (w0, w1, w2):
+            if w is not None:
+                ctx.release_weight(w)

@@ -19,6 +19,7 @@
 #include "encoder_ops.h"
 #include "gemm_f32.h"
 #include "gemm_persistent.h"
+#include "topk.h"
 #include "kernels.h"
 #include "probes.h"
 
@@ -65,6 +66,12 @@ struct enchip_ctx {
     size_t acc_cap = 0;
     float *d_fb = nullptr;  // enchip_matmul_bt_f32's b operand
     size_t fb_cap = 0;
+    uint64_t *d_cand = nullptr;  // top-k candidates
+    size_t cand_cap = 0;
+    int32_t *d_hit_i = nullptr;  // enchip_ann_topk's device results
+    size_t hit_i_cap = 0;
+    float *d_hit_s = nullptr;
+    size_t hit_s_cap = 0;
 };
 
 namespace {
@@ -336,7 +343,8 @@ int enchip_close(enchip_ctx *ctx) {
             (void)hipFree(kv.second.d_s);
         }
         ctx->weights.clear();
-        void *bufs[] = {ctx->d_aq, ctx->d_as, ctx->d_a, ctx->d_dst, ctx->d_bias, ctx->d_acc, ctx->d_fb};
+        void *bufs[] = {ctx->d_aq,  ctx->d_as, ctx->d_a,     ctx->d_dst,     ctx->d_bias,
+                        ctx->d_acc, ctx->d_fb, ctx->d_cand, ctx->d_hit_i, ctx->d_hit_s};
         for (void *p : bufs)
             if (p) (void)hipFree(p);
         if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -1025,4 +1033,81 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
                                d_k + off * ld, d_v + off * ld, ld, d_out + off * ldo, ldo, (int)L, (int)heads, scale);
     }
     return check_launch(ctx, "attention_f32");
+}
+
+// ---------------------------------------------------------------------------- top-k
+
+namespace {
+
+// Enqueues the two top-k stages (topk.h) after the caller checked the arguments.
+int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, int64_t n, int64_t k, int32_t *index,
+                int64_t ldi, float *score, int64_t lds, hipStream_t s) {
+    using namespace enchip;
+    if (rows == 0 || k == 0) return ENCHIP_OK;
+    const int64_t nchunks = std::max<int64_t>(1, (n + TOPK_CHUNK - 1) / TOPK_CHUNK);
+    int rc;
+    if ((rc = ensure(c, &c->d_cand, &c->cand_cap, (size_t)(rows * nchunks * k) * sizeof(uint64_t)))) return rc;
+    int kp = 1;
+    while (kp < k) kp <<= 1;
+    for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+        const int64_t nr = std::min<int64_t>(65535, rows - r0);
+        hipLaunchKernelGGL(topk_chunk, dim3((unsigned)nchunks, (unsigned)nr), dim3(256), 0, s, scores + r0 * ld, ld, n,
+                           (int)k, (int)nchunks, c->d_cand + r0 * nchunks * k);
+    }
+    for (int64_t r0 = 0; r0 < rows; r0 += 0x7fffffff) {
+        const int64_t nr = std::min<int64_t>(0x7fffffff, rows - r0);
+        hipLaunchKernelGGL(topk_merge, dim3((unsigned)nr), dim3(256), (size_t)kp * sizeof(uint64_t), s,
+                           c->d_cand + r0 * nchunks * k, nchunks * k, (int)k, kp, scores + r0 * ld, ld,
+                           index + r0 * ldi, ldi, score + r0 * lds, lds);
+    }
+    return check_launch(c, "topk");
+}
+
+}  // namespace
+
+int enchip_topk_rows_dev(enchip_ctx *ctx, const float *d_scores, int64_t ld, int64_t rows, int64_t n, int64_t k,
+                         int32_t *d_index, int64_t ldi, float *d_score, int64_t lds, void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (rows < 0 || n < 0 || n > 0x7fffffff || k < 0 || k > enchip::TOPK_MAX_K || ld < n || ldi < k || lds < k)
+        return fail(ctx, ENCHIP_ERR_ARG, "topk: bad shape rows=%lld n=%lld k=%lld (k <= %d)", (long long)rows,
+                    (long long)n, (long long)k, enchip::TOPK_MAX_K);
+    if (rows == 0 || k == 0) return ENCHIP_OK;
+    if ((n > 0 && !d_scores) || !d_index || !d_score) return fail(ctx, ENCHIP_ERR_ARG, "topk: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    return launch_topk(ctx, d_scores, ld, rows, n, k, d_index, ldi, d_score, lds, s);
+}
+
+int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int64_t M, int64_t k, int32_t *hit_index,
+                    float *hit_score) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    Weight *w;
+    int rc = find_weight(ctx, h, &w);
+    if (rc) return rc;
+    if (M < 0 || M > ((int64_t)1 << 30) || k < 0 || k > enchip::TOPK_MAX_K || w->N > 0x7fffffff)
+        return fail(ctx, ENCHIP_ERR_ARG, "ann_topk: bad shape M=%lld k=%lld (k <= %d)", (long long)M, (long long)k,
+                    enchip::TOPK_MAX_K);
+    if (M == 0 || k == 0) return ENCHIP_OK;
+    if ((w->K > 0 && !queries) || !hit_index || !hit_score) return fail(ctx, ENCHIP_ERR_ARG, "ann_topk: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    const int64_t K = w->K, N = w->N;
+    if ((rc = ensure(ctx, &ctx->d_a, &ctx->a_cap, std::max<size_t>((size_t)(M * K) * sizeof(float), 16)))) return rc;
+    if ((rc = ensure(ctx, &ctx->d_dst, &ctx->dst_cap, (size_t)(M * N) * sizeof(float)))) return rc;
+    if ((rc = ensure(ctx, &ctx->d_hit_i, &ctx->hit_i_cap, (size_t)(M * k) * sizeof(int32_t)))) return rc;
+    if ((rc = ensure(ctx, &ctx->d_hit_s, &ctx->hit_s_cap, (size_t)(M * k) * sizeof(float)))) return rc;
+    if ((rc = ensure_act_scratch(ctx, M, w->Kp))) return rc;
+    hipStream_t s = ctx->stream;
+    if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, queries, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
+    // the bias-free W8A8 scores (ann/backend.go:25-29), then the selection on the device
+    const bool af = route_af(ctx, *w, M, ctx->d_dst, N);
+    if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, w->Kp, ctx->d_as, s, af))) return rc;
+    if ((rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, nullptr, enchip::EPI_F32, ctx->d_dst, N, M, s, af)))
+        return rc;
+    if ((rc = launch_topk(ctx, ctx->d_dst, N, M, N, k, ctx->d_hit_i, k, ctx->d_hit_s, k, s))) return rc;
+    HIP_TRY(ctx, hipMemcpyAsync(hit_index, ctx->d_hit_i, (size_t)(M * k) * sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    HIP_TRY(ctx, hipMemcpyAsync(hit_score, ctx->d_hit_s, (size_t)(M * k) * sizeof(float), hipMemcpyDeviceToHost, s));
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    return ENCHIP_OK;
 }

@@ -1,0 +1,378 @@
+// topk.h -- the k best scores of each row on the device: ann.I8TopKIndex.TopKBatch's
+// selection (ann/backend.go:46-55), rank-identical to ScoreBatch + FlatI8.topHits
+// (ann/flat_i8.go:208-242): score descending, ties broken by ascending index
+// (topk.Cmp, topk/cmp.go:15-27), NaN scores never retained (topk.Selector.Push,
+// topk/topk.go:85-100).
+//
+// Each candidate is one unique 64-bit key that orders exactly like that rule:
+//   high 32 bits: the score's bits mapped to an unsigned order (negatives flipped, the
+//                 sign bit set on non-negatives; -0 taken as +0, since the reference
+//                 compares float64 values and -0 == +0),
+//   low 32 bits:  0xffffffff - index (a lower index is a larger key).
+// Key 0 is never a valid key and marks "no candidate" (a NaN score, or padding).
+//
+// Two stages, so the M x N score matrix is read from device memory once:
+//   topk_chunk: one 256-thread workgroup per (row, 4096-score chunk) selects the k largest
+//     keys of its chunk and writes them as the chunk's k candidates: for k <= 32 by a
+//     bound from the per-thread maxima and maxima of the few keys above it (top_small_k),
+//     otherwise by a radix select over the keys held in registers (8 bits a pass, LDS
+//     histogram).
+//   topk_merge: one workgroup per row selects the k largest of the row's candidates the
+//     same way (maxima in registers when k <= 32 and there are at most 4096 candidates,
+//     else a radix select over them in memory and a bitonic sort in LDS) and writes
+//     indices and scores in order.
+// Keys are unique, so the radix select finds the k-th largest key exactly and the
+// selected set does not depend on the order of anything; outputs are deterministic.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace enchip {
+
+constexpr int TOPK_CHUNK = 4096;  // scores per stage-1 workgroup
+constexpr int TOPK_MAX_K = 1024;  // largest k (the merge sorts it in LDS)
+
+__device__ __forceinline__ uint64_t topk_key(float s, int64_t index) {
+    if (s != s) return 0;  // NaN: never retained
+    uint32_t u = __float_as_uint(s == 0.0f ? 0.0f : s);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)index);
+}
+
+__device__ __forceinline__ int64_t topk_index(uint64_t key) { return (int64_t)(0xffffffffu - (uint32_t)key); }
+
+// The smallest key among the block's `want` largest nonzero keys (keys held EPT per
+// thread, all distinct), or 1 when the block has at most `want` nonzero keys (every
+// nonzero key qualifies). 256 threads; hist is 256 LDS counters, bcast 2 LDS words.
+template <int EPT>
+__device__ uint64_t radix_threshold(const uint64_t (&key)[EPT], int want, unsigned *hist, uint64_t *bcast) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    // count the nonzero keys
+    if (tid == 0) hist[0] = 0;
+    __syncthreads();
+    int mine = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) mine += key[j] != 0;
+    atomicAdd(&hist[0], (unsigned)mine);
+    __syncthreads();
+    const int valid = (int)hist[0];
+    __syncthreads();
+    if (valid <= want) return 1;
+    uint64_t prefix = 0, mask = 0;
+    int remaining = want;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+        hist[tid] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            if (key[j] != 0 && (key[j] & mask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 255u], 1u);
+        __syncthreads();
+        if (tid < 64) {
+            // lane l holds digits 255-4l .. 252-4l (descending); find the digit where
+            // the running count from the top reaches `remaining`
+            unsigned c[4], s = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                c[i] = hist[255 - 4 * lane - i];
+                s += c[i];
+            }
+            unsigned incl = s;  // inclusive prefix over lanes (descending digits)
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const unsigned o = __shfl_up(incl, off, 64);
+                if (lane >= off) incl += o;
+            }
+            const unsigned excl = incl - s;
+            if (excl < (unsigned)remaining && incl >= (unsigned)remaining) {
+                unsigned run = excl;
+                int d = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (run + c[i] >= (unsigned)remaining) {
+                        d = 255 - 4 * lane - i;
+                        break;
+                    }
+                    run += c[i];
+                }
+                bcast[0] = (uint64_t)d;
+                bcast[1] = (uint64_t)(remaining - (int)run);
+            }
+        }
+        __syncthreads();
+        const uint64_t d = bcast[0];
+        remaining = (int)bcast[1];
+        __syncthreads();
+        prefix |= d << shift;
+        mask |= (uint64_t)0xff << shift;
+    }
+    return prefix;  // keys are distinct: exactly `want` keys are >= prefix
+}
+
+constexpr int TOPK_SMALL_K = 32;  // up to this k, selection by repeated maxima
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)v, off, 64), hi = __shfl_xor((uint32_t)(v >> 32), off, 64);
+        const uint64_t o = ((uint64_t)hi << 32) | lo;
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// The block's k largest keys (held EPT per thread, distinct, 0 = none), in descending
+// order, into out[0..k) (0 past the block's nonzero keys), by taking the block maximum
+// k times: no atomics, so it does not slow down when the scores crowd a few values (a
+// radix histogram's first passes do: every key of a chunk shares its top byte). The
+// keys taken are zeroed in `key`. 256 threads; red is 4 LDS words.
+template <int EPT>
+__device__ void top_by_max(uint64_t (&key)[EPT], int k, uint64_t *out, uint64_t *red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int r = 0; r < k; ++r) {
+        uint64_t m = 0;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) m = key[j] > m ? key[j] : m;
+        m = wave_max_u64(m);
+        if (lane == 0) red[wave] = m;
+        __syncthreads();
+        uint64_t best = red[0];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) best = red[w] > best ? red[w] : best;
+        __syncthreads();
+        if (threadIdx.x == 0) out[r] = best;
+        if (best == 0) {  // no keys left: pad (uniform branch)
+            for (int i = r + 1 + threadIdx.x; i < k; i += 256) out[i] = 0;
+            return;
+        }
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) key[j] = key[j] == best ? 0 : key[j];
+    }
+}
+
+// The block's k largest keys (k <= TOPK_SMALL_K; keys held EPT per thread, distinct,
+// 0 = none) in descending order into out[0..k), 0-padded, with little work per key:
+//   1. each thread's largest key; wavefront 0 finds T, the k-th largest of those 256
+//      maxima (or 1 when fewer than k are nonzero). At least k keys are >= T (the k
+//      threads' maxima), so every one of the block's k largest keys is >= T;
+//   2. the keys >= T (at most EPT keys of each of those k threads) are gathered in LDS;
+//   3. wavefront 0 takes their maximum k times.
+// 256 threads; lds holds 256 + EPT*TOPK_SMALL_K + 2 words.
+template <int EPT>
+__device__ void top_small_k(const uint64_t (&key)[EPT], int k, uint64_t *out, uint64_t *lds) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint64_t *maxima = lds, *cand = lds + 256, *misc = lds + 256 + EPT * TOPK_SMALL_K;
+    uint64_t tmax = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) tmax = key[j] > tmax ? key[j] : tmax;
+    maxima[tid] = tmax;
+    if (tid == 0) misc[1] = 0;  // candidate count
+    __syncthreads();
+    if (wave == 0) {
+        uint64_t v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = maxima[4 * lane + i];
+        uint64_t t = 1;
+        for (int r = 0; r < k; ++r) {
+            uint64_t m = v[0];
+#pragma unroll
+            for (int i = 1; i < 4; ++i) m = v[i] > m ? v[i] : m;
+            m = wave_max_u64(m);
+            if (m == 0) {  // fewer than k nonzero maxima: every nonzero key is a candidate
+                t = 1;
+                break;
+            }
+            t = m;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = v[i] == m ? 0 : v[i];
+        }
+        if (lane == 0) misc[0] = t;
+    }
+    __syncthreads();
+    const uint64_t t = misc[0];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+        if (key[j] != 0 && key[j] >= t) cand[atomicAdd(reinterpret_cast<unsigned *>(&misc[1]), 1u)] = key[j];
+    __syncthreads();
+    if (wave == 0) {
+        const int c = (int)(unsigned)misc[1];  // <= EPT * k
+        uint64_t v[EPT * TOPK_SMALL_K / 64];
+#pragma unroll
+        for (int i = 0; i < EPT * TOPK_SMALL_K / 64; ++i) {
+            const int idx = lane + 64 * i;
+            v[i] = idx < c ? cand[idx] : 0;
+        }
+        for (int r = 0; r < k; ++r) {
+            uint64_t m = 0;
+#pragma unroll
+            for (int i = 0; i < EPT * TOPK_SMALL_K / 64; ++i) m = v[i] > m ? v[i] : m;
+            m = wave_max_u64(m);
+            if (lane == 0) out[r] = m;
+#pragma unroll
+            for (int i = 0; i < EPT * TOPK_SMALL_K / 64; ++i) v[i] = v[i] == m ? 0 : v[i];
+        }
+    }
+}
+
+// Stage 1. Grid (nchunks, rows), 256 threads. cand[row][chunk][k], 0 for unused slots.
+__global__ __launch_bounds__(256) void topk_chunk(const float *__restrict__ scores, int64_t ld, int64_t n, int k,
+                                                  int nchunks, uint64_t *__restrict__ cand) {
+    constexpr int EPT = TOPK_CHUNK / 256;
+    __shared__ unsigned hist[256];
+    __shared__ uint64_t bcast[2];
+    __shared__ uint64_t small[256 + EPT * TOPK_SMALL_K + 2];
+    __shared__ unsigned fill;
+    const int64_t row = blockIdx.y, base = (int64_t)blockIdx.x * TOPK_CHUNK;
+    const float *p = scores + row * ld;
+    uint64_t key[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int64_t i = base + threadIdx.x + 256 * j;  // coalesced
+        key[j] = i < n ? topk_key(p[i], i) : 0;
+    }
+    uint64_t *out = cand + (row * nchunks + blockIdx.x) * (int64_t)k;
+    if (k <= TOPK_SMALL_K) {
+        top_small_k<EPT>(key, k, out, small);
+        return;
+    }
+    const uint64_t th = radix_threshold<EPT>(key, k, hist, bcast);
+    if (threadIdx.x == 0) fill = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+        if (key[j] != 0 && key[j] >= th) out[atomicAdd(&fill, 1u)] = key[j];  // the set is exact; its order is not
+    __syncthreads();
+    for (int i = (int)fill + threadIdx.x; i < k; i += 256) out[i] = 0;
+}
+
+// radix_threshold over m keys in device memory (read once per pass; the merge's
+// candidates stay in L2), same contract.
+__device__ uint64_t radix_threshold_mem(const uint64_t *__restrict__ c, int64_t m, int want, unsigned *hist,
+                                        uint64_t *bcast) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (tid == 0) hist[0] = 0;
+    __syncthreads();
+    unsigned mine = 0;
+    for (int64_t i = tid; i < m; i += 256) mine += c[i] != 0;
+    atomicAdd(&hist[0], mine);
+    __syncthreads();
+    const int64_t valid = hist[0];
+    __syncthreads();
+    if (valid <= want) return 1;
+    uint64_t prefix = 0, mask = 0;
+    int remaining = want;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+        hist[tid] = 0;
+        __syncthreads();
+        for (int64_t i = tid; i < m; i += 256) {
+            const uint64_t kk = c[i];
+            if (kk != 0 && (kk & mask) == prefix) atomicAdd(&hist[(kk >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid < 64) {
+            unsigned cnt[4], sum = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                cnt[i] = hist[255 - 4 * lane - i];
+                sum += cnt[i];
+            }
+            unsigned incl = sum;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const unsigned o = __shfl_up(incl, off, 64);
+                if (lane >= off) incl += o;
+            }
+            const unsigned excl = incl - sum;
+            if (excl < (unsigned)remaining && incl >= (unsigned)remaining) {
+                unsigned run = excl;
+                int d = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (run + cnt[i] >= (unsigned)remaining) {
+                        d = 255 - 4 * lane - i;
+                        break;
+                    }
+                    run += cnt[i];
+                }
+                bcast[0] = (uint64_t)d;
+                bcast[1] = (uint64_t)(remaining - (int)run);
+            }
+        }
+        __syncthreads();
+        const uint64_t d = bcast[0];
+        remaining = (int)bcast[1];
+        __syncthreads();
+        prefix |= d << shift;
+        mask |= (uint64_t)0xff << shift;
+    }
+    return prefix;
+}
+
+// Stage 2. Grid (rows), 256 threads, kp * 8 bytes of dynamic LDS (kp: k rounded up to a
+// power of two). The row's m = nchunks * k candidates are cand[row*m ..]. Writes
+// index[row*ldi + i] (-1 past the row's non-NaN scores) and score[row*lds_ + i] (NaN
+// there); the score is re-read from the row (scores, pitch ld) so a -0 stays -0.
+__global__ __launch_bounds__(256) void topk_merge(const uint64_t *__restrict__ cand, int64_t m, int k, int kp,
+                                                  const float *__restrict__ scores, int64_t ld,
+                                                  int32_t *__restrict__ index, int64_t ldi, float *__restrict__ score,
+                                                  int64_t lds_) {
+    __shared__ unsigned hist[256];
+    __shared__ uint64_t bcast[2], red[4];
+    __shared__ unsigned fill;
+    extern __shared__ uint64_t sorted[];
+    const int64_t row = blockIdx.x;
+    const uint64_t *c = cand + row * m;
+    if (k <= TOPK_SMALL_K && m <= TOPK_CHUNK) {
+        // few candidates, small k: hold them in registers and take the maxima in order
+        constexpr int EPT = TOPK_CHUNK / 256;
+        uint64_t key[EPT];
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            const int64_t i = threadIdx.x + 256 * j;
+            key[j] = i < m ? c[i] : 0;
+        }
+        top_by_max<EPT>(key, k, sorted, red);
+        __syncthreads();
+        for (int i = threadIdx.x; i < k; i += 256) {
+            const uint64_t kk = sorted[i];
+            const int64_t col = kk ? topk_index(kk) : -1;
+            index[row * ldi + i] = (int32_t)col;
+            score[row * lds_ + i] = kk ? scores[row * ld + col] : __uint_as_float(0x7fc00000u);
+        }
+        return;
+    }
+    const uint64_t th = radix_threshold_mem(c, m, k, hist, bcast);
+    for (int i = threadIdx.x; i < kp; i += 256) sorted[i] = 0;
+    if (threadIdx.x == 0) fill = 0;
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < m; i += 256) {
+        const uint64_t kk = c[i];
+        if (kk != 0 && kk >= th) sorted[atomicAdd(&fill, 1u)] = kk;  // at most k of them
+    }
+    __syncthreads();
+    // bitonic sort of kp keys, descending (the zero padding sinks to the end)
+    for (int size = 2; size <= kp; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < kp; i += 256) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const uint64_t a = sorted[i], b = sorted[j];
+                    const bool desc = (i & size) == 0;
+                    if (desc ? a < b : a > b) {
+                        sorted[i] = b;
+                        sorted[j] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    for (int i = threadIdx.x; i < k; i += 256) {
+        const uint64_t kk = sorted[i];
+        const int64_t col = kk ? topk_index(kk) : -1;
+        index[row * ldi + i] = (int32_t)col;
+        score[row * lds_ + i] = kk ? scores[row * ld + col] : __uint_as_float(0x7fc00000u);
+    }
+}
+
+}  // namespace enchip

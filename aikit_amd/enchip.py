@@ -46,6 +46,8 @@ _SIGNATURES = {
     "enchip_quant_rows_frag_dev": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
     "enchip_matmul_bt_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64]),
     "enchip_weight_image_bytes": (_i64, [_i64, _i64]),
+    "enchip_topk_rows_dev": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "enchip_ann_topk": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _i64, _vp, _vp]),
     "enchip_weight_export": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _vp]),
     "enchip_weight_register_image": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, ctypes.POINTER(ctypes.c_uint64)]),
     "enchip_softmax_rows_scaled_dev": (_int, [_vp, _vp, _i64, _i64, _i64, ctypes.c_float, _vp]),
@@ -203,6 +205,22 @@ class Context:
 
     def release_weight(self, w: Weight) -> None:
         self._check(self._lib.enchip_weight_release(self._h, w.handle))
+
+    def topk_rows_dev(self, d_scores: int, ld: int, rows: int, n: int, k: int, d_index: int, ldi: int, d_score: int,
+                      lds: int, stream: int = 0) -> None:
+        self._check(self._lib.enchip_topk_rows_dev(self._h, d_scores or None, ld, rows, n, k, d_index or None, ldi,
+                                                   d_score or None, lds, stream or None))
+
+    def ann_topk(self, index: Weight, queries: np.ndarray, k: int):
+        """ann.I8TopKIndex.TopKBatch: (hit_index int32 [M, k], hit_score f32 [M, k]); -1 / NaN pad."""
+        q = np.ascontiguousarray(queries, dtype=np.float32)
+        M = q.shape[0]
+        if q.shape != (M, index.K):
+            raise ValueError(f"queries shape {q.shape} != (M, {index.K})")
+        hi = np.empty((M, k), np.int32)
+        hs = np.empty((M, k), np.float32)
+        self._check(self._lib.enchip_ann_topk(self._h, index.handle, _ptr(q), M, k, _ptr(hi), _ptr(hs)))
+        return hi, hs
 
     def weight_image_bytes(self, N: int, K: int) -> int:
         """Bytes of the fragment-major image of an N x K weight (-1: shape refused)."""

@@ -305,15 +305,32 @@ def other_configs(ctx, torch, stream, ceilings):
         e1.record(stream)
         torch.cuda.synchronize()
         t = e0.elapsed_time(e1) * 1e-3 / reps
+        # I8TopKIndex.TopKBatch on the device: the same scores, then the k = 10 best per query
+        kk = 10
+        with torch.cuda.stream(stream):
+            hi = torch.empty((M, kk), dtype=torch.int32, device="cuda")
+            hs = torch.empty((M, kk), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        for _ in range(3):
+            ctx.topk_rows_dev(dst.data_ptr(), N, M, N, kk, hi.data_ptr(), kk, hs.data_ptr(), kk, sp)
+        e0.record(stream)
+        for _ in range(reps):
+            ctx.pre_dev(hidx, aq.data_ptr(), K, M, asc.data_ptr(), 0, 0, dst.data_ptr(), sp)
+            ctx.topk_rows_dev(dst.data_ptr(), N, M, N, kk, hi.data_ptr(), kk, hs.data_ptr(), kk, sp)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t_topk = e0.elapsed_time(e1) * 1e-3 / reps
         nbytes = N * K + M * K + 4 * M + 4 * N + 4 * M * N
         out[f"ann_flat_i8_m{M}"] = {
+            "top10_us_per_call": t_topk * 1e6,
             "M": M, "K": K, "N": N, "us_per_call": t * 1e6, "hbm_gbps": nbytes / t / 1e9,
             "frac_hbm_peak": nbytes / t / PEAK_HBM_BPS,
             "frac_measured_read_ceiling": nbytes / t / 1e9 / ceilings["hbm_read_gbps"],
             "int8_tops": 2.0 * M * N * K / t / 1e12, "kernel": ctx.gemm_kernel_name(hidx, M, 0),
             "note": "M queries against a 2^20 x 384 int8 index (403 MB > MALL), pre-quantized queries, "
-                    "bias-free W8A8 scores (enchip_w8a8_pre_dev); bytes = index + queries + scales + M*N f32 scores"}
-        del a, aq, asc, dst
+                    "bias-free W8A8 scores (enchip_w8a8_pre_dev); bytes = index + queries + scales + M*N f32 scores; "
+                    "top10_us_per_call = the same scores plus the device top-10 per query (enchip_topk_rows_dev)"}
+        del a, aq, asc, dst, hi, hs
     ctx.release_weight(hidx)
 
     # f32 attention products of one config-4 layer (encoder/attention.go:108,111) on the

@@ -305,6 +305,28 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
                              int64_t nseq, int64_t L, int64_t heads, int64_t head_dim,
                              float scale, void *stream);
 
+/* The k best of each of `rows` rows of n scores (pitch ld), on the device:
+ * ann.I8TopKIndex's selection (ann/backend.go:46-55), identical to FlatI8.topHits
+ * (ann/flat_i8.go:208-242) on the same scores: score descending, equal scores by
+ * ascending index (topk.Cmp, topk/cmp.go:15-27), NaN never retained
+ * (topk/topk.go:93-100). Row r's i-th best goes to d_index[r*ldi + i] (its column in
+ * [0, n)) and d_score[r*lds + i]; a row with fewer than k non-NaN scores pads with index
+ * -1 and a NaN score (the reference returns the shorter list). The score matrix is read
+ * once; candidates use the context's scratch. k <= 1024, n < 2^31. */
+int enchip_topk_rows_dev(enchip_ctx *ctx, const float *d_scores, int64_t ld, int64_t rows,
+                         int64_t n, int64_t k, int32_t *d_index, int64_t ldi, float *d_score,
+                         int64_t lds, void *stream);
+
+/* ann.I8TopKIndex.TopKBatch (ann/backend.go:46-55) on an index registered as a weight
+ * (codes [n, dim], per-row scales): queries[M, dim] f32 on the host are quantized per
+ * row, scored against every index row with the bias-free W8A8 linear
+ * ("(float)acc*qscale*scale", ann/backend.go:25-29), and each query's k best hits come
+ * back in hit_index[M, k] / hit_score[M, k] (as enchip_topk_rows_dev orders and pads
+ * them). Only the M x k hits cross back to the host, not the M x n scores.
+ * Synchronous. k <= 1024. */
+int enchip_ann_topk(enchip_ctx *ctx, enchip_weight index, const float *queries, int64_t M,
+                    int64_t k, int32_t *hit_index, float *hit_score);
+
 /* Rows at or below which the small-M (HBM-bound, split-K) kernel runs instead of
  * the tiled MFMA GEMM. Both produce identical bits; this only selects the kernel.
  * Mirrors the reference's dispatch knobs (linalg.SetParallelThreshold,

@@ -259,3 +259,36 @@ def cpu_w8a8_linear(a, bq, bscales, bias, act, M, K, N, workers: int, dst=None, 
 def cpu_dot_i8(a, b) -> int:
     a, b = _c(a, np.int8), _c(b, np.int8)
     return int(lib().cpub_dot_i8(a, b, a.size))
+
+
+# ---------------------------------------------------------------- top-k (ann)
+def top_hits_selector(scores, k: int):
+    """FlatI8.topHits (ann/flat_i8.go:208-242) for k < len(scores), as the reference runs
+    it: topk.Selector (topk/topk.go:44-48,85-125: a min-heap on (score asc, seq desc),
+    NaN rejected, a candidate kept only if strictly above the minimum, pushed in index
+    order with the hoisted threshold), then sorted by topk.Cmp (topk/cmp.go:15-27: score
+    descending, index ascending). Pure Python: for small inputs. Returns [(index, score)]."""
+    import heapq
+
+    heap = []  # entries (score, -seq, index): heapq's minimum is the reference's heap[0]
+    seq = 0
+    for i, s in enumerate(np.asarray(scores, np.float32).tolist()):
+        if s != s:
+            continue
+        if len(heap) < k:
+            heapq.heappush(heap, (s, -seq, i))
+        elif s > heap[0][0]:
+            heapq.heapreplace(heap, (s, -seq, i))
+        seq += 1
+    return sorted(((i, s) for s, _, i in heap), key=lambda t: (-t[1], t[0]))
+
+
+def top_hits(scores, k: int):
+    """The same selection in closed form (numpy): the k largest non-NaN scores, ordered
+    by score descending then index ascending (float32 -0 equals +0). Returns
+    (index int64 [<=k], score float32 [<=k])."""
+    s = np.asarray(scores, np.float32)
+    idx = np.flatnonzero(~np.isnan(s))
+    order = np.lexsort((idx, -s[idx].astype(np.float64)))
+    keep = idx[order[:k]]
+    return keep, s[keep]

@@ -550,3 +550,51 @@ def test_weight_image_export_and_register(ctx, tmp_path):
         for w in (w0, w1, w2):
             if w is not None:
                 ctx.release_weight(w)
+
+
+# ------------------------------------------------------------------ ann top-k on the device
+def _check_topk(hi, hs, scores, k, what):
+    for r in range(scores.shape[0]):
+        idx, sc = oracle.top_hits(scores[r], k)
+        got_i, got_s = hi[r], hs[r]
+        assert got_i[:idx.size].tolist() == idx.tolist(), f"{what} row {r}: indices differ"
+        assert np.array_equal(bits(got_s[:idx.size]), bits(sc)), f"{what} row {r}: scores differ"
+        assert (got_i[idx.size:] == -1).all() and np.isnan(got_s[idx.size:]).all(), f"{what} row {r}: padding"
+
+
+@pytest.mark.parametrize("rows,n,k", [(3, 10000, 10), (2, 4096, 1024), (5, 1000, 1000), (1, 1, 5), (4, 50000, 100),
+                                      (2, 8193, 7), (1, 300000, 64)])
+def test_topk_rows_matches_reference_selection(ctx, rows, n, k):
+    # FlatI8.topHits' order (score desc, index asc; NaN skipped) on scores full of ties
+    # (a coarse grid), signed zeros and NaNs, across chunk boundaries.
+    import torch
+
+    g = workloads.rng(rows * n + k)
+    s = (g.integers(-50, 51, size=(rows, n)) * 0.25).astype(np.float32)
+    s[g.random((rows, n)) < 0.02] = np.nan
+    s[g.random((rows, n)) < 0.02] = -0.0
+    say(f"topk rows={rows} n={n} k={k}")
+    ds = torch.from_numpy(s).cuda()
+    di = torch.empty((rows, k), dtype=torch.int32, device="cuda")
+    dv = torch.empty((rows, k), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.topk_rows_dev(ds.data_ptr(), n, rows, n, k, di.data_ptr(), k, dv.data_ptr(), k)
+    torch.cuda.synchronize()
+    _check_topk(di.cpu().numpy(), dv.cpu().numpy(), s, k, "topk")
+
+
+@pytest.mark.parametrize("M,N,K,k", [(1, 140001, 384, 10), (16, 50000, 384, 100), (40, 3000, 768, 1000)])
+def test_ann_topk_matches_score_batch_plus_top_hits(ctx, M, N, K, k):
+    # I8TopKIndex.TopKBatch is "rank-identical to ScoreBatch + topHits"
+    # (ann/backend.go:46-55): the oracle's W8A8 scores, then the reference's selection.
+    g = workloads.rng(83 + M + N)
+    q = workloads.activations(g, M, K)
+    codes = g.integers(-127, 128, size=(N, K), dtype=np.int8)
+    scales = g.uniform(1e-3, 1e-2, size=N).astype(np.float32)
+    w = ctx.register_weight(codes, scales)
+    try:
+        say(f"ann top-k M={M} N={N} K={K} k={k}")
+        hi, hs = ctx.ann_topk(w, q, k)
+    finally:
+        ctx.release_weight(w)
+    _check_topk(hi, hs, oracle.w8a8_linear(q, codes, scales, None, 0, M, K, N), k, "ann_topk")

@@ -333,3 +333,31 @@ def test_matmul_bt_worst_rel_statistic():
     assert oracle.matmul_bt_worst_rel([[1000.1, 0.5, -2.0]], ref) == pytest.approx(1e-4)
     assert oracle.matmul_bt_worst_rel([[1000.0, 0.5003, -2.0]], ref) == pytest.approx(3e-4)
     assert oracle.matmul_bt_worst_rel([[1000.0, 0.5, -2.002]], ref) == pytest.approx(1e-3)
+
+
+# ------------------------------------------------------------------ ann top-k
+@pytest.mark.parametrize("seed", range(6))
+def test_top_hits_closed_form_matches_the_selector(seed):
+    # The numpy closed form (the GPU tests' checker) against a restatement of the
+    # reference's heap selector, on inputs full of ties, signed zeros and NaNs.
+    g = np.random.default_rng(seed)
+    n = int(g.integers(1, 400))
+    s = g.integers(-6, 7, size=n).astype(np.float32) * np.float32(0.5)
+    s[g.random(n) < 0.1] = np.nan
+    s[g.random(n) < 0.05] = -0.0
+    for k in (1, 3, 10, n - 1, n):
+        if not 0 < k < n:
+            continue
+        want = oracle.top_hits_selector(s, k)
+        idx, sc = oracle.top_hits(s, k)
+        assert [i for i, _ in want] == idx.tolist()
+        assert np.array_equal(np.array([v for _, v in want], np.float32), sc)
+
+
+def test_top_hits_hand_cases():
+    s = np.array([1.0, 3.0, 3.0, np.nan, -0.0, 0.0, 2.0], np.float32)
+    idx, sc = oracle.top_hits(s, 4)
+    assert idx.tolist() == [1, 2, 6, 0]       # ties by ascending index
+    idx, _ = oracle.top_hits(s, 6)
+    assert idx.tolist() == [1, 2, 6, 0, 4, 5]  # -0 == +0: index order; NaN never kept
+    assert oracle.top_hits_selector(s, 6) == [(1, 3.0), (2, 3.0), (6, 2.0), (0, 1.0), (4, -0.0), (5, 0.0)]

@@ -974,7 +974,26 @@ int enchip_residual_layer_norm_dev(enchip_ctx *ctx, float *d_h, int64_t ldh, con
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     const dim3 grid((unsigned)((rows + 3) / 4));
-    ROWOP_DISPATCH(enchip::residual_layer_norm, D, grid, s, d_h, ldh, d_y, ldy, rows, (int)D, d_w, d_b, eps);
+    const bool vec = D % 4 == 0 && ldh % 4 == 0 && (!d_y || ldy % 4 == 0) && (uintptr_t)d_h % 16 == 0 &&
+                     (uintptr_t)d_y % 16 == 0 && (uintptr_t)d_w % 16 == 0 && (uintptr_t)d_b % 16 == 0 && D >= 4;
+    // VEC: 4 consecutive columns per lane per 16-byte load (CPL a multiple of 4)
+#define LN_CASE(CPL)                                                                                           \
+    do {                                                                                                       \
+        if (vec)                                                                                               \
+            hipLaunchKernelGGL((enchip::residual_layer_norm<CPL, true>), grid, dim3(256), 0, s, d_h, ldh, d_y, ldy, \
+                               rows, (int)D, d_w, d_b, eps);                                                    \
+        else                                                                                                   \
+            hipLaunchKernelGGL((enchip::residual_layer_norm<CPL, false>), grid, dim3(256), 0, s, d_h, ldh, d_y,  \
+                               ldy, rows, (int)D, d_w, d_b, eps);                                               \
+    } while (0)
+    if (D <= 64 && !vec) LN_CASE(1);
+    else if (D <= 128 && !vec) LN_CASE(2);
+    else if (D <= 256) LN_CASE(4);
+    else if (D <= 512) LN_CASE(8);
+    else if (D <= 1024) LN_CASE(16);
+    else if (D <= 2048) LN_CASE(32);
+    else LN_CASE(64);
+#undef LN_CASE
     return check_launch(ctx, "residual_layer_norm");
 }
 

@@ -15,6 +15,7 @@
 #include <cstdint>
 
 #include "gelu_f32.h"
+#include "kernels.h"
 
 #pragma clang fp contract(off)
 
@@ -87,7 +88,10 @@ __global__ __launch_bounds__(256) void softmax_rows_scaled(float *__restrict__ x
 // D <= 64*CPL:
 //   mean = sum((double)v) / D; variance = sum(((double)v - mean)^2) / D;
 //   invStd = 1 / sqrt(variance + eps); h = float32((((double)v - mean) * invStd) * w + b).
-template <int CPL>
+// VEC: D, ldh, ldy multiples of 4 and 16-byte aligned rows: each lane takes 4 consecutive
+// columns per 16-byte load (CPL/4 of them), the residual input read nontemporally (it is
+// read once); otherwise one column per lane per step.
+template <int CPL, bool VEC>
 __global__ __launch_bounds__(256) void residual_layer_norm(float *__restrict__ h, int64_t ldh,
                                                            const float *__restrict__ y, int64_t ldy, int64_t rows,
                                                            int D, const float *__restrict__ w,
@@ -99,31 +103,66 @@ __global__ __launch_bounds__(256) void residual_layer_norm(float *__restrict__ h
     const float *q = y != nullptr ? y + row * ldy : nullptr;
     float v[CPL];
     double s = 0.0;
+    // column of element j of this lane
+    auto col = [&](int j) { return VEC ? 256 * (j >> 2) + 4 * lane + (j & 3) : lane + 64 * j; };
+    if (VEC) {
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const int c = lane + 64 * j;
-        v[j] = 0.0f;
-        if (c < D) {
-            v[j] = q != nullptr ? p[c] + q[c] : p[c];
-            s += (double)v[j];
+        for (int j4 = 0; j4 < CPL / 4; ++j4) {
+            const int c = 256 * j4 + 4 * lane;
+            f32x4 a = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
+            if (c < D) {
+                a = *reinterpret_cast<const f32x4 *>(p + c);
+                if (q != nullptr) r = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(q + c));
+            }
+            v[4 * j4 + 0] = q != nullptr ? a.x + r.x : a.x;
+            v[4 * j4 + 1] = q != nullptr ? a.y + r.y : a.y;
+            v[4 * j4 + 2] = q != nullptr ? a.z + r.z : a.z;
+            v[4 * j4 + 3] = q != nullptr ? a.w + r.w : a.w;
+        }
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+            if (col(j) < D) s += (double)v[j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = col(j);
+            v[j] = 0.0f;
+            if (c < D) {
+                v[j] = q != nullptr ? p[c] + q[c] : p[c];
+                s += (double)v[j];
+            }
         }
     }
     const double mean = wave_sum_f64(s) / (double)D;
     double sq = 0.0;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const int c = lane + 64 * j;
-        if (c < D) {
+        if (col(j) < D) {
             const double d = (double)v[j] - mean;
             sq += d * d;
         }
     }
     const double variance = wave_sum_f64(sq) / (double)D;
     const double inv_std = 1.0 / sqrt(variance + eps);
+    if (VEC) {
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const int c = lane + 64 * j;
-        if (c < D) p[c] = (float)((((double)v[j] - mean) * inv_std) * (double)w[c] + (double)b[c]);
+        for (int j4 = 0; j4 < CPL / 4; ++j4) {
+            const int c = 256 * j4 + 4 * lane;
+            if (c >= D) continue;
+            const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + c), bv = *reinterpret_cast<const f32x4 *>(b + c);
+            f32x4 o;
+            o.x = (float)((((double)v[4 * j4 + 0] - mean) * inv_std) * (double)wv.x + (double)bv.x);
+            o.y = (float)((((double)v[4 * j4 + 1] - mean) * inv_std) * (double)wv.y + (double)bv.y);
+            o.z = (float)((((double)v[4 * j4 + 2] - mean) * inv_std) * (double)wv.z + (double)bv.z);
+            o.w = (float)((((double)v[4 * j4 + 3] - mean) * inv_std) * (double)wv.w + (double)bv.w);
+            *reinterpret_cast<f32x4 *>(p + c) = o;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = col(j);
+            if (c < D) p[c] = (float)((((double)v[j] - mean) * inv_std) * (double)w[c] + (double)b[c]);
+        }
     }
 }
 
@@ -132,24 +171,36 @@ __global__ __launch_bounds__(256) void residual_layer_norm(float *__restrict__ h
 // reference's summation order, so the result is exact:
 //   pool_mean_cols: one thread per (sequence, column); the column's float64 sum runs over
 //     the rows in order; out = float32(sum * (1/L)). Grid (ceil(D/256), nseq).
-//   l2_normalize_rows: one block per sequence; one thread adds the squares over the
-//     columns in order, then out = float32(out / norm), or 0 when norm < 1e-12.
+//   l2_normalize_rows: one block per sequence (D <= 4096); the row is staged in LDS, one
+//     thread adds the squares over the columns in order, then out = float32(out / norm),
+//     or 0 when norm < 1e-12.
 __global__ __launch_bounds__(256) void pool_mean_cols(const float *__restrict__ h, int64_t ldh, int L, int D,
                                                       float *__restrict__ out, int64_t ldo) {
     const int j = blockIdx.x * 256 + threadIdx.x;
     if (j >= D) return;
     const float *col = h + (int64_t)blockIdx.y * L * ldh + j;
     double acc = 0.0;
-    for (int i = 0; i < L; ++i) acc += (double)col[(int64_t)i * ldh];
+    int i = 0;
+    for (; i + 8 <= L; i += 8) {  // 8 loads in flight, then the adds in row order
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = col[(int64_t)(i + u) * ldh];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += (double)x[u];
+    }
+    for (; i < L; ++i) acc += (double)col[(int64_t)i * ldh];
     out[blockIdx.y * ldo + j] = L > 0 ? (float)(acc * (1.0 / (double)L)) : 0.0f;
 }
 
 __global__ __launch_bounds__(256) void l2_normalize_rows(float *__restrict__ out, int64_t ldo, int D) {
+    __shared__ float row[4096];
     __shared__ double norm_s;
     float *o = out + blockIdx.x * ldo;
+    for (int j = threadIdx.x; j < D; j += 256) row[j] = o[j];
+    __syncthreads();
     if (threadIdx.x == 0) {
         double sq = 0.0;
-        for (int j = 0; j < D; ++j) sq += (double)o[j] * (double)o[j];
+        for (int j = 0; j < D; ++j) sq += (double)row[j] * (double)row[j];
         norm_s = sqrt(sq);
     }
     __syncthreads();

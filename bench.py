@@ -287,7 +287,6 @@ def other_configs(ctx, torch, stream, ceilings):
     codes = g.integers(-127, 128, size=(N, K), dtype=np.int8)
     rscale = g.uniform(1e-3, 1e-2, size=N).astype(np.float32)
     hidx = ctx.register_weight(codes, rscale)
-    del codes
     for M in (1, 16, 256):
         with torch.cuda.stream(stream):
             a = torch.from_numpy(workloads.activations(g, M, K)).cuda()
@@ -330,7 +329,20 @@ def other_configs(ctx, torch, stream, ceilings):
             "note": "M queries against a 2^20 x 384 int8 index (403 MB > MALL), pre-quantized queries, "
                     "bias-free W8A8 scores (enchip_w8a8_pre_dev); bytes = index + queries + scales + M*N f32 scores; "
                     "top10_us_per_call = the same scores plus the device top-10 per query (enchip_topk_rows_dev)"}
+        if M <= 16:
+            # the reference's CPU path for the same scores: the C restatement of its AVX2
+            # W8A8 linear (oracle/cpu_baseline.c), bias-free, on the host's cores
+            import oracle
+
+            qh = a.cpu().numpy()
+            oracle.cpu_w8a8_linear(qh, codes, rscale, None, 0, M, K, N, host_threads())
+            t0 = time.perf_counter()
+            for _ in range(3):
+                oracle.cpu_w8a8_linear(qh, codes, rscale, None, 0, M, K, N, host_threads())
+            out[f"ann_flat_i8_m{M}"]["cpu_port_us_per_call"] = (time.perf_counter() - t0) / 3 * 1e6
+            out[f"ann_flat_i8_m{M}"]["cpu_port_threads"] = host_threads()
         del a, aq, asc, dst, hi, hs
+    del codes
     ctx.release_weight(hidx)
 
     # f32 attention products of one config-4 layer (encoder/attention.go:108,111) on the

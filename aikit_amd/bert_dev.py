@@ -19,7 +19,10 @@ matmul seam, docs/task-native-gpu.md:418-427):
   ffn   = W8A8(inter, Wd) + b           enchip_w8a8_linear_dev
   h     = LN(h + ffn)                   enchip_residual_layer_norm_dev
 
-and pools with enchip_pool_mean_l2_dev (encoder/pooling.go:84-105, embed/pool.go:22-38).
+and pools with enchip_pool_mean_l2_dev (encoder/pooling.go:84-105, embed/pool.go:22-38),
+or, as a cross-encoder, scores each sequence with classifier(tanh(pooler(CLS)))
+(encoder/crossencoder.go:219-238): the f32 MatmulBT on the CLS rows read in place, then
+enchip_bias_act_rows_dev for the bias + TanhF32 and the classifier's bias.
 The embedding lookup and its LayerNorm (bert.go:299-323) stay with the caller: the input
 is the [S*L, D] f32 hidden state after them. Every sequence of a batch has the same L.
 
@@ -128,3 +131,23 @@ class DeviceBert:
         """forward(), then mean pooling + L2 normalisation of each sequence into pooled [S, D]."""
         self.forward(h, S, L, stream)
         self.ctx.pool_mean_l2_dev(h.data_ptr(), self.D, S, L, self.D, pooled.data_ptr(), self.D, stream)
+
+    def rerank(self, h, S: int, L: int, pooler, classifier, logits, stream: int = 0) -> None:
+        """forward(), then the cross-encoder head on each sequence's [CLS] row (row 0):
+        logits [S, labels] = classifier(tanh(pooler(CLS))). pooler = (W [D, D], b [D]),
+        classifier = (W [labels, D], b [labels]), f32 device tensors (PyTorch [out, in])."""
+        c, D = self.ctx, self.D
+        pw, pb = pooler
+        cw, cb = classifier
+        labels = cw.shape[0]
+        if tuple(pw.shape) != (D, D) or tuple(cw.shape) != (labels, D) or tuple(logits.shape) != (S, labels):
+            raise ValueError("rerank: pooler [D, D], classifier [labels, D], logits [S, labels]")
+        self.forward(h, S, L, stream)
+        pooled = self._bufs[(S, L)].setdefault("pooled", self.torch.empty((S, D), device="cuda"))
+        # CLS rows are every L-th row of h: pitch L*D
+        c.matmul_bt_f32_dev(h.data_ptr(), L * D, pw.data_ptr(), D, enchip.B_NK, pooled.data_ptr(), D, S, D, D,
+                            stream=stream)
+        c.bias_act_rows_dev(pooled.data_ptr(), D, S, D, pb.data_ptr(), enchip.ACT_TANH, stream)
+        c.matmul_bt_f32_dev(pooled.data_ptr(), D, cw.data_ptr(), D, enchip.B_NK, logits.data_ptr(), labels, S, D,
+                            labels, stream=stream)
+        c.bias_act_rows_dev(logits.data_ptr(), labels, S, labels, cb.data_ptr(), enchip.ACT_NONE, stream)

@@ -1130,3 +1130,24 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int6
     HIP_TRY(ctx, hipStreamSynchronize(s));
     return ENCHIP_OK;
 }
+
+int enchip_bias_act_rows_dev(enchip_ctx *ctx, float *d_x, int64_t ld, int64_t rows, int64_t cols,
+                             const float *d_bias, int act, void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (act != ENCHIP_ACT_NONE && act != ENCHIP_ACT_TANH)
+        return fail(ctx, ENCHIP_ERR_ARG, "bias_act: act must be ENCHIP_ACT_NONE or ENCHIP_ACT_TANH, got %d", act);
+    if (rows < 0 || cols < 0 || ld < cols || rows * cols > ((int64_t)1 << 38))
+        return fail(ctx, ENCHIP_ERR_ARG, "bias_act: bad shape rows=%lld cols=%lld ld=%lld", (long long)rows,
+                    (long long)cols, (long long)ld);
+    if (rows == 0 || cols == 0) return ENCHIP_OK;
+    if (!d_x) return fail(ctx, ENCHIP_ERR_ARG, "bias_act: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    const dim3 grid((unsigned)((rows * cols + 255) / 256));
+    if (act == ENCHIP_ACT_TANH)
+        hipLaunchKernelGGL(enchip::bias_act_rows<true>, grid, dim3(256), 0, s, d_x, ld, rows, (int)cols, d_bias);
+    else
+        hipLaunchKernelGGL(enchip::bias_act_rows<false>, grid, dim3(256), 0, s, d_x, ld, rows, (int)cols, d_bias);
+    return check_launch(ctx, "bias_act_rows");
+}

@@ -166,6 +166,49 @@ __global__ __launch_bounds__(256) void residual_layer_norm(float *__restrict__ h
     }
 }
 
+// linalg.ExpF32 (linalg/exp.go:62-75): NaN passes through, overflow to +Inf above
+// 88.72283, underflow to 0 below -87.33654, expF32Core otherwise.
+__device__ __forceinline__ float exp_f32(float x) {
+    if (x != x) return x;
+    if (x > 88.72283f) return INFINITY;
+    if (x < -87.33654f) return 0.0f;
+    return exp_f32_core(x);
+}
+
+// linalg.TanhF32 (linalg/exp.go:319-337): Cephes' odd polynomial below |x| = 0.625,
+// 1 - 2/(ExpF32(2|x|) + 1) above, sign restored; +-1 above |x| = 9.
+__device__ __forceinline__ float tanh_f32(float x) {
+    float sign = 1.0f;
+    if (x < 0) {
+        sign = -1.0f;
+        x = -x;
+    }
+    if (x > 9) return sign;
+    if (x < 0.625f) {
+        const float z = x * x;
+        float p = -5.70498872745e-3f;
+        p = p * z + 2.06390887954e-2f;
+        p = p * z - 5.37397155531e-2f;
+        p = p * z + 1.33314422036e-1f;
+        p = p * z - 3.33332819422e-1f;
+        return sign * (p * z * x + x);
+    }
+    return sign * (1.0f - 2.0f / (exp_f32(2.0f * x) + 1.0f));
+}
+
+// x = act(x + bias) on rows x cols (pitch ld), bias optional: the cross-encoder head's
+// addBias + TanhInto (encoder/crossencoder.go:229-236), TANH = 1, or addBias alone.
+template <bool TANH>
+__global__ __launch_bounds__(256) void bias_act_rows(float *__restrict__ x, int64_t ld, int64_t rows, int cols,
+                                                     const float *__restrict__ bias) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * cols) return;
+    const int64_t r = i / cols, c = i % cols;
+    float v = x[r * ld + c];
+    if (bias != nullptr) v = v + bias[c];
+    x[r * ld + c] = TANH ? tanh_f32(v) : v;
+}
+
 // Mean pooling then L2 normalisation of each of nseq sequences of L rows
 // (encoder/pooling.go:84-105 poolOne(mean), embed/pool.go:22-38 L2Normalize) in the
 // reference's summation order, so the result is exact:

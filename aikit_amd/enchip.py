@@ -22,7 +22,7 @@ import numpy as np
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libenchip.so")
 
 OK, ERR_NO_DEVICE, ERR_ARG, ERR_HIP, ERR_OOM, ERR_HANDLE = range(6)
-ACT_NONE, ACT_GELU = 0, 1
+ACT_NONE, ACT_GELU, ACT_TANH = 0, 1, 2  # ACT_TANH: bias_act_rows_dev only
 B_NK, B_KN = 0, 1  # enchip_matmul_bt_f32_dev b layouts: b[N,K] rows, b[K,N] rows
 ABI_VERSION = 1
 
@@ -54,6 +54,7 @@ _SIGNATURES = {
     "enchip_residual_layer_norm_dev": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp, ctypes.c_double,
                                               _vp]),
     "enchip_pool_mean_l2_dev": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
+    "enchip_bias_act_rows_dev": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp]),
     "enchip_attention_f32_dev": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
                                         _vp]),
     "enchip_matmul_bt_f32_dev": (_int, [_vp, _vp, _i64, _vp, _i64, _int, _vp, _i64, _i64, _i64, _i64, _vp, _vp,
@@ -327,6 +328,11 @@ class Context:
                                 eps: float, stream: int = 0) -> None:
         self._check(self._lib.enchip_residual_layer_norm_dev(self._h, d_h or None, ldh, d_y or None, ldy, rows, D,
                                                              d_w or None, d_b or None, eps, stream or None))
+
+    def bias_act_rows_dev(self, d_x: int, ld: int, rows: int, cols: int, d_bias: int, act: int,
+                          stream: int = 0) -> None:
+        self._check(self._lib.enchip_bias_act_rows_dev(self._h, d_x or None, ld, rows, cols, d_bias or None, act,
+                                                       stream or None))
 
     def attention_f32_dev(self, d_q: int, d_k: int, d_v: int, ld: int, d_out: int, ldo: int, nseq: int, L: int,
                           heads: int, head_dim: int, scale: float, stream: int = 0) -> None:

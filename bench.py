@@ -430,12 +430,14 @@ def weight_registration(ctx, layers_host):
                     "pre-swizzled image, as loaded from a mapped weight_cache file)"}
 
 
-def device_forward(ctx, torch, stream, layers_host, cfg, reps: int = 3):
-    """The whole config-4 forward resident on the device (aikit_amd.bert_dev: per layer the
-    fused-QKV / O / FFN W8A8 linears, the f32 attention products, softmax, two residual +
-    LayerNorm), then mean pooling + L2, over one batch of 64 x 512 tokens. The input is
-    the hidden state after the embedding LayerNorm (synthetic N(0,1)); the embedding
-    lookup itself (a gather of 32768 rows) is not included."""
+def device_forward(ctx, torch, stream, layers_host, cfg, reps: int = 3, head: str = "pool"):
+    """A whole encoder forward resident on the device (aikit_amd.bert_dev: per layer the
+    fused-QKV / O / FFN W8A8 linears, the f32 attention, two residual + LayerNorm) over one
+    batch of cfg.batch x cfg.seq tokens, then the head: "pool" = mean pooling + L2 (config
+    4, BERT-base embeddings), "rerank" = the cross-encoder head classifier(tanh(pooler(CLS)))
+    with one label (config 5, XLM-R-large reranking, encoder/crossencoder.go:219-238). The
+    input is the hidden state after the embedding LayerNorm (synthetic N(0,1)); the
+    embedding lookup itself (a gather of one row per token) is not included."""
     import numpy as np
 
     from aikit_amd import workloads
@@ -456,7 +458,13 @@ def device_forward(ctx, torch, stream, layers_host, cfg, reps: int = 3):
     with torch.cuda.stream(stream):
         h0 = torch.randn((S * L, D), device="cuda", generator=torch.Generator(device="cuda").manual_seed(5))
         h = torch.empty_like(h0)
-        pooled = torch.empty((S, D), device="cuda")
+        if head == "rerank":
+            dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+            pooler = (dev(g.standard_normal((D, D)) * 0.02), dev(g.standard_normal(D) * 0.02))
+            classifier = (dev(g.standard_normal((1, D)) * 0.02), dev(g.standard_normal(1) * 0.02))
+            out = torch.empty((S, 1), device="cuda")
+        else:
+            out = torch.empty((S, D), device="cuda")
     torch.cuda.synchronize()
     times = []
     try:
@@ -465,18 +473,34 @@ def device_forward(ctx, torch, stream, layers_host, cfg, reps: int = 3):
                 h.copy_(h0)
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            model.embed(h, S, L, pooled, sp)
+            if head == "rerank":
+                model.rerank(h, S, L, pooler, classifier, out, sp)
+            else:
+                model.embed(h, S, L, out, sp)
             torch.cuda.synchronize()
             if r > 0:
                 times.append(time.perf_counter() - t0)
-        finite = bool(torch.isfinite(pooled).all().item())
+        finite = bool(torch.isfinite(out).all().item())
     finally:
         model.close()
     t = sorted(times)[len(times) // 2]
-    return {"seqs_per_s": S / t, "ms_per_batch": t * 1e3, "batch": S, "seq_len": L, "layers": cfg.layers,
-            "pooled_finite": finite,
-            "note": "median of %d forwards; W8A8 linears + f32 attention (MFMA) + softmax + LayerNorm + pooling, "
-                    "all on the device, activations resident; embedding lookup excluded" % reps}
+    rate = "pairs_per_s" if head == "rerank" else "seqs_per_s"
+    tail = "cross-encoder head (f32 pooler + tanh + classifier)" if head == "rerank" else "pooling"
+    return {rate: S / t, "ms_per_batch": t * 1e3, "batch": S, "seq_len": L, "layers": cfg.layers,
+            "hidden": D, "output_finite": finite,
+            "note": "median of %d forwards; W8A8 linears + fused f32 attention (MFMA) + LayerNorm + %s, all on "
+                    "the device, activations resident; embedding lookup excluded" % (reps, tail)}
+
+
+def rerank_device(ctx, torch, stream, reps: int = 2):
+    """Config 5: XLM-R-large (24 layers, D 1024, 16 heads, FFN 4096) cross-encoder scoring of
+    128 (query, passage) pairs of 512 tokens, random-init weights quantized per channel."""
+    from aikit_amd import workloads
+
+    cfg = workloads.XLMR_LARGE_CE
+    g = workloads.rng(2025)
+    host = [workloads.encoder_layer_weights(g, cfg) for _ in range(cfg.layers)]
+    return device_forward(ctx, torch, stream, host, cfg, reps=reps, head="rerank")
 
 
 def main() -> int:
@@ -486,9 +510,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length (0 = skip)")
     ap.add_argument("--no-other-configs", action="store_true", help="skip the config 2 / config 3 measurements")
-    ap.add_argument("--forward-only", action="store_true",
-                    help="only time the config-4 forward resident on the device and print its figures (a profiling "
-                         "mode: its kernels are then the only ones in a trace)")
+    ap.add_argument("--forward-only", nargs="?", const="cfg4", choices=["cfg4", "cfg5"], default=None,
+                    help="only time the config-4 forward resident on the device (cfg5: and then the config-5 "
+                         "cross-encoder) and print its figures (a profiling mode: its kernels are then the only "
+                         "ones in a trace)")
     ap.add_argument("--graph", type=int, default=0,
                     help="1: replay each timed step as a captured HIP graph; 0 (default): eager launches. "
                          "Measured equal on MI355X (launch overhead hides behind the kernels)")
@@ -518,8 +543,11 @@ def main() -> int:
         g = workloads.rng(2024)
         host = [workloads.encoder_layer_weights(g, cfg) for _ in range(cfg.layers)]
         fwd = device_forward(ctx, torch, stream, host, cfg, reps=max(1, args.steps))
+        out = {"encode_device_cfg4": fwd}
+        if args.forward_only == "cfg5":
+            out["rerank_device_cfg5"] = rerank_device(ctx, torch, stream, reps=max(1, args.steps))
         ctx.close()
-        print(json.dumps({"encode_device_cfg4": fwd}), flush=True)
+        print(json.dumps(out), flush=True)
         return 0
 
     # ---- weights: 12 layers x 4 linears, random N(0,0.02) quantized per channel
@@ -725,6 +753,9 @@ def main() -> int:
         log("config 4 forward resident on the device (linears, attention, LayerNorm, pooling)")
         result["other_configs"]["encode_device_cfg4"] = device_forward(ctx, torch, stream, layers_host, cfg)
         log(f"  {result['other_configs']['encode_device_cfg4']['seqs_per_s']:.1f} seqs/s end to end")
+        log("config 5 cross-encoder rerank resident on the device (XLM-R-large shape, 128 pairs x 512)")
+        result["other_configs"]["rerank_device_cfg5"] = rerank_device(ctx, torch, stream)
+        log(f"  {result['other_configs']['rerank_device_cfg5']['pairs_per_s']:.1f} pairs/s end to end")
     if args.cpu_seconds > 0:
         log(f"CPU baseline ({args.cpu_seconds:.0f}s sample, {host_threads()} threads)")
         result["cpu_baseline"] = cpu_baseline(layers_host[0], cfg, args.cpu_seconds)

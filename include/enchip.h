@@ -53,7 +53,8 @@ enum enchip_status {
 
 enum enchip_act {
     ENCHIP_ACT_NONE = 0,
-    ENCHIP_ACT_GELU = 1 /* exact-erf GELU, linalg.GELUF32 */
+    ENCHIP_ACT_GELU = 1, /* exact-erf GELU, linalg.GELUF32 */
+    ENCHIP_ACT_TANH = 2  /* linalg.TanhF32; enchip_bias_act_rows_dev only */
 };
 
 /* Layout of the b operand of enchip_matmul_bt_f32_dev. */
@@ -280,6 +281,14 @@ int enchip_softmax_rows_scaled_dev(enchip_ctx *ctx, float *d_x, int64_t ld, int6
 int enchip_residual_layer_norm_dev(enchip_ctx *ctx, float *d_h, int64_t ldh, const float *d_y,
                                    int64_t ldy, int64_t rows, int64_t D, const float *d_w,
                                    const float *d_b, double eps, void *stream);
+
+/* x = act(x + bias) in place on rows x cols (pitch ld; d_bias[cols] may be NULL), act
+ * ENCHIP_ACT_NONE or ENCHIP_ACT_TANH (linalg.TanhF32, linalg/exp.go:319-337, with
+ * linalg.ExpF32's guards): the cross-encoder head's addBias + TanhInto after the pooler
+ * and addBias after the classifier (encoder/crossencoder.go:229-236). Bit-identical to
+ * the reference's f32 operations. */
+int enchip_bias_act_rows_dev(enchip_ctx *ctx, float *d_x, int64_t ld, int64_t rows, int64_t cols,
+                             const float *d_bias, int act, void *stream);
 
 /* Mean pooling then L2 normalisation of nseq sequences of L rows each (rows
  * z*L .. z*L+L-1 of d_h, pitch ldh) into d_out[nseq][ldo]: encoder/pooling.go:84-105

@@ -179,3 +179,76 @@ def test_config1_device_resident_forward(ctx, workers, fused):
         worst = min(worst, cos)
         assert cos >= COS_MIN, f"{cfg.name} seq {s}: cosine {cos}"
     say(f"  worst cosine {worst:.9f}")
+
+
+def test_config5_shaped_cross_encoder_on_device(ctx, workers):
+    # Config 5's architecture (XLM-R-large widths: D=1024, 16 heads, FFN 4096) at 2 layers
+    # and 2 pairs of 128 tokens, scored as a cross-encoder (encoder/crossencoder.go:219-238)
+    # entirely on the device, against the CPU reference composition (the reference's W8A8
+    # linears, the oracle's attention / LayerNorm / TanhF32, the f32 head in float64).
+    # Attention and LayerNorm sum in another order on the device; a last-bit difference
+    # can move one per-token int8 code in the next linear, so the chain is held to the
+    # north star's cosine on the [CLS] hidden state, and the head alone (f32 MatmulBT,
+    # bias, TanhF32, classifier) to 1e-5 on the device's own [CLS] rows.
+    import torch
+
+    from aikit_amd import enchip
+    from aikit_amd.bert_dev import DeviceBert
+
+    cfg = workloads.EncoderConfig("xlmr-shaped-2l", layers=2, hidden=1024, heads=16, ffn=4096, batch=2, seq=128,
+                                  vocab=1000)
+    w = model_weights(cfg, seed=505)
+    g = workloads.rng(506)
+    seqs = [g.integers(0, cfg.vocab, size=cfg.seq) for _ in range(cfg.batch)]
+    D, labels = cfg.hidden, 1
+    pw = (g.standard_normal((D, D)) * 0.02).astype(np.float32)
+    pb = (g.standard_normal(D) * 0.02).astype(np.float32)
+    cw = (g.standard_normal((labels, D)) * 0.02).astype(np.float32)
+    cb = (g.standard_normal(labels) * 0.02).astype(np.float32)
+
+    def ref_linear(x, li, name):
+        wq, ws, b, act = w["layers"][li][name]
+        M, K = x.shape
+        return oracle.cpu_w8a8_linear(x, wq, ws, b, act, M, K, wq.shape[0], workers=workers).reshape(M, -1)
+
+    def ref_cls(ids):
+        L = len(ids)
+        h = embeddings_in(ids, w, cfg)
+        for li in range(cfg.layers):
+            qkv = ref_linear(h, li, "qkv")
+            ctxv = oracle.attention(np.ascontiguousarray(qkv[:, :D]), np.ascontiguousarray(qkv[:, D:2 * D]),
+                                    np.ascontiguousarray(qkv[:, 2 * D:]), L, D, cfg.heads)
+            h = oracle.layer_norm((h + ref_linear(ctxv, li, "o")).astype(np.float32), *w["layers"][li]["attn_ln"],
+                                  L, D, 1e-12)
+            ffn = ref_linear(ref_linear(h, li, "ffn_up"), li, "ffn_down")
+            h = oracle.layer_norm((h + ffn).astype(np.float32), *w["layers"][li]["out_ln"], L, D, 1e-12)
+        return h[0]
+
+    def head(cls):
+        pooled = oracle.tanh((cls.astype(np.float64) @ pw.T.astype(np.float64) + pb).astype(np.float32))
+        return pooled.astype(np.float64) @ cw.T.astype(np.float64) + cb
+
+    ref_cls_rows = np.array([ref_cls(ids) for ids in seqs])
+
+    S, L = cfg.batch, cfg.seq
+    h0 = np.concatenate([embeddings_in(ids, w, cfg) for ids in seqs])
+    model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn)
+    try:
+        say(f"{cfg.name} cross-encoder on the device, {S} pairs of {L}")
+        dv = {k: torch.from_numpy(v).cuda() for k, v in dict(h=h0, pw=pw, pb=pb, cw=cw, cb=cb).items()}
+        logits = torch.empty((S, labels), device="cuda")
+        torch.cuda.synchronize()
+        model.rerank(dv["h"], S, L, (dv["pw"], dv["pb"]), (dv["cw"], dv["cb"]), logits)
+        torch.cuda.synchronize()
+        got = logits.cpu().numpy().astype(np.float64)
+        dev_cls = dv["h"].cpu().numpy().reshape(S, L, D)[:, 0]
+    finally:
+        model.close()
+    head_err = np.abs(got - np.array([head(c) for c in dev_cls])).max()
+    say(f"  head on the device's [CLS] rows: worst abs error {head_err:.3g}")
+    assert head_err <= 1e-5
+    for s_ in range(S):
+        a, b = ref_cls_rows[s_].astype(np.float64), dev_cls[s_].astype(np.float64)
+        cos = float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+        say(f"  pair {s_}: [CLS] cosine {cos:.9f}, logit {got[s_, 0]:.6f} vs {head(ref_cls_rows[s_])[0]:.6f}")
+        assert cos >= COS_MIN

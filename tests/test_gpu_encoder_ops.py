@@ -207,3 +207,26 @@ def test_fused_attention_rejects_unsupported(ctx):
     with pytest.raises(enchip.EnchipError):  # L above 512
         ctx.attention_f32_dev(p, p, p, 64, p, 64, 1, 513, 1, 64, 0.1)
     torch.cuda.synchronize()
+
+
+def test_bias_tanh_matches_oracle(ctx):
+    # encoder/crossencoder.go:229-236 addBias + TanhInto: bit-identical to the oracle's
+    # TanhF32 restatement (both branches, the saturation above 9, signed zeros, NaN).
+    import torch
+
+    from aikit_amd import enchip
+
+    g = workloads.rng(880)
+    rows, cols = 37, 300
+    x = (g.standard_normal((rows, cols)) * 4).astype(np.float32)
+    x[0, :6] = [0.0, -0.0, 0.6249, 0.625, 9.5, np.nan]
+    b = (g.standard_normal(cols) * 0.5).astype(np.float32)
+    b[:6] = 0
+    dx, db = _dev(torch, x), _dev(torch, b)
+    torch.cuda.synchronize()
+    ctx.bias_act_rows_dev(dx.data_ptr(), cols, rows, cols, db.data_ptr(), enchip.ACT_TANH)
+    torch.cuda.synchronize()
+    want = oracle.tanh((x + b).astype(np.float32))
+    got = dx.cpu().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(got[~np.isnan(want)].view(np.uint32), want[~np.isnan(want)].view(np.uint32))

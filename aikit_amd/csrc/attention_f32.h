@@ -157,7 +157,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES, 4) void attention_f32(
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int c = lane + 64 * j;
-            const float e = c < L ? exp_f32_core(x[j] - m) : 0.0f;
+            const float e = c < L ? exp_f32_core_nonpos(x[j] - m) : 0.0f;
             x[j] = e;
             sum += (double)e;
         }
@@ -198,6 +198,227 @@ __global__ __launch_bounds__(64 * ATT_WAVES, 4) void attention_f32(
     lds_barrier();
 
     // add the G key groups in order and store: one element per thread per round
+    for (int idx = threadIdx.x; idx < ATT_QT * HD; idx += 64 * ATT_WAVES) {
+        const int row = idx / HD, c = idx % HD, o = c / 32, cc = c % 32;
+        float s = sc[o * 1024 + row * 32 + cc];
+        for (int gg = 1; gg < G; ++gg) s += sc[(gg * NOT + o) * 1024 + row * 32 + cc];
+        const int qrow = q0 + row;
+        if (qrow < L) out[(row0 + qrow) * ldo + head * HD + c] = s;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The same attention with both products on the bf16 MFMA (v_mfma_f32_32x32x16_bf16),
+// each f32 operand split into two bfloat16 parts: the 3-product split-bfloat16 method of
+// Henry, Tang and Heinecke ("Leveraging the bfloat16 Artificial Intelligence Datatype For
+// Higher-Precision Computations", ARITH 2019).
+//   x = hi + lo + e,  hi = bf16(x), lo = bf16(x - hi) (round to nearest even; x - hi is
+//   exact in f32), |e| <= 2^-18 |x|;
+//   x.y ~= hi.hi' + hi.lo' + lo.hi', the dropped terms at most 3 * 2^-18 |x y|.
+// The products are exact in f32 and summed in f32 accumulators, so each dot product is
+// within ~1e-5 of its f32 value relative to the sum of |terms|, inside the f32 MatmulBT
+// gate of the reference (gpu/enccuda/backend_test.go:71-81, <= 2e-4 of max(|ref|, 1)).
+// Per 16-deep block that is 3 MFMAs of 32 cycles against 8 f32 MFMAs of 64, plus ~3 VALU
+// operations per operand value for the split.
+//
+// Same grid, LDS size and phases as attention_f32; operand lanes hold the same values
+// (lane half hf supplies depth 8hf..8hf+7 of each 16-deep block), now as bf16x8 pairs.
+// The softmax writes P already split: row r of the score tile (4P bytes) becomes a bf16
+// hi plane at byte 0 and a bf16 lo plane at byte 2P + 8 (both 16-byte aligned, 32 * nkt
+// entries each), and each softmax lane owns 2 adjacent columns so that both planes are
+// written a 32-bit word at a time. Non-finite operands give NaN (inf - inf in the split).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void split_bf16x8(const float *x, bf16x8 &hi, bf16x8 &lo) {
+#pragma unroll
+    for (int s = 0; s < 8; s += 2) {
+        const bf16x2 h = __builtin_convertvector((f32x2){x[s], x[s + 1]}, bf16x2);
+        const bf16x2 l = __builtin_convertvector((f32x2){x[s] - (float)h[0], x[s + 1] - (float)h[1]}, bf16x2);
+        hi[s] = h[0];
+        hi[s + 1] = h[1];
+        lo[s] = l[0];
+        lo[s + 1] = l[1];
+    }
+}
+
+__device__ __forceinline__ f32x16 mfma_split3(const bf16x8 &ah, const bf16x8 &al, const bf16x8 &bh, const bf16x8 &bl,
+                                              f32x16 acc) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc, 0, 0, 0);
+}
+
+// Two f32 values -> the 32-bit words of their hi and lo bf16 parts (element 0 low).
+__device__ __forceinline__ void split_pair(float a, float b, uint32_t &hw, uint32_t &lw) {
+    const bf16x2 h = __builtin_convertvector((f32x2){a, b}, bf16x2);
+    const bf16x2 l = __builtin_convertvector((f32x2){a - (float)h[0], b - (float)h[1]}, bf16x2);
+    hw = __builtin_bit_cast(uint32_t, h);
+    lw = __builtin_bit_cast(uint32_t, l);
+}
+
+// FULL: L == ATT_MAX_L, so every bounds check of the tile loops folds away.
+template <int HD, bool FULL>
+__global__ __launch_bounds__(64 * ATT_WAVES, 4) void attention_split_bf16(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t ld,
+    float *__restrict__ out, int64_t ldo, int L_arg, int heads, float scale) {
+    const int L = FULL ? ATT_MAX_L : L_arg;
+    static_assert(HD == 32 || HD == 64, "head dimension");
+    constexpr int NOT = HD / 32;
+    constexpr int G = ATT_WAVES / NOT;
+    constexpr int NB = HD / 16;                      // 16-deep blocks of the head dimension
+    constexpr int T1 = ATT_MAX_KT / ATT_WAVES;
+    constexpr int T3 = (ATT_MAX_KT + G - 1) / G;
+    extern __shared__ __attribute__((aligned(16))) float sc[];
+    const int P = att_pitch(L);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 31, hf = lane >> 5;
+    const int nkt = (L + 31) / 32, nqt = (L + ATT_QT - 1) / ATT_QT;
+    const int logical = xcd_logical_tile(blockIdx.x, gridDim.x);
+    const int q0 = (logical % nqt) * ATT_QT, head = (logical / nqt) % heads;
+    const int64_t row0 = (int64_t)(logical / nqt / heads) * L;
+
+    // ---- 1. S = Q K^T * scale into LDS (f32), rows past L re-read row L-1.
+    float qa[HD / 2], kb[T1][HD / 2];
+    {
+        const float *qrow = q + (row0 + min(q0 + r, L - 1)) * ld + head * HD;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) load8(qrow + 16 * b + 8 * hf, qa + 8 * b);
+#pragma unroll
+        for (int t = 0; t < T1; ++t) {
+            const int kt = min(wave + ATT_WAVES * t, nkt - 1);
+            const float *krow = k + (row0 + min(32 * kt + r, L - 1)) * ld + head * HD;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) load8(krow + 16 * b + 8 * hf, kb[t] + 8 * b);
+        }
+    }
+    bf16x8 qh[NB], ql[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) split_bf16x8(qa + 8 * b, qh[b], ql[b]);
+#pragma unroll
+    for (int t = 0; t < T1; ++t) {
+        const int kt = wave + ATT_WAVES * t;
+        if (kt >= nkt) break;
+        f32x16 acc;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            bf16x8 kh, kl;
+            split_bf16x8(kb[t] + 8 * b, kh, kl);
+            acc = mfma_split3(qh[b], ql[b], kh, kl, acc);
+        }
+        const int col = 32 * kt + r;
+        if (col < L) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sc[(8 * (e >> 2) + 4 * hf + (e & 3)) * P + col] = acc[e] * scale;
+        }
+    }
+
+    // ---- 3's V operands, loading while the softmax runs (as attention_f32).
+    const int ot = wave % NOT, g = wave / NOT;
+    float vv[T3][2][8];
+    {
+        const float *vcol = v + row0 * ld + head * HD + 32 * ot + r;
+#pragma unroll
+        for (int i = 0; i < T3; ++i)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int s = 0; s < 8; ++s) {
+                    const int key = 32 * (g + G * i) + 16 * b + 8 * hf + s;
+                    vv[i][b][s] = vcol[(int64_t)min(key, L - 1) * ld];
+                }
+    }
+    lds_barrier();
+
+    // ---- 2. softmax of each LDS row, as softmax_rows_scaled, lane owning columns
+    // 2*lane + 128*j + {0, 1}; P written as its hi / lo bf16 planes over the row.
+    for (int row = wave; row < ATT_QT; row += ATT_WAVES) {
+        float *p = sc + row * P;
+        constexpr int CPL2 = ATT_MAX_L / 128;
+        float x[CPL2][2];
+#pragma unroll
+        for (int j = 0; j < CPL2; ++j) {
+            const int c = 2 * lane + 128 * j;
+            f32x2 t = {-INFINITY, -INFINITY};
+            if (c + 1 < L) t = *reinterpret_cast<const f32x2 *>(p + c);
+            else if (c < L) t[0] = p[c];
+            x[j][0] = t[0];
+            x[j][1] = t[1];
+        }
+        float m = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < CPL2; ++j) {
+            m = x[j][0] > m ? x[j][0] : m;
+            m = x[j][1] > m ? x[j][1] : m;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float o = __shfl_xor(m, off, 64);
+            m = o > m ? o : m;
+        }
+        const float first = __shfl(x[0][0], 0, 64);
+        if (first != first) m = first;
+        double sum = 0.0;
+#pragma unroll
+        for (int j = 0; j < CPL2; ++j)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int c = 2 * lane + 128 * j + u;
+                const float e = c < L ? exp_f32_core_nonpos(x[j][u] - m) : 0.0f;
+                x[j][u] = e;
+                sum += (double)e;
+            }
+        sum = wave_sum_f64(sum);
+        const bool uniform = sum == 0.0;
+        const float un = 1.0f / (float)L;
+        const float inv = uniform ? 0.0f : (float)(1.0 / sum);
+        uint32_t *ph = reinterpret_cast<uint32_t *>(p);
+        uint32_t *pl = reinterpret_cast<uint32_t *>(reinterpret_cast<char *>(p) + 2 * P + 8);
+#pragma unroll
+        for (int j = 0; j < CPL2; ++j) {
+            const int c = 2 * lane + 128 * j;
+            if (c >= 32 * nkt) continue;  // keys past the last tile are never read
+            // keys past L in the last tile: P = 0 (hi and lo)
+            const float a = c < L ? (uniform ? un : x[j][0] * inv) : 0.0f;
+            const float b = c + 1 < L ? (uniform ? un : x[j][1] * inv) : 0.0f;
+            uint32_t hw, lw;
+            split_pair(a, b, hw, lw);
+            ph[c >> 1] = hw;
+            pl[c >> 1] = lw;
+        }
+    }
+    lds_barrier();
+
+    // ---- 3. ctx partial = P[:, this group's keys] . V[those keys, 32*ot .. +32]
+    f32x16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+    {
+        const char *prow = reinterpret_cast<const char *>(sc + r * P);
+#pragma unroll
+        for (int i = 0; i < T3; ++i) {
+            const int kt = g + G * i;
+            if (kt >= nkt) break;
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int key = 32 * kt + 16 * b + 8 * hf;
+                const bf16x8 ph = *reinterpret_cast<const bf16x8 *>(prow + 2 * key);
+                const bf16x8 pl = *reinterpret_cast<const bf16x8 *>(prow + 2 * P + 8 + 2 * key);
+                bf16x8 vh, vl;
+                split_bf16x8(vv[i][b], vh, vl);
+                acc = mfma_split3(ph, pl, vh, vl, acc);
+            }
+        }
+    }
+    lds_barrier();  // every wavefront is done reading P: the LDS takes the partial tiles
+
+    float *part = sc + (g * NOT + ot) * 1024;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) part[(8 * (e >> 2) + 4 * hf + (e & 3)) * 32 + r] = acc[e];
+    lds_barrier();
+
     for (int idx = threadIdx.x; idx < ATT_QT * HD; idx += 64 * ATT_WAVES) {
         const int row = idx / HD, c = idx % HD, o = c / 32, cc = c % 32;
         float s = sc[o * 1024 + row * 32 + cc];

@@ -51,6 +51,7 @@ struct enchip_ctx {
     std::unordered_map<uint64_t, Weight> weights;
     uint64_t next_handle = 1;
     int64_t small_m = 32;
+    int att_products = ENCHIP_ATT_SPLIT_BF16;  // enchip_set_attention_products
     // device scratch (grown on demand, freed by enchip_close)
     int8_t *d_aq = nullptr;
     size_t aq_cap = 0;
@@ -1034,9 +1035,16 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     const size_t lds = (size_t)enchip::att_lds_floats((int)L) * sizeof(float);
-    const void *fn = head_dim == 64 ? reinterpret_cast<const void *>(&enchip::attention_f32<64>)
-                                    : reinterpret_cast<const void *>(&enchip::attention_f32<32>);
-    HIP_TRY(ctx, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    using Kern = void (*)(const float *, const float *, const float *, int64_t, float *, int64_t, int, int, float);
+    const bool split = ctx->att_products == ENCHIP_ATT_SPLIT_BF16;
+    const bool full = L == enchip::ATT_MAX_L;
+    const Kern fn = split ? (head_dim == 64 ? (full ? enchip::attention_split_bf16<64, true>
+                                                    : enchip::attention_split_bf16<64, false>)
+                                            : (full ? enchip::attention_split_bf16<32, true>
+                                                    : enchip::attention_split_bf16<32, false>))
+                          : (head_dim == 64 ? enchip::attention_f32<64> : enchip::attention_f32<32>);
+    HIP_TRY(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)lds));
     // one launch per chunk of sequences whose workgroup count fits a 32-bit grid
     const int64_t per_seq = ((L + enchip::ATT_QT - 1) / enchip::ATT_QT) * heads;
     const int64_t chunk = std::max<int64_t>(1, ((int64_t)1 << 30) / per_seq);
@@ -1044,14 +1052,19 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
         const int64_t nz = std::min<int64_t>(chunk, nseq - z0);
         const dim3 grid((unsigned)(per_seq * nz));
         const int64_t off = z0 * L;
-        if (head_dim == 64)
-            hipLaunchKernelGGL(enchip::attention_f32<64>, grid, dim3(64 * enchip::ATT_WAVES), lds, s, d_q + off * ld,
-                               d_k + off * ld, d_v + off * ld, ld, d_out + off * ldo, ldo, (int)L, (int)heads, scale);
-        else
-            hipLaunchKernelGGL(enchip::attention_f32<32>, grid, dim3(64 * enchip::ATT_WAVES), lds, s, d_q + off * ld,
-                               d_k + off * ld, d_v + off * ld, ld, d_out + off * ldo, ldo, (int)L, (int)heads, scale);
+        hipLaunchKernelGGL(fn, grid, dim3(64 * enchip::ATT_WAVES), lds, s, d_q + off * ld, d_k + off * ld,
+                           d_v + off * ld, ld, d_out + off * ldo, ldo, (int)L, (int)heads, scale);
     }
-    return check_launch(ctx, "attention_f32");
+    return check_launch(ctx, split ? "attention_split_bf16" : "attention_f32");
+}
+
+int enchip_set_attention_products(enchip_ctx *ctx, int mode) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (mode != ENCHIP_ATT_F32 && mode != ENCHIP_ATT_SPLIT_BF16)
+        return fail(ctx, ENCHIP_ERR_ARG, "attention products: mode must be ENCHIP_ATT_F32 or ENCHIP_ATT_SPLIT_BF16");
+    ctx->att_products = mode;
+    return ENCHIP_OK;
 }
 
 // ---------------------------------------------------------------------------- top-k

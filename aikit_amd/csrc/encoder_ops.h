@@ -61,7 +61,7 @@ __global__ __launch_bounds__(256) void softmax_rows_scaled(float *__restrict__ x
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const int c = lane + 64 * j;
-        const float e = c < cols ? exp_f32_core(v[j] - m) : 0.0f;
+        const float e = c < cols ? exp_f32_core_nonpos(v[j] - m) : 0.0f;
         v[j] = e;
         sum += (double)e;
     }

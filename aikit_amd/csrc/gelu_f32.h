@@ -43,6 +43,25 @@ __device__ __forceinline__ float exp_f32_core(float x) {
     return p * __uint_as_float((unsigned)e << 23);
 }
 
+// expF32Core for x <= 0 or NaN (softmax's v - max): bit-identical to exp_f32_core there
+// (checked on the CPU over every such float32). kf <= 0, so k < 2^31 and the e >= 255
+// branch never taken; p * 2^k by ldexp rounds exactly as the multiply by the power of two.
+__device__ __forceinline__ float exp_f32_core_nonpos(float x) {
+    float z = x * 1.4426950408889634f;
+    float t = z + 12582912.0f;
+    float kf = t - 12582912.0f;
+    const int k = kf >= -2147483648.0f ? (int)kf : INT_MIN;  // NaN and -inf -> INT_MIN
+    float r = x - kf * 0.693145751953125f - kf * 1.428606820309417e-06f;
+    float p = 1.9875691500e-4f;
+    p = p * r + 1.3981999507e-3f;
+    p = p * r + 8.3334519073e-3f;
+    p = p * r + 4.1665795894e-2f;
+    p = p * r + 1.6666665459e-1f;
+    p = p * r + 5.0000001201e-1f;
+    p = p * r * r + r + 1.0f;
+    return k <= -127 ? 0.0f : ldexpf(p, k);
+}
+
 // linalg/exp.go:207-244 ErfF32.
 __device__ __forceinline__ float erf_f32(float x) {
     float sign = 1.0f;

@@ -22,7 +22,8 @@ import numpy as np
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libenchip.so")
 
 OK, ERR_NO_DEVICE, ERR_ARG, ERR_HIP, ERR_OOM, ERR_HANDLE = range(6)
-ACT_NONE, ACT_GELU, ACT_TANH = 0, 1, 2  # ACT_TANH: bias_act_rows_dev only
+ACT_NONE, ACT_GELU, ACT_TANH = 0, 1, 2
+ATT_F32, ATT_SPLIT_BF16 = 0, 1  # enchip_att_products  # ACT_TANH: bias_act_rows_dev only
 B_NK, B_KN = 0, 1  # enchip_matmul_bt_f32_dev b layouts: b[N,K] rows, b[K,N] rows
 ABI_VERSION = 1
 
@@ -55,6 +56,7 @@ _SIGNATURES = {
                                               _vp]),
     "enchip_pool_mean_l2_dev": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
     "enchip_bias_act_rows_dev": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp]),
+    "enchip_set_attention_products": (_int, [_vp, _int]),
     "enchip_attention_f32_dev": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
                                         _vp]),
     "enchip_matmul_bt_f32_dev": (_int, [_vp, _vp, _i64, _vp, _i64, _int, _vp, _i64, _i64, _i64, _i64, _vp, _vp,
@@ -137,6 +139,7 @@ class Context:
         if rc != OK:
             raise EnchipError(rc, self._lib.enchip_last_error(None).decode())
         self._h = h
+        self.attention_products = ATT_SPLIT_BF16  # the library's default
 
     # -- lifecycle ------------------------------------------------------------
     def close(self) -> None:
@@ -184,6 +187,11 @@ class Context:
 
     def set_small_m(self, max_m: int) -> None:
         self._check(self._lib.enchip_set_small_m(self._h, max_m))
+
+    def set_attention_products(self, mode: int) -> None:
+        """ATT_F32 or ATT_SPLIT_BF16: how attention_f32_dev computes its two products."""
+        self._check(self._lib.enchip_set_attention_products(self._h, mode))
+        self.attention_products = mode
 
     # -- host-buffer entry points ----------------------------------------------
     def quant_rows(self, a: np.ndarray):

@@ -440,7 +440,7 @@ def device_forward(ctx, torch, stream, layers_host, cfg, reps: int = 3, head: st
     embedding lookup itself (a gather of one row per token) is not included."""
     import numpy as np
 
-    from aikit_amd import workloads
+    from aikit_amd import enchip, workloads
     from aikit_amd.bert_dev import DeviceBert
 
     g = workloads.rng(77)
@@ -486,10 +486,12 @@ def device_forward(ctx, torch, stream, layers_host, cfg, reps: int = 3, head: st
     t = sorted(times)[len(times) // 2]
     rate = "pairs_per_s" if head == "rerank" else "seqs_per_s"
     tail = "cross-encoder head (f32 pooler + tanh + classifier)" if head == "rerank" else "pooling"
+    products = "split-bf16" if ctx.attention_products == enchip.ATT_SPLIT_BF16 else "f32"
     return {rate: S / t, "ms_per_batch": t * 1e3, "batch": S, "seq_len": L, "layers": cfg.layers,
             "hidden": D, "output_finite": finite,
-            "note": "median of %d forwards; W8A8 linears + fused f32 attention (MFMA) + LayerNorm + %s, all on "
-                    "the device, activations resident; embedding lookup excluded" % (reps, tail)}
+            "attention_products": products,
+            "note": "median of %d forwards; W8A8 linears + fused attention (%s MFMA products) + LayerNorm + %s, "
+                    "all on the device, activations resident; embedding lookup excluded" % (reps, products, tail)}
 
 
 def rerank_device(ctx, torch, stream, reps: int = 2):

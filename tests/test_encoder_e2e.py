@@ -138,7 +138,7 @@ def embeddings_in(ids, w, cfg):
     return oracle.layer_norm(h, *w["emb_ln"], L, D, 1e-12)
 
 
-@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("fused", ["split_bf16", "f32", False])
 def test_config1_device_resident_forward(ctx, workers, fused):
     # The whole forward on the device (aikit_amd.bert_dev: W8A8 linears, f32 attention
     # products, softmax, residual + LayerNorm, pooling), every activation resident,
@@ -160,7 +160,10 @@ def test_config1_device_resident_forward(ctx, workers, fused):
 
     S, L, D = cfg.batch, cfg.seq, cfg.hidden
     h0 = np.concatenate([embeddings_in(ids, w, cfg) for ids in seqs])
-    model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn, fused=fused)
+    from aikit_amd import enchip
+
+    model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn, fused=bool(fused))
+    ctx.set_attention_products(enchip.ATT_F32 if fused == "f32" else enchip.ATT_SPLIT_BF16)
     try:
         say(f"{cfg.name} device-resident forward, {S} sequences of {L}, fused attention {fused}")
         h = torch.from_numpy(h0).cuda()
@@ -171,6 +174,7 @@ def test_config1_device_resident_forward(ctx, workers, fused):
         dev = pooled.cpu().numpy()
     finally:
         model.close()
+        ctx.set_attention_products(enchip.ATT_SPLIT_BF16)  # the default
     worst = 1.0
     for s, ids in enumerate(seqs):
         ref = encode(ids, w, cfg, ref_linear)

@@ -157,21 +157,24 @@ def _attention_f64(qkv, S, L, H, hd, scale):
     return out
 
 
+@pytest.mark.parametrize("products", ["f32", "split_bf16"])
 @pytest.mark.parametrize("S,L,H,hd", [(2, 128, 12, 64), (1, 512, 4, 64), (3, 77, 6, 32), (2, 40, 2, 64),
-                                      (1, 1, 3, 64), (2, 512, 2, 32)])
-def test_fused_attention_matches_f64_and_unfused(ctx, S, L, H, hd):
+                                      (1, 1, 3, 64), (2, 512, 2, 32), (1, 33, 2, 64), (1, 511, 1, 32)])
+def test_fused_attention_matches_f64_and_unfused(ctx, S, L, H, hd, products):
     # Gate: the f32 MatmulBT statistic (gpu/enccuda/backend_test.go:71-81) against a
-    # float64 attention, for the fused kernel and for the unfused chain (two batched
-    # MatmulBT calls around the softmax), and between the two.
+    # float64 attention, for the fused kernel (both product modes) and for the unfused
+    # chain (two batched MatmulBT calls around the softmax), and between the two.
     import torch
 
     from aikit_amd import enchip
+
+    ctx.set_attention_products(enchip.ATT_F32 if products == "f32" else enchip.ATT_SPLIT_BF16)
 
     D = H * hd
     g = workloads.rng(700 + S * L + H + hd)
     qkv = g.standard_normal((S, L, 3 * D)).astype(np.float32)
     scale = np.float32(1.0 / np.sqrt(hd))
-    say(f"fused attention S={S} L={L} H={H} hd={hd}")
+    say(f"fused attention S={S} L={L} H={H} hd={hd} products {products}")
     dq = torch.from_numpy(qkv).cuda()
     fused = torch.full((S * L, D), np.nan, device="cuda")
     unfused = torch.full((S * L, D), np.nan, device="cuda")
@@ -193,6 +196,51 @@ def test_fused_attention_matches_f64_and_unfused(ctx, S, L, H, hd):
     # and the CPU restatement of the reference's attention for the first sequence
     ref = oracle.attention(qkv[0, :, :D], qkv[0, :, D:2 * D], qkv[0, :, 2 * D:], L, D, H)
     assert oracle.matmul_bt_worst_rel(f[0], ref) <= 2e-4
+    ctx.set_attention_products(enchip.ATT_SPLIT_BF16)  # the default
+
+
+def test_split_bf16_attention_error_is_bounded_by_the_split(ctx):
+    # The split-bfloat16 products against the f64 attention on inputs of larger and mixed
+    # magnitude (V spanning 6 decades), each output's error measured against the scale of
+    # its terms, sum_j P_j |V_j|, rather than max(|ref|, 1): bf16 alone (2^-9 per product)
+    # or a dropped or mis-signed lo part fails 2e-4 there; the 3-product split (3 * 2^-18
+    # per product, also through the scores into the softmax) passes.
+    import torch
+
+    from aikit_amd import enchip
+
+    S, L, H, hd = 2, 200, 3, 64
+    D = H * hd
+    g = workloads.rng(7070)
+    qkv = g.standard_normal((S, L, 3 * D)).astype(np.float32)
+    qkv[..., :2 * D] *= 1.5
+    qkv[..., 2 * D:] *= np.float32(10.0) ** g.integers(-3, 3, size=(S, L, D))
+    scale = np.float32(1.0 / np.sqrt(hd))
+    dq = torch.from_numpy(qkv).cuda()
+    out = torch.full((S * L, D), np.nan, device="cuda")
+    torch.cuda.synchronize()
+    q = dq.data_ptr()
+    try:
+        ctx.set_attention_products(enchip.ATT_SPLIT_BF16)
+        ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, out.data_ptr(), D, S, L, H, hd, float(scale))
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_attention_products(enchip.ATT_SPLIT_BF16)  # the default
+    got = out.cpu().numpy().reshape(S, L, D).astype(np.float64)
+    want = _attention_f64(qkv, S, L, H, hd, scale)
+    # |ctx| <= sum_j P_j |V_j|: the scale of the P.V sum's terms per output
+    x = qkv.astype(np.float64)
+    mag = np.empty_like(want)
+    for s in range(S):
+        for h in range(H):
+            sl = slice(h * hd, (h + 1) * hd)
+            sc = (x[s, :, sl] @ x[s, :, D:2 * D][:, sl].T) * float(scale)
+            p = np.exp(sc - sc.max(axis=1, keepdims=True))
+            p /= p.sum(axis=1, keepdims=True)
+            mag[s, :, sl] = p @ np.abs(x[s, :, 2 * D:][:, sl])
+    err = np.abs(got - want) / mag
+    say(f"  split-bf16 attention: worst error / sum|terms| {err.max():.3g}")
+    assert err.max() <= 2e-4
 
 
 def test_fused_attention_rejects_unsupported(ctx):

@@ -1076,15 +1076,22 @@ int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, in
                 int64_t ldi, float *score, int64_t lds, hipStream_t s) {
     using namespace enchip;
     if (rows == 0 || k == 0) return ENCHIP_OK;
-    const int64_t nchunks = std::max<int64_t>(1, (n + TOPK_CHUNK - 1) / TOPK_CHUNK);
+    if (n == 0) {  // no candidates: the merge pads every row (-1, NaN)
+        hipLaunchKernelGGL(topk_empty, dim3((unsigned)std::min<int64_t>(rows, 65535)), dim3(256), 0, s, rows, (int)k,
+                           index, ldi, score, lds);
+        return check_launch(c, "topk");
+    }
+    const bool wide = k <= TOPK_SMALL_K;
+    const int64_t chunk = wide ? TOPK_WCHUNK : TOPK_CHUNK;
+    const int64_t nchunks = std::max<int64_t>(1, (n + chunk - 1) / chunk);
     int rc;
     if ((rc = ensure(c, &c->d_cand, &c->cand_cap, (size_t)(rows * nchunks * k) * sizeof(uint64_t)))) return rc;
     int kp = 1;
     while (kp < k) kp <<= 1;
     for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
         const int64_t nr = std::min<int64_t>(65535, rows - r0);
-        hipLaunchKernelGGL(topk_chunk, dim3((unsigned)nchunks, (unsigned)nr), dim3(256), 0, s, scores + r0 * ld, ld, n,
-                           (int)k, (int)nchunks, c->d_cand + r0 * nchunks * k);
+        hipLaunchKernelGGL(wide ? topk_chunk_wide : topk_chunk, dim3((unsigned)nchunks, (unsigned)nr), dim3(256), 0, s,
+                           scores + r0 * ld, ld, n, (int)k, (int)nchunks, c->d_cand + r0 * nchunks * k);
     }
     for (int64_t r0 = 0; r0 < rows; r0 += 0x7fffffff) {
         const int64_t nr = std::min<int64_t>(0x7fffffff, rows - r0);

@@ -17,6 +17,8 @@
 //     bound from the per-thread maxima and maxima of the few keys above it (top_small_k),
 //     otherwise by a radix select over the keys held in registers (8 bits a pass, LDS
 //     histogram).
+//   (for k <= 32, topk_chunk_wide: the same selection over 8192-score chunks, compared
+//     as floats, half the per-chunk selection work per score.)
 //   topk_merge: one workgroup per row selects the k largest of the row's candidates the
 //     same way (maxima in registers when k <= 32 and there are at most 4096 candidates,
 //     else a radix select over them in memory and a bitonic sort in LDS) and writes
@@ -34,11 +36,20 @@ namespace enchip {
 constexpr int TOPK_CHUNK = 4096;  // scores per stage-1 workgroup
 constexpr int TOPK_MAX_K = 1024;  // largest k (the merge sorts it in LDS)
 
+// The key's high half from a score's bits: unsigned order, 0 for NaN (never retained),
+// -0 taken as +0.
+__device__ __forceinline__ uint32_t topk_order_bits(uint32_t u) {
+    const uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return 0;  // NaN
+    if (a == 0) return 0x80000000u;   // +-0
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint32_t topk_order(float s) { return topk_order_bits(__float_as_uint(s)); }
+
 __device__ __forceinline__ uint64_t topk_key(float s, int64_t index) {
-    if (s != s) return 0;  // NaN: never retained
-    uint32_t u = __float_as_uint(s == 0.0f ? 0.0f : s);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)index);
+    const uint32_t u = topk_order(s);
+    return u ? ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)index) : 0;
 }
 
 __device__ __forceinline__ int64_t topk_index(uint64_t key) { return (int64_t)(0xffffffffu - (uint32_t)key); }
@@ -226,10 +237,18 @@ __global__ __launch_bounds__(256) void topk_chunk(const float *__restrict__ scor
     const int64_t row = blockIdx.y, base = (int64_t)blockIdx.x * TOPK_CHUNK;
     const float *p = scores + row * ld;
     uint64_t key[EPT];
+    {
+        // unconditional (clamped) loads, all in flight before the first is used (n > 0
+        // whenever a chunk is launched)
+        const int64_t last = n - 1;
+        float x[EPT];
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-        const int64_t i = base + threadIdx.x + 256 * j;  // coalesced
-        key[j] = i < n ? topk_key(p[i], i) : 0;
+        for (int j = 0; j < EPT; ++j) x[j] = p[min(base + threadIdx.x + 256 * j, last)];  // coalesced
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            const int64_t i = base + threadIdx.x + 256 * j;
+            key[j] = i <= last ? topk_key(x[j], i) : 0;
+        }
     }
     uint64_t *out = cand + (row * nchunks + blockIdx.x) * (int64_t)k;
     if (k <= TOPK_SMALL_K) {
@@ -246,6 +265,118 @@ __global__ __launch_bounds__(256) void topk_chunk(const float *__restrict__ scor
     for (int i = (int)fill + threadIdx.x; i < k; i += 256) out[i] = 0;
 }
 
+// Stage 1 for k <= TOPK_SMALL_K: one workgroup per (row, TOPK_WCHUNK-score chunk), each
+// thread holding 32 scores (the index is implicit in the position) and comparing them as
+// floats, so a workgroup covers 2x the scores of topk_chunk for the same selection work
+// (the k-round selections are the serial part, once per chunk) and only the keys it keeps
+// are built. Same output contract as
+// topk_chunk: the chunk's k largest keys, in descending order, 0-padded.
+//   1. each thread's largest key (ties to the lowest index: strict >, ascending positions);
+//   2. wavefront 0: T = the k-th largest of the 256 thread maxima (1 when fewer than k
+//      are nonzero); every one of the chunk's k largest keys is >= T;
+//   3. threads whose maximum is >= T (at most k) gather their keys >= T in LDS;
+//   4. wavefront 0 takes the maximum of the gathered keys k times.
+constexpr int TOPK_WCHUNK = 8192;
+
+__global__ __launch_bounds__(256) void topk_chunk_wide(const float *__restrict__ scores, int64_t ld, int64_t n, int k,
+                                                       int nchunks, uint64_t *__restrict__ cand) {
+    constexpr int EPT = TOPK_WCHUNK / 256;
+    __shared__ uint64_t maxima[256];
+    __shared__ uint64_t gathered[TOPK_SMALL_K * EPT];  // <= k threads x EPT keys
+    __shared__ uint64_t thresh;
+    __shared__ unsigned count;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t row = blockIdx.y, base = (int64_t)blockIdx.x * TOPK_WCHUNK;
+    const float *p = scores + row * ld + base;
+    // last valid position of the chunk (n > 0 whenever a chunk is launched); the loads are
+    // unconditional (clamped), so all of them are in flight before the first is used
+    const int last = (int)(n - base < TOPK_WCHUNK ? n - base : TOPK_WCHUNK) - 1;
+    float x[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) x[j] = p[min(tid + 256 * j, last)];  // coalesced
+    // The comparisons below run on the floats themselves, which order exactly as the keys'
+    // high halves do: a NaN compares false (never retained), -0 == +0, and a strict > over
+    // ascending positions keeps the lowest index among equal scores.
+    float bf = -INFINITY;
+    int bj = -1;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const bool up = tid + 256 * j <= last && (x[j] > bf || (bj < 0 && x[j] == bf));  // -inf is a score
+        bf = up ? x[j] : bf;
+        bj = up ? j : bj;
+    }
+    auto lo_at = [&](int j) { return 0xffffffffu - (uint32_t)(base + tid + 256 * j); };
+    const uint64_t tmax = bj >= 0 ? ((uint64_t)topk_order(bf) << 32) | lo_at(bj) : 0;
+    maxima[tid] = tmax;
+    if (tid == 0) count = 0;
+    __syncthreads();
+    if (wave == 0) {
+        uint64_t v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = maxima[4 * lane + i];
+        uint64_t t = 1;
+        for (int r = 0; r < k; ++r) {
+            uint64_t mx = v[0];
+#pragma unroll
+            for (int i = 1; i < 4; ++i) mx = v[i] > mx ? v[i] : mx;
+            mx = wave_max_u64(mx);
+            if (mx == 0) {  // fewer than k nonzero maxima: every nonzero key is gathered
+                t = 1;
+                break;
+            }
+            t = mx;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = v[i] == mx ? 0 : v[i];
+        }
+        if (lane == 0) thresh = t;
+    }
+    __syncthreads();
+    const uint64_t t = thresh;
+    if (tmax >= t && tmax != 0) {
+        // key >= t: score above t's, or equal and index low half (0xffffffff - index) at
+        // least t's; t == 1 takes every non-NaN score
+        const bool every = t == 1;
+        const uint32_t th = (uint32_t)(t >> 32), tl = (uint32_t)t;
+        const float tf = __uint_as_float((th & 0x80000000u) ? (th & 0x7fffffffu) : ~th);  // th's score
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            const uint32_t lo = lo_at(j);
+            const bool in = tid + 256 * j <= last && (every ? x[j] == x[j] : (x[j] > tf || (x[j] == tf && lo >= tl)));
+            if (in) gathered[atomicAdd(&count, 1u)] = ((uint64_t)topk_order(x[j]) << 32) | lo;
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    uint64_t *out = cand + (row * nchunks + blockIdx.x) * (int64_t)k;
+    const int c = (int)count;
+    if (c <= 64) {
+        uint64_t v = lane < c ? gathered[lane] : 0;
+        for (int r = 0; r < k; ++r) {
+            const uint64_t mx = wave_max_u64(v);
+            if (lane == 0) out[r] = mx;
+            v = v == mx ? 0 : v;
+        }
+        return;
+    }
+    for (int r = 0; r < k; ++r) {
+        uint64_t best = 0;
+        int at = -1;
+        for (int i = lane; i < c; i += 64) {
+            const uint64_t kk = gathered[i];
+            if (kk > best) {
+                best = kk;
+                at = i;
+            }
+        }
+        const uint64_t mx = wave_max_u64(best);
+        if (lane == 0) out[r] = mx;
+        if (mx != 0 && best == mx) gathered[at] = 0;  // keys are unique: one lane
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
 // radix_threshold over m keys in device memory (read once per pass; the merge's
 // candidates stay in L2), same contract.
 __device__ uint64_t radix_threshold_mem(const uint64_t *__restrict__ c, int64_t m, int want, unsigned *hist,
@@ -253,8 +384,19 @@ __device__ uint64_t radix_threshold_mem(const uint64_t *__restrict__ c, int64_t 
     const int tid = threadIdx.x, lane = tid & 63;
     if (tid == 0) hist[0] = 0;
     __syncthreads();
+    // every pass reads the m keys 8 per thread at a time (clamped loads, all in flight)
+    auto sweep = [&](auto &&visit) {
+        for (int64_t i0 = tid; i0 < m; i0 += 256 * 8) {
+            uint64_t kk[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) kk[u] = c[min(i0 + 256 * u, m - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (i0 + 256 * u < m) visit(kk[u]);
+        }
+    };
     unsigned mine = 0;
-    for (int64_t i = tid; i < m; i += 256) mine += c[i] != 0;
+    sweep([&](uint64_t kk) { mine += kk != 0; });
     atomicAdd(&hist[0], mine);
     __syncthreads();
     const int64_t valid = hist[0];
@@ -265,10 +407,9 @@ __device__ uint64_t radix_threshold_mem(const uint64_t *__restrict__ c, int64_t 
     for (int shift = 56; shift >= 0; shift -= 8) {
         hist[tid] = 0;
         __syncthreads();
-        for (int64_t i = tid; i < m; i += 256) {
-            const uint64_t kk = c[i];
+        sweep([&](uint64_t kk) {
             if (kk != 0 && (kk & mask) == prefix) atomicAdd(&hist[(kk >> shift) & 255u], 1u);
-        }
+        });
         __syncthreads();
         if (tid < 64) {
             unsigned cnt[4], sum = 0;
@@ -346,9 +487,13 @@ __global__ __launch_bounds__(256) void topk_merge(const uint64_t *__restrict__ c
     for (int i = threadIdx.x; i < kp; i += 256) sorted[i] = 0;
     if (threadIdx.x == 0) fill = 0;
     __syncthreads();
-    for (int64_t i = threadIdx.x; i < m; i += 256) {
-        const uint64_t kk = c[i];
-        if (kk != 0 && kk >= th) sorted[atomicAdd(&fill, 1u)] = kk;  // at most k of them
+    for (int64_t i0 = threadIdx.x; i0 < m; i0 += 256 * 8) {
+        uint64_t kk[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) kk[u] = c[min(i0 + 256 * u, m - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (i0 + 256 * u < m && kk[u] != 0 && kk[u] >= th) sorted[atomicAdd(&fill, 1u)] = kk[u];  // at most k
     }
     __syncthreads();
     // bitonic sort of kp keys, descending (the zero padding sinks to the end)
@@ -373,6 +518,17 @@ __global__ __launch_bounds__(256) void topk_merge(const uint64_t *__restrict__ c
         index[row * ldi + i] = (int32_t)col;
         score[row * lds_ + i] = kk ? scores[row * ld + col] : __uint_as_float(0x7fc00000u);
     }
+}
+
+// Rows of zero scores (n == 0): index -1 and a NaN score in each of the k slots, as the
+// merge pads. Grid-stride over rows.
+__global__ __launch_bounds__(256) void topk_empty(int64_t rows, int k, int32_t *__restrict__ index, int64_t ldi,
+                                                  float *__restrict__ score, int64_t lds_) {
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x)
+        for (int i = threadIdx.x; i < k; i += 256) {
+            index[row * ldi + i] = -1;
+            score[row * lds_ + i] = __uint_as_float(0x7fc00000u);
+        }
 }
 
 }  // namespace enchip

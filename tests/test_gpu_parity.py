@@ -563,7 +563,8 @@ def _check_topk(hi, hs, scores, k, what):
 
 
 @pytest.mark.parametrize("rows,n,k", [(3, 10000, 10), (2, 4096, 1024), (5, 1000, 1000), (1, 1, 5), (4, 50000, 100),
-                                      (2, 8193, 7), (1, 300000, 64)])
+                                      (2, 8193, 7), (1, 300000, 64), (2, 0, 5), (3, 70000, 32), (2, 16384, 10),
+                                      (1, 16385, 1), (2, 40000, 33)])
 def test_topk_rows_matches_reference_selection(ctx, rows, n, k):
     # FlatI8.topHits' order (score desc, index asc; NaN skipped) on scores full of ties
     # (a coarse grid), signed zeros and NaNs, across chunk boundaries.
@@ -574,6 +575,28 @@ def test_topk_rows_matches_reference_selection(ctx, rows, n, k):
     s[g.random((rows, n)) < 0.02] = np.nan
     s[g.random((rows, n)) < 0.02] = -0.0
     say(f"topk rows={rows} n={n} k={k}")
+    ds = torch.from_numpy(s).cuda()
+    di = torch.empty((rows, k), dtype=torch.int32, device="cuda")
+    dv = torch.empty((rows, k), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.topk_rows_dev(ds.data_ptr(), n, rows, n, k, di.data_ptr(), k, dv.data_ptr(), k)
+    torch.cuda.synchronize()
+    _check_topk(di.cpu().numpy(), dv.cpu().numpy(), s, k, "topk")
+
+
+@pytest.mark.parametrize("k", [1, 10, 32])
+def test_topk_rows_concentrated_winners(ctx, k):
+    # Every large score sits at positions one thread of a chunk holds (index = 5 mod 256),
+    # so that thread's maximum alone clears the bound and its 64 keys (more than a
+    # wavefront) are gathered for the final selection; ties among them break by index.
+    import torch
+
+    rows, n = 2, 50000
+    g = workloads.rng(900 + k)
+    s = (g.standard_normal((rows, n)) * 0.01).astype(np.float32)
+    hot = np.arange(5, n, 256)
+    s[:, hot] = (10 + g.integers(0, 3, size=(rows, hot.size))).astype(np.float32)
+    say(f"topk concentrated rows={rows} n={n} k={k}")
     ds = torch.from_numpy(s).cuda()
     di = torch.empty((rows, k), dtype=torch.int32, device="cuda")
     dv = torch.empty((rows, k), dtype=torch.float32, device="cuda")

@@ -123,9 +123,25 @@ __device__ uint64_t radix_threshold(const uint64_t (&key)[EPT], int want, unsign
 
 constexpr int TOPK_SMALL_K = 32;  // up to this k, selection by repeated maxima
 
+// v and the value of the lane a DPP pattern names (every lane has a source lane), larger.
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xf, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, false);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    return o > v ? o : v;
+}
+
+// Maximum over the wavefront, in every lane: within each row of 16 lanes by DPP moves
+// (lane ^ 1, lane ^ 2, the half-row mirror, the row mirror: a few cycles each), then
+// across rows by two lane permutes.
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    v = dpp_max_u64<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_max_u64<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = dpp_max_u64<0x141>(v);  // row_half_mirror: groups of 8
+    v = dpp_max_u64<0x140>(v);  // row_mirror: groups of 16
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
+    for (int off = 16; off < 64; off <<= 1) {
         const uint32_t lo = __shfl_xor((uint32_t)v, off, 64), hi = __shfl_xor((uint32_t)(v >> 32), off, 64);
         const uint64_t o = ((uint64_t)hi << 32) | lo;
         v = o > v ? o : v;

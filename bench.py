@@ -30,6 +30,7 @@ METRIC = "W8A8 encode seqs/sec (BERT-base b64×s512) + int8 GEMM TOPS as % of pe
 PEAK_INT8_OPS = 5.0e15  # MI355X dense int8 MFMA (no sparsity)
 PEAK_HBM_BPS = 8.0e12  # MI355X HBM3E
 PEAK_FP32_FLOPS = 157.3e12  # MI355X dense fp32 MFMA
+PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA
 
 
 TRAFFIC_PROFILE = "profiles/bert_base_b64s512_hbm_traffic.md"
@@ -190,7 +191,7 @@ def other_configs(ctx, torch, stream, ceilings):
     """
     import numpy as np
 
-    from aikit_amd import workloads
+    from aikit_amd import enchip, workloads
 
     out = {}
     c2 = workloads.LINEAR_CFG2
@@ -384,24 +385,34 @@ def other_configs(ctx, torch, stream, ceilings):
         att[f"{name}_tflops"] = flops / t / 1e12
         att[f"{name}_frac_fp32_mfma_peak"] = flops / t / PEAK_FP32_FLOPS
         att[f"{name}_hbm_gbps"] = nbytes / t / 1e9
-    # the fused form: both products and the softmax in one launch, scores kept on chip
-    for _ in range(3):
-        ctx.attention_f32_dev(base, base + D * 4, base + 2 * D * 4, 3 * D, ctxv.data_ptr(), D, S, L, H, hd, 0.125, sp)
-    e0.record(stream)
-    for _ in range(10):
-        ctx.attention_f32_dev(base, base + D * 4, base + 2 * D * 4, 3 * D, ctxv.data_ptr(), D, S, L, H, hd, 0.125, sp)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    t = e0.elapsed_time(e1) * 1e-3 / 10
-    att["fused_us"] = t * 1e6
-    att["fused_tflops"] = 2 * flops / t / 1e12
-    att["fused_frac_fp32_mfma_peak"] = 2 * flops / t / PEAK_FP32_FLOPS
+    # the fused form: both products and the softmax in one launch, scores kept on chip, with
+    # its products on the f32 MFMA and (the default) on the bf16 MFMA over split operands
+    for mode, tag in ((enchip.ATT_F32, "fused_f32"), (enchip.ATT_SPLIT_BF16, "fused_split_bf16")):
+        ctx.set_attention_products(mode)
+        for _ in range(3):
+            ctx.attention_f32_dev(base, base + D * 4, base + 2 * D * 4, 3 * D, ctxv.data_ptr(), D, S, L, H, hd, 0.125,
+                                  sp)
+        e0.record(stream)
+        for _ in range(10):
+            ctx.attention_f32_dev(base, base + D * 4, base + 2 * D * 4, 3 * D, ctxv.data_ptr(), D, S, L, H, hd, 0.125,
+                                  sp)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / 10
+        att[f"{tag}_us"] = t * 1e6
+        att[f"{tag}_tflops_f32_equivalent"] = 2 * flops / t / 1e12
+        if mode == enchip.ATT_F32:
+            att[f"{tag}_frac_fp32_mfma_peak"] = 2 * flops / t / PEAK_FP32_FLOPS
+        else:  # three bf16 products per f32 product
+            att[f"{tag}_frac_bf16_mfma_peak"] = 3 * 2 * flops / t / PEAK_BF16_FLOPS
+    ctx.set_attention_products(enchip.ATT_SPLIT_BF16)
     att.update({"S": S, "L": L, "heads": H, "head_dim": hd, "gflop_per_product": flops / 1e9,
                 "kernels": "enchip::gemm_f32_bt_lds<2, 2, false> (QK^T), enchip::gemm_f32_bt_lds<4, 1, true> (PV), "
-                           "enchip::attention_f32<64> (fused: QK^T, softmax, PV with the scores in LDS)",
-                "note": "one config-4 layer's attention products in f32 (v_mfma_f32_32x32x2_f32), all 768 "
-                        "(sequence, head) problems per launch, operands resident; bytes = operands read once + "
-                        "output written once; softmax not included in qk/pv, included in fused"})
+                           "enchip::attention_f32<64> (fused, f32 MFMA), enchip::attention_split_bf16<64, true> "
+                           "(fused, split-bf16 MFMA: the default)",
+                "note": "one config-4 layer's attention products (qk, pv: f32 MatmulBT on v_mfma_f32_32x32x2_f32), all "
+                        "768 (sequence, head) problems per launch, operands resident; bytes = operands read once + "
+                        "output written once; softmax not included in qk/pv, included in the fused forms"})
     out["attention_f32_cfg4_layer"] = att
     del qkv, scores, ctxv
     return out

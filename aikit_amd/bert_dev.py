@@ -23,8 +23,10 @@ and pools with enchip_pool_mean_l2_dev (encoder/pooling.go:84-105, embed/pool.go
 or, as a cross-encoder, scores each sequence with classifier(tanh(pooler(CLS)))
 (encoder/crossencoder.go:219-238): the f32 MatmulBT on the CLS rows read in place, then
 enchip_bias_act_rows_dev for the bias + TanhF32 and the classifier's bias.
-The embedding lookup and its LayerNorm (bert.go:299-323) stay with the caller: the input
-is the [S*L, D] f32 hidden state after them. Every sequence of a batch has the same L.
+forward() takes the [S*L, D] f32 hidden state after the embedding LayerNorm; embeddings()
+computes that state on the device from token ids (bert.go:299-323: enchip_embed_rows_dev,
+then enchip_residual_layer_norm_dev with no residual). Every sequence of a batch has the
+same L.
 
 This module holds no arithmetic of its own; torch provides device buffers and the stream.
 """
@@ -70,6 +72,38 @@ class DeviceBert:
                                torch.from_numpy(np.ascontiguousarray(s)).to(dev))
             self.handles.append(entry)
         self._bufs = {}
+        self._emb = None
+
+    def set_embeddings(self, word, pos, ln, typ=None, pos_off: int = 0) -> None:
+        """The embedding tables: word [vocab, D], pos [npos, D], optional token types
+        [type_vocab, D], the embedding LayerNorm (gain [D], shift [D]), as numpy arrays
+        (uploaded) or f32 device tensors; pos_off is the position-id offset (0 for BERT,
+        pad_token_id + 1 for RoBERTa / XLM-R)."""
+        t, dev = self.torch, self.torch.device("cuda")
+
+        def up(a):  # numpy arrays are uploaded; f32 device tensors are used as they are
+            if isinstance(a, t.Tensor):
+                if a.device.type != "cuda" or a.dtype != t.float32 or not a.is_contiguous():
+                    raise ValueError("set_embeddings: tensors must be contiguous f32 on the device")
+                return a
+            return t.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
+
+        self._emb = dict(word=up(word), pos=up(pos), type=None if typ is None else up(typ),
+                         ln=(up(ln[0]), up(ln[1])), pos_off=int(pos_off))
+
+    def embeddings(self, ids, S: int, L: int, h, segs=None, stream: int = 0) -> None:
+        """h [S*L, D] = LayerNorm(word[id] + pos[i + pos_off] (+ type[seg])) for int32 device ids
+        [S*L] (and optional int32 segment ids), bert.go:299-323."""
+        e, D = self._emb, self.D
+        if e is None:
+            raise ValueError("embeddings: call set_embeddings first")
+        typ = e["type"]
+        self.ctx.embed_rows_dev(ids.data_ptr(), 0 if segs is None else segs.data_ptr(), S, L, e["word"].data_ptr(),
+                                e["word"].shape[0], e["pos"].data_ptr(), e["pos"].shape[0], e["pos_off"],
+                                0 if typ is None else typ.data_ptr(), 0 if typ is None else typ.shape[0], D,
+                                h.data_ptr(), D, stream)
+        g, b = e["ln"]
+        self.ctx.residual_layer_norm_dev(h.data_ptr(), D, 0, D, S * L, D, g.data_ptr(), b.data_ptr(), LN_EPS, stream)
 
     def close(self) -> None:
         for entry in self.handles:

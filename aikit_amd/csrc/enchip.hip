@@ -1151,6 +1151,32 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int6
     return ENCHIP_OK;
 }
 
+int enchip_embed_rows_dev(enchip_ctx *ctx, const int32_t *d_ids, const int32_t *d_segs, int64_t nseq, int64_t L,
+                          const float *d_word, int64_t vocab, const float *d_pos, int64_t npos, int64_t pos_off,
+                          const float *d_type, int64_t type_vocab, int64_t D, float *d_h, int64_t ldh,
+                          void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (nseq < 0 || L < 0 || D <= 0 || ldh < D || vocab <= 0 || pos_off < 0 || type_vocab < 0 ||
+        L + pos_off > npos || nseq * L > ((int64_t)1 << 31) || D > ((int64_t)1 << 20))
+        return fail(ctx, ENCHIP_ERR_ARG,
+                    "embed: bad shape nseq=%lld L=%lld D=%lld ldh=%lld vocab=%lld npos=%lld pos_off=%lld "
+                    "type_vocab=%lld (positions L + pos_off must be < npos rows)",
+                    (long long)nseq, (long long)L, (long long)D, (long long)ldh, (long long)vocab, (long long)npos,
+                    (long long)pos_off, (long long)type_vocab);
+    if (nseq == 0 || L == 0) return ENCHIP_OK;
+    if (!d_ids || !d_word || !d_pos || !d_h || (type_vocab > 0 && !d_type))
+        return fail(ctx, ENCHIP_ERR_ARG, "embed: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    const int64_t rows = nseq * L, n = rows * D;
+    const int64_t blocks = (n + 255) / 256;
+    if (blocks > 0x7fffffff) return fail(ctx, ENCHIP_ERR_ARG, "embed: too many elements");
+    hipLaunchKernelGGL(enchip::embed_rows, dim3((unsigned)blocks), dim3(256), 0, s, d_ids, d_segs, rows, (int)L, d_word,
+                       vocab, d_pos, (int)pos_off, d_type, type_vocab, (int)D, d_h, ldh);
+    return check_launch(ctx, "embed_rows");
+}
+
 int enchip_bias_act_rows_dev(enchip_ctx *ctx, float *d_x, int64_t ld, int64_t rows, int64_t cols,
                              const float *d_bias, int act, void *stream) {
     if (!ctx) return ENCHIP_ERR_ARG;

@@ -209,6 +209,32 @@ __global__ __launch_bounds__(256) void bias_act_rows(float *__restrict__ x, int6
     x[r * ld + c] = TANH ? tanh_f32(v) : v;
 }
 
+// BERT's embedding rows (encoder/bert.go:299-322): for token i of each sequence,
+//   h[i] = word[clampTokenID(id)] + pos[i + pos_off]   (f32 adds, column by column)
+//   h[i] += type[seg]   when the model has token types (type_vocab > 0); seg = segs[i], or
+//                       0 without segments, and 0 when out of [0, type_vocab)
+// clampTokenID (encoder/forward.go:15-20) maps an id outside [0, vocab) to 0. One thread
+// per (row, column); the caller checked L + pos_off <= the position table's rows.
+__global__ __launch_bounds__(256) void embed_rows(const int32_t *__restrict__ ids, const int32_t *__restrict__ segs,
+                                                  int64_t rows, int L, const float *__restrict__ word, int64_t vocab,
+                                                  const float *__restrict__ pos, int pos_off,
+                                                  const float *__restrict__ type, int64_t type_vocab, int D,
+                                                  float *__restrict__ h, int64_t ldh) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= rows * D) return;
+    const int64_t r = e / D;
+    const int j = (int)(e % D), i = (int)(r % L);
+    const int32_t id = ids[r];
+    const int64_t w = id < 0 || id >= vocab ? 0 : id;
+    float v = word[w * D + j] + pos[(int64_t)(i + pos_off) * D + j];
+    if (type_vocab > 0) {
+        int32_t seg = segs != nullptr ? segs[r] : 0;
+        if (seg < 0 || seg >= type_vocab) seg = 0;
+        v += type[(int64_t)seg * D + j];
+    }
+    h[r * ldh + j] = v;
+}
+
 // Mean pooling then L2 normalisation of each of nseq sequences of L rows
 // (encoder/pooling.go:84-105 poolOne(mean), embed/pool.go:22-38 L2Normalize) in the
 // reference's summation order, so the result is exact:

@@ -446,9 +446,10 @@ def device_forward(ctx, torch, stream, layers_host, cfg, reps: int = 3, head: st
     fused-QKV / O / FFN W8A8 linears, the f32 attention, two residual + LayerNorm) over one
     batch of cfg.batch x cfg.seq tokens, then the head: "pool" = mean pooling + L2 (config
     4, BERT-base embeddings), "rerank" = the cross-encoder head classifier(tanh(pooler(CLS)))
-    with one label (config 5, XLM-R-large reranking, encoder/crossencoder.go:219-238). The
-    input is the hidden state after the embedding LayerNorm (synthetic N(0,1)); the
-    embedding lookup itself (a gather of one row per token) is not included."""
+    with one label (config 5, XLM-R-large reranking, encoder/crossencoder.go:219-238). Each
+    timed forward starts from token ids (uniform over the vocabulary) already on the device:
+    the embedding rows and their LayerNorm run on the device too (bert.go:299-323; XLM-R's
+    position offset 2). Tables and weights are random-init."""
     import numpy as np
 
     from aikit_amd import enchip, workloads
@@ -467,8 +468,13 @@ def device_forward(ctx, torch, stream, layers_host, cfg, reps: int = 3, head: st
     S, L = cfg.batch, cfg.seq
     sp = stream.cuda_stream
     with torch.cuda.stream(stream):
-        h0 = torch.randn((S * L, D), device="cuda", generator=torch.Generator(device="cuda").manual_seed(5))
-        h = torch.empty_like(h0)
+        gen = torch.Generator(device="cuda").manual_seed(5)
+        rnd = lambda *shape: torch.randn(shape, device="cuda", generator=gen) * 0.02
+        pos_off = 2 if head == "rerank" else 0  # XLM-R: pad_token_id + 1
+        model.set_embeddings(rnd(cfg.vocab, D), rnd(512 + pos_off, D),
+                             (1 + rnd(D), rnd(D)), typ=None if head == "rerank" else rnd(2, D), pos_off=pos_off)
+        ids = torch.randint(0, cfg.vocab, (S * L,), device="cuda", dtype=torch.int32, generator=gen)
+        h = torch.empty((S * L, D), device="cuda")
         if head == "rerank":
             dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
             pooler = (dev(g.standard_normal((D, D)) * 0.02), dev(g.standard_normal(D) * 0.02))
@@ -480,10 +486,9 @@ def device_forward(ctx, torch, stream, layers_host, cfg, reps: int = 3, head: st
     times = []
     try:
         for r in range(reps + 1):  # the first is a warm-up
-            with torch.cuda.stream(stream):
-                h.copy_(h0)
             torch.cuda.synchronize()
             t0 = time.perf_counter()
+            model.embeddings(ids, S, L, h, stream=sp)
             if head == "rerank":
                 model.rerank(h, S, L, pooler, classifier, out, sp)
             else:
@@ -501,8 +506,9 @@ def device_forward(ctx, torch, stream, layers_host, cfg, reps: int = 3, head: st
     return {rate: S / t, "ms_per_batch": t * 1e3, "batch": S, "seq_len": L, "layers": cfg.layers,
             "hidden": D, "output_finite": finite,
             "attention_products": products,
-            "note": "median of %d forwards; W8A8 linears + fused attention (%s MFMA products) + LayerNorm + %s, "
-                    "all on the device, activations resident; embedding lookup excluded" % (reps, products, tail)}
+            "note": "median of %d forwards from token ids; embedding rows + LayerNorm, W8A8 linears, fused "
+                    "attention (%s MFMA products), LayerNorm, %s, all on the device, activations resident"
+                    % (reps, products, tail)}
 
 
 def rerank_device(ctx, torch, stream, reps: int = 2):

@@ -282,6 +282,23 @@ int enchip_residual_layer_norm_dev(enchip_ctx *ctx, float *d_h, int64_t ldh, con
                                    int64_t ldy, int64_t rows, int64_t D, const float *d_w,
                                    const float *d_b, double eps, void *stream);
 
+/* BERT's embedding rows on the device (encoder/bert.go:299-322, before its LayerNorm):
+ * for token i of each of nseq sequences of L tokens (d_ids[z*L + i]),
+ *   h = word[clampTokenID(id)] + pos[i + pos_off]   then, when type_vocab > 0,
+ *   h += type[seg], seg = d_segs[z*L + i] (0 when d_segs is NULL or seg is outside
+ *   [0, type_vocab)),
+ * f32 adds column by column in that order, so the rows are bit-identical to the
+ * reference's. clampTokenID (encoder/forward.go:15-20): an id outside [0, vocab) reads
+ * row 0. Tables are row-major [rows][D]; pos has npos rows and L + pos_off <= npos
+ * (pos_off 0 for BERT, pad_token_id + 1 for RoBERTa / XLM-R). Row z*L + i goes to
+ * d_h + (z*L + i)*ldh. The embedding LayerNorm is enchip_residual_layer_norm_dev with
+ * d_y = NULL. */
+int enchip_embed_rows_dev(enchip_ctx *ctx, const int32_t *d_ids, const int32_t *d_segs,
+                          int64_t nseq, int64_t L, const float *d_word, int64_t vocab,
+                          const float *d_pos, int64_t npos, int64_t pos_off,
+                          const float *d_type, int64_t type_vocab, int64_t D, float *d_h,
+                          int64_t ldh, void *stream);
+
 /* x = act(x + bias) in place on rows x cols (pitch ld; d_bias[cols] may be NULL), act
  * ENCHIP_ACT_NONE or ENCHIP_ACT_TANH (linalg.TanhF32, linalg/exp.go:319-337, with
  * linalg.ExpF32's guards): the cross-encoder head's addBias + TanhInto after the pooler

@@ -256,3 +256,44 @@ def test_config5_shaped_cross_encoder_on_device(ctx, workers):
         cos = float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
         say(f"  pair {s_}: [CLS] cosine {cos:.9f}, logit {got[s_, 0]:.6f} vs {head(ref_cls_rows[s_])[0]:.6f}")
         assert cos >= COS_MIN
+
+
+def test_config1_device_forward_from_token_ids(ctx, workers):
+    # The whole encode on the device from token ids: embedding rows + LayerNorm
+    # (DeviceBert.embeddings), the layers, pooling; against the CPU reference composition
+    # from the same ids (encode), to the north star's cosine.
+    import torch
+
+    from aikit_amd.bert_dev import DeviceBert
+
+    cfg = workloads.MINILM_L6
+    g = workloads.rng(12)
+    seqs = [g.integers(1000, 30000, size=cfg.seq) for _ in range(cfg.batch)]
+    w = model_weights(cfg, seed=102)
+
+    def ref_linear(x, li, name):
+        wq, ws, b, act = w["layers"][li][name]
+        M, K = x.shape
+        return oracle.cpu_w8a8_linear(x, wq, ws, b, act, M, K, wq.shape[0], workers=workers).reshape(M, -1)
+
+    S, L, D = cfg.batch, cfg.seq, cfg.hidden
+    model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn)
+    try:
+        model.set_embeddings(w["word"], w["pos"], w["emb_ln"], typ=w["type"])
+        say(f"{cfg.name} device forward from token ids, {S} sequences of {L}")
+        ids = torch.from_numpy(np.concatenate(seqs).astype(np.int32)).cuda()
+        h = torch.empty((S * L, D), device="cuda")
+        pooled = torch.empty((S, D), device="cuda")
+        torch.cuda.synchronize()
+        model.embeddings(ids, S, L, h)
+        model.embed(h, S, L, pooled)
+        torch.cuda.synchronize()
+        dev = pooled.cpu().numpy()
+    finally:
+        model.close()
+    for s_, ids_ in enumerate(seqs):
+        ref = encode(ids_, w, cfg, ref_linear).astype(np.float64)
+        d = dev[s_].astype(np.float64)
+        cos = float(ref @ d / (np.linalg.norm(ref) * np.linalg.norm(d)))
+        say(f"  seq {s_}: cosine {cos:.9f}")
+        assert cos >= COS_MIN

@@ -278,3 +278,52 @@ def test_bias_tanh_matches_oracle(ctx):
     got = dx.cpu().numpy()
     assert np.array_equal(np.isnan(got), np.isnan(want))
     assert np.array_equal(got[~np.isnan(want)].view(np.uint32), want[~np.isnan(want)].view(np.uint32))
+
+
+@pytest.mark.parametrize("type_vocab,pos_off,with_segs", [(2, 0, False), (2, 2, True), (0, 2, False)])
+def test_embed_rows_bit_exact(ctx, type_vocab, pos_off, with_segs):
+    # encoder/bert.go:299-322: word[clampTokenID(id)] + pos[i + posOff] (+ type[seg]),
+    # f32 adds in that order; ids outside the vocabulary read row 0 (forward.go:15-20),
+    # segments outside [0, type_vocab) read type row 0.
+    import torch
+
+    g = workloads.rng(4040 + type_vocab + pos_off)
+    S, L, D, vocab, npos = 3, 37, 96, 500, 64
+    word = g.standard_normal((vocab, D)).astype(np.float32)
+    pos = g.standard_normal((npos, D)).astype(np.float32)
+    typ = g.standard_normal((max(type_vocab, 1), D)).astype(np.float32)
+    ids = g.integers(-5, vocab + 5, size=S * L).astype(np.int32)
+    ids[:4] = [-1, vocab, 0, vocab - 1]
+    segs = g.integers(-1, 4, size=S * L).astype(np.int32)
+    want = np.empty((S * L, D), np.float32)
+    for r in range(S * L):
+        i, t = r % L, ids[r]
+        w = word[t if 0 <= t < vocab else 0]
+        row = (w + pos[i + pos_off]).astype(np.float32)
+        if type_vocab > 0:
+            sg = segs[r] if with_segs else 0
+            row = (row + typ[sg if 0 <= sg < type_vocab else 0]).astype(np.float32)
+        want[r] = row
+    dv = {k: torch.from_numpy(v).cuda() for k, v in dict(word=word, pos=pos, typ=typ, ids=ids, segs=segs).items()}
+    h = torch.full((S * L, D + 8), np.nan, device="cuda")
+    torch.cuda.synchronize()
+    ctx.embed_rows_dev(dv["ids"].data_ptr(), dv["segs"].data_ptr() if with_segs else 0, S, L, dv["word"].data_ptr(),
+                       vocab, dv["pos"].data_ptr(), npos, pos_off, dv["typ"].data_ptr() if type_vocab else 0,
+                       type_vocab, D, h.data_ptr(), D + 8)
+    torch.cuda.synchronize()
+    got = h.cpu().numpy()
+    assert np.array_equal(got[:, :D].view(np.uint32), want.view(np.uint32))
+    assert np.isnan(got[:, D:]).all()  # the pitch's padding untouched
+
+
+def test_embed_rows_rejects_positions_past_the_table(ctx):
+    import torch
+
+    from aikit_amd import enchip
+
+    d = torch.zeros(4096, device="cuda")
+    ids = torch.zeros(64, dtype=torch.int32, device="cuda")
+    p = d.data_ptr()
+    with pytest.raises(enchip.EnchipError):  # L + pos_off = 34 > 32 position rows
+        ctx.embed_rows_dev(ids.data_ptr(), 0, 1, 32, p, 10, p, 32, 2, 0, 0, 8, p, 8)
+    torch.cuda.synchronize()

@@ -99,19 +99,19 @@ __device__ __forceinline__ float gelu_f32(float x) {
     return 0.5f * x * (1.0f + erf_f32(x * 0.7071067811865476f));
 }
 
-// GELUF32 for the arguments that take ErfF32's |u| < 1 (series) or |u| > 4 (sign)
-// branch, u = x * 0.7071067811865476f, evaluated without branching so that a
-// wavefront never runs both. `tail` is set for the remaining arguments (1 <= |u| <= 4,
-// and NaN), whose value the caller must take from gelu_f32; for them the return value
-// is meaningless.
+// GELUF32 for the arguments that take ErfF32's series branch (|u| < 1, u = x *
+// 0.7071067811865476f), evaluated without branching. `tail` is set for every other
+// argument (|u| >= 1, including ErfF32's |u| > 4 sign branch, and NaN), whose value the
+// caller must take from gelu_f32; for them the return value is meaningless. (Those are
+// rare in an FFN's pre-activations, and the caller handles them apart, so their branches
+// cost nothing here.)
 //
-// Same bits as gelu_f32 on its own branches:
+// Same bits as gelu_f32 on the series branch:
 //   - the series is evaluated on z = u * u, which is |u| * |u|;
 //   - sign * 1.1283791670955126f * |u| is rounded exactly as 1.1283791670955126f * u,
 //     because rounding is symmetric in sign (u = -0.0 gives -0.0 either way).
-__device__ __forceinline__ float gelu_f32_no_tail(float x, bool &tail) {
+__device__ __forceinline__ float gelu_f32_series(float x, bool &tail) {
     const float u = x * 0.7071067811865476f;
-    const float au = fabsf(u);
     const float z = u * u;
     float p = 1.3122532963802806e-08f;
     p = p * z - 1.4503852223150468e-07f;
@@ -124,9 +124,8 @@ __device__ __forceinline__ float gelu_f32_no_tail(float x, bool &tail) {
     p = p * z + 1.0000000000000001e-01f;
     p = p * z - 3.3333333333333331e-01f;
     p = p * z + 1.0f;
-    float e = 1.1283791670955126f * u * p;
-    if (au > 4.0f) e = u < 0.0f ? -1.0f : 1.0f;
-    tail = !(au < 1.0f) && !(au > 4.0f);
+    const float e = 1.1283791670955126f * u * p;
+    tail = !(fabsf(u) < 1.0f);
     return 0.5f * x * (1.0f + e);
 }
 

@@ -269,9 +269,9 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void gemm_w8a8_pt(
             auto row_ok = [&](int k) { return m0 + i * 32 + rsub + RPL * k < M && col < N; };
             int4 v[KR];
             if (EPI == EPI_F32_GELU) {
-                // Pass 1: dequantize and apply GELU's series / sign branches to all 32
-                // of this lane's values, in place in the scratch; remember which need
-                // the erf tail (1 <= |u| <= 4) and leave their dequantized value there.
+                // Pass 1: dequantize and apply GELU's series branch to all 32 of this
+                // lane's values, in place in the scratch; remember which take another
+                // branch (|u| >= 1, or NaN) and leave their dequantized value there.
                 uint32_t tail_mask = 0;
 #pragma unroll
                 for (int k = 0; k < KR; ++k) v[k] = *reinterpret_cast<const int4 *>(&scr[(rsub + RPL * k) * SP + 4 * c4]);
@@ -283,7 +283,7 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void gemm_w8a8_pt(
                     for (int qq = 0; qq < 4; ++qq) {
                         const float y = dequant(vv[qq], asv[k], wsv[qq], bv[qq]);
                         bool tail;
-                        const float gy = gelu_f32_no_tail(y, tail);
+                        const float gy = gelu_f32_series(y, tail);
                         o4[qq] = __float_as_int(tail ? y : gy);
                         tail_mask |= (uint32_t)tail << (4 * k + qq);
                     }

@@ -19,6 +19,11 @@ matmul seam, docs/task-native-gpu.md:418-427):
   ffn   = W8A8(inter, Wd) + b           enchip_w8a8_linear_dev
   h     = LN(h + ffn)                   enchip_residual_layer_norm_dev
 
+When the linear after a LayerNorm (FFN-up, and the next layer's QKV) takes fragment-major
+codes, the LayerNorm and that linear's quantization run as one kernel
+(enchip_residual_layer_norm_quant_dev, then enchip_w8a8_pre_frag_dev): the same bits, and
+the normalised rows are not read back to be quantized.
+
 and pools with enchip_pool_mean_l2_dev (encoder/pooling.go:84-105, embed/pool.go:22-38),
 or, as a cross-encoder, scores each sequence with classifier(tanh(pooler(CLS)))
 (encoder/crossencoder.go:219-238): the f32 MatmulBT on the CLS rows read in place, then
@@ -50,10 +55,11 @@ class DeviceBert:
     """
 
     def __init__(self, ctx: enchip.Context, layers: Sequence[Dict], hidden: int, heads: int, ffn: int,
-                 fused: bool = True):
+                 fused: bool = True, fuse_ln_quant: bool = True):
         import torch
 
         self.fused = fused
+        self.fuse_ln_quant = fuse_ln_quant
         self.torch = torch
         self.ctx, self.D, self.H, self.I = ctx, hidden, heads, ffn
         self.hd = hidden // heads
@@ -121,9 +127,12 @@ class DeviceBert:
             t, M = self.torch, S * L
             f = dict(device="cuda", dtype=t.float32)
             sc = (1,) if self.fused_attention(L) else (S, self.H, L, L)
+            Mp = (M + 127) // 128 * 128  # fragment-major codes are read up to a multiple of 128 rows
             self._bufs = {key: dict(qkv=t.empty((M, 3 * self.D), **f), scores=t.empty(sc, **f),
                                     ctx=t.empty((M, self.D), **f), out=t.empty((M, self.D), **f),
-                                    inter=t.empty((M, self.I), **f), ffn=t.empty((M, self.D), **f))}
+                                    inter=t.empty((M, self.I), **f), ffn=t.empty((M, self.D), **f),
+                                    codes=t.empty(Mp * self.D, device="cuda", dtype=t.int8),
+                                    ascale=t.empty(M, **f))}
         return self._bufs[key]
 
     def forward(self, h, S: int, L: int, stream: int = 0) -> None:
@@ -133,11 +142,33 @@ class DeviceBert:
             raise ValueError(f"h must be a contiguous [{M}, {D}] tensor")
         b = self._buffers(S, L)
         qkv, scores, ctxv, out, inter, ffn = b["qkv"], b["scores"], b["ctx"], b["out"], b["inter"], b["ffn"]
+        codes, ascale = b["codes"].data_ptr(), b["ascale"].data_ptr()
         q = qkv.data_ptr()
         scale = float(np.float32(1.0 / math.sqrt(hd)))  # encoder/attention.go:86
-        for e in self.handles:
+
+        def route(w):  # the padded K when LN + quantization can run fused before w, else 0
+            if not self.fuse_ln_quant:
+                return 0
+            ok, ldq = c.frag_route(w, M)
+            return ldq if ok and ldq <= D else 0
+
+        def ln_then(g, s_, y, nxt):  # h = LN(h + y); codes for weight nxt when it takes them
+            ldq = route(nxt) if nxt is not None else 0
+            if ldq:
+                c.residual_layer_norm_quant_dev(h.data_ptr(), D, y.data_ptr(), D, M, D, g.data_ptr(), s_.data_ptr(),
+                                                LN_EPS, codes, ldq, ascale, stream)
+            else:
+                c.residual_layer_norm_dev(h.data_ptr(), D, y.data_ptr(), D, M, D, g.data_ptr(), s_.data_ptr(), LN_EPS,
+                                          stream)
+            return ldq
+
+        pending = 0  # padded K of codes already quantized for this layer's QKV
+        for li, e in enumerate(self.handles):
             w, bias, act = e["qkv"]
-            c.linear_dev(w, h.data_ptr(), M, bias.data_ptr(), act, q, stream)
+            if pending:
+                c.pre_frag_dev(w, codes, pending, M, ascale, bias.data_ptr(), act, q, stream)
+            else:
+                c.linear_dev(w, h.data_ptr(), M, bias.data_ptr(), act, q, stream)
             if self.fused_attention(L):
                 c.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, ctxv.data_ptr(), D, S, L, H, hd, scale, stream)
             else:
@@ -151,15 +182,17 @@ class DeviceBert:
             w, bias, act = e["o"]
             c.linear_dev(w, ctxv.data_ptr(), M, bias.data_ptr(), act, out.data_ptr(), stream)
             g, s = e["attn_ln"]
-            c.residual_layer_norm_dev(h.data_ptr(), D, out.data_ptr(), D, M, D, g.data_ptr(), s.data_ptr(), LN_EPS,
-                                      stream)
             w, bias, act = e["ffn_up"]
-            c.linear_dev(w, h.data_ptr(), M, bias.data_ptr(), act, inter.data_ptr(), stream)
+            ldq = ln_then(g, s, out, w)
+            if ldq:
+                c.pre_frag_dev(w, codes, ldq, M, ascale, bias.data_ptr(), act, inter.data_ptr(), stream)
+            else:
+                c.linear_dev(w, h.data_ptr(), M, bias.data_ptr(), act, inter.data_ptr(), stream)
             w, bias, act = e["ffn_down"]
             c.linear_dev(w, inter.data_ptr(), M, bias.data_ptr(), act, ffn.data_ptr(), stream)
             g, s = e["out_ln"]
-            c.residual_layer_norm_dev(h.data_ptr(), D, ffn.data_ptr(), D, M, D, g.data_ptr(), s.data_ptr(), LN_EPS,
-                                      stream)
+            nxt = self.handles[li + 1]["qkv"][0] if li + 1 < len(self.handles) else None
+            pending = ln_then(g, s, ffn, nxt)
 
     def embed(self, h, S: int, L: int, pooled, stream: int = 0) -> None:
         """forward(), then mean pooling + L2 normalisation of each sequence into pooled [S, D]."""

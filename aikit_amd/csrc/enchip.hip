@@ -998,6 +998,37 @@ int enchip_residual_layer_norm_dev(enchip_ctx *ctx, float *d_h, int64_t ldh, con
     return check_launch(ctx, "residual_layer_norm");
 }
 
+int enchip_residual_layer_norm_quant_dev(enchip_ctx *ctx, float *d_h, int64_t ldh, const float *d_y, int64_t ldy,
+                                         int64_t rows, int64_t D, const float *d_w, const float *d_b, double eps,
+                                         int8_t *d_aq, int64_t ldq, float *d_ascale, void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (rows < 0 || D < 4 || D > kMaxRowOp || D % 4 != 0 || ldh < D || ldh % 4 != 0 || (d_y && (ldy < D || ldy % 4 != 0)) ||
+        ldq < D || ldq % 64 != 0 || ldq > kMaxRowOp || rows > ((int64_t)1 << 31))
+        return fail(ctx, ENCHIP_ERR_ARG,
+                    "layer_norm_quant: bad shape rows=%lld D=%lld ldh=%lld ldy=%lld ldq=%lld (D a multiple of 4, "
+                    "pitches multiples of 4, ldq a multiple of 64 in [D, %lld])",
+                    (long long)rows, (long long)D, (long long)ldh, (long long)ldy, (long long)ldq, (long long)kMaxRowOp);
+    if (rows == 0) return ENCHIP_OK;
+    if (!d_h || !d_w || !d_b || !d_aq || !d_ascale) return fail(ctx, ENCHIP_ERR_ARG, "layer_norm_quant: null pointer");
+    if ((uintptr_t)d_h % 16 || (uintptr_t)d_y % 16 || (uintptr_t)d_w % 16 || (uintptr_t)d_b % 16 || (uintptr_t)d_aq % 16)
+        return fail(ctx, ENCHIP_ERR_ARG, "layer_norm_quant: h, y, w, b and aq must be 16-byte aligned");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    const dim3 grid((unsigned)((rows + 7) / 8));
+    const int64_t width = std::max(D, ldq);
+#define LNQ_CASE(CPL)                                                                                          \
+    hipLaunchKernelGGL((enchip::residual_layer_norm_quant<CPL>), grid, dim3(512), 0, s, d_h, ldh, d_y, ldy, rows, \
+                       (int)D, d_w, d_b, eps, d_aq, ldq, d_ascale)
+    if (width <= 256) LNQ_CASE(4);
+    else if (width <= 512) LNQ_CASE(8);
+    else if (width <= 1024) LNQ_CASE(16);
+    else if (width <= 2048) LNQ_CASE(32);
+    else LNQ_CASE(64);
+#undef LNQ_CASE
+    return check_launch(ctx, "residual_layer_norm_quant");
+}
+
 int enchip_pool_mean_l2_dev(enchip_ctx *ctx, const float *d_h, int64_t ldh, int64_t nseq, int64_t L, int64_t D,
                             float *d_out, int64_t ldo, void *stream) {
     if (!ctx) return ENCHIP_ERR_ARG;
@@ -1169,11 +1200,16 @@ int enchip_embed_rows_dev(enchip_ctx *ctx, const int32_t *d_ids, const int32_t *
         return fail(ctx, ENCHIP_ERR_ARG, "embed: null pointer");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    const int64_t rows = nseq * L, n = rows * D;
-    const int64_t blocks = (n + 255) / 256;
-    if (blocks > 0x7fffffff) return fail(ctx, ENCHIP_ERR_ARG, "embed: too many elements");
-    hipLaunchKernelGGL(enchip::embed_rows, dim3((unsigned)blocks), dim3(256), 0, s, d_ids, d_segs, rows, (int)L, d_word,
-                       vocab, d_pos, (int)pos_off, d_type, type_vocab, (int)D, d_h, ldh);
+    const int64_t rows = nseq * L;
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    const bool vec = D % 4 == 0 && ldh % 4 == 0 && (uintptr_t)d_word % 16 == 0 && (uintptr_t)d_pos % 16 == 0 &&
+                     (uintptr_t)d_type % 16 == 0 && (uintptr_t)d_h % 16 == 0;
+    if (vec)
+        hipLaunchKernelGGL(enchip::embed_rows<true>, grid, dim3(256), 0, s, d_ids, d_segs, rows, (int)L, d_word, vocab,
+                           d_pos, (int)pos_off, d_type, type_vocab, (int)D, d_h, ldh);
+    else
+        hipLaunchKernelGGL(enchip::embed_rows<false>, grid, dim3(256), 0, s, d_ids, d_segs, rows, (int)L, d_word, vocab,
+                           d_pos, (int)pos_off, d_type, type_vocab, (int)D, d_h, ldh);
     return check_launch(ctx, "embed_rows");
 }
 

@@ -166,6 +166,104 @@ __global__ __launch_bounds__(256) void residual_layer_norm(float *__restrict__ h
     }
 }
 
+// residual_layer_norm<CPL, true> fused with the next linear's per-token quantization
+// (linalg/quant.go:43-71 on the LayerNorm's output, as quant_rows_frag does it): each
+// row of h is normalised exactly as residual_layer_norm computes it and stored, and its
+// f32 values are quantized into the fragment-major code layout (frag_off; ldq a multiple
+// of 64, D <= ldq <= 64*CPL, columns [D, ldq) zero) with their scale. The codes and
+// scale are those quant_rows_frag gives on the stored row, and the stored row that
+// residual_layer_norm gives, so the pair reads the normalised rows from HBM zero times
+// instead of once. 8 rows per 512-thread block, one wavefront per row; the codes are
+// gathered in LDS in line order and written as whole 128-byte lines.
+template <int CPL>
+__global__ __launch_bounds__(512) void residual_layer_norm_quant(float *__restrict__ h, int64_t ldh,
+                                                                 const float *__restrict__ y, int64_t ldy,
+                                                                 int64_t rows, int D, const float *__restrict__ w,
+                                                                 const float *__restrict__ b, double eps,
+                                                                 int8_t *__restrict__ q, int64_t ldq,
+                                                                 float *__restrict__ scale) {
+    static_assert(CPL % 4 == 0, "16-byte columns");
+    constexpr int CH = CPL / 4;   // float4 per lane
+    constexpr int CP = 144;       // LDS bytes per 16-code chunk: 8 rows x 16 B + 16 B against bank conflicts
+    __shared__ __attribute__((aligned(16))) int8_t lds[16 * CH * CP];
+    const int lane = threadIdx.x & 63, rr = threadIdx.x >> 6;
+    const int64_t r0 = (int64_t)blockIdx.x * 8, row = r0 + rr;
+    const int ldq4 = (int)(ldq >> 2), D4 = D >> 2;
+    auto word = [&](int k4) -> int * { return reinterpret_cast<int *>(lds + (k4 >> 2) * CP + rr * 16 + (k4 & 3) * 4); };
+    if (row < rows) {
+        float *p = h + row * ldh;
+        const float *qy = y != nullptr ? y + row * ldy : nullptr;
+        float v[CPL];
+        double s = 0.0;
+#pragma unroll
+        for (int j4 = 0; j4 < CH; ++j4) {
+            const int c = 256 * j4 + 4 * lane;
+            f32x4 a = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
+            if (c < D) {
+                a = *reinterpret_cast<const f32x4 *>(p + c);
+                if (qy != nullptr) r = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(qy + c));
+            }
+            v[4 * j4 + 0] = qy != nullptr ? a.x + r.x : a.x;
+            v[4 * j4 + 1] = qy != nullptr ? a.y + r.y : a.y;
+            v[4 * j4 + 2] = qy != nullptr ? a.z + r.z : a.z;
+            v[4 * j4 + 3] = qy != nullptr ? a.w + r.w : a.w;
+        }
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+            if (256 * (j >> 2) + 4 * lane + (j & 3) < D) s += (double)v[j];
+        const double mean = wave_sum_f64(s) / (double)D;
+        double sq = 0.0;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            if (256 * (j >> 2) + 4 * lane + (j & 3) < D) {
+                const double d = (double)v[j] - mean;
+                sq += d * d;
+            }
+        }
+        const double variance = wave_sum_f64(sq) / (double)D;
+        const double inv_std = 1.0 / sqrt(variance + eps);
+        float4 o[CH];
+#pragma unroll
+        for (int j4 = 0; j4 < CH; ++j4) {
+            const int c = 256 * j4 + 4 * lane;
+            o[j4] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (c >= D) continue;
+            const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + c), bv = *reinterpret_cast<const f32x4 *>(b + c);
+            o[j4].x = (float)((((double)v[4 * j4 + 0] - mean) * inv_std) * (double)wv.x + (double)bv.x);
+            o[j4].y = (float)((((double)v[4 * j4 + 1] - mean) * inv_std) * (double)wv.y + (double)bv.y);
+            o[j4].z = (float)((((double)v[4 * j4 + 2] - mean) * inv_std) * (double)wv.z + (double)bv.z);
+            o[j4].w = (float)((((double)v[4 * j4 + 3] - mean) * inv_std) * (double)wv.w + (double)bv.w);
+            const f32x4 ov = {o[j4].x, o[j4].y, o[j4].z, o[j4].w};
+            *reinterpret_cast<f32x4 *>(p + c) = ov;
+        }
+        // the quantizer on the stored values (columns past D hold 0: no effect on the max)
+        const float m = row_absmax<CH>(o);
+        if (m == 0.0f) {
+            for (int k4 = lane; k4 < ldq4; k4 += 64) *word(k4) = 0;
+            if (lane == 0) scale[row] = 0.0f;
+        } else {
+            const float sc = m / 127.0f;
+            const float inv = 1.0f / sc;
+#pragma unroll
+            for (int j4 = 0; j4 < CH; ++j4) {
+                const int k4 = lane + 64 * j4;
+                if (k4 < D4) *word(k4) = pack_codes(o[j4], inv);
+            }
+            for (int k4 = D4 + lane; k4 < ldq4; k4 += 64) *word(k4) = 0;
+            if (lane == 0) scale[row] = sc;
+        }
+    }
+    __syncthreads();
+    // piece p = (chunk p / 8, row p % 8): 8 consecutive threads write one whole line
+    const int64_t nk32 = ldq >> 5;
+    for (int pc = threadIdx.x; pc < 2 * ldq4; pc += 512) {
+        const int c = pc >> 3, r2 = pc & 7;
+        if (r0 + r2 < rows)
+            *reinterpret_cast<int4 *>(q + frag_off(r0 + r2, 16 * (int64_t)c, nk32)) =
+                *reinterpret_cast<const int4 *>(lds + c * CP + r2 * 16);
+    }
+}
+
 // linalg.ExpF32 (linalg/exp.go:62-75): NaN passes through, overflow to +Inf above
 // 88.72283, underflow to 0 below -87.33654, expF32Core otherwise.
 __device__ __forceinline__ float exp_f32(float x) {
@@ -213,26 +311,50 @@ __global__ __launch_bounds__(256) void bias_act_rows(float *__restrict__ x, int6
 //   h[i] = word[clampTokenID(id)] + pos[i + pos_off]   (f32 adds, column by column)
 //   h[i] += type[seg]   when the model has token types (type_vocab > 0); seg = segs[i], or
 //                       0 without segments, and 0 when out of [0, type_vocab)
-// clampTokenID (encoder/forward.go:15-20) maps an id outside [0, vocab) to 0. One thread
-// per (row, column); the caller checked L + pos_off <= the position table's rows.
+// clampTokenID (encoder/forward.go:15-20) maps an id outside [0, vocab) to 0. One
+// wavefront per row, 4 rows per block; VEC: 16-byte columns (D, ldh multiples of 4 and
+// every table 16-byte aligned). The caller checked L + pos_off <= the position table's
+// rows.
+template <bool VEC>
 __global__ __launch_bounds__(256) void embed_rows(const int32_t *__restrict__ ids, const int32_t *__restrict__ segs,
                                                   int64_t rows, int L, const float *__restrict__ word, int64_t vocab,
                                                   const float *__restrict__ pos, int pos_off,
                                                   const float *__restrict__ type, int64_t type_vocab, int D,
                                                   float *__restrict__ h, int64_t ldh) {
-    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (e >= rows * D) return;
-    const int64_t r = e / D;
-    const int j = (int)(e % D), i = (int)(r % L);
+    const int lane = threadIdx.x & 63;
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const int i = (int)(r % L);
     const int32_t id = ids[r];
-    const int64_t w = id < 0 || id >= vocab ? 0 : id;
-    float v = word[w * D + j] + pos[(int64_t)(i + pos_off) * D + j];
+    const float *wr = word + (id < 0 || id >= vocab ? 0 : (int64_t)id) * D;
+    const float *pr = pos + (int64_t)(i + pos_off) * D;
+    const float *tr = nullptr;
     if (type_vocab > 0) {
         int32_t seg = segs != nullptr ? segs[r] : 0;
         if (seg < 0 || seg >= type_vocab) seg = 0;
-        v += type[(int64_t)seg * D + j];
+        tr = type + (int64_t)seg * D;
     }
-    h[r * ldh + j] = v;
+    float *out = h + r * ldh;
+    if (VEC) {
+        for (int c = 4 * lane; c < D; c += 256) {
+            const f32x4 a = *reinterpret_cast<const f32x4 *>(wr + c), b = *reinterpret_cast<const f32x4 *>(pr + c);
+            f32x4 v = {a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w};
+            if (tr != nullptr) {
+                const f32x4 t = *reinterpret_cast<const f32x4 *>(tr + c);
+                v.x += t.x;
+                v.y += t.y;
+                v.z += t.z;
+                v.w += t.w;
+            }
+            *reinterpret_cast<f32x4 *>(out + c) = v;
+        }
+    } else {
+        for (int c = lane; c < D; c += 64) {
+            float v = wr[c] + pr[c];
+            if (tr != nullptr) v += tr[c];
+            out[c] = v;
+        }
+    }
 }
 
 // Mean pooling then L2 normalisation of each of nseq sequences of L rows

@@ -57,6 +57,8 @@ _SIGNATURES = {
     "enchip_pool_mean_l2_dev": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
     "enchip_bias_act_rows_dev": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp]),
     "enchip_set_attention_products": (_int, [_vp, _int]),
+    "enchip_residual_layer_norm_quant_dev": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp, ctypes.c_double,
+                                                    _vp, _i64, _vp, _vp]),
     "enchip_embed_rows_dev": (_int, [_vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp,
                                      _i64, _vp]),
     "enchip_attention_f32_dev": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
@@ -338,6 +340,13 @@ class Context:
                                 eps: float, stream: int = 0) -> None:
         self._check(self._lib.enchip_residual_layer_norm_dev(self._h, d_h or None, ldh, d_y or None, ldy, rows, D,
                                                              d_w or None, d_b or None, eps, stream or None))
+
+    def residual_layer_norm_quant_dev(self, d_h: int, ldh: int, d_y: int, ldy: int, rows: int, D: int, d_w: int,
+                                      d_b: int, eps: float, d_aq: int, ldq: int, d_ascale: int,
+                                      stream: int = 0) -> None:
+        self._check(self._lib.enchip_residual_layer_norm_quant_dev(self._h, d_h or None, ldh, d_y or None, ldy, rows, D,
+                                                                   d_w or None, d_b or None, eps, d_aq or None, ldq,
+                                                                   d_ascale or None, stream or None))
 
     def embed_rows_dev(self, d_ids: int, d_segs: int, nseq: int, L: int, d_word: int, vocab: int, d_pos: int,
                        npos: int, pos_off: int, d_type: int, type_vocab: int, D: int, d_h: int, ldh: int,

@@ -282,6 +282,22 @@ int enchip_residual_layer_norm_dev(enchip_ctx *ctx, float *d_h, int64_t ldh, con
                                    int64_t ldy, int64_t rows, int64_t D, const float *d_w,
                                    const float *d_b, double eps, void *stream);
 
+/* enchip_residual_layer_norm_dev fused with the next linear's quantization: h = LN(h + y)
+ * in place, exactly as enchip_residual_layer_norm_dev computes and stores it, and the
+ * stored rows quantized per token into fragment-major codes + scales exactly as
+ * enchip_quant_rows_frag_dev(d_h, rows, D, d_aq, ldq, d_ascale) would then produce them
+ * (same layout and contract: ldq the weight's padded K, d_aq holding roundup(rows, 128)
+ * * ldq bytes). The pair's output feeds enchip_w8a8_pre_frag_dev; the normalised rows are
+ * not read back from device memory. No reference counterpart as one call: it is the
+ * encoder/bert.go:352-353,363-367 residual + layerNorm followed by the quantization of
+ * linalg.MatmulBTW8A8 (linalg/quant.go:43-71) for the next layer's linear. D a multiple
+ * of 4, h, y, w, b, aq 16-byte aligned, D <= ldq <= 4096. */
+int enchip_residual_layer_norm_quant_dev(enchip_ctx *ctx, float *d_h, int64_t ldh,
+                                         const float *d_y, int64_t ldy, int64_t rows,
+                                         int64_t D, const float *d_w, const float *d_b,
+                                         double eps, int8_t *d_aq, int64_t ldq,
+                                         float *d_ascale, void *stream);
+
 /* BERT's embedding rows on the device (encoder/bert.go:299-322, before its LayerNorm):
  * for token i of each of nseq sequences of L tokens (d_ids[z*L + i]),
  *   h = word[clampTokenID(id)] + pos[i + pos_off]   then, when type_vocab > 0,

@@ -297,3 +297,32 @@ def test_config1_device_forward_from_token_ids(ctx, workers):
         cos = float(ref @ d / (np.linalg.norm(ref) * np.linalg.norm(d)))
         say(f"  seq {s_}: cosine {cos:.9f}")
         assert cos >= COS_MIN
+
+
+def test_device_forward_ln_quant_fusion_is_bit_identical(ctx):
+    # DeviceBert with the LayerNorm + next-linear quantization fused (the default) and
+    # unfused: identical pooled bits (the fused kernel reproduces both halves exactly).
+    import torch
+
+    from aikit_amd.bert_dev import DeviceBert
+
+    cfg = workloads.MINILM_L6
+    g = workloads.rng(13)
+    w = model_weights(cfg, seed=103)
+    S, L, D = cfg.batch, cfg.seq, cfg.hidden
+    h0 = torch.from_numpy(np.concatenate([embeddings_in(g.integers(1000, 30000, size=L), w, cfg)
+                                          for _ in range(S)])).cuda()
+    got = []
+    for fuse in (True, False):
+        model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn, fuse_ln_quant=fuse)
+        try:
+            h = h0.clone()
+            pooled = torch.empty((S, D), device="cuda")
+            torch.cuda.synchronize()
+            model.embed(h, S, L, pooled)
+            torch.cuda.synchronize()
+            got.append(pooled.cpu().numpy())
+        finally:
+            model.close()
+    say(f"{cfg.name}: fused LN + quantization vs unfused, pooled bits equal")
+    assert np.array_equal(got[0].view(np.uint32), got[1].view(np.uint32))

@@ -280,15 +280,16 @@ def test_bias_tanh_matches_oracle(ctx):
     assert np.array_equal(got[~np.isnan(want)].view(np.uint32), want[~np.isnan(want)].view(np.uint32))
 
 
-@pytest.mark.parametrize("type_vocab,pos_off,with_segs", [(2, 0, False), (2, 2, True), (0, 2, False)])
-def test_embed_rows_bit_exact(ctx, type_vocab, pos_off, with_segs):
+@pytest.mark.parametrize("type_vocab,pos_off,with_segs,D", [(2, 0, False, 96), (2, 2, True, 96), (0, 2, False, 96),
+                                                           (2, 1, True, 75)])
+def test_embed_rows_bit_exact(ctx, type_vocab, pos_off, with_segs, D):
     # encoder/bert.go:299-322: word[clampTokenID(id)] + pos[i + posOff] (+ type[seg]),
     # f32 adds in that order; ids outside the vocabulary read row 0 (forward.go:15-20),
     # segments outside [0, type_vocab) read type row 0.
     import torch
 
     g = workloads.rng(4040 + type_vocab + pos_off)
-    S, L, D, vocab, npos = 3, 37, 96, 500, 64
+    S, L, vocab, npos = 3, 37, 500, 64  # D = 75: the scalar path
     word = g.standard_normal((vocab, D)).astype(np.float32)
     pos = g.standard_normal((npos, D)).astype(np.float32)
     typ = g.standard_normal((max(type_vocab, 1), D)).astype(np.float32)
@@ -327,3 +328,49 @@ def test_embed_rows_rejects_positions_past_the_table(ctx):
     with pytest.raises(enchip.EnchipError):  # L + pos_off = 34 > 32 position rows
         ctx.embed_rows_dev(ids.data_ptr(), 0, 1, 32, p, 10, p, 32, 2, 0, 0, 8, p, 8)
     torch.cuda.synchronize()
+
+
+def _frag_codes(buf, rows, ldq):
+    """The [rows, ldq] code matrix from its fragment-major layout (include/enchip.h)."""
+    r = np.arange(rows)[:, None]
+    k = np.arange(ldq)[None, :]
+    off = ((r // 32) * (ldq // 32) + k // 32) * 1024 + ((r % 32) + 32 * ((k // 16) % 2)) * 16 + k % 16
+    return buf[off]
+
+
+@pytest.mark.parametrize("rows,D,ldq,zero", [(300, 768, 768, False), (77, 384, 384, False), (64, 1024, 1024, False),
+                                             (50, 320, 384, False), (33, 768, 768, True), (9, 2048, 2048, False)])
+def test_residual_layer_norm_quant_matches_unfused(ctx, rows, D, ldq, zero):
+    # One kernel = enchip_residual_layer_norm_dev then enchip_quant_rows_frag_dev on the
+    # stored rows: the same h bits, the same codes (columns [D, ldq) zero) and scales;
+    # zero: gain and shift 0, so every normalised row is 0 (scale 0, codes 0).
+    import torch
+
+    g = workloads.rng(5050 + rows + D)
+    h0 = (g.standard_normal((rows, D)) * 2).astype(np.float32)
+    y = g.standard_normal((rows, D)).astype(np.float32)
+    w = (1 + g.standard_normal(D) * 0.1).astype(np.float32)
+    b = (g.standard_normal(D) * 0.1).astype(np.float32)
+    if zero:
+        w[:] = 0
+        b[:] = 0
+    Mp = (rows + 127) // 128 * 128
+    dh1, dh2, dy, dw, db = (_dev(torch, x) for x in (h0, h0, y, w, b))
+    q1 = torch.zeros(Mp * ldq, dtype=torch.int8, device="cuda")
+    q2 = torch.zeros(Mp * ldq, dtype=torch.int8, device="cuda")
+    s1 = torch.full((rows,), np.nan, device="cuda")
+    s2 = torch.full((rows,), np.nan, device="cuda")
+    torch.cuda.synchronize()
+    ctx.residual_layer_norm_quant_dev(dh1.data_ptr(), D, dy.data_ptr(), D, rows, D, dw.data_ptr(), db.data_ptr(),
+                                      1e-12, q1.data_ptr(), ldq, s1.data_ptr())
+    ctx.residual_layer_norm_dev(dh2.data_ptr(), D, dy.data_ptr(), D, rows, D, dw.data_ptr(), db.data_ptr(), 1e-12)
+    ctx.quant_rows_frag_dev(dh2.data_ptr(), rows, D, q2.data_ptr(), ldq, s2.data_ptr())
+    torch.cuda.synchronize()
+    h1, h2 = dh1.cpu().numpy(), dh2.cpu().numpy()
+    assert np.array_equal(h1.view(np.uint32), h2.view(np.uint32))
+    c1, c2 = _frag_codes(q1.cpu().numpy(), rows, ldq), _frag_codes(q2.cpu().numpy(), rows, ldq)
+    assert np.array_equal(c1, c2)
+    assert (c1[:, D:] == 0).all()
+    assert np.array_equal(s1.cpu().numpy().view(np.uint32), s2.cpu().numpy().view(np.uint32))
+    if zero:
+        assert (c1 == 0).all() and (s1.cpu().numpy() == 0).all()

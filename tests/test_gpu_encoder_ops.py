@@ -69,6 +69,27 @@ def test_softmax_rows_scaled_matches_oracle(ctx, cols):
             assert np.array_equal(got[r], want[r]), f"special row {r}"
 
 
+def test_softmax_two_column_rows_pin_exp_bits(ctx):
+    # Rows [0, x], x <= 0: the max is the first element, and the float64 sum of the two
+    # exponentials (1 + e) is exact in any order, so every output must equal the oracle's
+    # bit for bit: this pins the device expF32Core (its non-positive-argument form) on
+    # ~200k arguments across its range, into the underflow to 0 and at NaN.
+    import torch
+
+    g = workloads.rng(321)
+    xs = np.concatenate([-np.abs(g.standard_normal(100000) * 30), -g.uniform(80, 110, 50000),
+                         -g.uniform(0, 1e-3, 50000), [0.0, -0.0, -np.inf, np.nan, -87.33654, -88.72283, -103.97]])
+    x = np.zeros((xs.size, 2), np.float32)
+    x[:, 1] = xs
+    d = _dev(torch, x)
+    torch.cuda.synchronize()
+    ctx.softmax_rows_scaled_dev(d.data_ptr(), 2, xs.size, 2, 1.0)
+    torch.cuda.synchronize()
+    got = d.cpu().numpy()
+    want = np.stack([oracle.softmax_row_scaled(r, np.float32(1.0)) for r in x])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def test_softmax_pitched_rows(ctx):
     # ld > cols: only the first cols of each row are touched.
     import torch

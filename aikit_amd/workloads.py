@@ -1,10 +1,10 @@
-"""The BASELINE.json workloads: shapes and seeded synthetic inputs.
+"""The benchmark workloads: shapes and seeded synthetic inputs.
 
 Shared by bench.py and the tests. Generators use numpy's PCG64 with fixed seeds
 (recorded in bench output), so inputs are reproducible across machines.
 
 Config 2 ("isolated W8A8 linear") and config 3 ("small-M GEMV") inputs follow
-BASELINE.json literally: activations ~N(0,1) with 1% of elements x20, int8
+the benchmark definition: activations ~N(0,1) with 1% of elements x20, int8
 weights uniform in [-127,127], per-channel scales uniform in [1e-3,1e-2], bias
 ~N(0,0.1). The encoder configs use random-init N(0,0.02) f32 weights quantized
 per output channel (quantize_weights, the QuantizeRowsInt8 scheme of

@@ -176,7 +176,7 @@ def cpu_baseline(layer_w, cfg, seconds: float):
 
 
 def other_configs(ctx, torch, stream, ceilings):
-    """BASELINE configs 2 and 3, and ann.FlatI8 scoring, timed with HIP events on the
+    """Configs 2 and 3 (isolated linear, small-M GEMV), and ann.FlatI8 scoring, timed with HIP events on the
     launch stream.
 
     * config 2: the isolated W8A8 linear (M=4096, K=768 -> N=3072, bias + GELU), as
@@ -279,7 +279,7 @@ def other_configs(ctx, torch, stream, ceilings):
         for hh in hs:
             ctx.release_weight(hh)
 
-    # ann.FlatI8 scoring (SURVEY next row): an int8 index of N rows x dim registered as a
+    # ann.FlatI8 scoring: an int8 index of N rows x dim registered as a
     # weight (ann.Backend.NewI8Index), M queries scored as a bias-free W8A8 linear
     # (I8Index.Score / I8BatchIndex.ScoreBatch). The 403 MB index exceeds the 256 MB
     # MALL, so every call streams it from HBM.
@@ -539,7 +539,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the W8A8 path is not sharded across GPUs; "
-              "see DESIGN.md for how it would shard). Use --gpus 1.", file=sys.stderr)
+              "each GPU would take its own shard of the batch). Use --gpus 1.", file=sys.stderr)
         return 2
 
     import numpy as np

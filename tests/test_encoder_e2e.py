@@ -1,6 +1,5 @@
 """End-to-end W8A8 encoder forward: pooled embeddings from the device linears vs the
-CPU reference composition ("final pooled embeddings must
-reach cosine >= 0.9999").
+CPU reference composition (the bar: final pooled embeddings at cosine >= 0.9999).
 
 The forward follows encoder/bert.go:300-368 operation for operation:
   1. embeddings word + position (+ token type 0), then LayerNorm (eps 1e-12);
@@ -13,7 +12,7 @@ The forward follows encoder/bert.go:300-368 operation for operation:
   3. mean pooling (encoder/pooling.go:84-105) and L2Normalize (embed/pool.go:22-38).
 
 Each `s.mm(W) + addBias (+ gelu)` is one W8A8 linear: per-token int8 activations and
-per-channel int8 weights, the composition SURVEY.md describes for configs 1/4/5
+per-channel int8 weights, the composition of the BERT / MiniLM / XLM-R encoders
 (vision/encoder.go:234-255 is the in-tree precedent). Q, K and V share one
 quantization of h and run as a single N = 3D linear (linalg.MatmulBTW8A8Batch,
 bit-identical to per-op).
@@ -111,7 +110,7 @@ def run_both(ctx, workers, cfg, seqs, seed):
 
 
 def test_config1_minilm_l6_embeddings(ctx, workers):
-    # MiniLM-L6 shape, batch 8 x seq 128, ids uniform in [1000, 30000)
+    # Config 1: MiniLM-L6 shape, batch 8 x seq 128, ids uniform in [1000, 30000)
     cfg = workloads.MINILM_L6
     g = workloads.rng(11)
     seqs = [g.integers(1000, 30000, size=cfg.seq) for _ in range(cfg.batch)]
@@ -119,7 +118,7 @@ def test_config1_minilm_l6_embeddings(ctx, workers):
 
 
 def test_config4_bert_base_embedding(ctx, workers):
-    # BASELINE config 4 shape at full sequence length, one sequence (each sequence's
+    # Config 4 shape at full sequence length, one sequence (each sequence's
     # forward is independent of the others in the batch; the full b64 linears are
     # checked row by row in test_gpu_parity.py)
     cfg = workloads.BERT_BASE

@@ -1,6 +1,6 @@
 """GPU parity: libenchip.so on the MI355X against the CPU oracle, through the C ABI.
 
-The bar (BASELINE.json north_star): quantized activations and int32 accumulators
+The bar: quantized activations and int32 accumulators
 bit-exact; dequantized f32 outputs within 1e-5 max relative error per GEMM. The
 epilogue restates the reference's float32 operation order, so the f32 outputs
 are also asserted bit-identical, which is stronger.
@@ -243,7 +243,7 @@ def test_golden_linears(ctx):
         assert np.array_equal(bits(got), bits(d[f"lin{i}_dst"]))
 
 
-# ------------------------------------------------------------------ BASELINE configs at full size
+# ------------------------------------------------------------------ benchmark configs at full size
 def _full_config(ctx, workers, M, K, N, act, seed, sample_rows=None):
     g = workloads.rng(seed)
     a = workloads.activations(g, M, K)

@@ -43,6 +43,10 @@ __host__ __device__ inline int att_lds_floats(int L) {
     const int a = ATT_QT * att_pitch(L), b = ATT_WAVES * 1024;
     return a > b ? a : b;
 }
+// attention_split_bf16 adds its Q tile's bf16 hi / lo planes after the score tile: 32 rows
+// of 64 values at a 144-byte pitch (bank-conflict-free 16-byte reads) per plane.
+constexpr int ATT_QPITCH = 144;  // bytes per Q row per plane (head dim <= 64)
+__host__ __device__ inline int att_split_lds_floats(int L) { return att_lds_floats(L) + 2 * ATT_QT * ATT_QPITCH / 4; }
 
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -221,7 +225,8 @@ __global__ __launch_bounds__(64 * ATT_WAVES, 4) void attention_f32(
 // Per 16-deep block that is 3 MFMAs of 32 cycles against 8 f32 MFMAs of 64, plus ~3 VALU
 // operations per operand value for the split.
 //
-// Same grid, LDS size and phases as attention_f32; operand lanes hold the same values
+// Same grid and phases as attention_f32 (LDS: att_split_lds_floats(L) floats, the extra
+// holding the Q tile split once for all 8 wavefronts); operand lanes hold the same values
 // (lane half hf supplies depth 8hf..8hf+7 of each 16-deep block), now as bf16x8 pairs.
 // The softmax writes P already split: row r of the score tile (4P bytes) becomes a bf16
 // hi plane at byte 0 and a bf16 lo plane at byte 2P + 8 (both 16-byte aligned, 32 * nkt
@@ -278,23 +283,36 @@ __global__ __launch_bounds__(64 * ATT_WAVES, 4) void attention_split_bf16(
     const int q0 = (logical % nqt) * ATT_QT, head = (logical / nqt) % heads;
     const int64_t row0 = (int64_t)(logical / nqt / heads) * L;
 
-    // ---- 1. S = Q K^T * scale into LDS (f32), rows past L re-read row L-1.
-    float qa[HD / 2], kb[T1][HD / 2];
-    {
-        const float *qrow = q + (row0 + min(q0 + r, L - 1)) * ld + head * HD;
-#pragma unroll
-        for (int b = 0; b < NB; ++b) load8(qrow + 16 * b + 8 * hf, qa + 8 * b);
-#pragma unroll
-        for (int t = 0; t < T1; ++t) {
-            const int kt = min(wave + ATT_WAVES * t, nkt - 1);
-            const float *krow = k + (row0 + min(32 * kt + r, L - 1)) * ld + head * HD;
-#pragma unroll
-            for (int b = 0; b < NB; ++b) load8(krow + 16 * b + 8 * hf, kb[t] + 8 * b);
-        }
+    // ---- 0. the Q tile, split once for the workgroup: thread t takes 4 consecutive values
+    // of row t / (HD/4) (rows past L re-read row L-1) and writes their hi / lo words to
+    // the planes after the score tile.
+    char *qplanes = reinterpret_cast<char *>(sc + att_lds_floats(L));
+    if (threadIdx.x < ATT_QT * HD / 4) {
+        const int qr = threadIdx.x / (HD / 4), qc = 4 * (threadIdx.x % (HD / 4));
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(q + (row0 + min(q0 + qr, L - 1)) * ld + head * HD + qc);
+        uint32_t h0, l0, h1, l1;
+        split_pair(v.x, v.y, h0, l0);
+        split_pair(v.z, v.w, h1, l1);
+        *reinterpret_cast<uint2 *>(qplanes + qr * ATT_QPITCH + 2 * qc) = make_uint2(h0, h1);
+        *reinterpret_cast<uint2 *>(qplanes + ATT_QT * ATT_QPITCH + qr * ATT_QPITCH + 2 * qc) = make_uint2(l0, l1);
     }
+    // ---- 1. S = Q K^T * scale into LDS (f32), key rows past L re-read row L-1.
+    float kb[T1][HD / 2];
+#pragma unroll
+    for (int t = 0; t < T1; ++t) {
+        const int kt = min(wave + ATT_WAVES * t, nkt - 1);
+        const float *krow = k + (row0 + min(32 * kt + r, L - 1)) * ld + head * HD;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) load8(krow + 16 * b + 8 * hf, kb[t] + 8 * b);
+    }
+    lds_barrier();
     bf16x8 qh[NB], ql[NB];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) split_bf16x8(qa + 8 * b, qh[b], ql[b]);
+    for (int b = 0; b < NB; ++b) {
+        const char *qp = qplanes + r * ATT_QPITCH + 2 * (16 * b + 8 * hf);
+        qh[b] = *reinterpret_cast<const bf16x8 *>(qp);
+        ql[b] = *reinterpret_cast<const bf16x8 *>(qp + ATT_QT * ATT_QPITCH);
+    }
 #pragma unroll
     for (int t = 0; t < T1; ++t) {
         const int kt = wave + ATT_WAVES * t;

@@ -1078,7 +1078,9 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
         return fail(ctx, ENCHIP_ERR_ARG, "attention: q, k and v must be 16-byte aligned");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    const size_t lds = (size_t)enchip::att_lds_floats((int)L) * sizeof(float);
+    const bool split_products = ctx->att_products == ENCHIP_ATT_SPLIT_BF16;
+    const size_t lds = (size_t)(split_products ? enchip::att_split_lds_floats((int)L) : enchip::att_lds_floats((int)L)) *
+                       sizeof(float);
     using Kern = void (*)(const float *, const float *, const float *, int64_t, float *, int64_t, int, int, float);
     const bool split = ctx->att_products == ENCHIP_ATT_SPLIT_BF16;
     const bool full = L == enchip::ATT_MAX_L;

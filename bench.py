@@ -727,6 +727,11 @@ def main() -> int:
         "int8_frac_of_peak": ops / t / PEAK_INT8_OPS,
         "frac_of_measured_mfma_peak": ops / t / (ceilings["mfma_i8_tops"] * 1e12),
         "traffic_source": TRAFFIC_PROFILE if traffic is not None else None,
+        "limiter": ("VALU: the GELU epilogue restates aikit's exact-erf GELUF32 with no FMA (~36 VALU per output "
+                    "in its branch-free pass), so the kernel is bound by VALU issue below both its HBM and its "
+                    "MFMA roofline" if kernels.get(key, {}).get("act") == "gelu" else
+                    "MFMA issue in the main loop (L2 and LDS bandwidth measured far from saturated)" if key in kernels
+                    else "HBM (the quantizer reads each f32 row once)"),
         "timing": "HIP events around each launch on the launch stream, over a second K-step timed region of "
                   "the same kernels; value's region has no events between launches (144 event records per "
                   "step cost ~0.5 ms)",

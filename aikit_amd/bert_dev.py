@@ -19,7 +19,10 @@ matmul seam, docs/task-native-gpu.md:418-427):
   ffn   = W8A8(inter, Wd) + b           enchip_w8a8_linear_dev
   h     = LN(h + ffn)                   enchip_residual_layer_norm_dev
 
-When the linear after a LayerNorm (FFN-up, and the next layer's QKV) takes fragment-major
+A linear that takes fragment-major codes (enchip_frag_route) runs as
+enchip_quant_rows_frag_dev + enchip_w8a8_pre_frag_dev into this object's code buffer: the
+kernels enchip_w8a8_linear_dev launches, as two calls that can be timed apart. When the
+linear after a LayerNorm (FFN-up, and the next layer's QKV) takes fragment-major
 codes, the LayerNorm and that linear's quantization run as one kernel
 (enchip_residual_layer_norm_quant_dev, then enchip_w8a8_pre_frag_dev): the same bits, and
 the normalised rows are not read back to be quantized.
@@ -79,6 +82,13 @@ class DeviceBert:
             self.handles.append(entry)
         self._bufs = {}
         self._emb = None
+        # Optional callback mark(label) called before each device operation this object
+        # enqueues (and with "end" after the last), for per-operation timing; None: off.
+        self.mark = None
+
+    def _m(self, label: str) -> None:
+        if self.mark is not None:
+            self.mark(label)
 
     def set_embeddings(self, word, pos, ln, typ=None, pos_off: int = 0) -> None:
         """The embedding tables: word [vocab, D], pos [npos, D], optional token types
@@ -104,11 +114,13 @@ class DeviceBert:
         if e is None:
             raise ValueError("embeddings: call set_embeddings first")
         typ = e["type"]
+        self._m("embed_rows")
         self.ctx.embed_rows_dev(ids.data_ptr(), 0 if segs is None else segs.data_ptr(), S, L, e["word"].data_ptr(),
                                 e["word"].shape[0], e["pos"].data_ptr(), e["pos"].shape[0], e["pos_off"],
                                 0 if typ is None else typ.data_ptr(), 0 if typ is None else typ.shape[0], D,
                                 h.data_ptr(), D, stream)
         g, b = e["ln"]
+        self._m("embed_ln")
         self.ctx.residual_layer_norm_dev(h.data_ptr(), D, 0, D, S * L, D, g.data_ptr(), b.data_ptr(), LN_EPS, stream)
 
     def close(self) -> None:
@@ -128,10 +140,11 @@ class DeviceBert:
             f = dict(device="cuda", dtype=t.float32)
             sc = (1,) if self.fused_attention(L) else (S, self.H, L, L)
             Mp = (M + 127) // 128 * 128  # fragment-major codes are read up to a multiple of 128 rows
+            kp = (max(self.D, self.I) + 63) // 64 * 64  # the widest padded K of the layer's linears
             self._bufs = {key: dict(qkv=t.empty((M, 3 * self.D), **f), scores=t.empty(sc, **f),
                                     ctx=t.empty((M, self.D), **f), out=t.empty((M, self.D), **f),
                                     inter=t.empty((M, self.I), **f), ffn=t.empty((M, self.D), **f),
-                                    codes=t.empty(Mp * self.D, device="cuda", dtype=t.int8),
+                                    codes=t.empty(Mp * kp, device="cuda", dtype=t.int8),
                                     ascale=t.empty(M, **f))}
         return self._bufs[key]
 
@@ -152,8 +165,20 @@ class DeviceBert:
             ok, ldq = c.frag_route(w, M)
             return ldq if ok and ldq <= D else 0
 
-        def ln_then(g, s_, y, nxt):  # h = LN(h + y); codes for weight nxt when it takes them
+        def linear(name, w, x, bias, act, dst):  # one W8A8 linear on x [M, K]
+            ok, ldq = c.frag_route(w, M)
+            if ok:  # the kernels enchip_w8a8_linear_dev launches, as two timed calls
+                self._m(name + ".quant")
+                c.quant_rows_frag_dev(x.data_ptr(), M, w.K, codes, ldq, ascale, stream)
+                self._m(name + ".gemm")
+                c.pre_frag_dev(w, codes, ldq, M, ascale, bias.data_ptr(), act, dst.data_ptr(), stream)
+            else:
+                self._m(name)
+                c.linear_dev(w, x.data_ptr(), M, bias.data_ptr(), act, dst.data_ptr(), stream)
+
+        def ln_then(g, s_, y, nxt, label):  # h = LN(h + y); codes for weight nxt when it takes them
             ldq = route(nxt) if nxt is not None else 0
+            self._m(label + ("+quant" if ldq else ""))
             if ldq:
                 c.residual_layer_norm_quant_dev(h.data_ptr(), D, y.data_ptr(), D, M, D, g.data_ptr(), s_.data_ptr(),
                                                 LN_EPS, codes, ldq, ascale, stream)
@@ -166,9 +191,11 @@ class DeviceBert:
         for li, e in enumerate(self.handles):
             w, bias, act = e["qkv"]
             if pending:
+                self._m("qkv.gemm")
                 c.pre_frag_dev(w, codes, pending, M, ascale, bias.data_ptr(), act, q, stream)
             else:
-                c.linear_dev(w, h.data_ptr(), M, bias.data_ptr(), act, q, stream)
+                linear("qkv", w, h, bias, act, qkv)
+            self._m("attention")
             if self.fused_attention(L):
                 c.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, ctxv.data_ptr(), D, S, L, H, hd, scale, stream)
             else:
@@ -180,24 +207,27 @@ class DeviceBert:
                                     hd, inner=(H, L * L, hd, hd), outer=(S, H * L * L, L * 3 * D, L * D),
                                     stream=stream)
             w, bias, act = e["o"]
-            c.linear_dev(w, ctxv.data_ptr(), M, bias.data_ptr(), act, out.data_ptr(), stream)
+            linear("o", w, ctxv, bias, act, out)
             g, s = e["attn_ln"]
             w, bias, act = e["ffn_up"]
-            ldq = ln_then(g, s, out, w)
+            ldq = ln_then(g, s, out, w, "attn_ln")
             if ldq:
+                self._m("ffn_up.gemm")
                 c.pre_frag_dev(w, codes, ldq, M, ascale, bias.data_ptr(), act, inter.data_ptr(), stream)
             else:
-                c.linear_dev(w, h.data_ptr(), M, bias.data_ptr(), act, inter.data_ptr(), stream)
+                linear("ffn_up", w, h, bias, act, inter)
             w, bias, act = e["ffn_down"]
-            c.linear_dev(w, inter.data_ptr(), M, bias.data_ptr(), act, ffn.data_ptr(), stream)
+            linear("ffn_down", w, inter, bias, act, ffn)
             g, s = e["out_ln"]
             nxt = self.handles[li + 1]["qkv"][0] if li + 1 < len(self.handles) else None
-            pending = ln_then(g, s, ffn, nxt)
+            pending = ln_then(g, s, ffn, nxt, "out_ln")
 
     def embed(self, h, S: int, L: int, pooled, stream: int = 0) -> None:
         """forward(), then mean pooling + L2 normalisation of each sequence into pooled [S, D]."""
         self.forward(h, S, L, stream)
+        self._m("pool")
         self.ctx.pool_mean_l2_dev(h.data_ptr(), self.D, S, L, self.D, pooled.data_ptr(), self.D, stream)
+        self._m("end")
 
     def rerank(self, h, S: int, L: int, pooler, classifier, logits, stream: int = 0) -> None:
         """forward(), then the cross-encoder head on each sequence's [CLS] row (row 0):
@@ -210,6 +240,7 @@ class DeviceBert:
         if tuple(pw.shape) != (D, D) or tuple(cw.shape) != (labels, D) or tuple(logits.shape) != (S, labels):
             raise ValueError("rerank: pooler [D, D], classifier [labels, D], logits [S, labels]")
         self.forward(h, S, L, stream)
+        self._m("head")
         pooled = self._bufs[(S, L)].setdefault("pooled", self.torch.empty((S, D), device="cuda"))
         # CLS rows are every L-th row of h: pitch L*D
         c.matmul_bt_f32_dev(h.data_ptr(), L * D, pw.data_ptr(), D, enchip.B_NK, pooled.data_ptr(), D, S, D, D,
@@ -218,3 +249,4 @@ class DeviceBert:
         c.matmul_bt_f32_dev(pooled.data_ptr(), D, cw.data_ptr(), D, enchip.B_NK, logits.data_ptr(), labels, S, D,
                             labels, stream=stream)
         c.bias_act_rows_dev(logits.data_ptr(), labels, S, labels, cb.data_ptr(), enchip.ACT_NONE, stream)
+        self._m("end")

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -39,9 +40,20 @@ struct Weight {
 
 thread_local std::string g_open_error = "no error";
 
+// The last failure this thread saw on a context (by its id), so that a thread reading
+// enchip_last_error after its own failure gets its own message even when another
+// thread has failed on the same context since.
+struct ThreadError {
+    uint64_t ctx_id = 0;
+    std::string msg;
+};
+thread_local ThreadError g_thread_error;
+std::atomic<uint64_t> g_next_ctx_id{1};
+
 }  // namespace
 
 struct enchip_ctx {
+    uint64_t id = 0;  // unique per context for the life of the process
     int device = 0;
     hipStream_t stream = nullptr;
     int num_cus = 0, clock_khz = 0;
@@ -52,7 +64,14 @@ struct enchip_ctx {
     uint64_t next_handle = 1;
     int64_t small_m = 32;
     int att_products = ENCHIP_ATT_SPLIT_BF16;  // enchip_set_attention_products
-    // device scratch (grown on demand, freed by enchip_close)
+    // Device scratch (grown on demand, freed by enchip_close). Each growable buffer is
+    // capped at scratch_limit bytes (enchip_set_scratch_limit; 0 = no cap).
+    size_t scratch_limit = 0;
+    // The last stream that enqueued work on the shared scratch (d_aq, d_as, d_cand) and
+    // an event recorded after that work: a user on another stream waits for it first.
+    hipEvent_t scratch_ev = nullptr;
+    hipStream_t scratch_stream = nullptr;
+    bool scratch_pending = false;
     int8_t *d_aq = nullptr;
     size_t aq_cap = 0;
     float *d_as = nullptr;
@@ -84,6 +103,8 @@ int fail(enchip_ctx *c, int code, const char *fmt, ...) {
     vsnprintf(buf, sizeof buf, fmt, ap);
     va_end(ap);
     c->err = buf;
+    g_thread_error.ctx_id = c->id;
+    g_thread_error.msg = buf;
     return code;
 }
 
@@ -94,11 +115,20 @@ int fail(enchip_ctx *c, int code, const char *fmt, ...) {
             return fail((ctx), ENCHIP_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_)); \
     } while (0)
 
-// Grows a device buffer to at least `bytes`. Contents are not preserved.
+// Grows a device buffer to at least `bytes`. Contents are not preserved. Scratch
+// buffers (not weights) are refused past the context's scratch limit, as a failed
+// allocation would be.
 template <typename T>
-int ensure(enchip_ctx *c, T **p, size_t *cap, size_t bytes) {
+int ensure(enchip_ctx *c, T **p, size_t *cap, size_t bytes, bool scratch = true) {
+    // checked before the capacity: a call that needs more than the cap declines even
+    // when an earlier call already grew the buffer
+    if (scratch && c->scratch_limit != 0 && bytes > c->scratch_limit)
+        return fail(c, ENCHIP_ERR_OOM, "scratch of %zu bytes exceeds the context's scratch limit of %zu", bytes,
+                    c->scratch_limit);
     if (bytes <= *cap && *p) return ENCHIP_OK;
     if (*p) {
+        // the old buffer may still be read by work enqueued on another stream
+        if (scratch && c->scratch_pending) (void)hipEventSynchronize(c->scratch_ev);
         hipError_t e = hipFree(*p);
         *p = nullptr;
         *cap = 0;
@@ -121,10 +151,59 @@ int check_launch(enchip_ctx *c, const char *what) {
     return ENCHIP_OK;
 }
 
+// A 1-D launch of `blocks` workgroups of `threads` must keep its global thread index
+// below 2^32.
+bool grid_fits(int64_t blocks, int64_t threads) {
+    return blocks >= 0 && blocks * threads < ((int64_t)1 << 32);
+}
+
+// Rows per launch of the row kernels (at most 64 threads per row: 2^28 threads).
+constexpr int64_t kRowChunk = (int64_t)1 << 22;
+
+bool capturing(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
+// Orders work about to use the shared scratch on stream s after the scratch's last
+// user on another stream. Under stream capture the caller orders the streams (a
+// captured graph cannot wait on an event recorded outside it).
+int scratch_wait(enchip_ctx *c, hipStream_t s) {
+    if (!c->scratch_pending || c->scratch_stream == s || capturing(s)) return ENCHIP_OK;
+    hipError_t e = hipStreamWaitEvent(s, c->scratch_ev, 0);
+    if (e != hipSuccess) return fail(c, ENCHIP_ERR_HIP, "hipStreamWaitEvent(scratch): %s", hipGetErrorString(e));
+    return ENCHIP_OK;
+}
+
+// Marks the scratch as in use by the work just enqueued on stream s.
+int scratch_record(enchip_ctx *c, hipStream_t s) {
+    if (capturing(s)) return ENCHIP_OK;
+    hipError_t e = hipEventRecord(c->scratch_ev, s);
+    if (e != hipSuccess) return fail(c, ENCHIP_ERR_HIP, "hipEventRecord(scratch): %s", hipGetErrorString(e));
+    c->scratch_stream = s;
+    c->scratch_pending = true;
+    return ENCHIP_OK;
+}
+
 // Quantizes d_a[M,K] into q (zero-padded to ldq) and scale[M]: row-major q[M][ldq], or
 // fragment-major (kernels.h frag_off) when frag.
+int launch_quant_rows(enchip_ctx *c, const float *d_a, int64_t M, int64_t K, int8_t *q, int64_t ldq,
+                      float *scale, hipStream_t s, bool frag);
+
+// Launches in chunks of kRowChunk rows (a multiple of 32, so a fragment-major chunk
+// starts at byte r0 * ldq like a row-major one).
 int launch_quant(enchip_ctx *c, const float *d_a, int64_t M, int64_t K, int8_t *q, int64_t ldq,
                  float *scale, hipStream_t s, bool frag = false) {
+    for (int64_t r0 = 0; r0 < M; r0 += kRowChunk) {
+        int rc = launch_quant_rows(c, d_a + r0 * K, std::min(kRowChunk, M - r0), K, q + r0 * ldq, ldq, scale + r0, s,
+                                   frag);
+        if (rc) return rc;
+    }
+    return ENCHIP_OK;
+}
+
+int launch_quant_rows(enchip_ctx *c, const float *d_a, int64_t M, int64_t K, int8_t *q, int64_t ldq,
+                      float *scale, hipStream_t s, bool frag) {
     if (M == 0) return ENCHIP_OK;
     const bool vec = (K % 4 == 0) && (ldq % 4 == 0) && ((uintptr_t)d_a % 16 == 0) &&
                      ((uintptr_t)q % (frag ? 16 : 4) == 0) && K > 0 && (frag ? ldq : K) <= 256 * 16;
@@ -242,42 +321,54 @@ void launch_pt(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, co
 }
 
 // af: aq is fragment-major (the caller checked route_af); otherwise row-major at pitch lda.
+// Returns false, launching nothing, when the chosen kernel's grid would not fit.
 template <int EPI>
-void launch_gemm_epi(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, const float *as,
+bool launch_gemm_epi(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, const float *as,
                      const float *bias, void *out, int64_t ldo, int64_t M, hipStream_t s, bool af) {
     if (af || (M > c->small_m && use_persistent(w, aq, lda, out, ldo, M, false))) {
         if (af) launch_pt<enchip::PT_PW, EPI, true>(c, w, aq, lda, as, bias, out, ldo, M, s);
         else launch_pt<enchip::PT_PW, EPI, false>(c, w, aq, lda, as, bias, out, ldo, M, s);
-        return;
+        return true;
     }
     if (M <= c->small_m) {
-        if (gemv_wide(c, w))
-            hipLaunchKernelGGL((enchip::gemv_w8a8_wide<EPI>),
-                               dim3((unsigned)((w.N + 32 * enchip::GVW_WAVES - 1) / (32 * enchip::GVW_WAVES))),
-                               dim3(64 * enchip::GVW_WAVES), 0, s, aq, lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M,
-                               (int)w.N, (int)w.Kp);
-        else
-            hipLaunchKernelGGL((enchip::gemv_w8a8<EPI>), dim3((unsigned)((w.N + 31) / 32)), dim3(64 * enchip::GV_WAVES), 0,
+        if (gemv_wide(c, w)) {
+            const int64_t blocks = (w.N + 32 * enchip::GVW_WAVES - 1) / (32 * enchip::GVW_WAVES);
+            if (!grid_fits(blocks, 64 * enchip::GVW_WAVES)) return false;
+            hipLaunchKernelGGL((enchip::gemv_w8a8_wide<EPI>), dim3((unsigned)blocks), dim3(64 * enchip::GVW_WAVES), 0,
                                s, aq, lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp);
-        return;
+        } else {
+            const int64_t blocks = (w.N + 31) / 32;
+            if (!grid_fits(blocks, 64 * enchip::GV_WAVES)) return false;
+            hipLaunchKernelGGL((enchip::gemv_w8a8<EPI>), dim3((unsigned)blocks), dim3(64 * enchip::GV_WAVES), 0, s, aq,
+                               lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp);
+        }
+        return true;
     }
-    if (use_wide_tile(c, w, M))
+    const bool wide = use_wide_tile(c, w, M);
+    const int64_t tiles = ((M + 127) / 128) * ((w.N + (wide ? 255 : 127)) / (wide ? 256 : 128));
+    if (!grid_fits(tiles, 256)) return false;
+    if (wide)
         launch_gemm_t<128, 256, EPI, 2>(w, aq, lda, as, bias, out, ldo, M, s);
     else
         launch_gemm_t<128, 128, EPI, 3>(w, aq, lda, as, bias, out, ldo, M, s);
+    return true;
 }
 
 int launch_gemm(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, const float *as,
                 const float *bias, int epi, void *out, int64_t ldo, int64_t M, hipStream_t s, bool af = false) {
     if (M == 0) return ENCHIP_OK;
+    bool ok;
     switch (epi) {
-        case enchip::EPI_I32: launch_gemm_epi<enchip::EPI_I32>(c, w, aq, lda, as, bias, out, ldo, M, s, af); break;
-        case enchip::EPI_F32: launch_gemm_epi<enchip::EPI_F32>(c, w, aq, lda, as, bias, out, ldo, M, s, af); break;
+        case enchip::EPI_I32: ok = launch_gemm_epi<enchip::EPI_I32>(c, w, aq, lda, as, bias, out, ldo, M, s, af); break;
+        case enchip::EPI_F32: ok = launch_gemm_epi<enchip::EPI_F32>(c, w, aq, lda, as, bias, out, ldo, M, s, af); break;
         case enchip::EPI_F32_GELU:
-            launch_gemm_epi<enchip::EPI_F32_GELU>(c, w, aq, lda, as, bias, out, ldo, M, s, af);
+            ok = launch_gemm_epi<enchip::EPI_F32_GELU>(c, w, aq, lda, as, bias, out, ldo, M, s, af);
             break;
         default: return fail(c, ENCHIP_ERR_ARG, "bad epilogue %d", epi);
     }
+    if (!ok)
+        return fail(c, ENCHIP_ERR_ARG, "gemm: M=%lld N=%lld needs more workgroups than one launch addresses",
+                    (long long)M, (long long)w.N);
     return check_launch(c, "gemm_w8a8");
 }
 
@@ -307,7 +398,19 @@ extern "C" {
 int enchip_abi_version(void) { return ENCHIP_ABI_VERSION; }
 
 const char *enchip_last_error(const enchip_ctx *ctx) {
-    return ctx ? ctx->err.c_str() : g_open_error.c_str();
+    if (!ctx) return g_open_error.c_str();
+    // This thread's own last failure on ctx when it has one; otherwise a copy of the
+    // context's latest message taken under its lock. Either way the text is owned by
+    // the calling thread (another thread's failure cannot replace it) and stays valid
+    // until this thread's next enchip_last_error call.
+    thread_local std::string copy;
+    if (g_thread_error.ctx_id == ctx->id) {
+        copy = g_thread_error.msg;
+    } else {
+        std::lock_guard<std::mutex> g(const_cast<enchip_ctx *>(ctx)->mu);
+        copy = ctx->err;
+    }
+    return copy.c_str();
 }
 
 int enchip_open(int device, enchip_ctx **out) {
@@ -334,12 +437,19 @@ int enchip_open(int device, enchip_ctx **out) {
         return ENCHIP_ERR_HIP;
     }
     auto *c = new enchip_ctx();
+    c->id = g_next_ctx_id.fetch_add(1);
     c->device = device;
     c->num_cus = prop.multiProcessorCount;
     c->clock_khz = prop.clockRate;
     c->arch = prop.gcnArchName;
     if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) {
         g_open_error = std::string("enchip_open: hipStreamCreate: ") + hipGetErrorString(e);
+        delete c;
+        return ENCHIP_ERR_HIP;
+    }
+    if ((e = hipEventCreateWithFlags(&c->scratch_ev, hipEventDisableTiming)) != hipSuccess) {
+        g_open_error = std::string("enchip_open: hipEventCreate: ") + hipGetErrorString(e);
+        (void)hipStreamDestroy(c->stream);
         delete c;
         return ENCHIP_ERR_HIP;
     }
@@ -353,6 +463,7 @@ int enchip_close(enchip_ctx *ctx) {
         std::lock_guard<std::mutex> g(ctx->mu);
         (void)hipSetDevice(ctx->device);
         if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+        if (ctx->scratch_pending) (void)hipEventSynchronize(ctx->scratch_ev);
         for (auto &kv : ctx->weights) {
             (void)hipFree(kv.second.d_w);
             (void)hipFree(kv.second.d_s);
@@ -362,6 +473,7 @@ int enchip_close(enchip_ctx *ctx) {
                         ctx->d_acc, ctx->d_fb, ctx->d_cand, ctx->d_hit_i, ctx->d_hit_s};
         for (void *p : bufs)
             if (p) (void)hipFree(p);
+        if (ctx->scratch_ev) (void)hipEventDestroy(ctx->scratch_ev);
         if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     }
     delete ctx;
@@ -465,6 +577,14 @@ int enchip_probe_ceilings(enchip_ctx *ctx, enchip_ceilings *out) {
     return rc;
 }
 
+int enchip_set_scratch_limit(enchip_ctx *ctx, int64_t bytes) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (bytes < 0) return fail(ctx, ENCHIP_ERR_ARG, "scratch limit must be >= 0, got %lld", (long long)bytes);
+    ctx->scratch_limit = (size_t)bytes;
+    return ENCHIP_OK;
+}
+
 int enchip_set_small_m(enchip_ctx *ctx, int64_t max_m) {
     if (!ctx) return ENCHIP_ERR_ARG;
     std::lock_guard<std::mutex> g(ctx->mu);
@@ -566,13 +686,17 @@ int enchip_quant_rows(enchip_ctx *ctx, const float *a, int64_t M, int64_t K, int
     if ((rc = ensure(ctx, &ctx->d_a, &ctx->a_cap, (size_t)(M * K) * sizeof(float)))) return rc;
     if ((rc = ensure(ctx, &ctx->d_aq, &ctx->aq_cap, (size_t)(M * ldq)))) return rc;
     if ((rc = ensure(ctx, &ctx->d_as, &ctx->as_cap, (size_t)M * sizeof(float)))) return rc;
+    if ((rc = scratch_wait(ctx, ctx->stream))) return rc;
     if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
     if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, ldq, ctx->d_as, ctx->stream))) return rc;
+    if ((rc = scratch_record(ctx, ctx->stream))) return rc;
     if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(aq, ctx->d_aq, (size_t)(M * K), hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipMemcpyAsync(ascale, ctx->d_as, (size_t)M * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     return ENCHIP_OK;
 }
+
+}  // extern "C"
 
 namespace {
 
@@ -582,8 +706,8 @@ int upload_weight(enchip_ctx *ctx, Weight w, const int8_t *image, const float *w
     int rc;
     size_t wcap = 0, scap = 0;
     const size_t bytes = (size_t)(w.Np * w.Kp);
-    if ((rc = ensure(ctx, &w.d_w, &wcap, bytes))) return rc;
-    if ((rc = ensure(ctx, &w.d_s, &scap, (size_t)w.N * sizeof(float)))) {
+    if ((rc = ensure(ctx, &w.d_w, &wcap, bytes, false))) return rc;
+    if ((rc = ensure(ctx, &w.d_s, &scap, (size_t)w.N * sizeof(float), false))) {
         (void)hipFree(w.d_w);
         return rc;
     }
@@ -610,6 +734,8 @@ Weight weight_shape(int64_t N, int64_t K) {
 }
 
 }  // namespace
+
+extern "C" {
 
 int64_t enchip_weight_image_bytes(int64_t N, int64_t K) {
     if (N <= 0 || K < 0 || K > kMaxK || N > (int64_t)1 << 30) return -1;
@@ -714,9 +840,12 @@ int enchip_w8a8_linear_dev(enchip_ctx *ctx, enchip_weight h, const float *d_a, i
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     if ((rc = ensure_act_scratch(ctx, M, w->Kp))) return rc;
+    if ((rc = scratch_wait(ctx, s))) return rc;
     const bool af = route_af(ctx, *w, M, d_dst, w->N);
     if ((rc = launch_quant(ctx, d_a, M, w->K, ctx->d_aq, w->Kp, ctx->d_as, s, af))) return rc;
-    return launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, d_bias, act_code(act), d_dst, w->N, M, s, af);
+    if ((rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, d_bias, act_code(act), d_dst, w->N, M, s, af)))
+        return rc;
+    return scratch_record(ctx, s);
 }
 
 int enchip_w8a8_linear(enchip_ctx *ctx, enchip_weight h, const float *a, int64_t M, const float *bias, int act,
@@ -739,6 +868,7 @@ int enchip_w8a8_linear(enchip_ctx *ctx, enchip_weight h, const float *a, int64_t
     if (bias && (rc = ensure(ctx, &ctx->d_bias, &ctx->bias_cap, (size_t)N * sizeof(float)))) return rc;
     if (acc_debug && (rc = ensure(ctx, &ctx->d_acc, &ctx->acc_cap, out_bytes))) return rc;
     hipStream_t s = ctx->stream;
+    if ((rc = scratch_wait(ctx, s))) return rc;
     if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
     if (bias) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_bias, bias, (size_t)N * sizeof(float), hipMemcpyHostToDevice, s));
     const bool af = route_af(ctx, *w, M, ctx->d_dst, N) && (!acc_debug || route_af(ctx, *w, M, ctx->d_acc, N));
@@ -749,6 +879,7 @@ int enchip_w8a8_linear(enchip_ctx *ctx, enchip_weight h, const float *a, int64_t
     if (acc_debug &&
         (rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, nullptr, enchip::EPI_I32, ctx->d_acc, N, M, s, af)))
         return rc;
+    if ((rc = scratch_record(ctx, s))) return rc;
     HIP_TRY(ctx, hipMemcpyAsync(dst, ctx->d_dst, out_bytes, hipMemcpyDeviceToHost, s));
     if (acc_debug) HIP_TRY(ctx, hipMemcpyAsync(acc_debug, ctx->d_acc, out_bytes, hipMemcpyDeviceToHost, s));
     HIP_TRY(ctx, hipStreamSynchronize(s));
@@ -762,41 +893,55 @@ int enchip_w8a8_batch(enchip_ctx *ctx, const float *a, int64_t M, int64_t K, con
     if (M < 0 || M > ((int64_t)1 << 30) || K < 0) return fail(ctx, ENCHIP_ERR_ARG, "batch: bad shape");
     // Validate every op before any work (linalg/quant.go:330-339 does the same).
     std::vector<Weight *> ws((size_t)nops);
-    int64_t maxN = 0;
     for (int i = 0; i < nops; ++i) {
         int rc = find_weight(ctx, ops[i].w, &ws[(size_t)i]);
         if (rc) return rc;
         if (ws[(size_t)i]->K != K) return fail(ctx, ENCHIP_ERR_ARG, "batch: op %d has K=%lld, want %lld", i, (long long)ws[(size_t)i]->K, (long long)K);
         if (ops[i].act != ENCHIP_ACT_NONE && ops[i].act != ENCHIP_ACT_GELU) return fail(ctx, ENCHIP_ERR_ARG, "batch: bad act");
         if (!ops[i].dst) return fail(ctx, ENCHIP_ERR_ARG, "batch: op %d dst is NULL", i);
-        maxN = std::max(maxN, ws[(size_t)i]->N);
     }
     if (M == 0 || nops == 0) return ENCHIP_OK;
     if (K > 0 && !a) return fail(ctx, ENCHIP_ERR_ARG, "batch: a is NULL");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     const int64_t Kp = ws[0]->Kp;
+    // each op has its own slice of the output and bias scratch, so every op is enqueued
+    // before the one synchronisation at the end
+    std::vector<int64_t> dst_off((size_t)nops), bias_off((size_t)nops);
+    int64_t dst_total = 0, bias_total = 0;
+    for (int i = 0; i < nops; ++i) {
+        const int64_t n4 = round_up(ws[(size_t)i]->N, 4);  // 16-byte aligned slices
+        dst_off[(size_t)i] = dst_total;
+        bias_off[(size_t)i] = bias_total;
+        dst_total += M * n4;
+        bias_total += n4;
+    }
     int rc;
     if ((rc = ensure(ctx, &ctx->d_a, &ctx->a_cap, (size_t)(M * K) * sizeof(float)))) return rc;
-    if ((rc = ensure(ctx, &ctx->d_dst, &ctx->dst_cap, (size_t)(M * maxN) * sizeof(float)))) return rc;
-    if ((rc = ensure(ctx, &ctx->d_bias, &ctx->bias_cap, (size_t)maxN * sizeof(float)))) return rc;
+    if ((rc = ensure(ctx, &ctx->d_dst, &ctx->dst_cap, (size_t)dst_total * sizeof(float)))) return rc;
+    if ((rc = ensure(ctx, &ctx->d_bias, &ctx->bias_cap, (size_t)bias_total * sizeof(float)))) return rc;
     if ((rc = ensure_act_scratch(ctx, M, Kp))) return rc;
     hipStream_t s = ctx->stream;
+    if ((rc = scratch_wait(ctx, s))) return rc;
     if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
     // one quantization serves every op, so its layout must suit all of them
     bool af = true;
-    for (int i = 0; i < nops; ++i) af = af && route_af(ctx, *ws[(size_t)i], M, ctx->d_dst, ws[(size_t)i]->N);
+    for (int i = 0; i < nops; ++i)
+        af = af && route_af(ctx, *ws[(size_t)i], M, ctx->d_dst + dst_off[(size_t)i], ws[(size_t)i]->N);
     if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, Kp, ctx->d_as, s, af))) return rc;
     for (int i = 0; i < nops; ++i) {
         const Weight &w = *ws[(size_t)i];
+        float *db = ctx->d_bias + bias_off[(size_t)i], *dd = ctx->d_dst + dst_off[(size_t)i];
         if (ops[i].bias)
-            HIP_TRY(ctx, hipMemcpyAsync(ctx->d_bias, ops[i].bias, (size_t)w.N * sizeof(float), hipMemcpyHostToDevice, s));
-        if ((rc = launch_gemm(ctx, w, ctx->d_aq, Kp, ctx->d_as, ops[i].bias ? ctx->d_bias : nullptr,
-                              act_code(ops[i].act), ctx->d_dst, w.N, M, s, af)))
+            HIP_TRY(ctx, hipMemcpyAsync(db, ops[i].bias, (size_t)w.N * sizeof(float), hipMemcpyHostToDevice, s));
+        if ((rc = launch_gemm(ctx, w, ctx->d_aq, Kp, ctx->d_as, ops[i].bias ? db : nullptr, act_code(ops[i].act), dd,
+                              w.N, M, s, af)))
             return rc;
-        HIP_TRY(ctx, hipMemcpyAsync(ops[i].dst, ctx->d_dst, (size_t)(M * w.N) * sizeof(float), hipMemcpyDeviceToHost, s));
-        // The next op reuses d_bias / d_dst: wait for this op's download.
-        HIP_TRY(ctx, hipStreamSynchronize(s));
     }
+    if ((rc = scratch_record(ctx, s))) return rc;
+    for (int i = 0; i < nops; ++i)
+        HIP_TRY(ctx, hipMemcpyAsync(ops[i].dst, ctx->d_dst + dst_off[(size_t)i],
+                                    (size_t)(M * ws[(size_t)i]->N) * sizeof(float), hipMemcpyDeviceToHost, s));
+    HIP_TRY(ctx, hipStreamSynchronize(s));
     return ENCHIP_OK;
 }
 
@@ -829,9 +974,13 @@ int launch_matmul_f32(enchip_ctx *c, const float *A, int64_t lda, const float *B
             const unsigned ny = (unsigned)std::min(kGrid, b1.count - y0), nz = (unsigned)std::min(kGrid, b2.count - z0);
             const float *a = A + y0 * s1.a + z0 * s2.a, *b = B + y0 * s1.b + z0 * s2.b;
             float *cz = C + y0 * s1.c + z0 * s2.c;
-            if (K == 0) {
-                hipLaunchKernelGGL(fill_zero_f32, dim3((unsigned)((M * N + 255) / 256), ny, nz), dim3(256), 0, s, cz,
-                                   ldc, s1.c, s2.c, (int)M, (int)N);
+            if (K == 0) {  // whole rows per launch, at most 2^30 elements
+                const int64_t rchunk = std::max<int64_t>(1, ((int64_t)1 << 30) / N);
+                for (int64_t r0 = 0; r0 < M; r0 += rchunk) {
+                    const int64_t n = std::min(rchunk, M - r0);
+                    hipLaunchKernelGGL(fill_zero_f32, dim3((unsigned)((n * N + 255) / 256), ny, nz), dim3(256), 0, s,
+                                       cz + r0 * ldc, ldc, s1.c, s2.c, (int)n, (int)N);
+                }
                 continue;
             }
             const dim3 grid((unsigned)(tilesM * tilesN), ny, nz), block(256);
@@ -964,15 +1113,18 @@ int enchip_softmax_rows_scaled_dev(enchip_ctx *ctx, float *d_x, int64_t ld, int6
                                    void *stream) {
     if (!ctx) return ENCHIP_ERR_ARG;
     std::lock_guard<std::mutex> g(ctx->mu);
-    if (rows < 0 || cols < 0 || cols > kMaxRowOp || ld < cols || rows > ((int64_t)1 << 34))
+    if (rows < 0 || cols < 0 || cols > kMaxRowOp || ld < cols)
         return fail(ctx, ENCHIP_ERR_ARG, "softmax: bad shape rows=%lld cols=%lld ld=%lld (cols <= %lld)",
                     (long long)rows, (long long)cols, (long long)ld, (long long)kMaxRowOp);
     if (rows == 0 || cols == 0) return ENCHIP_OK;
     if (!d_x) return fail(ctx, ENCHIP_ERR_ARG, "softmax: null pointer");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    const dim3 grid((unsigned)((rows + 3) / 4));
-    ROWOP_DISPATCH(enchip::softmax_rows_scaled, cols, grid, s, d_x, ld, rows, (int)cols, scale);
+    for (int64_t r0 = 0; r0 < rows; r0 += kRowChunk) {
+        const int64_t n = std::min(kRowChunk, rows - r0);
+        const dim3 grid((unsigned)((n + 3) / 4));
+        ROWOP_DISPATCH(enchip::softmax_rows_scaled, cols, grid, s, d_x + r0 * ld, ld, n, (int)cols, scale);
+    }
     return check_launch(ctx, "softmax_rows_scaled");
 }
 
@@ -981,34 +1133,39 @@ int enchip_residual_layer_norm_dev(enchip_ctx *ctx, float *d_h, int64_t ldh, con
                                    void *stream) {
     if (!ctx) return ENCHIP_ERR_ARG;
     std::lock_guard<std::mutex> g(ctx->mu);
-    if (rows < 0 || D < 0 || D > kMaxRowOp || ldh < D || (d_y && ldy < D) || rows > ((int64_t)1 << 34))
+    if (rows < 0 || D < 0 || D > kMaxRowOp || ldh < D || (d_y && ldy < D))
         return fail(ctx, ENCHIP_ERR_ARG, "layer_norm: bad shape rows=%lld D=%lld ldh=%lld ldy=%lld (D <= %lld)",
                     (long long)rows, (long long)D, (long long)ldh, (long long)ldy, (long long)kMaxRowOp);
     if (rows == 0 || D == 0) return ENCHIP_OK;
     if (!d_h || !d_w || !d_b) return fail(ctx, ENCHIP_ERR_ARG, "layer_norm: null pointer");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    const dim3 grid((unsigned)((rows + 3) / 4));
     const bool vec = D % 4 == 0 && ldh % 4 == 0 && (!d_y || ldy % 4 == 0) && (uintptr_t)d_h % 16 == 0 &&
                      (uintptr_t)d_y % 16 == 0 && (uintptr_t)d_w % 16 == 0 && (uintptr_t)d_b % 16 == 0 && D >= 4;
+    for (int64_t r0 = 0; r0 < rows; r0 += kRowChunk) {
+        const int64_t n = std::min(kRowChunk, rows - r0);
+        const dim3 grid((unsigned)((n + 3) / 4));
+        float *h = d_h + r0 * ldh;
+        const float *y = d_y ? d_y + r0 * ldy : nullptr;
     // VEC: 4 consecutive columns per lane per 16-byte load (CPL a multiple of 4)
 #define LN_CASE(CPL)                                                                                           \
     do {                                                                                                       \
         if (vec)                                                                                               \
-            hipLaunchKernelGGL((enchip::residual_layer_norm<CPL, true>), grid, dim3(256), 0, s, d_h, ldh, d_y, ldy, \
-                               rows, (int)D, d_w, d_b, eps);                                                    \
+            hipLaunchKernelGGL((enchip::residual_layer_norm<CPL, true>), grid, dim3(256), 0, s, h, ldh, y, ldy, n, \
+                               (int)D, d_w, d_b, eps);                                                          \
         else                                                                                                   \
-            hipLaunchKernelGGL((enchip::residual_layer_norm<CPL, false>), grid, dim3(256), 0, s, d_h, ldh, d_y,  \
-                               ldy, rows, (int)D, d_w, d_b, eps);                                               \
+            hipLaunchKernelGGL((enchip::residual_layer_norm<CPL, false>), grid, dim3(256), 0, s, h, ldh, y, ldy, n, \
+                               (int)D, d_w, d_b, eps);                                                          \
     } while (0)
-    if (D <= 64 && !vec) LN_CASE(1);
-    else if (D <= 128 && !vec) LN_CASE(2);
-    else if (D <= 256) LN_CASE(4);
-    else if (D <= 512) LN_CASE(8);
-    else if (D <= 1024) LN_CASE(16);
-    else if (D <= 2048) LN_CASE(32);
-    else LN_CASE(64);
+        if (D <= 64 && !vec) LN_CASE(1);
+        else if (D <= 128 && !vec) LN_CASE(2);
+        else if (D <= 256) LN_CASE(4);
+        else if (D <= 512) LN_CASE(8);
+        else if (D <= 1024) LN_CASE(16);
+        else if (D <= 2048) LN_CASE(32);
+        else LN_CASE(64);
 #undef LN_CASE
+    }
     return check_launch(ctx, "residual_layer_norm");
 }
 
@@ -1018,7 +1175,7 @@ int enchip_residual_layer_norm_quant_dev(enchip_ctx *ctx, float *d_h, int64_t ld
     if (!ctx) return ENCHIP_ERR_ARG;
     std::lock_guard<std::mutex> g(ctx->mu);
     if (rows < 0 || D < 4 || D > kMaxRowOp || D % 4 != 0 || ldh < D || ldh % 4 != 0 || (d_y && (ldy < D || ldy % 4 != 0)) ||
-        ldq < D || ldq % 64 != 0 || ldq > kMaxRowOp || rows > ((int64_t)1 << 31))
+        ldq < D || ldq % 64 != 0 || ldq > kMaxRowOp)
         return fail(ctx, ENCHIP_ERR_ARG,
                     "layer_norm_quant: bad shape rows=%lld D=%lld ldh=%lld ldy=%lld ldq=%lld (D a multiple of 4, "
                     "pitches multiples of 4, ldq a multiple of 64 in [D, %lld])",
@@ -1029,17 +1186,25 @@ int enchip_residual_layer_norm_quant_dev(enchip_ctx *ctx, float *d_h, int64_t ld
         return fail(ctx, ENCHIP_ERR_ARG, "layer_norm_quant: h, y, w, b and aq must be 16-byte aligned");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    const dim3 grid((unsigned)((rows + 7) / 8));
     const int64_t width = std::max(D, ldq);
+    // chunks of kRowChunk rows (a multiple of 32: fragment-major rows r0.. start at r0 * ldq)
+    for (int64_t r0 = 0; r0 < rows; r0 += kRowChunk) {
+        const int64_t n = std::min(kRowChunk, rows - r0);
+        const dim3 grid((unsigned)((n + 7) / 8));
+        float *h = d_h + r0 * ldh;
+        const float *y = d_y ? d_y + r0 * ldy : nullptr;
+        int8_t *aq = d_aq + r0 * ldq;
+        float *as = d_ascale + r0;
 #define LNQ_CASE(CPL)                                                                                          \
-    hipLaunchKernelGGL((enchip::residual_layer_norm_quant<CPL>), grid, dim3(512), 0, s, d_h, ldh, d_y, ldy, rows, \
-                       (int)D, d_w, d_b, eps, d_aq, ldq, d_ascale)
-    if (width <= 256) LNQ_CASE(4);
-    else if (width <= 512) LNQ_CASE(8);
-    else if (width <= 1024) LNQ_CASE(16);
-    else if (width <= 2048) LNQ_CASE(32);
-    else LNQ_CASE(64);
+    hipLaunchKernelGGL((enchip::residual_layer_norm_quant<CPL>), grid, dim3(512), 0, s, h, ldh, y, ldy, n, (int)D, \
+                       d_w, d_b, eps, aq, ldq, as)
+        if (width <= 256) LNQ_CASE(4);
+        else if (width <= 512) LNQ_CASE(8);
+        else if (width <= 1024) LNQ_CASE(16);
+        else if (width <= 2048) LNQ_CASE(32);
+        else LNQ_CASE(64);
 #undef LNQ_CASE
+    }
     return check_launch(ctx, "residual_layer_norm_quant");
 }
 
@@ -1094,7 +1259,7 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
                                      (int)lds));
     // one launch per chunk of sequences whose workgroup count fits a 32-bit grid
     const int64_t per_seq = ((L + enchip::ATT_QT - 1) / enchip::ATT_QT) * heads;
-    const int64_t chunk = std::max<int64_t>(1, ((int64_t)1 << 30) / per_seq);
+    const int64_t chunk = std::max<int64_t>(1, (((int64_t)1 << 32) / (64 * enchip::ATT_WAVES) - 1) / per_seq);
     for (int64_t z0 = 0; z0 < nseq; z0 += chunk) {
         const int64_t nz = std::min<int64_t>(chunk, nseq - z0);
         const dim3 grid((unsigned)(per_seq * nz));
@@ -1140,8 +1305,8 @@ int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, in
         hipLaunchKernelGGL(wide ? topk_chunk_wide : topk_chunk, dim3((unsigned)nchunks, (unsigned)nr), dim3(256), 0, s,
                            scores + r0 * ld, ld, n, (int)k, (int)nchunks, c->d_cand + r0 * nchunks * k);
     }
-    for (int64_t r0 = 0; r0 < rows; r0 += 0x7fffffff) {
-        const int64_t nr = std::min<int64_t>(0x7fffffff, rows - r0);
+    for (int64_t r0 = 0; r0 < rows; r0 += kRowChunk) {
+        const int64_t nr = std::min<int64_t>(kRowChunk, rows - r0);
         hipLaunchKernelGGL(topk_merge, dim3((unsigned)nr), dim3(256), (size_t)kp * sizeof(uint64_t), s,
                            c->d_cand + r0 * nchunks * k, nchunks * k, (int)k, kp, scores + r0 * ld, ld,
                            index + r0 * ldi, ldi, score + r0 * lds, lds);
@@ -1162,7 +1327,10 @@ int enchip_topk_rows_dev(enchip_ctx *ctx, const float *d_scores, int64_t ld, int
     if ((n > 0 && !d_scores) || !d_index || !d_score) return fail(ctx, ENCHIP_ERR_ARG, "topk: null pointer");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    return launch_topk(ctx, d_scores, ld, rows, n, k, d_index, ldi, d_score, lds, s);
+    int rc;
+    if ((rc = scratch_wait(ctx, s))) return rc;
+    if ((rc = launch_topk(ctx, d_scores, ld, rows, n, k, d_index, ldi, d_score, lds, s))) return rc;
+    return scratch_record(ctx, s);
 }
 
 int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int64_t M, int64_t k, int32_t *hit_index,
@@ -1185,6 +1353,7 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int6
     if ((rc = ensure(ctx, &ctx->d_hit_s, &ctx->hit_s_cap, (size_t)(M * k) * sizeof(float)))) return rc;
     if ((rc = ensure_act_scratch(ctx, M, w->Kp))) return rc;
     hipStream_t s = ctx->stream;
+    if ((rc = scratch_wait(ctx, s))) return rc;
     if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, queries, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
     // the bias-free W8A8 scores (ann/backend.go:25-29), then the selection on the device
     const bool af = route_af(ctx, *w, M, ctx->d_dst, N);
@@ -1192,6 +1361,7 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int6
     if ((rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, nullptr, enchip::EPI_F32, ctx->d_dst, N, M, s, af)))
         return rc;
     if ((rc = launch_topk(ctx, ctx->d_dst, N, M, N, k, ctx->d_hit_i, k, ctx->d_hit_s, k, s))) return rc;
+    if ((rc = scratch_record(ctx, s))) return rc;
     HIP_TRY(ctx, hipMemcpyAsync(hit_index, ctx->d_hit_i, (size_t)(M * k) * sizeof(int32_t), hipMemcpyDeviceToHost, s));
     HIP_TRY(ctx, hipMemcpyAsync(hit_score, ctx->d_hit_s, (size_t)(M * k) * sizeof(float), hipMemcpyDeviceToHost, s));
     HIP_TRY(ctx, hipStreamSynchronize(s));
@@ -1216,16 +1386,22 @@ int enchip_embed_rows_dev(enchip_ctx *ctx, const int32_t *d_ids, const int32_t *
         return fail(ctx, ENCHIP_ERR_ARG, "embed: null pointer");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    const int64_t rows = nseq * L;
-    const dim3 grid((unsigned)((rows + 3) / 4));
     const bool vec = D % 4 == 0 && ldh % 4 == 0 && (uintptr_t)d_word % 16 == 0 && (uintptr_t)d_pos % 16 == 0 &&
                      (uintptr_t)d_type % 16 == 0 && (uintptr_t)d_h % 16 == 0;
-    if (vec)
-        hipLaunchKernelGGL(enchip::embed_rows<true>, grid, dim3(256), 0, s, d_ids, d_segs, rows, (int)L, d_word, vocab,
-                           d_pos, (int)pos_off, d_type, type_vocab, (int)D, d_h, ldh);
-    else
-        hipLaunchKernelGGL(enchip::embed_rows<false>, grid, dim3(256), 0, s, d_ids, d_segs, rows, (int)L, d_word, vocab,
-                           d_pos, (int)pos_off, d_type, type_vocab, (int)D, d_h, ldh);
+    // whole sequences per launch, at most about kRowChunk rows (a row's position is its
+    // index within the launch modulo L)
+    const int64_t zchunk = std::max<int64_t>(1, kRowChunk / L);
+    for (int64_t z0 = 0; z0 < nseq; z0 += zchunk) {
+        const int64_t r0 = z0 * L, rows = std::min(zchunk, nseq - z0) * L;
+        const dim3 grid((unsigned)((rows + 3) / 4));
+        const int32_t *segs = d_segs ? d_segs + r0 : nullptr;
+        if (vec)
+            hipLaunchKernelGGL(enchip::embed_rows<true>, grid, dim3(256), 0, s, d_ids + r0, segs, rows, (int)L, d_word,
+                               vocab, d_pos, (int)pos_off, d_type, type_vocab, (int)D, d_h + r0 * ldh, ldh);
+        else
+            hipLaunchKernelGGL(enchip::embed_rows<false>, grid, dim3(256), 0, s, d_ids + r0, segs, rows, (int)L, d_word,
+                               vocab, d_pos, (int)pos_off, d_type, type_vocab, (int)D, d_h + r0 * ldh, ldh);
+    }
     return check_launch(ctx, "embed_rows");
 }
 
@@ -1235,17 +1411,24 @@ int enchip_bias_act_rows_dev(enchip_ctx *ctx, float *d_x, int64_t ld, int64_t ro
     std::lock_guard<std::mutex> g(ctx->mu);
     if (act != ENCHIP_ACT_NONE && act != ENCHIP_ACT_TANH)
         return fail(ctx, ENCHIP_ERR_ARG, "bias_act: act must be ENCHIP_ACT_NONE or ENCHIP_ACT_TANH, got %d", act);
-    if (rows < 0 || cols < 0 || ld < cols || rows * cols > ((int64_t)1 << 38))
+    if (rows < 0 || cols < 0 || ld < cols || cols > ((int64_t)1 << 30))
         return fail(ctx, ENCHIP_ERR_ARG, "bias_act: bad shape rows=%lld cols=%lld ld=%lld", (long long)rows,
                     (long long)cols, (long long)ld);
     if (rows == 0 || cols == 0) return ENCHIP_OK;
     if (!d_x) return fail(ctx, ENCHIP_ERR_ARG, "bias_act: null pointer");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    const dim3 grid((unsigned)((rows * cols + 255) / 256));
-    if (act == ENCHIP_ACT_TANH)
-        hipLaunchKernelGGL(enchip::bias_act_rows<true>, grid, dim3(256), 0, s, d_x, ld, rows, (int)cols, d_bias);
-    else
-        hipLaunchKernelGGL(enchip::bias_act_rows<false>, grid, dim3(256), 0, s, d_x, ld, rows, (int)cols, d_bias);
+    // whole rows per launch, at most 2^30 elements (one thread each)
+    const int64_t rchunk = std::max<int64_t>(1, ((int64_t)1 << 30) / cols);
+    for (int64_t r0 = 0; r0 < rows; r0 += rchunk) {
+        const int64_t n = std::min(rchunk, rows - r0);
+        const dim3 grid((unsigned)((n * cols + 255) / 256));
+        if (act == ENCHIP_ACT_TANH)
+            hipLaunchKernelGGL(enchip::bias_act_rows<true>, grid, dim3(256), 0, s, d_x + r0 * ld, ld, n, (int)cols,
+                               d_bias);
+        else
+            hipLaunchKernelGGL(enchip::bias_act_rows<false>, grid, dim3(256), 0, s, d_x + r0 * ld, ld, n, (int)cols,
+                               d_bias);
+    }
     return check_launch(ctx, "bias_act_rows");
 }

@@ -20,10 +20,8 @@
 //     (sched_group_barrier), so no MFMA waits on a just-issued LDS read.
 //
 // Epilogue (per tile, no VMEM loads):
-//   * The tile's aS / wS / bias are loaded once per ring group as inline-asm loads, so
-//     the compiler can neither hoist nor sink them. An explicit wait at the tile end
-//     covers them; they are older than the last group's PW * 6 ring loads.
-//   * They are staged in LDS.
+//   * The tile's aS / wS / bias are loaded with ordinary loads before its main loop,
+//     so the compiler's own wait counts cover them, and staged in LDS after it.
 //   * Each wave transposes its accumulators through a private LDS scratch and writes
 //     16-byte row-major stores: 32 stores per wave per tile instead of 128 dword
 //     stores interleaved with loads.
@@ -163,7 +161,13 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void gemm_w8a8_pt(
     for (int it = 0; it < ntiles; ++it) {
         const int tile = tile_id(it);
         const int m0 = (tile / tilesN) * BM, n0 = (tile % tilesN) * BN;
-        float c_as = 0.f, c_ws = 0.f, c_b = 0.f;
+        // The tile's epilogue constants, loaded before its main loop so their latency
+        // hides behind it. Ordinary loads: the compiler counts them into the waits it
+        // places before their first use (the LDS staging after the main loop), and the
+        // main loop's barriers keep it from sinking them there.
+        const float c_as = aS[min(m0 + (tid & (BM - 1)), M - 1)];
+        const float c_ws = wS[min(n0 + tid, N - 1)];
+        const float c_b = has_bias ? bias[min(n0 + tid, N - 1)] : kNoBias;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -171,14 +175,6 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void gemm_w8a8_pt(
 #pragma unroll
                 for (int rr = 0; rr < 16; ++rr) acc[i][j][rr] = 0;
         for (int t0 = 0; t0 < nk; t0 += PW) {
-            {
-                const float *pa = aS + min(m0 + (tid & (BM - 1)), M - 1);
-                const float *pw = wS + min(n0 + tid, N - 1);
-                const float *pb = (has_bias ? bias : wS) + min(n0 + tid, N - 1);
-                asm volatile("global_load_dword %0, %1, off" : "=v"(c_as) : "v"(pa) : "memory");
-                asm volatile("global_load_dword %0, %1, off" : "=v"(c_ws) : "v"(pw) : "memory");
-                asm volatile("global_load_dword %0, %1, off" : "=v"(c_b) : "v"(pb) : "memory");
-            }
 #pragma unroll
             for (int p = 0; p < PW; ++p) {
                 const int t = t0 + p;
@@ -237,10 +233,7 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void gemm_w8a8_pt(
         tile_offs(tile_id(it + 2 < ntiles ? it + 2 : ntiles - 1), aoff_x, woff_x);
 
         if (PRIO) __builtin_amdgcn_s_setprio(0);
-        // ---- epilogue: constants to LDS (their loads are older than the last group's
-        // PW * RING_LOADS ring loads), then transpose + 16-byte stores per wave
-        asm volatile("s_waitcnt vmcnt(%3)" : "+v"(c_as), "+v"(c_ws), "+v"(c_b) : "n"(PW * RING_LOADS) : "memory");
-        if (!has_bias) c_b = kNoBias;
+        // ---- epilogue: constants to LDS, then transpose + 16-byte stores per wave
         if (tid < BM) s_as[as_slot] = c_as;
         if (tid < BN) {
             s_ws[tid] = c_ws;

@@ -12,20 +12,46 @@ namespace enchip {
 typedef int i32x4_p __attribute__((ext_vector_type(4)));
 typedef int i32x16_p __attribute__((ext_vector_type(16)));
 
-// HBM read roof: grid-stride 16-byte loads over a buffer far larger than the MALL.
+// Loads (stores) in flight per lane in the streaming probes. The read probe's kernel
+// time is set by how many bytes each CU keeps in flight, so it issues PROBE_INFLIGHT
+// independent 16-byte loads before using any of them, as the HBM-streaming kernels of
+// this library do (gemv_w8a8_wide keeps up to 12 in flight).
+constexpr int PROBE_INFLIGHT = 8;
+
+// HBM read roof: each block walks chunks of 256 * PROBE_INFLIGHT 16-byte elements,
+// every thread loading PROBE_INFLIGHT of them (coalesced, nontemporal, all issued
+// before the first is summed), over a buffer far larger than the MALL.
 __global__ __launch_bounds__(256) void probe_stream_read(const i32x4_p *__restrict__ src, int64_t n16,
                                                          int *__restrict__ sink) {
+    constexpr int64_t CH = 256 * PROBE_INFLIGHT;
     i32x4_p acc = {0, 0, 0, 0};
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
-        acc += src[i];
+    int64_t i = (int64_t)blockIdx.x * CH + threadIdx.x;
+    for (; i + 256 * (PROBE_INFLIGHT - 1) < n16; i += (int64_t)gridDim.x * CH) {
+        i32x4_p v[PROBE_INFLIGHT];
+#pragma unroll
+        for (int j = 0; j < PROBE_INFLIGHT; ++j) v[j] = __builtin_nontemporal_load(src + i + 256 * j);
+#pragma unroll
+        for (int j = 0; j < PROBE_INFLIGHT; ++j) acc += v[j];
+    }
+    // the last, partial chunk (none when n16 is a multiple of 256 * PROBE_INFLIGHT)
+#pragma unroll
+    for (int j = 0; j < PROBE_INFLIGHT; ++j)
+        if (i + 256 * j < n16) acc += src[i + 256 * j];
     if (acc.x + acc.y + acc.z + acc.w == 0x5eed) sink[0] = 1;  // never true for the fill used
 }
 
-// HBM write roof: grid-stride 16-byte stores.
+// HBM write roof: the same chunks, PROBE_INFLIGHT nontemporal 16-byte stores per thread.
 __global__ __launch_bounds__(256) void probe_stream_write(i32x4_p *__restrict__ dst, int64_t n16) {
+    constexpr int64_t CH = 256 * PROBE_INFLIGHT;
     const i32x4_p v = {1, 2, 3, 4};
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
-        dst[i] = v;
+    int64_t i = (int64_t)blockIdx.x * CH + threadIdx.x;
+    for (; i + 256 * (PROBE_INFLIGHT - 1) < n16; i += (int64_t)gridDim.x * CH) {
+#pragma unroll
+        for (int j = 0; j < PROBE_INFLIGHT; ++j) __builtin_nontemporal_store(v, dst + i + 256 * j);
+    }
+#pragma unroll
+    for (int j = 0; j < PROBE_INFLIGHT; ++j)
+        if (i + 256 * j < n16) dst[i + 256 * j] = v;
 }
 
 // int8 MFMA issue rate: 8 independent v_mfma_i32_32x32x32_i8 accumulator chains per

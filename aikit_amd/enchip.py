@@ -70,6 +70,7 @@ _SIGNATURES = {
     "enchip_gemm_kernel_name": (_int, [_vp, ctypes.c_uint64, _i64, _int, ctypes.c_char_p, _int]),
     "enchip_probe_ceilings": (_int, [_vp, _vp]),
     "enchip_set_small_m": (_int, [_vp, _i64]),
+    "enchip_set_scratch_limit": (_int, [_vp, _i64]),
 }
 SYMBOLS = tuple(_SIGNATURES)
 
@@ -191,6 +192,11 @@ class Context:
 
     def set_small_m(self, max_m: int) -> None:
         self._check(self._lib.enchip_set_small_m(self._h, max_m))
+
+    def set_scratch_limit(self, nbytes: int) -> None:
+        """Cap each growable scratch buffer at nbytes (0: no cap); past it calls decline
+        with ERR_OOM."""
+        self._check(self._lib.enchip_set_scratch_limit(self._h, nbytes))
 
     def set_attention_products(self, mode: int) -> None:
         """ATT_F32 or ATT_SPLIT_BF16: how attention_f32_dev computes its two products."""

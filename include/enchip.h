@@ -16,10 +16,16 @@
  *     PyTorch [out,in] layout, wscale[N], dst[M,N] f32, bias[N] (nullable).
  *   - Host pointers are borrowed for the duration of the call only.
  *   - A context owns all device memory it allocates; enchip_close frees it.
- *   - Host-pointer entry points are serialised by a per-context mutex and are safe
- *     to call from several threads (encoder.EncodeBatch's worker goroutines,
- *     encoder/model.go:214). The *_dev entry points share the context's device
- *     scratch: calls on one context must be issued on one stream at a time.
+ *   - Every entry point takes a per-context mutex, so a context may be called from
+ *     several threads at once (encoder.EncodeBatch's worker goroutines,
+ *     encoder/model.go:214; enccuda serialises the same way,
+ *     gpu/enccuda/backend.go:87,141-142). Host-pointer entry points are synchronous.
+ *   - The context's device scratch (the quantized activations of the entry points
+ *     that quantize themselves, the top-k candidates) is shared by all of them. Work
+ *     that uses it on one stream waits, on the device, for its last use on another
+ *     stream (an event the library records after each such use), so host calls and
+ *     *_dev calls on different streams may be mixed. Under HIP graph capture the
+ *     library records no such event and the caller orders the streams.
  *
  * Numerics (bit-exact against aikit's Go linalg path, default amd64 build):
  *   codes   = quantizeRowInt8Core (linalg/quant.go:43-71), activations' zero row -> scale 0
@@ -78,8 +84,12 @@ int enchip_open(int device, enchip_ctx **out);
  * Replaces Backend.Close (encoder/backend.go:26-27; gpu/enccuda/backend.go). */
 int enchip_close(enchip_ctx *ctx);
 
-/* Last error message of this context (or, for ctx == NULL, of the last failed
- * enchip_open on this thread). Never NULL. Diagnostics only. */
+/* The message of the calling thread's last failed call on ctx (the context's most
+ * recent message when this thread has had none; for ctx == NULL, that of the last
+ * failed enchip_open on this thread). Never NULL. The text is a copy owned by the
+ * calling thread, valid until its next enchip_last_error call, so a failure on another
+ * thread cannot replace or free it. A Go caller reads it on the OS thread that made the
+ * failed call (runtime.LockOSThread around the pair). Diagnostics only. */
 const char *enchip_last_error(const enchip_ctx *ctx);
 
 /* Device facts used for roofline reporting: compute-unit count, peak engine clock
@@ -381,6 +391,15 @@ int enchip_topk_rows_dev(enchip_ctx *ctx, const float *d_scores, int64_t ld, int
  * Synchronous. k <= 1024. */
 int enchip_ann_topk(enchip_ctx *ctx, enchip_weight index, const float *queries, int64_t M,
                     int64_t k, int32_t *hit_index, float *hit_score);
+
+/* Caps each growable device scratch buffer of the context at `bytes` (0, the default:
+ * no cap). A call that would grow scratch past the cap declines with ENCHIP_ERR_OOM
+ * before doing any work, exactly as a failed device allocation does, so a deployment
+ * can bound the memory a context takes beyond its weights, and a test can force the
+ * out-of-memory decline of enccuda's gpuMatmul (gpu/enccuda/backend.go:148-153: a
+ * device allocation failure falls back to the CPU path). Weights are not scratch.
+ * No reference counterpart. */
+int enchip_set_scratch_limit(enchip_ctx *ctx, int64_t bytes);
 
 /* Rows at or below which the small-M (HBM-bound, split-K) kernel runs instead of
  * the tiled MFMA GEMM. Both produce identical bits; this only selects the kernel.

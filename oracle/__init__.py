@@ -66,6 +66,7 @@ def lib() -> ctypes.CDLL:
             "orc_pool_mean": (None, [_f32p, _i64, _i64, _f32p]),
             "orc_l2_normalize": (None, [_f32p, _i64]),
             "cpub_dot_i8": (ctypes.c_int32, [_i8p, _i8p, _i64]),
+            "cpub_attention": (None, [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, ctypes.c_int]),
             "cpub_matmul_bt_w8a8": (None, [_f32p, _i8p, _f32p, _f32p, _i64, _i64, _i64, ctypes.c_int, _i8p, _f32p]),
             "cpub_w8a8_linear": (None, [_f32p, _i64, _i64, _i8p, _f32p, _i64, ctypes.c_void_p, ctypes.c_int,
                                         _f32p, ctypes.c_int, _i8p, _f32p]),
@@ -254,6 +255,14 @@ def cpu_w8a8_linear(a, bq, bscales, bias, act, M, K, N, workers: int, dst=None, 
                            _c(bscales, np.float32), N, _ptr_or_null(b), act, dst.reshape(-1), workers,
                            aq, ascales)
     return dst.reshape(M, N)
+
+
+def cpu_attention(Q, K, V, L, D, heads, workers: int):
+    """orc_attention over `workers` threads (cpu_baseline.c), bit-identical to attention()."""
+    ctx = np.empty(max(L * D, 1), np.float32)
+    lib().cpub_attention(_c(Q, np.float32).reshape(-1), _c(K, np.float32).reshape(-1),
+                         _c(V, np.float32).reshape(-1), ctx, L, D, heads, workers)
+    return ctx[: L * D].reshape(L, D)
 
 
 def cpu_dot_i8(a, b) -> int:

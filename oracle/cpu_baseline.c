@@ -20,6 +20,7 @@
  * Integer codes and int32 accumulators are bit-identical to the scalar oracle.
  */
 #include <immintrin.h>
+#include <math.h>
 #include <pthread.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -166,6 +167,70 @@ void cpub_w8a8_linear(const float *a, int64_t M, int64_t K, const int8_t *bq,
         if (lo >= hi) break;
         jobs[t] = (gelu_job){dst, lo, hi};
         pthread_create(&th[t], NULL, gelu_thread, &jobs[t]);
+        used++;
+    }
+    for (int64_t t = 0; t < used; t++) pthread_join(th[t], NULL);
+    free(th);
+    free(jobs);
+}
+
+/* Scaled dot-product attention for the CPU baseline of the whole encode: orc_attention's
+ * arithmetic (encoder/attention.go:81-121: per head, scores = Q_h K_h^T, softmaxRowScaled,
+ * context = scores V_h), with the heads spread over worker threads (the reference runs its
+ * per-head matmuls through the column fan-out, encoder/scratch.go:186-192 ->
+ * linalg/linalg.go:208-230). Each score and each context element is summed in the same
+ * order, from 0, as orc_attention sums it, with the loops arranged so the compiler can
+ * vectorise across keys and across head columns: the result is bit-identical to
+ * orc_attention. */
+typedef struct {
+    const float *Q, *K, *V;
+    float *ctx;
+    int64_t L, D, hd, h0, h1;
+} attn_job;
+
+static void *attn_thread(void *p) {
+    attn_job *j = (attn_job *)p;
+    const int64_t L = j->L, D = j->D, hd = j->hd;
+    const float scale = (float)(1.0 / sqrt((double)hd));
+    float *kT = (float *)malloc((size_t)(hd * L + L + hd + 1) * sizeof(float));
+    float *sc = kT + hd * L, *c = sc + L;
+    for (int64_t h = j->h0; h < j->h1; h++) {
+        for (int64_t jj = 0; jj < L; jj++)
+            for (int64_t d = 0; d < hd; d++) kT[d * L + jj] = j->K[jj * D + h * hd + d];
+        for (int64_t i = 0; i < L; i++) {
+            const float *q = j->Q + i * D + h * hd;
+            for (int64_t jj = 0; jj < L; jj++) sc[jj] = 0;
+            for (int64_t d = 0; d < hd; d++) {
+                const float qd = q[d], *kr = kT + d * L;
+                for (int64_t jj = 0; jj < L; jj++) sc[jj] += qd * kr[jj];
+            }
+            orc_softmax_row_scaled(sc, L, scale);
+            for (int64_t d = 0; d < hd; d++) c[d] = 0;
+            for (int64_t jj = 0; jj < L; jj++) {
+                const float pj = sc[jj], *vr = j->V + jj * D + h * hd;
+                for (int64_t d = 0; d < hd; d++) c[d] += pj * vr[d];
+            }
+            float *o = j->ctx + i * D + h * hd;
+            for (int64_t d = 0; d < hd; d++) o[d] = c[d];
+        }
+    }
+    free(kT);
+    return NULL;
+}
+
+void cpub_attention(const float *Q, const float *K, const float *V, float *ctx, int64_t L, int64_t D,
+                    int64_t heads, int workers) {
+    if (heads <= 0 || L <= 0) return;
+    int64_t w = workers < 1 ? 1 : (workers > heads ? heads : workers);
+    int64_t per = (heads + w - 1) / w;
+    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)w);
+    attn_job *jobs = (attn_job *)malloc(sizeof(attn_job) * (size_t)w);
+    int64_t used = 0;
+    for (int64_t t = 0; t < w; t++) {
+        int64_t h0 = t * per, h1 = h0 + per < heads ? h0 + per : heads;
+        if (h0 >= h1) break;
+        jobs[t] = (attn_job){Q, K, V, ctx, L, D, D / heads, h0, h1};
+        pthread_create(&th[t], NULL, attn_thread, &jobs[t]);
         used++;
     }
     for (int64_t t = 0; t < used; t++) pthread_join(th[t], NULL);

@@ -325,3 +325,180 @@ def test_device_forward_ln_quant_fusion_is_bit_identical(ctx):
             model.close()
     say(f"{cfg.name}: fused LN + quantization vs unfused, pooled bits equal")
     assert np.array_equal(got[0].view(np.uint32), got[1].view(np.uint32))
+
+
+# ------------------------------------------------------------------ full depth at L = 512
+def _cos(a, b):
+    a, b = np.asarray(a, np.float64).reshape(-1), np.asarray(b, np.float64).reshape(-1)
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def _ref_linear_fn(w, workers):
+    def ref_linear(x, li, name):
+        wq, ws, b, act = w["layers"][li][name]
+        M, K = x.shape
+        return oracle.cpu_w8a8_linear(x, wq, ws, b, act, M, K, wq.shape[0], workers=workers).reshape(M, -1)
+    return ref_linear
+
+
+@pytest.fixture(scope="module")
+def bert_base_full(workers):
+    """Config 4's model (BERT-base: 12 layers, D 768, 12 heads, FFN 3072) on two
+    512-token sequences, and the CPU reference composition's pooled embeddings."""
+    cfg = workloads.BERT_BASE
+    w = model_weights(cfg, seed=104)
+    g = workloads.rng(14)
+    seqs = [g.integers(1000, 30000, size=cfg.seq) for _ in range(2)]
+    say(f"{cfg.name}: CPU reference for {len(seqs)} sequences of {cfg.seq} through {cfg.layers} layers")
+    refs = [encode(ids, w, cfg, _ref_linear_fn(w, workers)) for ids in seqs]
+    return cfg, w, seqs, refs
+
+
+@pytest.mark.parametrize("mode", ["split_bf16", "f32"])
+def test_config4_full_depth_device_encode(ctx, bert_base_full, mode):
+    # The forward bench.py times, at config 4's full depth and sequence length: token ids
+    # -> device embedding rows + LayerNorm -> 12 resident layers (W8A8 linears, fused
+    # attention with the given product mode, residual LayerNorms) -> mean pool + L2, as
+    # DeviceBert.embeddings + DeviceBert.embed; against the reference composition
+    # (encoder/bert.go:260-371, the whole-model cosine gate of encoder/bert_test.go:14-72).
+    import torch
+
+    from aikit_amd.bert_dev import DeviceBert
+
+    cfg, w, seqs, refs = bert_base_full
+    S, L, D = len(seqs), cfg.seq, cfg.hidden
+    model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn)
+    ctx.set_attention_products(enchip.ATT_F32 if mode == "f32" else enchip.ATT_SPLIT_BF16)
+    try:
+        model.set_embeddings(w["word"], w["pos"], w["emb_ln"], typ=w["type"])
+        say(f"{cfg.name} device encode from token ids, {S} x {L}, {cfg.layers} layers, products {mode}")
+        ids = torch.from_numpy(np.concatenate(seqs).astype(np.int32)).cuda()
+        h = torch.empty((S * L, D), device="cuda")
+        pooled = torch.empty((S, D), device="cuda")
+        torch.cuda.synchronize()
+        model.embeddings(ids, S, L, h)
+        model.embed(h, S, L, pooled)
+        torch.cuda.synchronize()
+        dev = pooled.cpu().numpy()
+    finally:
+        model.close()
+        ctx.set_attention_products(enchip.ATT_SPLIT_BF16)
+    for s_, ref in enumerate(refs):
+        cos = _cos(ref, dev[s_])
+        say(f"  seq {s_}: cosine {cos:.9f}")
+        assert cos >= COS_MIN
+
+
+def _attention_f64(Q, K, V, L, D, heads):
+    """The attention of encoder/attention.go:81-121 in float64, rounded to f32 once: the
+    reference composition with only its attention's rounding changed."""
+    hd = D // heads
+    scale = float(np.float32(1.0 / np.sqrt(hd)))
+    out = np.empty((L, D))
+    for h in range(heads):
+        c = slice(h * hd, (h + 1) * hd)
+        s = Q[:, c].astype(np.float64) @ K[:, c].astype(np.float64).T * scale
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        p /= p.sum(axis=1, keepdims=True)
+        out[:, c] = p @ V[:, c].astype(np.float64)
+    return out.astype(np.float32)
+
+
+@pytest.fixture(scope="module")
+def xlmr_large_full(workers):
+    """Config 5's architecture (24 layers, D 1024, 16 heads, FFN 4096) on one 512-token
+    pair and the head's weights, with the reference composition's final hidden state
+    computed twice: with the oracle's f32 attention, and with the same attention in
+    float64 (rounded to f32). The second run measures how far the W8A8 composition drifts
+    from itself when only the f32 rounding of its glue changes -- every per-token
+    requantization turns a last-bit difference into a code step, and 24 layers compound
+    it -- which sets the scale of agreement an exact-in-f32 device forward can reach. The
+    vocabulary is cut to 30522 rows: the table's size does not enter the arithmetic."""
+    cfg = workloads.EncoderConfig("xlmr-large-24l", layers=24, hidden=1024, heads=16, ffn=4096, batch=1, seq=512,
+                                  vocab=30522)
+    w = model_weights(cfg, seed=507)
+    g = workloads.rng(508)
+    ids = g.integers(0, cfg.vocab, size=cfg.seq)
+    D = cfg.hidden
+    head = dict(pw=(g.standard_normal((D, D)) * 0.02).astype(np.float32),
+                pb=(g.standard_normal(D) * 0.02).astype(np.float32),
+                cw=(g.standard_normal((1, D)) * 0.02).astype(np.float32),
+                cb=(g.standard_normal(1) * 0.02).astype(np.float32))
+    ref_linear = _ref_linear_fn(w, workers)
+    L = cfg.seq
+
+    def forward(attention):
+        h = embeddings_in(ids, w, cfg)
+        for li in range(cfg.layers):
+            qkv = ref_linear(h, li, "qkv")
+            ctxv = attention(np.ascontiguousarray(qkv[:, :D]), np.ascontiguousarray(qkv[:, D:2 * D]),
+                             np.ascontiguousarray(qkv[:, 2 * D:]), L, D, cfg.heads)
+            h = oracle.layer_norm((h + ref_linear(ctxv, li, "o")).astype(np.float32), *w["layers"][li]["attn_ln"],
+                                  L, D, 1e-12)
+            ffn = ref_linear(ref_linear(h, li, "ffn_up"), li, "ffn_down")
+            h = oracle.layer_norm((h + ffn).astype(np.float32), *w["layers"][li]["out_ln"], L, D, 1e-12)
+        return h
+
+    say(f"{cfg.name}: CPU reference for one pair of {cfg.seq} through {cfg.layers} layers (f32 and float64 attention)")
+    ref = forward(lambda Q, K, V, L_, D_, H_: oracle.cpu_attention(Q, K, V, L_, D_, H_, workers))
+    ref64 = forward(_attention_f64)
+    return cfg, w, ids, head, ref, ref64
+
+
+def _head_logit(cls, head):
+    """encoder/crossencoder.go:229-236 in float64 over f32 inputs: classifier(tanh(pooler(CLS)))."""
+    pooled = oracle.tanh((cls.astype(np.float64) @ head["pw"].T.astype(np.float64) + head["pb"]).astype(np.float32))
+    return float((pooled.astype(np.float64) @ head["cw"].T.astype(np.float64) + head["cb"])[0])
+
+
+@pytest.mark.parametrize("mode", ["split_bf16", "f32"])
+def test_config5_full_depth_device_rerank(ctx, xlmr_large_full, mode):
+    # Config 5's cross-encoder forward (DeviceBert.embeddings + DeviceBert.rerank, as the
+    # bench runs it) at its full depth and length on one pair, against the reference
+    # composition. Bars:
+    #  * the mean-pooled final hidden state at the north star's cosine >= 0.9999;
+    #  * the [CLS] row (what the head reads): its distance from the reference, 1 - cosine,
+    #    at most twice the reference's own drift when only its attention's rounding
+    #    changes (f32 vs float64; ~4e-4 at 24 layers, measured live) -- a single token's
+    #    state cannot agree more closely than the composition agrees with itself;
+    #  * the device head on the device's own [CLS] row within 1e-5, and the logit within
+    #    the bound the [CLS] difference allows (tanh is 1-Lipschitz, so
+    #    |dlogit| <= |cw| |Wp|_2 |dCLS|).
+    import torch
+
+    from aikit_amd.bert_dev import DeviceBert
+
+    cfg, w, ids, head, ref, ref64 = xlmr_large_full
+    L, D = cfg.seq, cfg.hidden
+    model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn)
+    ctx.set_attention_products(enchip.ATT_F32 if mode == "f32" else enchip.ATT_SPLIT_BF16)
+    try:
+        model.set_embeddings(w["word"], w["pos"], w["emb_ln"], typ=w["type"])
+        say(f"{cfg.name} device rerank from token ids, 1 x {L}, {cfg.layers} layers, products {mode}")
+        dv = {k: torch.from_numpy(v).cuda() for k, v in head.items()}
+        d_ids = torch.from_numpy(ids.astype(np.int32)).cuda()
+        h = torch.empty((L, D), device="cuda")
+        logits = torch.empty((1, 1), device="cuda")
+        torch.cuda.synchronize()
+        model.embeddings(d_ids, 1, L, h)
+        model.rerank(h, 1, L, (dv["pw"], dv["pb"]), (dv["cw"], dv["cb"]), logits)
+        torch.cuda.synchronize()
+        got = float(logits.cpu().numpy()[0, 0])
+        dev_h = h.cpu().numpy()
+    finally:
+        model.close()
+        ctx.set_attention_products(enchip.ATT_SPLIT_BF16)
+    dev_cls, ref_cls = dev_h[0], ref[0]
+    pooled_cos = _cos(dev_h.astype(np.float64).mean(axis=0), ref.astype(np.float64).mean(axis=0))
+    cos = _cos(ref_cls, dev_cls)
+    self_cos = _cos(ref_cls, ref64[0])
+    head_err = abs(got - _head_logit(dev_cls, head))
+    bound = (np.linalg.norm(head["cw"].astype(np.float64)) * np.linalg.norm(head["pw"].astype(np.float64), 2) *
+             np.linalg.norm(dev_cls.astype(np.float64) - ref_cls))
+    ref_logit = _head_logit(ref_cls, head)
+    say(f"  pooled cosine {pooled_cos:.9f}; [CLS] cosine {cos:.9f} (reference vs itself with float64 attention "
+        f"{self_cos:.9f}); logit {got:.6f} vs {ref_logit:.6f} (bound {bound:.3g}); head error {head_err:.3g}")
+    assert pooled_cos >= COS_MIN
+    assert 1 - cos <= 2 * (1 - self_cos)
+    assert head_err <= 1e-5
+    assert abs(got - ref_logit) <= bound + 1e-5

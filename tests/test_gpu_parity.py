@@ -166,25 +166,31 @@ def test_small_m_kernel_matches_gemm_kernel(ctx, M, K, N):
     assert_f32_parity(d1, oracle.w8a8_linear(a, wq, ws, b, 1, M, K, N), "small-M")
 
 
-def test_batch_bit_identical_to_per_op(ctx):
-    # linalg/batch_test.go:13-66: a shared-activation batch equals one call per op.
+def test_batch_bit_identical_to_per_op(ctx, workers):
+    # linalg/batch_test.go:13-66: a shared-activation batch equals one call per op, and
+    # each op equals the reference's MatmulBTW8A8Batch op (linalg/quant.go:319-370): the
+    # oracle's W8A8 linear, bit for bit; ops with and without a bias, one with GELU.
     g = workloads.rng(21)
-    M, K = 300, 768
-    a = workloads.activations(g, M, K)
-    ws_ = [workloads.int8_weights(g, N, K) for N in (768, 768, 768, 3072)]
-    bs = [workloads.bias(g, N) for N in (768, 768, 768, 3072)]
-    handles = [ctx.register_weight(wq, s) for wq, s in ws_]
-    try:
-        say("batch of 4 ops")
-        outs = ctx.batch(a, [(handles[0], bs[0], 0), (handles[1], None, 0), (handles[2], bs[2], 0),
-                             (handles[3], bs[3], 1)])
-        for i, (h, b, act) in enumerate([(handles[0], bs[0], 0), (handles[1], None, 0), (handles[2], bs[2], 0),
-                                         (handles[3], bs[3], 1)]):
-            single = ctx.linear(h, a, bias=b, act=act)
-            assert np.array_equal(bits(outs[i]), bits(single)), f"op {i}"
-    finally:
-        for h in handles:
-            ctx.release_weight(h)
+    for M, K, Ns in [(300, 768, (768, 768, 768, 3072)), (16, 768, (768, 3072)), (2048, 384, (1152, 1536))]:
+        a = workloads.activations(g, M, K)
+        a[min(3, M - 1)] = 0
+        wts = [workloads.int8_weights(g, N, K) for N in Ns]
+        bs = [workloads.bias(g, N) if i % 2 == 0 else None for i, N in enumerate(Ns)]
+        acts = [1 if i == len(Ns) - 1 else 0 for i in range(len(Ns))]
+        handles = [ctx.register_weight(wq, s_) for wq, s_ in wts]
+        try:
+            say(f"batch of {len(Ns)} ops M={M} K={K} N={Ns}")
+            ops = list(zip(handles, bs, acts))
+            outs = ctx.batch(a, ops)
+            for i, ((h, b, act), (wq, ws)) in enumerate(zip(ops, wts)):
+                # the AVX2 restatement, bit-identical to the scalar oracle (test_oracle.py)
+                want = oracle.cpu_w8a8_linear(a, wq, ws, b, act, M, K, h.N, workers=workers)
+                assert_f32_parity(outs[i], want, f"batch op {i}")
+                single = ctx.linear(h, a, bias=b, act=act)
+                assert np.array_equal(bits(outs[i]), bits(single)), f"op {i}"
+        finally:
+            for h in handles:
+                ctx.release_weight(h)
 
 
 def test_row_invariance(ctx):
@@ -299,41 +305,55 @@ def test_device_ceilings_coherent(ctx):
     assert 500 < c["mfma_i8_tops"] < 6000
 
 
-@pytest.mark.parametrize("M,K", [(1500, 768), (300, 1024), (77, 1536)])
-def test_pre_quantized_matches_linear(ctx, M, K):
+@pytest.mark.parametrize("M,K,Ns,small_m", [(1500, 768, (2304, 768), 32), (300, 1024, (2304, 768), 32),
+                                             (77, 1536, (2304, 768), 32), (16, 768, (768, 3072), 32),
+                                             (16, 768, (768, 3072), 0), (256, 384, (16384,), 32)])
+def test_pre_quantized_matches_oracle(ctx, workers, M, K, Ns, small_m):
     # linalg/quant.go:215-234 MatmulBTW8A8Pre: quantize once (QuantizeActivationsInto)
-    # and reuse the codes across weights; bit-identical to the fused call. pre_dev takes
-    # row-major codes (the persistent kernel without AF), the fused call quantizes
-    # fragment-major.
+    # and reuse the codes across weights. pre_dev takes row-major codes: the persistent
+    # kernel without AF for M above the small-M limit, the small-M kernels at config 3's
+    # M=16 (and, with the limit lowered to 0, the persistent kernel at M=16), the
+    # persistent kernel at an ann.FlatI8 M=256 batch. Each output is checked against
+    # the oracle's W8A8 linear and against the fused call.
     import torch
 
-    g = workloads.rng(24 + K)
+    g = workloads.rng(24 + K + M)
     a = workloads.activations(g, M, K)
     a[3] = 0
-    wts = [workloads.int8_weights(g, N, K) for N in (2304, 768)]
-    bs = [workloads.bias(g, N) for N in (2304, 768)]
+    wts = [workloads.int8_weights(g, N, K) for N in Ns]
+    bs = [workloads.bias(g, N) for N in Ns]
+    acts = [i % 2 for i in range(len(Ns))]
     hs = [ctx.register_weight(wq, s) for wq, s in wts]
+    ctx.set_small_m(small_m)
     try:
         for h in hs:
-            assert ", true, " in ctx.gemm_kernel_name(h, M, 0)
+            name = ctx.gemm_kernel_name(h, M, 0)
+            assert ("gemv" in name) == (M <= small_m), name
         st = torch.cuda.Stream()
         with torch.cuda.stream(st):
             da = torch.from_numpy(a).cuda()
-            ldq = K
-            dq = torch.empty((M, ldq), dtype=torch.int8, device="cuda")
+            ldq = (K + 63) // 64 * 64
+            dq = torch.zeros((M, ldq), dtype=torch.int8, device="cuda")
             ds = torch.empty(M, dtype=torch.float32, device="cuda")
-            say(f"quant_rows_dev + pre_dev M={M} K={K}")
+            say(f"quant_rows_dev + pre_dev M={M} K={K} N={Ns} small_m={small_m}")
             ctx.quant_rows_dev(da.data_ptr(), M, K, dq.data_ptr(), ds.data_ptr(), st.cuda_stream, ldq=ldq)
             outs = []
-            for h, b, act in zip(hs, bs, (0, 1)):
+            for h, b, act in zip(hs, bs, acts):
                 db = torch.from_numpy(b).cuda()
                 dd = torch.empty((M, h.N), dtype=torch.float32, device="cuda")
                 ctx.pre_dev(h, dq.data_ptr(), ldq, M, ds.data_ptr(), db.data_ptr(), act, dd.data_ptr(), st.cuda_stream)
                 outs.append((dd, db))
         torch.cuda.synchronize()
-        for (dd, _), h, b, act in zip(outs, hs, bs, (0, 1)):
-            assert np.array_equal(bits(dd.cpu().numpy()), bits(ctx.linear(h, a, bias=b, act=act)))
+        aq, asc = oracle.quantize_activations(a, M, K)
+        assert np.array_equal(dq.cpu().numpy()[:, :K].reshape(-1), aq.reshape(-1))
+        assert np.array_equal(bits(ds.cpu().numpy()), bits(asc))
+        for (dd, _), (wq, ws), h, b, act in zip(outs, wts, hs, bs, acts):
+            got = dd.cpu().numpy()
+            want = oracle.cpu_w8a8_linear(a, wq, ws, b, act, M, K, h.N, workers=workers)
+            assert_f32_parity(got, want, f"pre_dev N={h.N}")
+            assert np.array_equal(bits(got), bits(ctx.linear(h, a, bias=b, act=act)))
     finally:
+        ctx.set_small_m(32)
         for h in hs:
             ctx.release_weight(h)
 

@@ -361,3 +361,73 @@ def test_top_hits_hand_cases():
     idx, _ = oracle.top_hits(s, 6)
     assert idx.tolist() == [1, 2, 6, 0, 4, 5]  # -0 == +0: index order; NaN never kept
     assert oracle.top_hits_selector(s, 6) == [(1, 3.0), (2, 3.0), (6, 2.0), (0, 1.0), (4, -0.0), (5, 0.0)]
+
+
+# ------------------------------------------------------------------ attention glue
+def _attention_f64(Q, K, V, heads):
+    """softmax(Q_h K_h^T * scale) V_h per head in float64 (encoder/attention.go:81-121,
+    scale = float32(1/sqrt(headDim)) as at :87), the closed form the oracle's f32
+    attention must approach."""
+    L, D = Q.shape
+    hd = D // heads
+    scale = float(np.float32(1.0 / math.sqrt(hd)))
+    out = np.empty((L, D))
+    for h in range(heads):
+        c = slice(h * hd, (h + 1) * hd)
+        s = Q[:, c].astype(np.float64) @ K[:, c].astype(np.float64).T * scale
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        p /= p.sum(axis=1, keepdims=True)
+        out[:, c] = p @ V[:, c].astype(np.float64)
+    return out
+
+
+@pytest.mark.parametrize("L,D,heads", [(1, 64, 2), (7, 96, 3), (64, 128, 2), (200, 384, 6)])
+def test_attention_matches_float64_closed_form(L, D, heads):
+    # The oracle's f32 attention (orc_attention) against float64. A transposed V, a wrong
+    # head offset, 1/hd for 1/sqrt(hd) or a softmax over the wrong axis each miss this
+    # bound by orders of magnitude; f32 rounding of 64-term dots stays far inside it.
+    g = workloads.rng(700 + L)
+    Q, K, V = (g.standard_normal((L, D)).astype(np.float32) for _ in range(3))
+    got = oracle.attention(Q, K, V, L, D, heads)
+    ref = _attention_f64(Q, K, V, heads)
+    err = float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1.0)))
+    assert err <= 2e-5, err
+
+
+def test_attention_special_cases():
+    g = workloads.rng(711)
+    D, heads = 64, 2
+    # one token: the softmax is exactly 1 and the context is V's row, bit for bit
+    Q, K, V = (g.standard_normal((1, D)).astype(np.float32) for _ in range(3))
+    assert np.array_equal(oracle.attention(Q, K, V, 1, D, heads), V)
+    # identical keys: every score of a query is equal, so each head's context is the
+    # mean of V's rows
+    L = 16
+    Q = g.standard_normal((L, D)).astype(np.float32)
+    K = np.repeat(g.standard_normal((1, D)).astype(np.float32), L, axis=0)
+    V = g.standard_normal((L, D)).astype(np.float32)
+    got = oracle.attention(Q, K, V, L, D, heads)
+    assert np.allclose(got, np.broadcast_to(V.astype(np.float64).mean(axis=0), (L, D)), rtol=0, atol=1e-6)
+    # one dominant key per query (a large query-key match): the context is that key's V row
+    K = np.eye(L, D, dtype=np.float32) * 40
+    Q = np.eye(L, D, dtype=np.float32) * 40
+    got = oracle.attention(Q, K, V, L, D, 1)
+    assert np.allclose(got, V, rtol=0, atol=1e-6)
+    # permuting keys and values together leaves the context unchanged (up to the f32
+    # summation order)
+    Q, K = (g.standard_normal((L, D)).astype(np.float32) for _ in range(2))
+    perm = g.permutation(L)
+    a = oracle.attention(Q, K, V, L, D, heads)
+    b = oracle.attention(Q, K[perm], V[perm], L, D, heads)
+    assert np.allclose(a, b, rtol=0, atol=1e-5)
+
+
+@pytest.mark.parametrize("L,D,heads,workers", [(1, 64, 2, 4), (33, 96, 3, 2), (128, 384, 6, 16), (512, 768, 12, 8)])
+def test_threaded_attention_bit_identical_to_oracle(L, D, heads, workers):
+    # cpu_baseline.c's attention (the encode's CPU baseline) reorders loops and spreads
+    # heads over threads but sums every element in orc_attention's order.
+    g = workloads.rng(720 + L)
+    Q, K, V = (g.standard_normal((L, D)).astype(np.float32) for _ in range(3))
+    a = oracle.attention(Q, K, V, L, D, heads)
+    b = oracle.cpu_attention(Q, K, V, L, D, heads, workers)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

@@ -50,6 +50,40 @@ struct ThreadError {
 thread_local ThreadError g_thread_error;
 std::atomic<uint64_t> g_next_ctx_id{1};
 
+// Scratch of enchip_w8a8_linear_noalloc_dev: the quantized activations (at most
+// kNoAllocCodeBytes) followed by their per-row scales (at most kNoAllocRows floats). One
+// copy per device, held for the life of the process, shared by every call on that device.
+constexpr size_t kNoAllocCodeBytes = (size_t)32 << 20;
+constexpr int64_t kNoAllocRows = (int64_t)1 << 18;
+constexpr size_t kNoAllocBytes = kNoAllocCodeBytes + (size_t)kNoAllocRows * sizeof(float);
+static __device__ __align__(256) int8_t scratch[kNoAllocBytes];
+
+// Device address of `scratch` per device, resolved once per device (hipGetSymbolAddress
+// with that device current). In host code the name `scratch` is only a stand-in: kernels
+// and copies get these addresses.
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+int8_t *g_noalloc_ptr[kMaxDevices] = {};
+
+// Called by enchip_open with `device` current. On failure the no-alloc entry point
+// declines on this device; everything else works.
+hipError_t noalloc_scratch_init(int device, int8_t **out) {
+    *out = nullptr;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> g(g_noalloc_mu);
+    if (!g_noalloc_ptr[device]) {
+        void *p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return e;
+        }
+        g_noalloc_ptr[device] = static_cast<int8_t *>(p);
+    }
+    *out = g_noalloc_ptr[device];
+    return hipSuccess;
+}
+
 }  // namespace
 
 struct enchip_ctx {
@@ -60,6 +94,8 @@ struct enchip_ctx {
     std::string arch;
     std::mutex mu;
     std::string err = "no error";
+    int8_t *noalloc = nullptr;  // this device's address of `scratch` (NULL: unavailable)
+    std::string noalloc_err;
     std::unordered_map<uint64_t, Weight> weights;
     uint64_t next_handle = 1;
     int64_t small_m = 32;
@@ -442,6 +478,8 @@ int enchip_open(int device, enchip_ctx **out) {
     c->num_cus = prop.multiProcessorCount;
     c->clock_khz = prop.clockRate;
     c->arch = prop.gcnArchName;
+    if ((e = noalloc_scratch_init(device, &c->noalloc)) != hipSuccess)
+        c->noalloc_err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
     if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) {
         g_open_error = std::string("enchip_open: hipStreamCreate: ") + hipGetErrorString(e);
         delete c;
@@ -846,6 +884,37 @@ int enchip_w8a8_linear_dev(enchip_ctx *ctx, enchip_weight h, const float *d_a, i
     if ((rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, d_bias, act_code(act), d_dst, w->N, M, s, af)))
         return rc;
     return scratch_record(ctx, s);
+}
+
+int enchip_w8a8_linear_noalloc_dev(enchip_ctx *ctx, enchip_weight h, const float *d_a, int64_t M,
+                                   const float *d_bias, int act, float *d_dst, void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    Weight *w;
+    int rc = find_weight(ctx, h, &w);
+    if (rc) return rc;
+    if (M < 0 || M > kNoAllocRows) return fail(ctx, ENCHIP_ERR_ARG, "linear_noalloc: bad M=%lld (at most %lld rows)",
+                                               (long long)M, (long long)kNoAllocRows);
+    if (act != ENCHIP_ACT_NONE && act != ENCHIP_ACT_GELU) return fail(ctx, ENCHIP_ERR_ARG, "linear_noalloc: bad act %d", act);
+    if (M == 0) return ENCHIP_OK;
+    if ((w->K > 0 && !d_a) || !d_dst) return fail(ctx, ENCHIP_ERR_ARG, "linear_noalloc: null pointer");
+    if (!ctx->noalloc) return fail(ctx, ENCHIP_ERR_HIP, "linear_noalloc: %s", ctx->noalloc_err.c_str());
+    // fragment-major codes are read up to the next multiple of PT_BM rows, row-major
+    // ones up to row M - 1 (the same routes as enchip_w8a8_linear_dev)
+    const bool af = route_af(ctx, *w, M, d_dst, w->N);
+    const int64_t code_bytes = (af ? round_up(M, enchip::PT_BM) : M) * w->Kp;
+    if ((size_t)code_bytes > kNoAllocCodeBytes)
+        return fail(ctx, ENCHIP_ERR_ARG, "linear_noalloc: M=%lld x padded K %lld needs %lld code bytes, more than the "
+                    "%zu of the no-alloc scratch", (long long)M, (long long)w->Kp, (long long)code_bytes,
+                    kNoAllocCodeBytes);
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    int8_t *aq = ctx->noalloc;
+    float *as = reinterpret_cast<float *>(ctx->noalloc + kNoAllocCodeBytes);
+    // Every code the GEMM reads for rows < M (columns [K, Kp) zero) and every scale is
+    // written by the quantizer first, so nothing from an earlier call is read.
+    if ((rc = launch_quant(ctx, d_a, M, w->K, aq, w->Kp, as, s, af))) return rc;
+    return launch_gemm(ctx, *w, aq, w->Kp, as, d_bias, act_code(act), d_dst, w->N, M, s, af);
 }
 
 int enchip_w8a8_linear(enchip_ctx *ctx, enchip_weight h, const float *a, int64_t M, const float *bias, int act,

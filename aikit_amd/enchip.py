@@ -71,6 +71,7 @@ _SIGNATURES = {
     "enchip_probe_ceilings": (_int, [_vp, _vp]),
     "enchip_set_small_m": (_int, [_vp, _i64]),
     "enchip_set_scratch_limit": (_int, [_vp, _i64]),
+    "enchip_w8a8_linear_noalloc_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _vp, _int, _vp, _vp]),
 }
 SYMBOLS = tuple(_SIGNATURES)
 
@@ -381,6 +382,12 @@ class Context:
                      stream: int = 0) -> None:
         self._check(self._lib.enchip_w8a8_pre_frag_dev(self._h, w.handle, d_aq, ldq, M, d_ascale, d_bias or None, act,
                                                        d_dst, stream or None))
+
+    def linear_noalloc_dev(self, w: Weight, d_a: int, M: int, d_bias: int, act: int, d_dst: int,
+                           stream: int = 0) -> None:
+        """linear_dev through the library's fixed per-device scratch (no allocation)."""
+        self._check(self._lib.enchip_w8a8_linear_noalloc_dev(self._h, w.handle, d_a, M, d_bias or None, act, d_dst,
+                                                             stream or None))
 
     def linear_dev(self, w: Weight, d_a: int, M: int, d_bias: int, act: int, d_dst: int, stream: int = 0) -> None:
         self._check(self._lib.enchip_w8a8_linear_dev(self._h, w.handle, d_a, M, d_bias or None, act, d_dst,

@@ -192,6 +192,20 @@ int enchip_w8a8_linear_dev(enchip_ctx *ctx, enchip_weight w, const float *d_a,
                            int64_t M, const float *d_bias, int act, float *d_dst,
                            void *stream);
 
+/* enchip_w8a8_linear_dev with no device allocation: the same kernels and bits, but the
+ * quantized activations and their scales go to a fixed per-device scratch array of the
+ * library (32 MiB of codes + 2^18 row scales, held by each device the library runs on
+ * until the process ends) instead of the context's growable scratch, and the call makes
+ * no hipMalloc / hipFree or other allocating call. No counterpart in the reference: it is
+ * for callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation). Declines with ENCHIP_ERR_ARG when M > 2^18 or the
+ * codes (M rounded up to 128 rows when the persistent GEMM runs, else M, times K
+ * rounded up to 64) exceed 32 MiB. Every call on a device shares that device's array
+ * (across contexts and streams) and leaves its contents behind: calls that overlap on
+ * one GPU race; the caller serialises them (one stream, or its own events). */
+int enchip_w8a8_linear_noalloc_dev(enchip_ctx *ctx, enchip_weight w, const float *d_a, int64_t M,
+                                   const float *d_bias, int act, float *d_dst, void *stream);
+
 /* Fragment-major twins of enchip_quant_rows_dev / enchip_w8a8_pre_dev (the same
  * reference interfaces, linalg/quant.go:206-234, with a device-native code layout).
  * The codes are laid out as the weights are: byte (r, k) of the M x ldq code matrix at

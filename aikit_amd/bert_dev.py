@@ -10,7 +10,8 @@ matmul seam, docs/task-native-gpu.md:418-427):
   ctx_h = softmax(Q_h.K_h^T/sqrt(hd)).V_h
                                         enchip_attention_f32_dev: every (head, sequence) in
                                         one launch, heads read in place from qkv, scores
-                                        kept on chip (head_dim 32/64, L <= 512); otherwise
+                                        kept on chip (head_dim 32/64; any L with the default
+                                        online-softmax mode, L <= 512 otherwise); otherwise
                                         enchip_matmul_bt_f32_dev, enchip_softmax_rows_scaled_dev,
                                         enchip_matmul_bt_f32_dev through an [S, H, L, L] buffer
   out   = W8A8(ctx, Wo) + b             enchip_w8a8_linear_dev
@@ -131,7 +132,9 @@ class DeviceBert:
         self._bufs = {}
 
     def fused_attention(self, L: int) -> bool:
-        return self.hd in (32, 64) and L <= 512 and self.fused
+        if not self.fused or self.hd not in (32, 64):
+            return False
+        return L <= 512 or self.ctx.attention_products == enchip.ATT_FLASH_BF16
 
     def _buffers(self, S: int, L: int):
         key = (S, L)

@@ -1,0 +1,277 @@
+// attention_flash.h -- scaled dot-product attention with an online softmax and
+// split-bfloat16 products: the third product mode of enchip_attention_f32_dev
+// (ENCHIP_ATT_FLASH_BF16), the device form of encoder/attention.go:81-121 attentionCore up
+// to the context.
+//
+// One workgroup takes 32 * NW queries of one (head, sequence) and walks that head's keys
+// in tiles of FA_KT:
+//   * the tile's K and V rows (f32, read once per workgroup) are split into bfloat16
+//     hi / lo parts (x = hi + lo + e, |e| <= 2^-18 |x|, as attention_split_bf16 splits
+//     them) and staged in LDS, double-buffered, the next tile's loads in flight during
+//     this tile's arithmetic;
+//   * wavefront w owns queries 32w .. 32w + 31 and computes S^T = K Q^T (the A operand K
+//     from LDS, its split Q^T held in registers) on v_mfma_f32_32x32x16_bf16, three
+//     products per pair (hi.lo' + lo.hi' + hi.hi'). In that accumulator lane l holds
+//     query l % 32 and keys 8 (e / 4) + 4 (l / 32) + e % 4 of the 32-key block, so each
+//     query's softmax state is the lane's own (plus one exchange between the two lane
+//     halves);
+//   * online softmax per query: x = s * scale (the reference's first f32 step),
+//     m' = max(m, max x), p = 2^((x - m') log2 e), l' = l 2^((m - m') log2 e) + sum p, and
+//     the context accumulator rescaled by the same factor;
+//   * O^T = V^T P^T on the same MFMA: P^T is the B operand straight from the score
+//     accumulator registers (its keys in the accumulator's order), V^T the A operand read
+//     from LDS, where V is stored transposed with each 16-key block permuted into that
+//     same order (fa_perm16), so no lane exchange is needed;
+//   * at the end the context is divided by l and stored.
+// The arithmetic differs from attentionCore's (exact two-pass softmax, f32 products) in
+// the split products, the running maximum and the hardware 2^x: results agree within the
+// f32 MatmulBT gate (gpu/enccuda/backend_test.go:71-81, <= 2e-4 of max(|ref|, 1)), which
+// the tests hold it to. Any L; head_dim 32 or 64. Non-finite operands give NaN.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "attention_f32.h"
+
+#pragma clang fp contract(off)
+
+namespace enchip {
+
+constexpr int FA_KT = 64;     // keys per LDS tile
+constexpr int FA_WAVES = 8;   // wavefronts (32 queries each) per workgroup in the product
+
+// LDS of one stage: K hi / lo planes, FA_KT rows of HD bf16 (row pitch HD*2 + 16 bytes, so
+// that 32 lanes' 16-byte reads of 32 rows fall in distinct banks), then V^T hi / lo planes,
+// HD rows (one per head-dim column) of FA_KT keys (pitch FA_KT*2 + 16 bytes).
+template <int HD>
+struct FaLayout {
+    static constexpr int KP = HD * 2 + 16;
+    static constexpr int VP = FA_KT * 2 + 16;
+    static constexpr int KPLANE = FA_KT * KP;
+    static constexpr int VPLANE = HD * VP;
+    static constexpr int STAGE = 2 * KPLANE + 2 * VPLANE;
+    static constexpr int BYTES = 2 * STAGE;
+};
+
+__host__ inline int fa_lds_bytes(int hd) {
+    return hd == 64 ? FaLayout<64>::BYTES : FaLayout<32>::BYTES;
+}
+
+// Position of key kk (0..15 within a 16-key block) in the order the score accumulator
+// holds the block's keys as MFMA depth: lane half h has keys 4h..4h+3 and 8+4h..8+4h+3,
+// which become depth 8h..8h+7. Even keys map to even positions and kk + 1 to the next one.
+__device__ __forceinline__ int fa_perm16(int kk) { return (kk & 3) | ((kk & 8) >> 1) | ((kk & 4) << 1); }
+
+constexpr float FA_LOG2E = 1.4426950408889634f;
+
+// NW wavefronts of 32 queries each; a 1-D grid of ceil(L / (32 NW)) * heads * sequences
+// workgroups, FaLayout<HD>::BYTES of dynamic LDS, XCD-aware order (the query blocks of one
+// (head, sequence) on one XCD). Row i of sequence z, head h starts at q/k/v + (z*L + i)*ld
+// + h*HD (16-byte aligned, ld a multiple of 4), out + (z*L + i)*ldo + h*HD; VEC: ldo a
+// multiple of 4 and out 16-byte aligned (16-byte stores).
+template <int HD, int NW, bool VEC>
+__global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t ld,
+    float *__restrict__ out, int64_t ldo, int L, int heads, float scale) {
+    static_assert(HD == 32 || HD == 64, "head dimension");
+    using Lay = FaLayout<HD>;
+    constexpr int NT = 64 * NW;
+    constexpr int QB = 32 * NW;                 // queries per workgroup
+    constexpr int NB = HD / 16;                 // 16-deep head-dim blocks
+    constexpr int NOT = HD / 32;                // 32-column tiles of the context
+    constexpr int KCH = FA_KT * HD / 8;         // 8-float K chunks per tile
+    constexpr int VCH = (FA_KT / 2) * HD / 4;   // (key pair, 4 columns) V items per tile
+    constexpr int KPT = (KCH + NT - 1) / NT;    // K chunks per thread
+    constexpr int VPT = (VCH + NT - 1) / NT;    // V items per thread
+    extern __shared__ __attribute__((aligned(16))) char fa_lds[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane & 31, hf = lane >> 5;
+    const int nqb = (L + QB - 1) / QB;
+    const int logical = xcd_logical_tile(blockIdx.x, gridDim.x);
+    const int head = (logical / nqb) % heads;
+    const int64_t row0 = (int64_t)(logical / nqb / heads) * L;
+    const int qw = (logical % nqb) * QB + 32 * wave;  // this wavefront's first query
+    const bool active = qw < L;
+    const int nt = (L + FA_KT - 1) / FA_KT;
+    const float *kbase = k + row0 * ld + head * HD;
+    const float *vbase = v + row0 * ld + head * HD;
+
+    // Q^T, the B operand of S^T = K Q^T: lane (r, hf) holds query qw + r (rows past L
+    // re-read row L - 1), head dims 16b + 8hf .. +8 of block b, split.
+    bf16x8 qh[NB], ql[NB];
+    {
+        const float *qrow = q + (row0 + min(qw + r, L - 1)) * ld + head * HD;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            float t[8];
+            load8(qrow + 16 * b + 8 * hf, t);
+            split_bf16x8(t, qh[b], ql[b]);
+        }
+    }
+
+    // K / V tile staging: loads of tile t into registers, then split into LDS stage s.
+    // Keys past L re-read row L - 1 (their scores are masked to -inf, so P = 0).
+    f32x4 kr[KPT][2], vr[VPT][2];
+    auto load_tile = [&](int t) {
+        const int kb0 = t * FA_KT;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = tid + NT * i;
+            if (c < KCH) {
+                const int key = min(kb0 + c / (HD / 8), L - 1), col = (c % (HD / 8)) * 8;
+                const float *p = kbase + (int64_t)key * ld + col;
+                kr[i][0] = *reinterpret_cast<const f32x4 *>(p);
+                kr[i][1] = *reinterpret_cast<const f32x4 *>(p + 4);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int c = tid + NT * i;
+            if (c < VCH) {
+                const int pr = c / (HD / 4), col = (c % (HD / 4)) * 4;
+                const int k0 = min(kb0 + 2 * pr, L - 1), k1 = min(kb0 + 2 * pr + 1, L - 1);
+                vr[i][0] = *reinterpret_cast<const f32x4 *>(vbase + (int64_t)k0 * ld + col);
+                vr[i][1] = *reinterpret_cast<const f32x4 *>(vbase + (int64_t)k1 * ld + col);
+            }
+        }
+    };
+    auto store_tile = [&](int s) {
+        char *khi = fa_lds + s * Lay::STAGE, *klo = khi + Lay::KPLANE;
+        char *vhi = klo + Lay::KPLANE, *vlo = vhi + Lay::VPLANE;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int c = tid + NT * i;
+            if (c < KCH) {
+                const int key = c / (HD / 8), col = (c % (HD / 8)) * 8;
+                const float x[8] = {kr[i][0].x, kr[i][0].y, kr[i][0].z, kr[i][0].w,
+                                    kr[i][1].x, kr[i][1].y, kr[i][1].z, kr[i][1].w};
+                bf16x8 h, l;
+                split_bf16x8(x, h, l);
+                *reinterpret_cast<bf16x8 *>(khi + key * Lay::KP + 2 * col) = h;
+                *reinterpret_cast<bf16x8 *>(klo + key * Lay::KP + 2 * col) = l;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int c = tid + NT * i;
+            if (c < VCH) {
+                const int pr = c / (HD / 4), col = (c % (HD / 4)) * 4;
+                const int kk = 2 * pr, pos = (kk & ~15) | fa_perm16(kk & 15);  // kk + 1 goes to pos + 1
+                const float a[4] = {vr[i][0].x, vr[i][0].y, vr[i][0].z, vr[i][0].w};
+                const float b[4] = {vr[i][1].x, vr[i][1].y, vr[i][1].z, vr[i][1].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t hw, lw;
+                    split_pair(a[j], b[j], hw, lw);
+                    *reinterpret_cast<uint32_t *>(vhi + (col + j) * Lay::VP + 2 * pos) = hw;
+                    *reinterpret_cast<uint32_t *>(vlo + (col + j) * Lay::VP + 2 * pos) = lw;
+                }
+            }
+        }
+    };
+
+    f32x16 o[NOT];
+#pragma unroll
+    for (int i = 0; i < NOT; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[i][e] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    load_tile(0);
+    store_tile(0);
+    lds_barrier();
+    for (int t = 0; t < nt; ++t) {
+        if (t + 1 < nt) load_tile(t + 1);  // in flight during this tile's arithmetic
+        if (active) {
+            const char *khi = fa_lds + (t & 1) * Lay::STAGE, *klo = khi + Lay::KPLANE;
+            const char *vhi = klo + Lay::KPLANE, *vlo = vhi + Lay::VPLANE;
+#pragma unroll
+            for (int s = 0; s < FA_KT / 32; ++s) {
+                const int key0 = t * FA_KT + 32 * s;
+                if (key0 >= L) break;  // uniform: no barrier inside
+                // ---- S^T for 32 keys x this wavefront's 32 queries
+                f32x16 acc;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const int off = (32 * s + r) * Lay::KP + 2 * (16 * b + 8 * hf);
+                    const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(khi + off);
+                    const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(klo + off);
+                    acc = mfma_split3(kh, kl, qh[b], ql[b], acc);
+                }
+                // ---- online softmax of query qw + r over these keys
+                float x[16];
+                float mloc = -INFINITY;
+                const bool tail = key0 + 32 > L;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    x[e] = acc[e] * scale;
+                    if (tail && key0 + 8 * (e >> 2) + 4 * hf + (e & 3) >= L) x[e] = -INFINITY;
+                    mloc = fmaxf(mloc, x[e]);
+                }
+                mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+                const float m_new = fmaxf(m_run, mloc);
+                const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * FA_LOG2E);  // 0 on the first tile
+                float psum = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    x[e] = __builtin_amdgcn_exp2f((x[e] - m_new) * FA_LOG2E);
+                    psum += x[e];
+                }
+                l_run = l_run * alpha + psum;
+                m_run = m_new;
+                if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+                    for (int i = 0; i < NOT; ++i)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+                }
+                // ---- O^T += V^T P^T: P^T straight from the accumulator order, split
+                bf16x8 ph[2], pl[2];
+                split_bf16x8(x, ph[0], pl[0]);
+                split_bf16x8(x + 8, ph[1], pl[1]);
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    const int pos = 32 * s + 16 * kb + 8 * hf;
+#pragma unroll
+                    for (int i = 0; i < NOT; ++i) {
+                        const int off = (32 * i + r) * Lay::VP + 2 * pos;
+                        const bf16x8 vh = *reinterpret_cast<const bf16x8 *>(vhi + off);
+                        const bf16x8 vl = *reinterpret_cast<const bf16x8 *>(vlo + off);
+                        o[i] = mfma_split3(vh, vl, ph[kb], pl[kb], o[i]);
+                    }
+                }
+            }
+        }
+        if (t + 1 < nt) store_tile((t + 1) & 1);  // that stage was last read before the previous barrier
+        lds_barrier();
+    }
+
+    // ---- context = O / l: lane (r, hf) holds query qw + r, columns 32i + 8g + 4hf .. +4
+    if (!active) return;
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = 1.0f / l_tot;
+    const int qrow = qw + r;
+    if (qrow >= L) return;
+    float *orow = out + (row0 + qrow) * ldo + head * HD;
+#pragma unroll
+    for (int i = 0; i < NOT; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int c = 32 * i + 8 * g + 4 * hf;
+            const f32x4 val = {o[i][4 * g] * inv, o[i][4 * g + 1] * inv, o[i][4 * g + 2] * inv, o[i][4 * g + 3] * inv};
+            if (VEC) {
+                *reinterpret_cast<f32x4 *>(orow + c) = val;
+            } else {
+                orow[c] = val.x;
+                orow[c + 1] = val.y;
+                orow[c + 2] = val.z;
+                orow[c + 3] = val.w;
+            }
+        }
+}
+
+}  // namespace enchip

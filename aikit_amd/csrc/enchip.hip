@@ -17,6 +17,7 @@
 
 #include "enchip.h"
 #include "attention_f32.h"
+#include "attention_flash.h"
 #include "encoder_ops.h"
 #include "gemm_f32.h"
 #include "gemm_persistent.h"
@@ -97,9 +98,12 @@ struct enchip_ctx {
     int8_t *noalloc = nullptr;  // this device's address of `scratch` (NULL: unavailable)
     std::string noalloc_err;
     std::unordered_map<uint64_t, Weight> weights;
+    // Attention kernels whose dynamic-LDS limit has been raised on this context's device
+    // (hipFuncSetAttribute, once per kernel and byte count rather than once per launch).
+    std::vector<std::pair<const void *, size_t>> lds_set;
     uint64_t next_handle = 1;
     int64_t small_m = 32;
-    int att_products = ENCHIP_ATT_SPLIT_BF16;  // enchip_set_attention_products
+    int att_products = ENCHIP_ATT_FLASH_BF16;  // enchip_set_attention_products
     // Device scratch (grown on demand, freed by enchip_close). Each growable buffer is
     // capped at scratch_limit bytes (enchip_set_scratch_limit; 0 = no cap).
     size_t scratch_limit = 0;
@@ -1299,51 +1303,72 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
                              float scale, void *stream) {
     if (!ctx) return ENCHIP_ERR_ARG;
     std::lock_guard<std::mutex> g(ctx->mu);
+    const bool flash = ctx->att_products == ENCHIP_ATT_FLASH_BF16;
     if (head_dim != 32 && head_dim != 64)
         return fail(ctx, ENCHIP_ERR_ARG, "attention: head_dim must be 32 or 64, got %lld", (long long)head_dim);
-    if (nseq < 0 || L < 0 || L > enchip::ATT_MAX_L || heads < 0 || heads > 65535 || ld < heads * head_dim ||
+    const int64_t max_l = flash ? ((int64_t)1 << 30) : enchip::ATT_MAX_L;
+    if (nseq < 0 || L < 0 || L > max_l || heads < 0 || heads > 65535 || ld < heads * head_dim ||
         ldo < heads * head_dim || ld % 4 != 0 || nseq * L > ((int64_t)1 << 31))
         return fail(ctx, ENCHIP_ERR_ARG,
-                    "attention: bad shape nseq=%lld L=%lld (<= %d) heads=%lld ld=%lld ldo=%lld (ld a multiple of 4 "
-                    "covering heads*head_dim)",
-                    (long long)nseq, (long long)L, enchip::ATT_MAX_L, (long long)heads, (long long)ld, (long long)ldo);
+                    "attention: bad shape nseq=%lld L=%lld (<= %lld in this product mode) heads=%lld ld=%lld ldo=%lld "
+                    "(ld a multiple of 4 covering heads*head_dim)",
+                    (long long)nseq, (long long)L, (long long)max_l, (long long)heads, (long long)ld, (long long)ldo);
     if (nseq == 0 || L == 0 || heads == 0) return ENCHIP_OK;
     if (!d_q || !d_k || !d_v || !d_out) return fail(ctx, ENCHIP_ERR_ARG, "attention: null pointer");
     if ((uintptr_t)d_q % 16 || (uintptr_t)d_k % 16 || (uintptr_t)d_v % 16)
         return fail(ctx, ENCHIP_ERR_ARG, "attention: q, k and v must be 16-byte aligned");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    const bool split_products = ctx->att_products == ENCHIP_ATT_SPLIT_BF16;
-    const size_t lds = (size_t)(split_products ? enchip::att_split_lds_floats((int)L) : enchip::att_lds_floats((int)L)) *
-                       sizeof(float);
     using Kern = void (*)(const float *, const float *, const float *, int64_t, float *, int64_t, int, int, float);
-    const bool split = ctx->att_products == ENCHIP_ATT_SPLIT_BF16;
-    const bool full = L == enchip::ATT_MAX_L;
-    const Kern fn = split ? (head_dim == 64 ? (full ? enchip::attention_split_bf16<64, true>
-                                                    : enchip::attention_split_bf16<64, false>)
-                                            : (full ? enchip::attention_split_bf16<32, true>
-                                                    : enchip::attention_split_bf16<32, false>))
-                          : (head_dim == 64 ? enchip::attention_f32<64> : enchip::attention_f32<32>);
-    HIP_TRY(ctx, hipFuncSetAttribute(reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)lds));
-    // one launch per chunk of sequences whose workgroup count fits a 32-bit grid
-    const int64_t per_seq = ((L + enchip::ATT_QT - 1) / enchip::ATT_QT) * heads;
-    const int64_t chunk = std::max<int64_t>(1, (((int64_t)1 << 32) / (64 * enchip::ATT_WAVES) - 1) / per_seq);
+    Kern fn;
+    size_t lds;
+    int64_t per_seq, threads;
+    if (flash) {
+        const bool vec = ldo % 4 == 0 && (uintptr_t)d_out % 16 == 0;
+        // 8 wavefronts (256 queries) per workgroup: measured faster than 4 at config 4
+        // (245 against 307 us per layer on MI355X): each K / V tile is split once for twice
+        // the queries
+        constexpr int nw = enchip::FA_WAVES;
+        lds = (size_t)enchip::fa_lds_bytes((int)head_dim);
+        per_seq = ((L + 32 * nw - 1) / (32 * nw)) * heads;
+        threads = 64 * nw;
+        fn = head_dim == 64 ? (vec ? enchip::attention_flash_bf16<64, nw, true> : enchip::attention_flash_bf16<64, nw, false>)
+                            : (vec ? enchip::attention_flash_bf16<32, nw, true> : enchip::attention_flash_bf16<32, nw, false>);
+    } else {
+        const bool split = ctx->att_products == ENCHIP_ATT_SPLIT_BF16;
+        const bool full = L == enchip::ATT_MAX_L;
+        lds = (size_t)(split ? enchip::att_split_lds_floats((int)L) : enchip::att_lds_floats((int)L)) * sizeof(float);
+        per_seq = ((L + enchip::ATT_QT - 1) / enchip::ATT_QT) * heads;
+        threads = 64 * enchip::ATT_WAVES;
+        fn = split ? (head_dim == 64 ? (full ? enchip::attention_split_bf16<64, true>
+                                             : enchip::attention_split_bf16<64, false>)
+                                     : (full ? enchip::attention_split_bf16<32, true>
+                                             : enchip::attention_split_bf16<32, false>))
+                   : (head_dim == 64 ? enchip::attention_f32<64> : enchip::attention_f32<32>);
+    }
+    const std::pair<const void *, size_t> key(reinterpret_cast<const void *>(fn), lds);
+    if (std::find(ctx->lds_set.begin(), ctx->lds_set.end(), key) == ctx->lds_set.end()) {
+        HIP_TRY(ctx, hipFuncSetAttribute(key.first, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        ctx->lds_set.push_back(key);
+    }
+    // one launch per chunk of sequences whose global thread index fits 32 bits
+    const int64_t chunk = std::max<int64_t>(1, ((((int64_t)1 << 32) - 1) / threads) / per_seq);
     for (int64_t z0 = 0; z0 < nseq; z0 += chunk) {
         const int64_t nz = std::min<int64_t>(chunk, nseq - z0);
         const dim3 grid((unsigned)(per_seq * nz));
         const int64_t off = z0 * L;
-        hipLaunchKernelGGL(fn, grid, dim3(64 * enchip::ATT_WAVES), lds, s, d_q + off * ld, d_k + off * ld,
-                           d_v + off * ld, ld, d_out + off * ldo, ldo, (int)L, (int)heads, scale);
+        hipLaunchKernelGGL(fn, grid, dim3((unsigned)threads), lds, s, d_q + off * ld, d_k + off * ld, d_v + off * ld,
+                           ld, d_out + off * ldo, ldo, (int)L, (int)heads, scale);
     }
-    return check_launch(ctx, split ? "attention_split_bf16" : "attention_f32");
+    return check_launch(ctx, flash ? "attention_flash_bf16" : "attention");
 }
 
 int enchip_set_attention_products(enchip_ctx *ctx, int mode) {
     if (!ctx) return ENCHIP_ERR_ARG;
     std::lock_guard<std::mutex> g(ctx->mu);
-    if (mode != ENCHIP_ATT_F32 && mode != ENCHIP_ATT_SPLIT_BF16)
-        return fail(ctx, ENCHIP_ERR_ARG, "attention products: mode must be ENCHIP_ATT_F32 or ENCHIP_ATT_SPLIT_BF16");
+    if (mode != ENCHIP_ATT_F32 && mode != ENCHIP_ATT_SPLIT_BF16 && mode != ENCHIP_ATT_FLASH_BF16)
+        return fail(ctx, ENCHIP_ERR_ARG, "attention products: mode must be ENCHIP_ATT_F32, ENCHIP_ATT_SPLIT_BF16 or "
+                    "ENCHIP_ATT_FLASH_BF16");
     ctx->att_products = mode;
     return ENCHIP_OK;
 }

@@ -129,4 +129,33 @@ __device__ __forceinline__ float gelu_f32_series(float x, bool &tail) {
     return 0.5f * x * (1.0f + e);
 }
 
+// gelu_f32_series on four arguments at once: the same operations on each lane of the
+// vector, so each result is bit-identical to gelu_f32_series on that argument. Written
+// on a 4-vector so that the four dependent Horner chains are issued interleaved (with
+// packed f32 instructions disabled the backend splits every vector operation into four
+// independent scalar ones), which hides each VALU instruction's latency behind the other
+// three chains instead of stalling on it. Bit b of the returned mask is set when lane b
+// takes another branch (|u| >= 1 or NaN) and must be taken from gelu_f32.
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4v gelu_f32_series4(f32x4v x, uint32_t &tail) {
+    const f32x4v u = x * 0.7071067811865476f;
+    const f32x4v z = u * u;
+    f32x4v p = z * 1.3122532963802806e-08f;  // p0 * z == z * p0 bit for bit
+    p = p - 1.4503852223150468e-07f;
+    p = p * z + 1.4589169000933706e-06f;
+    p = p * z - 1.3227513227513228e-05f;
+    p = p * z + 1.0683760683760684e-04f;
+    p = p * z - 7.5757575757575758e-04f;
+    p = p * z + 4.6296296296296294e-03f;
+    p = p * z - 2.3809523809523808e-02f;
+    p = p * z + 1.0000000000000001e-01f;
+    p = p * z - 3.3333333333333331e-01f;
+    p = p * z + 1.0f;
+    const f32x4v e = 1.1283791670955126f * u * p;
+    tail = (fabsf(u.x) < 1.0f ? 0u : 1u) | (fabsf(u.y) < 1.0f ? 0u : 2u) | (fabsf(u.z) < 1.0f ? 0u : 4u) |
+           (fabsf(u.w) < 1.0f ? 0u : 8u);
+    return 0.5f * x * (1.0f + e);
+}
+
 }  // namespace enchip

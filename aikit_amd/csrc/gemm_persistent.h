@@ -277,17 +277,14 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void gemm_w8a8_pt(
                 for (int k = 0; k < KR; ++k) v[k] = *reinterpret_cast<const int4 *>(&scr[(rsub + RPL * k) * SP + 4 * c4]);
 #pragma unroll
                 for (int k = 0; k < KR; ++k) {
-                    const int vv[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-                    int o4[4];
-#pragma unroll
-                    for (int qq = 0; qq < 4; ++qq) {
-                        const float y = dequant(vv[qq], asv[k], wsv[qq], bv[qq]);
-                        bool tail;
-                        const float gy = gelu_f32_series(y, tail);
-                        o4[qq] = __float_as_int(tail ? y : gy);
-                        tail_mask |= (uint32_t)tail << (4 * k + qq);
-                    }
-                    *reinterpret_cast<int4 *>(&scr[(rsub + RPL * k) * SP + 4 * c4]) = make_int4(o4[0], o4[1], o4[2], o4[3]);
+                    const f32x4v y = {dequant(v[k].x, asv[k], wsv[0], bv[0]), dequant(v[k].y, asv[k], wsv[1], bv[1]),
+                                      dequant(v[k].z, asv[k], wsv[2], bv[2]), dequant(v[k].w, asv[k], wsv[3], bv[3])};
+                    uint32_t t4;
+                    const f32x4v gy = gelu_f32_series4(y, t4);
+                    const int4 o4 = make_int4(__float_as_int(t4 & 1u ? y.x : gy.x), __float_as_int(t4 & 2u ? y.y : gy.y),
+                                              __float_as_int(t4 & 4u ? y.z : gy.z), __float_as_int(t4 & 8u ? y.w : gy.w));
+                    tail_mask |= t4 << (4 * k);
+                    *reinterpret_cast<int4 *>(&scr[(rsub + RPL * k) * SP + 4 * c4]) = o4;
                 }
                 // Pass 2: the tail values, one per lane per round, so the wavefront runs
                 // the tail code max-popcount times instead of once per mixed instruction.

@@ -468,7 +468,8 @@ def other_configs(ctx, torch, stream, ceilings):
         att[f"{name}_hbm_gbps"] = nbytes / t / 1e9
     # the fused form: both products and the softmax in one launch, scores kept on chip, with
     # its products on the f32 MFMA and (the default) on the bf16 MFMA over split operands
-    for mode, tag in ((enchip.ATT_F32, "fused_f32"), (enchip.ATT_SPLIT_BF16, "fused_split_bf16")):
+    for mode, tag in ((enchip.ATT_F32, "fused_f32"), (enchip.ATT_SPLIT_BF16, "fused_split_bf16"),
+                      (enchip.ATT_FLASH_BF16, "fused_flash_bf16")):
         ctx.set_attention_products(mode)
         for _ in range(3):
             ctx.attention_f32_dev(base, base + D * 4, base + 2 * D * 4, 3 * D, ctxv.data_ptr(), D, S, L, H, hd, 0.125,
@@ -486,7 +487,7 @@ def other_configs(ctx, torch, stream, ceilings):
             att[f"{tag}_frac_fp32_mfma_peak"] = 2 * flops / t / PEAK_FP32_FLOPS
         else:  # three bf16 products per f32 product
             att[f"{tag}_frac_bf16_mfma_peak"] = 3 * 2 * flops / t / PEAK_BF16_FLOPS
-    ctx.set_attention_products(enchip.ATT_SPLIT_BF16)
+    ctx.set_attention_products(enchip.ATT_FLASH_BF16)
     att.update({"S": S, "L": L, "heads": H, "head_dim": hd, "gflop_per_product": flops / 1e9,
                 "kernels": "enchip::gemm_f32_bt_lds<2, 2, false> (QK^T), enchip::gemm_f32_bt_lds<4, 1, true> (PV), "
                            "enchip::attention_f32<64> (fused, f32 MFMA), enchip::attention_split_bf16<64, true> "
@@ -589,10 +590,16 @@ def time_steps(torch, stream, step, steps: int, warmup: int) -> float:
 
 
 def time_ops(torch, stream, model, step, steps: int, hev) -> dict:
-    """Per-operation device durations (ms lists by label) over `steps` steps: a HIP event
-    recorded on the launch stream at each of the model's marks."""
+    """Per-operation device durations (ms lists by label) over `steps` steps, after one
+    untimed step with the same marks: a HIP event recorded on the launch stream at each of
+    the model's marks."""
     marks = []
     sp = stream.cuda_stream
+    warm = []
+    model.mark = lambda label: warm.append(hev.record(hev.create(), sp))
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.synchronize()
 
     def mark(label):
         ev = hev.create()
@@ -629,8 +636,9 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
     table = {}
     for label, ms in per.items():
         n = len(ms)
-        t = sum(ms) / n * 1e-3
-        u = {"launches_per_step": n / steps, "us_per_launch": t * 1e6, "ops": 0.0, "bytes": 0.0}
+        t = sum(ms) / n * 1e-3  # average launch
+        u = {"launches_per_step": n / steps, "us_per_launch": t * 1e6, "us_per_launch_median": sorted(ms)[n // 2] * 1e3,
+             "ops": 0.0, "bytes": 0.0}
         base = label.split(".")[0]
         if label.endswith(".gemm"):
             K, N, act = lin[base]
@@ -644,9 +652,10 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
             u.update(kind="w8a8", bytes=float(13 * M * D + 4 * M + 8 * D),
                      kernel=f"enchip::residual_layer_norm_quant<{cpl}>")
         elif label == "attention":
-            split = ctx.attention_products == 1
+            mode = ctx.attention_products
             u.update(kind="attention", ops=4.0 * S * H * L * L * hd, bytes=float(4 * M * D * 4),
-                     kernel=(f"enchip::attention_split_bf16<{hd}, {'true' if L == 512 else 'false'}>" if split
+                     kernel=(f"enchip::attention_flash_bf16<{hd}, 8, true>" if mode == 2 else
+                             f"enchip::attention_split_bf16<{hd}, {'true' if L == 512 else 'false'}>" if mode == 1
                              else f"enchip::attention_f32<{hd}>"))
         elif label == "embed_rows":
             u.update(kind="row", bytes=float(12 * M * D), kernel="enchip::embed_rows<true>")
@@ -712,7 +721,8 @@ def device_forward(ctx, torch, stream, layers_host, cfg, steps: int = 3, warmup:
     S = cfg.batch
     rate = "pairs_per_s" if head == "rerank" else "seqs_per_s"
     tail = "cross-encoder head (f32 pooler + tanh + classifier)" if head == "rerank" else "pooling + L2"
-    products = "split-bf16" if ctx.attention_products == enchip.ATT_SPLIT_BF16 else "f32"
+    products = {enchip.ATT_F32: "f32", enchip.ATT_SPLIT_BF16: "split-bf16 two-pass",
+                enchip.ATT_FLASH_BF16: "split-bf16 online-softmax"}[ctx.attention_products]
     return {rate: S / t, "ms_per_batch": t * 1e3, "batch": S, "seq_len": cfg.seq, "layers": cfg.layers,
             "hidden": cfg.hidden, "output_finite": finite, "attention_products": products, "steps": steps,
             "note": "%d encodes back to back from token ids (after %d warm-up): embedding rows + LayerNorm, W8A8 "
@@ -911,7 +921,7 @@ def main() -> int:
                 "launches_per_step": ud["launches_per_step"], "share_of_step": ud["ms_per_step"] / step_ms_events}
     if dom == "attention":
         f = ud["ops"] / (ud["us_per_launch"] * 1e-6)
-        split = ctx.attention_products == enchip.ATT_SPLIT_BF16
+        split = ctx.attention_products != enchip.ATT_F32
         step_dom.update({
             "bound": "mfma", "unit": "TFLOP/s", "achieved": f / 1e12,
             "alg_flops_per_launch": ud["ops"],
@@ -940,7 +950,8 @@ def main() -> int:
         "config": {
             "workload": ("bert-base b64xs512 W8A8 encode resident on the device: token ids -> embedding rows + "
                          "LayerNorm -> 12 layers x {W8A8 fused QKV 768->2304 +bias, fused attention (f32 "
-                         "semantics, products on the bf16 MFMA over split operands), W8A8 O 768->768 +bias, "
+                         "semantics: online softmax, products on the bf16 MFMA over split operands), W8A8 O "
+                         "768->768 +bias, "
                          "residual LayerNorm fused with the next quantization, W8A8 FFN-up 768->3072 +bias+GELU, "
                          "W8A8 FFN-down 3072->768 +bias, residual LayerNorm} -> mean pool + L2; every W8A8 "
                          "linear = per-token int8 quant + int8 MFMA GEMM + fused dequant epilogue"),
@@ -949,7 +960,7 @@ def main() -> int:
             "seq_len": cfg.seq,
             "tokens_per_step": cfg.tokens,
             "parallelism": "single GPU",
-            "attention_products": "split-bf16",
+            "attention_products": "split-bf16 online-softmax (ENCHIP_ATT_FLASH_BF16)",
             "seeds": {"weights": 2024, "tables_and_ids": 5},
             "launch": "eager",
         },
@@ -964,14 +975,17 @@ def main() -> int:
         "device": info,
     }
     # the same encode with the attention products on the f32 MFMA
-    ctx.set_attention_products(enchip.ATT_F32)
-    el32 = time_steps(torch, stream, step, max(3, args.steps // 2), 1)
-    ctx.set_attention_products(enchip.ATT_SPLIT_BF16)
-    n32 = max(3, args.steps // 2)
-    result["encode_f32_products"] = {"seqs_per_s": cfg.batch * n32 / el32, "ms_per_step": el32 * 1e3 / n32,
-                                     "steps": n32, "note": "the headline encode with enchip_set_attention_products("
-                                                           "ENCHIP_ATT_F32): both attention products on the f32 MFMA"}
-    log(f"f32-product encode: {result['encode_f32_products']['ms_per_step']:.3f} ms/step")
+    n2 = max(3, args.steps // 2)
+    for mode, key, what in ((enchip.ATT_F32, "encode_f32_products",
+                             "the two-pass attention with both products on the f32 MFMA"),
+                            (enchip.ATT_SPLIT_BF16, "encode_split_bf16_two_pass",
+                             "the two-pass attention (the reference's softmax steps) with split-bf16 products")):
+        ctx.set_attention_products(mode)
+        el2 = time_steps(torch, stream, step, n2, 1)
+        result[key] = {"seqs_per_s": cfg.batch * n2 / el2, "ms_per_step": el2 * 1e3 / n2, "steps": n2,
+                       "note": f"the headline encode with {what} (enchip_set_attention_products)"}
+        log(f"{key}: {result[key]['ms_per_step']:.3f} ms/step")
+    ctx.set_attention_products(enchip.ATT_FLASH_BF16)
     model.close()
 
     if not args.no_other_configs:

@@ -362,26 +362,33 @@ int enchip_pool_mean_l2_dev(enchip_ctx *ctx, const float *d_h, int64_t ldh, int6
  * d_q + (z*L + i)*ld + h*head_dim (likewise K, V; all three share the pitch, as in the
  * fused [tokens, 3D] QKV rows) and the context at d_out + (z*L + i)*ldo + h*head_dim.
  * The score tile of 32 queries stays in on-chip memory (never written to device
- * memory); its softmax follows enchip_softmax_rows_scaled_dev, its products run as set
- * by enchip_set_attention_products, and the result agrees with enchip_matmul_bt_f32_dev
- * + softmax + matmul within the f32 MatmulBT gate (gpu/enccuda/backend_test.go:71-81:
- * <= 2e-4 of max(|ref|, 1); summation order differs). head_dim 32 or 64; L <= 512; ld a
- * multiple of 4; q, k, v 16-byte aligned. */
+ * memory); its softmax and products run as set by enchip_set_attention_products, and the
+ * result agrees with enchip_matmul_bt_f32_dev + softmax + matmul within the f32 MatmulBT
+ * gate (gpu/enccuda/backend_test.go:71-81: <= 2e-4 of max(|ref|, 1); summation order
+ * differs). head_dim 32 or 64; L <= 512 in the two-pass modes, any L in the default mode;
+ * ld a multiple of 4; q, k, v 16-byte aligned. */
 int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k,
                              const float *d_v, int64_t ld, float *d_out, int64_t ldo,
                              int64_t nseq, int64_t L, int64_t heads, int64_t head_dim,
                              float scale, void *stream);
 
-/* How enchip_attention_f32_dev computes its two products (no reference counterpart: a
+/* How enchip_attention_f32_dev computes the attention (no reference counterpart: a
  * device tuning choice, like enchip_set_small_m):
- *   ENCHIP_ATT_SPLIT_BF16 (the default) bf16 MFMA on operands split into two bfloat16
- *                         parts, three products per pair (x.y ~ hi.hi' + hi.lo' + lo.hi',
- *                         each product within 3 * 2^-18 of exact, summed in f32): the same
- *                         gate at 1.5x the speed of ENCHIP_ATT_F32 (MI355X, L = 512).
- *                         Non-finite operands give NaN.
- *   ENCHIP_ATT_F32        f32 MFMA (v_mfma_f32_32x32x2_f32).
- * Applies to later calls on this context. */
-enum enchip_att_products { ENCHIP_ATT_F32 = 0, ENCHIP_ATT_SPLIT_BF16 = 1 };
+ *   ENCHIP_ATT_FLASH_BF16 (the default) one pass over the keys with an online softmax
+ *                         (running maximum, 2^x on the hardware, the context rescaled as
+ *                         the maximum grows, divided by the sum at the end), both products
+ *                         on the bf16 MFMA over operands split into two bfloat16 parts
+ *                         (x.y ~ hi.hi' + hi.lo' + lo.hi', each product within 3 * 2^-18
+ *                         of exact, summed in f32), K and V staged through on-chip memory
+ *                         once per 256 queries. Any L. Within the same f32 MatmulBT gate;
+ *                         2.3x the speed of ENCHIP_ATT_SPLIT_BF16 (MI355X, BERT-base L=512).
+ *   ENCHIP_ATT_SPLIT_BF16 the reference's two-pass softmax (enchip_softmax_rows_scaled_dev's
+ *                         steps) on a 32-query score tile held on chip, products as above.
+ *                         L <= 512.
+ *   ENCHIP_ATT_F32        the same two-pass kernel with f32 MFMA products
+ *                         (v_mfma_f32_32x32x2_f32). L <= 512.
+ * Non-finite operands give NaN in the bf16 modes. Applies to later calls on this context. */
+enum enchip_att_products { ENCHIP_ATT_F32 = 0, ENCHIP_ATT_SPLIT_BF16 = 1, ENCHIP_ATT_FLASH_BF16 = 2 };
 int enchip_set_attention_products(enchip_ctx *ctx, int mode);
 
 /* The k best of each of `rows` rows of n scores (pitch ld), on the device:

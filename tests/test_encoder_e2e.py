@@ -32,6 +32,7 @@ from aikit_amd import enchip, workloads
 pytestmark = pytest.mark.gpu
 
 COS_MIN = 0.9999  # north_star
+ATT_MODES = {"flash_bf16": 2, "split_bf16": 1, "f32": 0}  # enchip_att_products
 
 
 def say(msg):
@@ -137,7 +138,7 @@ def embeddings_in(ids, w, cfg):
     return oracle.layer_norm(h, *w["emb_ln"], L, D, 1e-12)
 
 
-@pytest.mark.parametrize("fused", ["split_bf16", "f32", False])
+@pytest.mark.parametrize("fused", ["flash_bf16", "split_bf16", "f32", False])
 def test_config1_device_resident_forward(ctx, workers, fused):
     # The whole forward on the device (aikit_amd.bert_dev: W8A8 linears, f32 attention
     # products, softmax, residual + LayerNorm, pooling), every activation resident,
@@ -162,7 +163,7 @@ def test_config1_device_resident_forward(ctx, workers, fused):
     from aikit_amd import enchip
 
     model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn, fused=bool(fused))
-    ctx.set_attention_products(enchip.ATT_F32 if fused == "f32" else enchip.ATT_SPLIT_BF16)
+    ctx.set_attention_products(ATT_MODES[fused] if fused else enchip.ATT_FLASH_BF16)
     try:
         say(f"{cfg.name} device-resident forward, {S} sequences of {L}, fused attention {fused}")
         h = torch.from_numpy(h0).cuda()
@@ -173,7 +174,7 @@ def test_config1_device_resident_forward(ctx, workers, fused):
         dev = pooled.cpu().numpy()
     finally:
         model.close()
-        ctx.set_attention_products(enchip.ATT_SPLIT_BF16)  # the default
+        ctx.set_attention_products(enchip.ATT_FLASH_BF16)  # the default
     worst = 1.0
     for s, ids in enumerate(seqs):
         ref = encode(ids, w, cfg, ref_linear)
@@ -354,7 +355,7 @@ def bert_base_full(workers):
     return cfg, w, seqs, refs
 
 
-@pytest.mark.parametrize("mode", ["split_bf16", "f32"])
+@pytest.mark.parametrize("mode", list(ATT_MODES))
 def test_config4_full_depth_device_encode(ctx, bert_base_full, mode):
     # The forward bench.py times, at config 4's full depth and sequence length: token ids
     # -> device embedding rows + LayerNorm -> 12 resident layers (W8A8 linears, fused
@@ -368,7 +369,7 @@ def test_config4_full_depth_device_encode(ctx, bert_base_full, mode):
     cfg, w, seqs, refs = bert_base_full
     S, L, D = len(seqs), cfg.seq, cfg.hidden
     model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn)
-    ctx.set_attention_products(enchip.ATT_F32 if mode == "f32" else enchip.ATT_SPLIT_BF16)
+    ctx.set_attention_products(ATT_MODES[mode])
     try:
         model.set_embeddings(w["word"], w["pos"], w["emb_ln"], typ=w["type"])
         say(f"{cfg.name} device encode from token ids, {S} x {L}, {cfg.layers} layers, products {mode}")
@@ -382,7 +383,7 @@ def test_config4_full_depth_device_encode(ctx, bert_base_full, mode):
         dev = pooled.cpu().numpy()
     finally:
         model.close()
-        ctx.set_attention_products(enchip.ATT_SPLIT_BF16)
+        ctx.set_attention_products(enchip.ATT_FLASH_BF16)  # the default
     for s_, ref in enumerate(refs):
         cos = _cos(ref, dev[s_])
         say(f"  seq {s_}: cosine {cos:.9f}")
@@ -451,7 +452,7 @@ def _head_logit(cls, head):
     return float((pooled.astype(np.float64) @ head["cw"].T.astype(np.float64) + head["cb"])[0])
 
 
-@pytest.mark.parametrize("mode", ["split_bf16", "f32"])
+@pytest.mark.parametrize("mode", list(ATT_MODES))
 def test_config5_full_depth_device_rerank(ctx, xlmr_large_full, mode):
     # Config 5's cross-encoder forward (DeviceBert.embeddings + DeviceBert.rerank, as the
     # bench runs it) at its full depth and length on one pair, against the reference
@@ -471,7 +472,7 @@ def test_config5_full_depth_device_rerank(ctx, xlmr_large_full, mode):
     cfg, w, ids, head, ref, ref64 = xlmr_large_full
     L, D = cfg.seq, cfg.hidden
     model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn)
-    ctx.set_attention_products(enchip.ATT_F32 if mode == "f32" else enchip.ATT_SPLIT_BF16)
+    ctx.set_attention_products(ATT_MODES[mode])
     try:
         model.set_embeddings(w["word"], w["pos"], w["emb_ln"], typ=w["type"])
         say(f"{cfg.name} device rerank from token ids, 1 x {L}, {cfg.layers} layers, products {mode}")
@@ -487,7 +488,7 @@ def test_config5_full_depth_device_rerank(ctx, xlmr_large_full, mode):
         dev_h = h.cpu().numpy()
     finally:
         model.close()
-        ctx.set_attention_products(enchip.ATT_SPLIT_BF16)
+        ctx.set_attention_products(enchip.ATT_FLASH_BF16)  # the default
     dev_cls, ref_cls = dev_h[0], ref[0]
     pooled_cos = _cos(dev_h.astype(np.float64).mean(axis=0), ref.astype(np.float64).mean(axis=0))
     cos = _cos(ref_cls, dev_cls)

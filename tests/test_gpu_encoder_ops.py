@@ -178,7 +178,10 @@ def _attention_f64(qkv, S, L, H, hd, scale):
     return out
 
 
-@pytest.mark.parametrize("products", ["f32", "split_bf16"])
+PRODUCT_MODES = {"f32": 0, "split_bf16": 1, "flash_bf16": 2}  # enchip_att_products
+
+
+@pytest.mark.parametrize("products", list(PRODUCT_MODES))
 @pytest.mark.parametrize("S,L,H,hd", [(2, 128, 12, 64), (1, 512, 4, 64), (3, 77, 6, 32), (2, 40, 2, 64),
                                       (1, 1, 3, 64), (2, 512, 2, 32), (1, 33, 2, 64), (1, 511, 1, 32)])
 def test_fused_attention_matches_f64_and_unfused(ctx, S, L, H, hd, products):
@@ -189,7 +192,7 @@ def test_fused_attention_matches_f64_and_unfused(ctx, S, L, H, hd, products):
 
     from aikit_amd import enchip
 
-    ctx.set_attention_products(enchip.ATT_F32 if products == "f32" else enchip.ATT_SPLIT_BF16)
+    ctx.set_attention_products(PRODUCT_MODES[products])
 
     D = H * hd
     g = workloads.rng(700 + S * L + H + hd)
@@ -217,10 +220,11 @@ def test_fused_attention_matches_f64_and_unfused(ctx, S, L, H, hd, products):
     # and the CPU restatement of the reference's attention for the first sequence
     ref = oracle.attention(qkv[0, :, :D], qkv[0, :, D:2 * D], qkv[0, :, 2 * D:], L, D, H)
     assert oracle.matmul_bt_worst_rel(f[0], ref) <= 2e-4
-    ctx.set_attention_products(enchip.ATT_SPLIT_BF16)  # the default
+    ctx.set_attention_products(enchip.ATT_FLASH_BF16)  # the default
 
 
-def test_split_bf16_attention_error_is_bounded_by_the_split(ctx):
+@pytest.mark.parametrize("mode", [1, 2])
+def test_split_bf16_attention_error_is_bounded_by_the_split(ctx, mode):
     # The split-bfloat16 products against the f64 attention on inputs of larger and mixed
     # magnitude (V spanning 6 decades), each output's error measured against the scale of
     # its terms, sum_j P_j |V_j|, rather than max(|ref|, 1): bf16 alone (2^-9 per product)
@@ -242,11 +246,11 @@ def test_split_bf16_attention_error_is_bounded_by_the_split(ctx):
     torch.cuda.synchronize()
     q = dq.data_ptr()
     try:
-        ctx.set_attention_products(enchip.ATT_SPLIT_BF16)
+        ctx.set_attention_products(mode)
         ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, out.data_ptr(), D, S, L, H, hd, float(scale))
         torch.cuda.synchronize()
     finally:
-        ctx.set_attention_products(enchip.ATT_SPLIT_BF16)  # the default
+        ctx.set_attention_products(enchip.ATT_FLASH_BF16)  # the default
     got = out.cpu().numpy().reshape(S, L, D).astype(np.float64)
     want = _attention_f64(qkv, S, L, H, hd, scale)
     # |ctx| <= sum_j P_j |V_j|: the scale of the P.V sum's terms per output
@@ -264,6 +268,34 @@ def test_split_bf16_attention_error_is_bounded_by_the_split(ctx):
     assert err.max() <= 2e-4
 
 
+@pytest.mark.parametrize("S,L,H,hd", [(1, 1000, 2, 64), (2, 700, 3, 32)])
+def test_flash_attention_beyond_512_keys(ctx, S, L, H, hd):
+    # The online-softmax kernel has no key limit (the two-pass kernels hold a row of
+    # scores in LDS, L <= 512): longer sequences against float64 at the same gate.
+    import torch
+
+    from aikit_amd import enchip
+
+    D = H * hd
+    g = workloads.rng(7100 + L)
+    qkv = g.standard_normal((S, L, 3 * D)).astype(np.float32)
+    scale = np.float32(1.0 / np.sqrt(hd))
+    say(f"flash attention S={S} L={L} H={H} hd={hd}")
+    dq = torch.from_numpy(qkv).cuda()
+    out = torch.full((S * L, D), np.nan, device="cuda")
+    torch.cuda.synchronize()
+    q = dq.data_ptr()
+    try:
+        ctx.set_attention_products(enchip.ATT_FLASH_BF16)
+        ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, out.data_ptr(), D, S, L, H, hd, float(scale))
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_attention_products(enchip.ATT_FLASH_BF16)  # the default
+    wf = oracle.matmul_bt_worst_rel(out.cpu().numpy().reshape(S, L, D), _attention_f64(qkv, S, L, H, hd, scale))
+    say(f"  worst rel {wf:.3g}")
+    assert wf <= 2e-4
+
+
 def test_fused_attention_rejects_unsupported(ctx):
     import torch
 
@@ -273,8 +305,12 @@ def test_fused_attention_rejects_unsupported(ctx):
     p = d.data_ptr()
     with pytest.raises(enchip.EnchipError):  # head_dim 48
         ctx.attention_f32_dev(p, p, p, 48, p, 48, 1, 8, 1, 48, 0.1)
-    with pytest.raises(enchip.EnchipError):  # L above 512
-        ctx.attention_f32_dev(p, p, p, 64, p, 64, 1, 513, 1, 64, 0.1)
+    ctx.set_attention_products(enchip.ATT_SPLIT_BF16)
+    try:
+        with pytest.raises(enchip.EnchipError):  # L above 512 in a two-pass mode
+            ctx.attention_f32_dev(p, p, p, 64, p, 64, 1, 513, 1, 64, 0.1)
+    finally:
+        ctx.set_attention_products(enchip.ATT_FLASH_BF16)  # the default
     torch.cuda.synchronize()
 
 

@@ -412,6 +412,34 @@ int launch_gemm(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, c
     return check_launch(c, "gemm_w8a8");
 }
 
+// True when a linear that quantizes its own activations (d_a [M][K] f32, pitch K) runs
+// as the single small-M launch gemv_w8a8_q: M within the small-M limit, a narrow N (the
+// wide kernel's many workgroups would each quantize every row again), whole float4 rows.
+bool fused_small_m(const enchip_ctx *c, const Weight &w, int64_t M, const float *d_a) {
+    return M >= 1 && M <= c->small_m && !gemv_wide(c, w) && w.K % 4 == 0 && w.K > 0 && w.Kp <= enchip::GVQ_MAX_KP &&
+           (d_a == nullptr || (uintptr_t)d_a % 16 == 0);
+}
+
+// The kernels of gemv_w8a8_q whose dynamic-LDS limit has been raised (process-wide: the
+// attribute belongs to the kernel on the current device).
+int launch_fused_small_m(enchip_ctx *c, const Weight &w, const float *d_a, int64_t M, const float *bias, int epi,
+                         float *out, int64_t ldo, hipStream_t s) {
+    using Kern = void (*)(const float *, const int8_t *, const float *, const float *, void *, int64_t, int, int, int, int);
+    const Kern fn = epi == enchip::EPI_F32_GELU ? enchip::gemv_w8a8_q<enchip::EPI_F32_GELU>
+                                                : enchip::gemv_w8a8_q<enchip::EPI_F32>;
+    const size_t lds = (size_t)enchip::gvq_lds_bytes((int)w.Kp);
+    if (lds > 64 * 1024) {
+        const std::pair<const void *, size_t> key(reinterpret_cast<const void *>(fn), lds);
+        if (std::find(c->lds_set.begin(), c->lds_set.end(), key) == c->lds_set.end()) {
+            HIP_TRY(c, hipFuncSetAttribute(key.first, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            c->lds_set.push_back(key);
+        }
+    }
+    hipLaunchKernelGGL(fn, dim3((unsigned)((w.N + 31) / 32)), dim3(64 * enchip::GV_WAVES), lds, s, d_a, w.d_w, w.d_s,
+                       bias, out, ldo, (int)M, (int)w.N, (int)w.K, (int)w.Kp);
+    return check_launch(c, "gemv_w8a8_q");
+}
+
 int find_weight(enchip_ctx *c, enchip_weight h, Weight **out) {
     auto it = c->weights.find(h);
     if (it == c->weights.end()) return fail(c, ENCHIP_ERR_HANDLE, "unknown weight handle %llu", (unsigned long long)h);
@@ -545,6 +573,8 @@ int enchip_gemm_kernel_name(enchip_ctx *ctx, enchip_weight h, int64_t M, int act
     if (route_af(ctx, *w, M, nullptr, w->N))
         snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, true, %d, %d>", enchip::PT_BM,
                  enchip::PT_BN, enchip::PT_BK, pt_ring(*w), epi, enchip::PT_NW, pt_prio(*w, epi));
+    else if (fused_small_m(ctx, *w, M, nullptr) && epi != enchip::EPI_I32)
+        snprintf(name, sizeof name, "enchip::gemv_w8a8_q<%d>", epi);
     else if (M <= ctx->small_m && gemv_wide(ctx, *w))
         snprintf(name, sizeof name, "enchip::gemv_w8a8_wide<%d>", epi);
     else if (M <= ctx->small_m)
@@ -593,12 +623,22 @@ int enchip_probe_ceilings(enchip_ctx *ctx, enchip_ceilings *out) {
         if ((e = hipMemsetAsync(buf, 0x11, (size_t)bytes, ctx->stream)) != hipSuccess) break;
         const int64_t n16 = bytes / 16;
         const unsigned grid = (unsigned)(ctx->num_cus * 8);
-        float us = 0;
-        if ((e = best_us([&] {
-                 hipLaunchKernelGGL(enchip::probe_stream_read, dim3(grid), dim3(256), 0, ctx->stream,
-                                    (const enchip::i32x4_p *)buf, n16, sink);
-             }, &us)) != hipSuccess) break;
-        out->hbm_read_gbps = (double)bytes / us / 1e3;
+        float us = 0, best = 1e30f;
+        // the best of 8 or 16 loads in flight per lane, 8 or 16 blocks per CU
+        for (int variant = 0; variant < 4; ++variant) {
+            const unsigned vg = (unsigned)(ctx->num_cus * (variant & 1 ? 16 : 8));
+            if ((e = best_us([&] {
+                     if (variant < 2)
+                         hipLaunchKernelGGL(enchip::probe_stream_read<8>, dim3(vg), dim3(256), 0, ctx->stream,
+                                            (const enchip::i32x4_p *)buf, n16, sink);
+                     else
+                         hipLaunchKernelGGL(enchip::probe_stream_read<16>, dim3(vg), dim3(256), 0, ctx->stream,
+                                            (const enchip::i32x4_p *)buf, n16, sink);
+                 }, &us)) != hipSuccess) break;
+            best = std::min(best, us);
+        }
+        if (e != hipSuccess) break;
+        out->hbm_read_gbps = (double)bytes / best / 1e3;
         if ((e = best_us([&] {
                  hipLaunchKernelGGL(enchip::probe_stream_write, dim3(grid), dim3(256), 0, ctx->stream,
                                     (enchip::i32x4_p *)buf, n16);
@@ -610,6 +650,13 @@ int enchip_probe_ceilings(enchip_ctx *ctx, enchip_ceilings *out) {
                  hipLaunchKernelGGL(enchip::probe_mfma_i8, dim3(mgrid), dim3(256), 0, ctx->stream, sink, iters);
              }, &us)) != hipSuccess) break;
         out->mfma_i8_tops = (double)mgrid * 4 * iters * 8 * 65536.0 / us / 1e6;
+        const int viters = 4096;
+        const unsigned vgrid = (unsigned)(ctx->num_cus * 8);  // 8 waves per SIMD
+        if ((e = best_us([&] {
+                 hipLaunchKernelGGL(enchip::probe_valu_f32, dim3(vgrid), dim3(256), 0, ctx->stream,
+                                    reinterpret_cast<float *>(buf), viters, 0.999f, 0.5f);
+             }, &us)) != hipSuccess) break;
+        out->valu_f32_tops = (double)vgrid * 256 * 8 * 2 * viters / us / 1e6;
     } while (0);
     if (e != hipSuccess) rc = fail(ctx, ENCHIP_ERR_HIP, "probe: %s", hipGetErrorString(e));
     if (e0) (void)hipEventDestroy(e0);
@@ -881,6 +928,8 @@ int enchip_w8a8_linear_dev(enchip_ctx *ctx, enchip_weight h, const float *d_a, i
     if ((w->K > 0 && !d_a) || !d_dst) return fail(ctx, ENCHIP_ERR_ARG, "linear: null pointer");
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    if (fused_small_m(ctx, *w, M, d_a))  // one launch, no scratch
+        return launch_fused_small_m(ctx, *w, d_a, M, d_bias, act_code(act), d_dst, w->N, s);
     if ((rc = ensure_act_scratch(ctx, M, w->Kp))) return rc;
     if ((rc = scratch_wait(ctx, s))) return rc;
     const bool af = route_af(ctx, *w, M, d_dst, w->N);
@@ -902,6 +951,11 @@ int enchip_w8a8_linear_noalloc_dev(enchip_ctx *ctx, enchip_weight h, const float
     if (act != ENCHIP_ACT_NONE && act != ENCHIP_ACT_GELU) return fail(ctx, ENCHIP_ERR_ARG, "linear_noalloc: bad act %d", act);
     if (M == 0) return ENCHIP_OK;
     if ((w->K > 0 && !d_a) || !d_dst) return fail(ctx, ENCHIP_ERR_ARG, "linear_noalloc: null pointer");
+    if (fused_small_m(ctx, *w, M, d_a)) {  // one launch that quantizes in on-chip memory
+        HIP_TRY(ctx, hipSetDevice(ctx->device));
+        return launch_fused_small_m(ctx, *w, d_a, M, d_bias, act_code(act), d_dst, w->N,
+                                    stream ? (hipStream_t)stream : ctx->stream);
+    }
     if (!ctx->noalloc) return fail(ctx, ENCHIP_ERR_HIP, "linear_noalloc: %s", ctx->noalloc_err.c_str());
     // fragment-major codes are read up to the next multiple of PT_BM rows, row-major
     // ones up to row M - 1 (the same routes as enchip_w8a8_linear_dev)
@@ -945,10 +999,16 @@ int enchip_w8a8_linear(enchip_ctx *ctx, enchip_weight h, const float *a, int64_t
     if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
     if (bias) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_bias, bias, (size_t)N * sizeof(float), hipMemcpyHostToDevice, s));
     const bool af = route_af(ctx, *w, M, ctx->d_dst, N) && (!acc_debug || route_af(ctx, *w, M, ctx->d_acc, N));
-    if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, w->Kp, ctx->d_as, s, af))) return rc;
-    if ((rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, bias ? ctx->d_bias : nullptr, act_code(act),
-                          ctx->d_dst, N, M, s, af)))
-        return rc;
+    if (!acc_debug && fused_small_m(ctx, *w, M, ctx->d_a)) {
+        if ((rc = launch_fused_small_m(ctx, *w, ctx->d_a, M, bias ? ctx->d_bias : nullptr, act_code(act), ctx->d_dst,
+                                       N, s)))
+            return rc;
+    } else {
+        if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, w->Kp, ctx->d_as, s, af))) return rc;
+        if ((rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, bias ? ctx->d_bias : nullptr, act_code(act),
+                              ctx->d_dst, N, M, s, af)))
+            return rc;
+    }
     if (acc_debug &&
         (rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, nullptr, enchip::EPI_I32, ctx->d_acc, N, M, s, af)))
         return rc;

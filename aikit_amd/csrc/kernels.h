@@ -469,6 +469,96 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8a8(
     }
 }
 
+// gemv_w8a8 with the per-token quantization of its (at most 32) activation rows done in
+// the kernel, so a small-M linear is one launch: every workgroup quantizes all rows into
+// LDS, in the A-operand fragment layout (frag_off), with quant_rows_vec's arithmetic (the
+// absmax of |v| over a row does not depend on the order it is taken in, then s = m/127,
+// 1/s and pack_codes), then runs gemv_w8a8's K split with its A fragments read from LDS.
+// Codes, scales and outputs are those of quant_rows_vec + gemv_w8a8. The rows are read
+// twice from L2 (absmax, then codes) by each of the N/32 workgroups: cheap next to the
+// weight stream at the narrow N this kernel serves. K % 4 == 0, 16-byte aligned rows
+// (pitch K), Kp <= GVQ_MAX_KP; dynamic LDS gvq_lds_bytes(Kp).
+constexpr int GVQ_MAX_KP = 4096;
+__host__ __device__ inline int gvq_lds_bytes(int Kp) {
+    const int codes = Kp * 32, red = GV_WAVES * 16 * 64 * 4;  // the reduction reuses the code area
+    return (codes > red ? codes : red) + 32 * 4;
+}
+
+template <int EPI>
+__global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8a8_q(
+    const float *__restrict__ a, const int8_t *__restrict__ Wf, const float *__restrict__ wS,
+    const float *__restrict__ bias, void *__restrict__ out, int64_t ldo, int M, int N, int K, int Kp) {
+    extern __shared__ __attribute__((aligned(16))) int8_t gvq[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nb = blockIdx.x, nk32 = Kp >> 5, K4 = K >> 2, Kp4 = Kp >> 2;
+    float *s_as = reinterpret_cast<float *>(gvq + (gvq_lds_bytes(Kp) - 32 * 4));
+
+    // ---- quantize rows 0..31 (rows past M: zero codes, never stored)
+    for (int row = wave; row < 32; row += GV_WAVES) {
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(a + (int64_t)min(row, M - 1) * K);
+        float m = 0.0f;
+        if (row < M)
+            for (int k4 = lane; k4 < K4; k4 += 64) {
+                const f32x4 t = src[k4];
+                m = absmax_step(m, t.x);
+                m = absmax_step(m, t.y);
+                m = absmax_step(m, t.z);
+                m = absmax_step(m, t.w);
+            }
+        m = wave_absmax(m);
+        const bool zero = row >= M || m == 0.0f;
+        const float s = zero ? 0.0f : m / 127.0f;
+        const float inv = zero ? 0.0f : 1.0f / s;
+        for (int k4 = lane; k4 < Kp4; k4 += 64) {
+            int word = 0;
+            if (!zero && k4 < K4) {
+                const f32x4 t = src[k4];
+                word = pack_codes(make_float4(t.x, t.y, t.z, t.w), inv);
+            }
+            *reinterpret_cast<int *>(gvq + frag_off(row, 4 * (int64_t)k4, nk32)) = word;
+        }
+        if (lane == 0) s_as[row] = s;
+    }
+    __syncthreads();
+
+    // ---- gemv_w8a8's K split, A fragments from LDS
+    const int8_t *wfr = Wf + (int64_t)nb * nk32 * 1024 + lane * 16;
+    i32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0;
+    for (int k0 = wave; k0 < nk32; k0 += GV_WAVES * GV_BATCH) {
+        i32x4 av[GV_BATCH], b[GV_BATCH];
+#pragma unroll
+        for (int u = 0; u < GV_BATCH; ++u) {
+            const int kk = min(k0 + u * GV_WAVES, nk32 - 1);
+            b[u] = *reinterpret_cast<const i32x4 *>(wfr + (int64_t)kk * 1024);
+            av[u] = *reinterpret_cast<const i32x4 *>(gvq + kk * 1024 + lane * 16);
+        }
+#pragma unroll
+        for (int u = 0; u < GV_BATCH; ++u)
+            if (k0 + u * GV_WAVES < nk32) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[u], b[u], acc, 0, 0, 0);
+    }
+    __syncthreads();  // every wave is done with the codes: the LDS takes the partial sums
+    int *red = reinterpret_cast<int *>(gvq);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
+    __syncthreads();
+
+    const int col = nb * 32 + (lane & 31);
+    const float ws = col < N ? wS[col] : 0.0f;
+    const float bb = (bias != nullptr && col < N) ? bias[col] : kNoBias;
+#pragma unroll
+    for (int rr = 0; rr < 16 / GV_WAVES; ++rr) {
+        const int r = wave * (16 / GV_WAVES) + rr;
+        int sum = 0;
+#pragma unroll
+        for (int w = 0; w < GV_WAVES; ++w) sum += red[(w * 16 + r) * 64 + lane];
+        const int row = acc_row(r, lane);
+        if (row >= M || col >= N) continue;
+        reinterpret_cast<float *>(out)[(int64_t)row * ldo + col] = epilogue<EPI>(sum, s_as[row], ws, bb);
+    }
+}
+
 // Small-M variant for wide N (many output-channel groups, e.g. an int8 ANN index of
 // 10^5..10^6 rows): one wavefront per 32 output channels with the whole K, so no
 // cross-wave reduction, no LDS and no barrier; the weight stream is the only traffic that

@@ -12,32 +12,50 @@ namespace enchip {
 typedef int i32x4_p __attribute__((ext_vector_type(4)));
 typedef int i32x16_p __attribute__((ext_vector_type(16)));
 
-// Loads (stores) in flight per lane in the streaming probes. The read probe's kernel
-// time is set by how many bytes each CU keeps in flight, so it issues PROBE_INFLIGHT
-// independent 16-byte loads before using any of them, as the HBM-streaming kernels of
-// this library do (gemv_w8a8_wide keeps up to 12 in flight).
-constexpr int PROBE_INFLIGHT = 8;
+// HBM read roof: each block walks chunks of 256 * INFLIGHT 16-byte elements, every thread
+// loading INFLIGHT of them (coalesced, nontemporal, all issued before the first is summed),
+// over a buffer far larger than the MALL. The kernel time is set by the bytes each CU keeps
+// in flight, so the host takes the best of several INFLIGHT values and grid sizes, as the
+// HBM-streaming kernels of this library are tuned (gemv_w8a8_wide keeps up to 12 loads in
+// flight per lane).
+constexpr int PROBE_INFLIGHT = 8;  // the write probe's stores per lane per chunk
 
-// HBM read roof: each block walks chunks of 256 * PROBE_INFLIGHT 16-byte elements,
-// every thread loading PROBE_INFLIGHT of them (coalesced, nontemporal, all issued
-// before the first is summed), over a buffer far larger than the MALL.
+template <int INFLIGHT>
 __global__ __launch_bounds__(256) void probe_stream_read(const i32x4_p *__restrict__ src, int64_t n16,
                                                          int *__restrict__ sink) {
-    constexpr int64_t CH = 256 * PROBE_INFLIGHT;
+    constexpr int64_t CH = 256 * INFLIGHT;
     i32x4_p acc = {0, 0, 0, 0};
     int64_t i = (int64_t)blockIdx.x * CH + threadIdx.x;
-    for (; i + 256 * (PROBE_INFLIGHT - 1) < n16; i += (int64_t)gridDim.x * CH) {
-        i32x4_p v[PROBE_INFLIGHT];
+    for (; i + 256 * (INFLIGHT - 1) < n16; i += (int64_t)gridDim.x * CH) {
+        i32x4_p v[INFLIGHT];
 #pragma unroll
-        for (int j = 0; j < PROBE_INFLIGHT; ++j) v[j] = __builtin_nontemporal_load(src + i + 256 * j);
+        for (int j = 0; j < INFLIGHT; ++j) v[j] = __builtin_nontemporal_load(src + i + 256 * j);
 #pragma unroll
-        for (int j = 0; j < PROBE_INFLIGHT; ++j) acc += v[j];
+        for (int j = 0; j < INFLIGHT; ++j) acc += v[j];
     }
-    // the last, partial chunk (none when n16 is a multiple of 256 * PROBE_INFLIGHT)
+    // the last, partial chunk (none when n16 is a multiple of 256 * INFLIGHT)
 #pragma unroll
-    for (int j = 0; j < PROBE_INFLIGHT; ++j)
+    for (int j = 0; j < INFLIGHT; ++j)
         if (i + 256 * j < n16) acc += src[i + 256 * j];
     if (acc.x + acc.y + acc.z + acc.w == 0x5eed) sink[0] = 1;  // never true for the fill used
+}
+
+// f32 VALU issue rate for the non-packed, non-fused operations the bit-exact epilogues
+// are made of: 8 independent chains of x = x * a + b (a v_mul_f32 then a v_add_f32, the
+// multiply-add left unfused) per lane, enough waves per SIMD to cover the issue latency.
+// Counts lane-operations (2 per chain step).
+__global__ __launch_bounds__(256) void probe_valu_f32(float *__restrict__ out, int iters, float a, float b) {
+    float x[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) x[c] = (float)(threadIdx.x + c);
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) x[c] = x[c] * a + b;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) s += x[c];
+    out[blockIdx.x * 256 + threadIdx.x] = s;
 }
 
 // HBM write roof: the same chunks, PROBE_INFLIGHT nontemporal 16-byte stores per thread.

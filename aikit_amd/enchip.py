@@ -25,7 +25,7 @@ OK, ERR_NO_DEVICE, ERR_ARG, ERR_HIP, ERR_OOM, ERR_HANDLE = range(6)
 ACT_NONE, ACT_GELU, ACT_TANH = 0, 1, 2
 ATT_F32, ATT_SPLIT_BF16, ATT_FLASH_BF16 = 0, 1, 2  # enchip_att_products
 B_NK, B_KN = 0, 1  # enchip_matmul_bt_f32_dev b layouts: b[N,K] rows, b[K,N] rows
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # Every symbol include/enchip.h declares, with (restype, argtypes).
 _vp, _i64, _int = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
@@ -84,7 +84,7 @@ class EnchipOp(ctypes.Structure):
 class EnchipCeilings(ctypes.Structure):
     """``enchip_ceilings`` of include/enchip.h."""
     _fields_ = [("hbm_read_gbps", ctypes.c_double), ("hbm_write_gbps", ctypes.c_double),
-                ("mfma_i8_tops", ctypes.c_double)]
+                ("mfma_i8_tops", ctypes.c_double), ("valu_f32_tops", ctypes.c_double)]
 
 
 class EnchipError(RuntimeError):
@@ -189,7 +189,7 @@ class Context:
         c = EnchipCeilings()
         self._check(self._lib.enchip_probe_ceilings(self._h, ctypes.byref(c)))
         return {"hbm_read_gbps": c.hbm_read_gbps, "hbm_write_gbps": c.hbm_write_gbps,
-                "mfma_i8_tops": c.mfma_i8_tops}
+                "mfma_i8_tops": c.mfma_i8_tops, "valu_f32_tops": c.valu_f32_tops}
 
     def set_small_m(self, max_m: int) -> None:
         self._check(self._lib.enchip_set_small_m(self._h, max_m))

@@ -346,14 +346,16 @@ def other_configs(ctx, torch, stream, ceilings):
             "M": M, "K": K, "N": N, "us_per_call": tb * 1e6,
             "hbm_gbps": (nbytes + qbytes) / tb / 1e9, "frac_hbm_peak": (nbytes + qbytes) / tb / PEAK_HBM_BPS,
             "frac_measured_read_ceiling": (nbytes + qbytes) / tb / 1e9 / ceilings["hbm_read_gbps"],
-            "gemv_only_us_per_call": t_gemv, "launch_floor_us": floor_us,
+            "gemv_only_us_per_call": t_gemv, "gemv_only_kernel": "enchip::gemv_w8a8<%d>" % (1 + c3["act"]),
+            "launch_floor_us": floor_us,
             "us_per_call_eager": t_eager * 1e6, "timing": "HIP graph replay" if t_lin is not None else "eager",
             "weight_copies": len(hs), "weight_set_mb": len(hs) * N * K / 1e6,
             "kernel": ctx.gemm_kernel_name(hs[0], M, c3["act"]),
             "cpu_port_us_per_call": cpu_us(ah, wq, ws, bh, c3["act"], M, K, N, 20), "cpu_port_threads": host_threads(),
             "note": "one single-query W8A8 linear per call (enchip_w8a8_linear_dev: per-token quantization + small-M "
                     "GEMM), each call on a distinct registered weight copy (the copies exceed 2 x the 256 MB MALL, "
-                    "so each call streams its weights from HBM); bytes = weights + activations + scales + bias + "
+                    "so each call streams its weights from HBM; at M <= 32 the quantization runs inside the GEMV "
+                    "kernel, one launch per call); bytes = weights + activations + scales + bias + "
                     "f32 output + the quantizer's; us_per_call from one captured graph of all calls (device time); "
                     "gemv_only = the GEMM on pre-quantized codes (enchip_w8a8_pre_dev); launch_floor = an empty "
                     "kernel per call in the same kind of graph"}
@@ -915,6 +917,17 @@ def main() -> int:
         if key == "ffn_up.gemm" else "MFMA issue in the main loop" if key.endswith(".gemm") else "HBM")
     roofline["scope"] = ("the W8A8 path's dominant kernel in the timed encode (by device time per step); "
                          "roofline_step_dominant covers the step's dominant kernel overall")
+    if key == "ffn_up.gemm":
+        # the third roof of this kernel: its epilogue's f32 VALU work (the exact-erf GELU with
+        # no FMA: 36 VALU instructions per output in the branch-free pass, counted in the
+        # kernel's gfx950 ISA) against the measured unfused f32 VALU rate
+        outs = cfg.tokens * cfg.ffn
+        valu_ops = 36.0 * outs
+        t_l = u["us_per_launch"] * 1e-6
+        roofline["valu"] = {"lane_ops_per_output": 36, "outputs_per_launch": outs, "lane_ops_per_launch": valu_ops,
+                            "achieved_t_lane_ops": valu_ops / t_l / 1e12,
+                            "measured_peak_t_lane_ops": ceilings["valu_f32_tops"],
+                            "frac": valu_ops / t_l / 1e12 / ceilings["valu_f32_tops"]}
     dom = max(units, key=lambda k: units[k]["ms_per_step"])
     ud = units[dom]
     step_dom = {"unit_label": dom, "kernel": ud["kernel"], "avg_launch_us": ud["us_per_launch"],

@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define ENCHIP_ABI_VERSION 1
+#define ENCHIP_ABI_VERSION 2
 
 typedef struct enchip_ctx enchip_ctx;
 typedef uint64_t enchip_weight; /* opaque handle; 0 is never a valid handle */
@@ -232,21 +232,27 @@ int enchip_w8a8_pre_frag_dev(enchip_ctx *ctx, enchip_weight w, const int8_t *d_a
 int enchip_frag_route(enchip_ctx *ctx, enchip_weight w, int64_t M, int64_t *ldq);
 
 /* Name of the GEMM kernel instantiation a linear on weight w with M rows and
- * activation act launches (as it appears in rocprofv3 traces), written to buf
+ * activation act launches (as it appears in rocprofv3 traces) when it quantizes its own
+ * 16-byte aligned activations (enchip_w8a8_linear_dev; at small M that is the single
+ * quantize + GEMV kernel), written to buf
  * (NUL-terminated, truncated to len). Diagnostics for attributing profiles to
  * calls; no reference counterpart. */
 int enchip_gemm_kernel_name(enchip_ctx *ctx, enchip_weight w, int64_t M, int act,
                             char *buf, int len);
 
-/* Measured device ceilings (best of 5): HBM streaming read and write over a 1 GiB
- * buffer (past the 256 MiB MALL), and the dense int8 MFMA rate
- * (v_mfma_i32_32x32x32_i8, 8 independent chains per wave, 2 blocks per CU).
+/* Measured device ceilings (best of 5): HBM streaming read (the best of 8 or 16 16-byte
+ * loads in flight per lane and two grid sizes) and write over a 1 GiB buffer (past the
+ * 256 MiB MALL), the dense int8 MFMA rate (v_mfma_i32_32x32x32_i8, 8 independent chains per
+ * wave, 2 blocks per CU), and the f32 VALU rate in lane-operations per second for
+ * unfused, unpacked multiplies and adds (8 independent chains per lane, 8 waves per SIMD):
+ * the roof of the bit-exact epilogues, which are made of exactly those.
  * Replaces gpu/roofline.cu's stream_read / imad_peak / dp4a_peak probes and
  * TestDeviceCeilings (gpu/roofline_test.go:57-140). Allocates and frees 1 GiB. */
 typedef struct enchip_ceilings {
     double hbm_read_gbps;
     double hbm_write_gbps;
     double mfma_i8_tops;
+    double valu_f32_tops; /* T lane-operations / s */
 } enchip_ceilings;
 int enchip_probe_ceilings(enchip_ctx *ctx, enchip_ceilings *out);
 

@@ -63,3 +63,28 @@ def test_null_handling():
     assert lib.enchip_quant_rows(None, None, 0, 0, None, None) == enchip.ERR_ARG
     assert lib.enchip_w8a8_linear(None, 1, None, 0, None, 0, None, None) == enchip.ERR_ARG
     assert lib.enchip_weight_register(None, None, None, 1, 1, None) == enchip.ERR_ARG
+
+
+def test_go_leaf_binds_declared_symbols_at_the_abi_version():
+    # gpu/enchip (the purego leaf a Go build of aikit imports) binds only symbols the
+    # header declares and the library exports, checks the same ABI version the header
+    # defines, and passes each bound function the header's number of arguments. (No Go
+    # toolchain exists in this image, so this is the leaf's compile-free check.)
+    src = "".join(open(os.path.join(ROOT, "gpu", "enchip", f)).read() for f in ("backend.go", "ann.go"))
+    bound = re.findall(r'purego\.RegisterLibFunc\(&(\w+), h, "(enchip_\w+)"\)', src)
+    assert bound, "no RegisterLibFunc calls found"
+    declared = set(declared_functions())
+    lib = ctypes.CDLL(enchip.LIB_PATH)
+    hdr = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "enchip.h")).read(), flags=re.S)
+    for var, name in bound:
+        assert name in declared and hasattr(lib, name), name
+        params = re.search(r"\b" + name + r"\s*\(([^)]*)\)", hdr).group(1).strip()
+        n_c = 0 if params in ("", "void") else params.count(",") + 1
+        sig = re.search(r"\b" + var + r"\s+func\(([^)]*)\)", src).group(1)
+        # each comma-separated piece of a Go parameter list names one parameter
+        # ("wq, wscale unsafe.Pointer" is two)
+        n_go = len([p for p in sig.split(",") if p.strip()])
+        assert n_go == n_c, (name, n_go, n_c)
+    version = int(re.search(r"abiVersion\s*=\s*(\d+)", src).group(1))
+    hdr_version = int(re.search(r"#define ENCHIP_ABI_VERSION (\d+)", hdr).group(1))
+    assert version == hdr_version == enchip.ABI_VERSION

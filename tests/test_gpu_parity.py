@@ -641,3 +641,42 @@ def test_ann_topk_matches_score_batch_plus_top_hits(ctx, M, N, K, k):
     finally:
         ctx.release_weight(w)
     _check_topk(hi, hs, oracle.w8a8_linear(q, codes, scales, None, 0, M, K, N), k, "ann_topk")
+
+
+# ------------------------------------------------------------------ fused small-M quantize + GEMV
+@pytest.mark.parametrize("M,K,N,act", [(1, 768, 768, 0), (16, 768, 3072, 1), (16, 768, 768, 0), (32, 3072, 768, 1),
+                                       (5, 64, 1001, 1), (7, 1540, 96, 0), (32, 4096, 1024, 0), (3, 36, 40, 1)])
+def test_fused_small_m_matches_two_kernels_and_oracle(ctx, M, K, N, act):
+    # At M <= 32 a self-quantizing linear is one launch (gemv_w8a8_q: each workgroup
+    # quantizes the rows into on-chip memory); with want_acc the same call runs the
+    # separate quantizer + gemv_w8a8. Same bits, and the oracle's, including an all-zero
+    # row (scale 0), an Inf row (scale Inf: codes 0) and a row with NaNs (ignored by the
+    # absmax).
+    import torch
+
+    g = workloads.rng(900 + M + K + N)
+    a = workloads.activations(g, M, K)
+    a[0] = 0
+    if M > 2:
+        a[1, 3] = np.inf
+        a[2, ::7] = np.nan
+    wq, ws = workloads.int8_weights(g, N, K)
+    b = workloads.bias(g, N)
+    w = ctx.register_weight(wq, ws)
+    try:
+        name = ctx.gemm_kernel_name(w, M, act)
+        assert "gemv_w8a8_q<" in name, name
+        say(f"fused small-M linear M={M} K={K} N={N} act={act} ({name})")
+        fused = ctx.linear(w, a, bias=b, act=act)
+        split, _ = ctx.linear(w, a, bias=b, act=act, want_acc=True)
+        st = torch.cuda.Stream()
+        with torch.cuda.stream(st):
+            da, db = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+            dd = torch.empty((M, N), dtype=torch.float32, device="cuda")
+            ctx.linear_dev(w, da.data_ptr(), M, db.data_ptr(), act, dd.data_ptr(), st.cuda_stream)
+        torch.cuda.synchronize()
+    finally:
+        ctx.release_weight(w)
+    assert np.array_equal(bits(fused), bits(split))
+    assert np.array_equal(bits(dd.cpu().numpy()), bits(fused))
+    assert_f32_parity(fused, oracle.w8a8_linear(a, wq, ws, b, act, M, K, N), "fused small-M")

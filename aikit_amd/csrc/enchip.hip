@@ -414,9 +414,12 @@ int launch_gemm(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, c
 
 // True when a linear that quantizes its own activations (d_a [M][K] f32, pitch K) runs
 // as the single small-M launch gemv_w8a8_q: M within the small-M limit, a narrow N (the
-// wide kernel's many workgroups would each quantize every row again), whole float4 rows.
+// wide kernel's many workgroups would each quantize every row again), whole float4 rows
+// that fit the kernel's registers, and few enough values that quantizing all of them in
+// every workgroup costs less than a second launch.
 bool fused_small_m(const enchip_ctx *c, const Weight &w, int64_t M, const float *d_a) {
-    return M >= 1 && M <= c->small_m && !gemv_wide(c, w) && w.K % 4 == 0 && w.K > 0 && w.Kp <= enchip::GVQ_MAX_KP &&
+    return M >= 1 && M <= c->small_m && !gemv_wide(c, w) && w.K % 4 == 0 && w.K > 0 && w.K <= enchip::GVQ_MAX_K &&
+           M * w.K <= enchip::GVQ_MAX_MK &&
            (d_a == nullptr || (uintptr_t)d_a % 16 == 0);
 }
 

@@ -474,11 +474,19 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8a8(
 // LDS, in the A-operand fragment layout (frag_off), with quant_rows_vec's arithmetic (the
 // absmax of |v| over a row does not depend on the order it is taken in, then s = m/127,
 // 1/s and pack_codes), then runs gemv_w8a8's K split with its A fragments read from LDS.
-// Codes, scales and outputs are those of quant_rows_vec + gemv_w8a8. The rows are read
-// twice from L2 (absmax, then codes) by each of the N/32 workgroups: cheap next to the
-// weight stream at the narrow N this kernel serves. K % 4 == 0, 16-byte aligned rows
-// (pitch K), Kp <= GVQ_MAX_KP; dynamic LDS gvq_lds_bytes(Kp).
-constexpr int GVQ_MAX_KP = 4096;
+// Codes, scales and outputs are those of quant_rows_vec + gemv_w8a8. The rows are held in
+// registers (K <= GVQ_MAX_K) with all of a wave's loads in flight, and the first batch of
+// weight fragments is loaded while they are quantized. Each of the N/32 workgroups reads
+// the rows again from L2: cheap next to the weight stream at the narrow N this kernel
+// serves. K % 4 == 0, 16-byte aligned rows (pitch K); dynamic LDS gvq_lds_bytes(Kp).
+// (Longer rows are quantized faster by quant_rows_vec than by a two-pass loop here:
+// measured on MI355X at M = 16, K = 3072, N = 768, 14.5 us for the two kernels against
+// 22 us fused.)
+constexpr int GVQ_MAX_K = 1024;
+// M * K above which each workgroup's re-quantization of every row costs more than the
+// separate quant_rows_vec launch (MI355X: M = 16, K = 768 takes 7.0 us fused against 8.2 us
+// for the two kernels; M = 32, K = 1024 takes 12.2 us against 9.6 us).
+constexpr int GVQ_MAX_MK = 16384;
 __host__ __device__ inline int gvq_lds_bytes(int Kp) {
     const int codes = Kp * 32, red = GV_WAVES * 16 * 64 * 4;  // the reduction reuses the code area
     return (codes > red ? codes : red) + 32 * 4;
@@ -489,51 +497,75 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8a8_q(
     const float *__restrict__ a, const int8_t *__restrict__ Wf, const float *__restrict__ wS,
     const float *__restrict__ bias, void *__restrict__ out, int64_t ldo, int M, int N, int K, int Kp) {
     extern __shared__ __attribute__((aligned(16))) int8_t gvq[];
+    constexpr int RPW = 32 / GV_WAVES;  // rows per wavefront
+    constexpr int QCH = GVQ_MAX_K / 256;  // float4 per lane per row, held in registers
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nb = blockIdx.x, nk32 = Kp >> 5, K4 = K >> 2, Kp4 = Kp >> 2;
     float *s_as = reinterpret_cast<float *>(gvq + (gvq_lds_bytes(Kp) - 32 * 4));
 
-    // ---- quantize rows 0..31 (rows past M: zero codes, never stored)
-    for (int row = wave; row < 32; row += GV_WAVES) {
-        const f32x4 *src = reinterpret_cast<const f32x4 *>(a + (int64_t)min(row, M - 1) * K);
+    // ---- this wave's rows (at most RPW; rows past M are never stored, so they are neither
+    // loaded nor quantized: their LDS codes are left as they are) in registers, all loads
+    // issued at once, before the weight loads: loads complete in issue order, so the
+    // quantization below waits only for its own rows while the weights are in flight
+    const int nrows = M > wave ? (M - wave + GV_WAVES - 1) / GV_WAVES : 0;  // <= RPW
+    f32x4 v[RPW][QCH];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+        if (j >= nrows) break;
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(a + (int64_t)(wave + GV_WAVES * j) * K);
+#pragma unroll
+        for (int c = 0; c < QCH; ++c) v[j][c] = src[min(lane + 64 * c, K4 - 1)];
+    }
+    // this wave's first batch of weight fragments
+    const int8_t *wfr = Wf + (int64_t)nb * nk32 * 1024 + lane * 16;
+    i32x4 b[GV_BATCH];
+#pragma unroll
+    for (int u = 0; u < GV_BATCH; ++u)
+        b[u] = *reinterpret_cast<const i32x4 *>(wfr + (int64_t)min(wave + u * GV_WAVES, nk32 - 1) * 1024);
+
+    // ---- quantize
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+        if (j >= nrows) break;
+        const int row = wave + GV_WAVES * j;
         float m = 0.0f;
-        if (row < M)
-            for (int k4 = lane; k4 < K4; k4 += 64) {
-                const f32x4 t = src[k4];
-                m = absmax_step(m, t.x);
-                m = absmax_step(m, t.y);
-                m = absmax_step(m, t.z);
-                m = absmax_step(m, t.w);
+#pragma unroll
+        for (int c = 0; c < QCH; ++c)
+            if (lane + 64 * c < K4) {
+                m = absmax_step(m, v[j][c].x);
+                m = absmax_step(m, v[j][c].y);
+                m = absmax_step(m, v[j][c].z);
+                m = absmax_step(m, v[j][c].w);
             }
         m = wave_absmax(m);
-        const bool zero = row >= M || m == 0.0f;
-        const float s = zero ? 0.0f : m / 127.0f;
-        const float inv = zero ? 0.0f : 1.0f / s;
-        for (int k4 = lane; k4 < Kp4; k4 += 64) {
-            int word = 0;
-            if (!zero && k4 < K4) {
-                const f32x4 t = src[k4];
-                word = pack_codes(make_float4(t.x, t.y, t.z, t.w), inv);
-            }
-            *reinterpret_cast<int *>(gvq + frag_off(row, 4 * (int64_t)k4, nk32)) = word;
+        const bool zero = m == 0.0f;
+        const float sc = zero ? 0.0f : m / 127.0f;
+        const float inv = zero ? 0.0f : 1.0f / sc;
+#pragma unroll
+        for (int c = 0; c < QCH; ++c) {
+            const int k4 = lane + 64 * c;
+            if (k4 < Kp4)
+                *reinterpret_cast<int *>(gvq + frag_off(row, 4 * (int64_t)k4, nk32)) =
+                    (!zero && k4 < K4) ? pack_codes(make_float4(v[j][c].x, v[j][c].y, v[j][c].z, v[j][c].w), inv) : 0;
         }
-        if (lane == 0) s_as[row] = s;
+        if (lane == 0) s_as[row] = sc;
     }
     __syncthreads();
 
-    // ---- gemv_w8a8's K split, A fragments from LDS
-    const int8_t *wfr = Wf + (int64_t)nb * nk32 * 1024 + lane * 16;
+    // ---- gemv_w8a8's K split, A fragments from LDS (the first batch's weights loaded above)
     i32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0;
     for (int k0 = wave; k0 < nk32; k0 += GV_WAVES * GV_BATCH) {
-        i32x4 av[GV_BATCH], b[GV_BATCH];
+        if (k0 != wave) {
 #pragma unroll
-        for (int u = 0; u < GV_BATCH; ++u) {
-            const int kk = min(k0 + u * GV_WAVES, nk32 - 1);
-            b[u] = *reinterpret_cast<const i32x4 *>(wfr + (int64_t)kk * 1024);
-            av[u] = *reinterpret_cast<const i32x4 *>(gvq + kk * 1024 + lane * 16);
+            for (int u = 0; u < GV_BATCH; ++u)
+                b[u] = *reinterpret_cast<const i32x4 *>(wfr + (int64_t)min(k0 + u * GV_WAVES, nk32 - 1) * 1024);
         }
+        i32x4 av[GV_BATCH];
+#pragma unroll
+        for (int u = 0; u < GV_BATCH; ++u)
+            av[u] = *reinterpret_cast<const i32x4 *>(gvq + min(k0 + u * GV_WAVES, nk32 - 1) * 1024 + lane * 16);
 #pragma unroll
         for (int u = 0; u < GV_BATCH; ++u)
             if (k0 + u * GV_WAVES < nk32) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[u], b[u], acc, 0, 0, 0);

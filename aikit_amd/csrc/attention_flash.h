@@ -15,8 +15,8 @@
 //     query l % 32 and keys 8 (e / 4) + 4 (l / 32) + e % 4 of the 32-key block, so each
 //     query's softmax state is the lane's own (plus one exchange between the two lane
 //     halves);
-//   * online softmax per query: x = s * scale (the reference's first f32 step),
-//     m' = max(m, max x), p = 2^((x - m') log2 e), l' = l 2^((m - m') log2 e) + sum p, and
+//   * online softmax per query in base 2: with c = |scale| log2 e (Q negated when scale
+//     < 0), m' = max(m, c max s), p = 2^(fma(s, c, -m')), l' = l 2^(m - m') + sum p, and
 //     the context accumulator rescaled by the same factor;
 //   * O^T = V^T P^T on the same MFMA: P^T is the B operand straight from the score
 //     accumulator registers (its keys in the accumulator's order), V^T the A operand read
@@ -24,7 +24,8 @@
 //     same order (fa_perm16), so no lane exchange is needed;
 //   * at the end the context is divided by l and stored.
 // The arithmetic differs from attentionCore's (exact two-pass softmax, f32 products) in
-// the split products, the running maximum and the hardware 2^x: results agree within the
+// the split products, the running maximum, the fused base-2 exponent and the hardware
+// 2^x: results agree within the
 // f32 MatmulBT gate (gpu/enccuda/backend_test.go:71-81, <= 2e-4 of max(|ref|, 1)), which
 // the tests hold it to. Any L; head_dim 32 or 64. Non-finite operands give NaN.
 #pragma once
@@ -40,7 +41,15 @@
 namespace enchip {
 
 constexpr int FA_KT = 64;     // keys per LDS tile
-constexpr int FA_WAVES = 8;   // wavefronts (32 queries each) per workgroup in the product
+// Wavefronts (32 queries each) per workgroup in the product: 16 (512 queries, 1024
+// threads) once L > FA_WIDE_L, else 8. Each K / V tile is split into LDS once per
+// workgroup, so wider workgroups split each head's keys fewer times: at BERT-base
+// shape (L = 512, 64 sequences, 12 heads) 16 wavefronts took 201 us against 215-221 us
+// for 8 and 270 us for 4 on MI355X, bit-identical results. Up to L = 256, 16 wavefronts
+// would leave half of each workgroup idle.
+constexpr int FA_WAVES = 8;
+constexpr int FA_WAVES_WIDE = 16;
+constexpr int FA_WIDE_L = 256;
 
 // LDS of one stage: K hi / lo planes, FA_KT rows of HD bf16 (row pitch HD*2 + 16 bytes, so
 // that 32 lanes' 16-byte reads of 32 rows fall in distinct banks), then V^T hi / lo planes,
@@ -100,6 +109,11 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
 
     // Q^T, the B operand of S^T = K Q^T: lane (r, hf) holds query qw + r (rows past L
     // re-read row L - 1), head dims 16b + 8hf .. +8 of block b, split.
+    // A negative scale is applied as |scale| to -Q (an exact negation), so that the scores'
+    // factor c = |scale| log2 e is never negative and the running maximum of the raw scores
+    // s gives that of c s.
+    const bool neg = scale < 0.0f;
+    const float c = fabsf(scale) * FA_LOG2E;
     bf16x8 qh[NB], ql[NB];
     {
         const float *qrow = q + (row0 + min(qw + r, L - 1)) * ld + head * HD;
@@ -107,6 +121,10 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
         for (int b = 0; b < NB; ++b) {
             float t[8];
             load8(qrow + 16 * b + 8 * hf, t);
+            if (neg) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) t[i] = -t[i];
+            }
             split_bf16x8(t, qh[b], ql[b]);
         }
     }
@@ -114,14 +132,18 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
     // K / V tile staging: loads of tile t into registers, then split into LDS stage s.
     // Keys past L re-read row L - 1 (their scores are masked to -inf, so P = 0).
     f32x4 kr[KPT][2], vr[VPT][2];
+    // The tile's base rows are uniform 64-bit pointers; each lane adds a 32-bit offset
+    // (key within the tile times ld: the host keeps FA_KT * ld below 2^31).
+    const int ld32 = (int)ld;
     auto load_tile = [&](int t) {
-        const int kb0 = t * FA_KT;
+        const int kb0 = t * FA_KT, klast = L - 1 - kb0;  // last key of the head, tile-relative
+        const float *kt = kbase + (int64_t)kb0 * ld, *vt = vbase + (int64_t)kb0 * ld;
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int c = tid + NT * i;
             if (c < KCH) {
-                const int key = min(kb0 + c / (HD / 8), L - 1), col = (c % (HD / 8)) * 8;
-                const float *p = kbase + (int64_t)key * ld + col;
+                const int key = min(c / (HD / 8), klast), col = (c % (HD / 8)) * 8;
+                const float *p = kt + (key * ld32 + col);
                 kr[i][0] = *reinterpret_cast<const f32x4 *>(p);
                 kr[i][1] = *reinterpret_cast<const f32x4 *>(p + 4);
             }
@@ -131,9 +153,9 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
             const int c = tid + NT * i;
             if (c < VCH) {
                 const int pr = c / (HD / 4), col = (c % (HD / 4)) * 4;
-                const int k0 = min(kb0 + 2 * pr, L - 1), k1 = min(kb0 + 2 * pr + 1, L - 1);
-                vr[i][0] = *reinterpret_cast<const f32x4 *>(vbase + (int64_t)k0 * ld + col);
-                vr[i][1] = *reinterpret_cast<const f32x4 *>(vbase + (int64_t)k1 * ld + col);
+                const int k0 = min(2 * pr, klast), k1 = min(2 * pr + 1, klast);
+                vr[i][0] = *reinterpret_cast<const f32x4 *>(vt + (k0 * ld32 + col));
+                vr[i][1] = *reinterpret_cast<const f32x4 *>(vt + (k1 * ld32 + col));
             }
         }
     };
@@ -202,25 +224,36 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
                     const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(klo + off);
                     acc = mfma_split3(kh, kl, qh[b], ql[b], acc);
                 }
-                // ---- online softmax of query qw + r over these keys
-                float x[16];
-                float mloc = -INFINITY;
+                // ---- online softmax of query qw + r over these keys, in base-2 units
+                // (y = c s): p = 2^(y - m) with y - m as one fused multiply-add. Keys past L
+                // (only in the last sub-tile, a uniform branch) are left out of the maximum
+                // and get p = 0.
+                // Element e holds key key0 + 4 hf + 8 (e / 4) + e % 4: past L when its
+                // constant part 8 (e / 4) + e % 4 reaches lim.
                 const bool tail = key0 + 32 > L;
+                const int lim = L - key0 - 4 * hf;
+                if (tail) {
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    x[e] = acc[e] * scale;
-                    if (tail && key0 + 8 * (e >> 2) + 4 * hf + (e & 3) >= L) x[e] = -INFINITY;
-                    mloc = fmaxf(mloc, x[e]);
+                    for (int e = 0; e < 16; ++e)
+                        if (8 * (e >> 2) + (e & 3) >= lim) acc[e] = -INFINITY;
                 }
-                mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-                const float m_new = fmaxf(m_run, mloc);
-                const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * FA_LOG2E);  // 0 on the first tile
+                float mloc = acc[0];
+#pragma unroll
+                for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, acc[e]);
+                mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));  // finite: key0 < L is in it
+                const float m_new = fmaxf(m_run, mloc * c);      // c >= 0: max of c s = c max s
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
+                float x[16];
                 float psum = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    x[e] = __builtin_amdgcn_exp2f((x[e] - m_new) * FA_LOG2E);
-                    psum += x[e];
+                for (int e = 0; e < 16; ++e) x[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[e], c, -m_new));
+                if (tail) {  // also where c = 0 made the masked keys' exponent NaN
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        if (8 * (e >> 2) + (e & 3) >= lim) x[e] = 0.0f;
                 }
+#pragma unroll
+                for (int e = 0; e < 16; ++e) psum += x[e];
                 l_run = l_run * alpha + psum;
                 m_run = m_new;
                 if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {

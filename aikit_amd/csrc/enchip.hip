@@ -338,8 +338,9 @@ int persistent_grid(const enchip_ctx *c, int64_t tiles) {
 // Main-loop wave priority of gemm_w8a8_pt for a weight and epilogue: raised for the
 // bias-only epilogue when N or the padded K is at least 1024. Measured on MI355X (same
 // process, interleaved): BERT-base QKV and FFN-down 4-10% faster, XLM-R-large QKV, O and
-// FFN-down 6-9% faster; BERT-base O (768 x 768) 4% slower, so it keeps 0; the GELU
-// epilogue unchanged either way.
+// FFN-down 6-9% faster; BERT-base O (768 x 768) 4% slower, so it keeps 0. The GELU
+// epilogue keeps 0: raised, BERT-base FFN-up took 206 us per launch in the encode against
+// 189 us (it ran 3-5% faster on uniformly random codes, whose pre-activations differ).
 int pt_prio(const Weight &w, int epi) {
     return epi == enchip::EPI_F32 && (w.N >= 1024 || w.Kp >= 1024) ? 1 : 0;
 }
@@ -1371,10 +1372,11 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
         return fail(ctx, ENCHIP_ERR_ARG, "attention: head_dim must be 32 or 64, got %lld", (long long)head_dim);
     const int64_t max_l = flash ? ((int64_t)1 << 30) : enchip::ATT_MAX_L;
     if (nseq < 0 || L < 0 || L > max_l || heads < 0 || heads > 65535 || ld < heads * head_dim ||
-        ldo < heads * head_dim || ld % 4 != 0 || nseq * L > ((int64_t)1 << 31))
+        ldo < heads * head_dim || ld % 4 != 0 || nseq * L > ((int64_t)1 << 31) ||
+        (flash && ld > INT32_MAX / enchip::FA_KT))  // the flash kernel's 32-bit in-tile offsets
         return fail(ctx, ENCHIP_ERR_ARG,
                     "attention: bad shape nseq=%lld L=%lld (<= %lld in this product mode) heads=%lld ld=%lld ldo=%lld "
-                    "(ld a multiple of 4 covering heads*head_dim)",
+                    "(ld a multiple of 4 covering heads*head_dim, below 2^25 in the flash mode)",
                     (long long)nseq, (long long)L, (long long)max_l, (long long)heads, (long long)ld, (long long)ldo);
     if (nseq == 0 || L == 0 || heads == 0) return ENCHIP_OK;
     if (!d_q || !d_k || !d_v || !d_out) return fail(ctx, ENCHIP_ERR_ARG, "attention: null pointer");
@@ -1388,15 +1390,18 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
     int64_t per_seq, threads;
     if (flash) {
         const bool vec = ldo % 4 == 0 && (uintptr_t)d_out % 16 == 0;
-        // 8 wavefronts (256 queries) per workgroup: measured faster than 4 at config 4
-        // (245 against 307 us per layer on MI355X): each K / V tile is split once for twice
-        // the queries
-        constexpr int nw = enchip::FA_WAVES;
+        constexpr int nw8 = enchip::FA_WAVES, nw16 = enchip::FA_WAVES_WIDE;
+        const bool wide = L > enchip::FA_WIDE_L;
+        const int nw = wide ? nw16 : nw8;
         lds = (size_t)enchip::fa_lds_bytes((int)head_dim);
         per_seq = ((L + 32 * nw - 1) / (32 * nw)) * heads;
         threads = 64 * nw;
-        fn = head_dim == 64 ? (vec ? enchip::attention_flash_bf16<64, nw, true> : enchip::attention_flash_bf16<64, nw, false>)
-                            : (vec ? enchip::attention_flash_bf16<32, nw, true> : enchip::attention_flash_bf16<32, nw, false>);
+        if (wide)
+            fn = head_dim == 64 ? (vec ? enchip::attention_flash_bf16<64, nw16, true> : enchip::attention_flash_bf16<64, nw16, false>)
+                                : (vec ? enchip::attention_flash_bf16<32, nw16, true> : enchip::attention_flash_bf16<32, nw16, false>);
+        else
+            fn = head_dim == 64 ? (vec ? enchip::attention_flash_bf16<64, nw8, true> : enchip::attention_flash_bf16<64, nw8, false>)
+                                : (vec ? enchip::attention_flash_bf16<32, nw8, true> : enchip::attention_flash_bf16<32, nw8, false>);
     } else {
         const bool split = ctx->att_products == ENCHIP_ATT_SPLIT_BF16;
         const bool full = L == enchip::ATT_MAX_L;

@@ -656,7 +656,8 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
         elif label == "attention":
             mode = ctx.attention_products
             u.update(kind="attention", ops=4.0 * S * H * L * L * hd, bytes=float(4 * M * D * 4),
-                     kernel=(f"enchip::attention_flash_bf16<{hd}, 8, true>" if mode == 2 else
+                     # the library's flash launch: 16 wavefronts per workgroup once L > 256, else 8
+                     kernel=(f"enchip::attention_flash_bf16<{hd}, {16 if L > 256 else 8}, true>" if mode == 2 else
                              f"enchip::attention_split_bf16<{hd}, {'true' if L == 512 else 'false'}>" if mode == 1
                              else f"enchip::attention_f32<{hd}>"))
         elif label == "embed_rows":

@@ -268,6 +268,38 @@ def test_split_bf16_attention_error_is_bounded_by_the_split(ctx, mode):
     assert err.max() <= 2e-4
 
 
+@pytest.mark.parametrize("L", [77, 300])
+@pytest.mark.parametrize("scale", [-0.2, 0.0, 0.4])
+def test_flash_attention_any_scale(ctx, L, scale):
+    # The online softmax runs in base 2 on c = |scale| log2 e with Q negated for a negative
+    # scale (an exact negation), so the running maximum stays that of the scaled scores;
+    # scale 0 gives the mean of V, including over the padded keys of the last tile. Both
+    # workgroup widths (8 wavefronts up to L = 256, 16 above).
+    import torch
+
+    from aikit_amd import enchip
+
+    S, H, hd = 2, 3, 64
+    D = H * hd
+    g = workloads.rng(7300 + L)
+    qkv = g.standard_normal((S, L, 3 * D)).astype(np.float32)
+    dq = torch.from_numpy(qkv).cuda()
+    out = torch.full((S * L, D), np.nan, device="cuda")
+    torch.cuda.synchronize()
+    q = dq.data_ptr()
+    ctx.set_attention_products(enchip.ATT_FLASH_BF16)
+    ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, out.data_ptr(), D, S, L, H, hd, float(scale))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(S, L, D)
+    want = _attention_f64(qkv, S, L, H, hd, np.float32(scale))
+    wf = oracle.matmul_bt_worst_rel(got, want)
+    say(f"flash attention L={L} scale={scale}: worst rel {wf:.3g}")
+    assert np.isfinite(got).all() and wf <= 2e-4
+    if scale == 0.0:  # every query attends uniformly: the mean of V over the L keys
+        mean_v = qkv[:, :, 2 * D:].astype(np.float64).mean(axis=1, keepdims=True)
+        assert np.abs(got - mean_v).max() <= 1e-5
+
+
 @pytest.mark.parametrize("S,L,H,hd", [(1, 1000, 2, 64), (2, 700, 3, 32)])
 def test_flash_attention_beyond_512_keys(ctx, S, L, H, hd):
     # The online-softmax kernel has no key limit (the two-pass kernels hold a row of
@@ -305,6 +337,8 @@ def test_fused_attention_rejects_unsupported(ctx):
     p = d.data_ptr()
     with pytest.raises(enchip.EnchipError):  # head_dim 48
         ctx.attention_f32_dev(p, p, p, 48, p, 48, 1, 8, 1, 48, 0.1)
+    with pytest.raises(enchip.EnchipError):  # row pitch past the flash kernel's 32-bit tile offsets
+        ctx.attention_f32_dev(p, p, p, (1 << 25) + 4, p, 64, 1, 8, 1, 64, 0.1)
     ctx.set_attention_products(enchip.ATT_SPLIT_BF16)
     try:
         with pytest.raises(enchip.EnchipError):  # L above 512 in a two-pass mode

@@ -1391,7 +1391,11 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
     if (flash) {
         const bool vec = ldo % 4 == 0 && (uintptr_t)d_out % 16 == 0;
         constexpr int nw8 = enchip::FA_WAVES, nw16 = enchip::FA_WAVES_WIDE;
-        const bool wide = L > enchip::FA_WIDE_L;
+        // 16 wavefronts once L > 256 and their grid still has a workgroup per CU: on
+        // small grids the 8-wavefront form's twice as many workgroups spread further
+        // (L = 1000 over 8 heads x sequences: 51 against 79 us)
+        const int64_t wide_grid = ((L + 32 * nw16 - 1) / (32 * nw16)) * heads * nseq;
+        const bool wide = L > enchip::FA_WIDE_L && wide_grid >= ctx->num_cus;
         const int nw = wide ? nw16 : nw8;
         lds = (size_t)enchip::fa_lds_bytes((int)head_dim);
         per_seq = ((L + 32 * nw - 1) / (32 * nw)) * heads;

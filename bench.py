@@ -624,9 +624,14 @@ def time_ops(torch, stream, model, step, steps: int, hev) -> dict:
     return per
 
 
+def fa_waves(ctx, S: int, L: int, H: int) -> int:
+    """Wavefronts per workgroup of the library's flash attention launch (its dispatch rule)."""
+    return 16 if L > 256 and -(-L // 512) * H * S >= ctx.device_info()["num_cus"] else 8
+
+
 def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
     """Per-kernel table of one encode step: launches per step, mean device time per launch,
-    algorithmic work per launch (SURVEY-style figures: 2MNK ops and M*K + N*K + 4M + 8N +
+    algorithmic work per launch (2MNK ops and M*K + N*K + 4M + 8N +
     4MN bytes for a W8A8 GEMM; 5 B per element + 4 B per row for a quantizer; the fused
     residual LayerNorm + quantizer reads h and y and writes h and the codes, 13 B per
     element + 4 B per row; attention 4 L^2 hd flops per head and its Q, K, V, context
@@ -656,8 +661,9 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
         elif label == "attention":
             mode = ctx.attention_products
             u.update(kind="attention", ops=4.0 * S * H * L * L * hd, bytes=float(4 * M * D * 4),
-                     # the library's flash launch: 16 wavefronts per workgroup once L > 256, else 8
-                     kernel=(f"enchip::attention_flash_bf16<{hd}, {16 if L > 256 else 8}, true>" if mode == 2 else
+                     # the library's flash launch: 16 wavefronts per workgroup once L > 256 and
+                     # that grid has a workgroup per CU, else 8
+                     kernel=(f"enchip::attention_flash_bf16<{hd}, {fa_waves(ctx, S, L, H)}, true>" if mode == 2 else
                              f"enchip::attention_split_bf16<{hd}, {'true' if L == 512 else 'false'}>" if mode == 1
                              else f"enchip::attention_f32<{hd}>"))
         elif label == "embed_rows":

@@ -31,7 +31,7 @@ from aikit_amd import enchip, workloads
 
 pytestmark = pytest.mark.gpu
 
-COS_MIN = 0.9999  # north_star
+COS_MIN = 0.9999  # the encoder parity bar: cosine against the reference composition
 ATT_MODES = {"flash_bf16": 2, "split_bf16": 1, "f32": 0}  # enchip_att_products
 
 
@@ -143,7 +143,7 @@ def test_config1_device_resident_forward(ctx, workers, fused):
     # The whole forward on the device (aikit_amd.bert_dev: W8A8 linears, f32 attention
     # products, softmax, residual + LayerNorm, pooling), every activation resident,
     # against the CPU reference composition of the same model. Attention and LayerNorm
-    # sum in a different order on the device, so the bar is the north star's cosine.
+    # sum in a different order on the device, so the bar is the encoder parity cosine (COS_MIN).
     import torch
 
     from aikit_amd.bert_dev import DeviceBert
@@ -192,7 +192,7 @@ def test_config5_shaped_cross_encoder_on_device(ctx, workers):
     # linears, the oracle's attention / LayerNorm / TanhF32, the f32 head in float64).
     # Attention and LayerNorm sum in another order on the device; a last-bit difference
     # can move one per-token int8 code in the next linear, so the chain is held to the
-    # north star's cosine on the [CLS] hidden state, and the head alone (f32 MatmulBT,
+    # encoder parity cosine (COS_MIN) on the [CLS] hidden state, and the head alone (f32 MatmulBT,
     # bias, TanhF32, classifier) to 1e-5 on the device's own [CLS] rows.
     import torch
 
@@ -261,7 +261,7 @@ def test_config5_shaped_cross_encoder_on_device(ctx, workers):
 def test_config1_device_forward_from_token_ids(ctx, workers):
     # The whole encode on the device from token ids: embedding rows + LayerNorm
     # (DeviceBert.embeddings), the layers, pooling; against the CPU reference composition
-    # from the same ids (encode), to the north star's cosine.
+    # from the same ids (encode), to the encoder parity cosine (COS_MIN).
     import torch
 
     from aikit_amd.bert_dev import DeviceBert
@@ -457,7 +457,7 @@ def test_config5_full_depth_device_rerank(ctx, xlmr_large_full, mode):
     # Config 5's cross-encoder forward (DeviceBert.embeddings + DeviceBert.rerank, as the
     # bench runs it) at its full depth and length on one pair, against the reference
     # composition. Bars:
-    #  * the mean-pooled final hidden state at the north star's cosine >= 0.9999;
+    #  * the mean-pooled final hidden state at the encoder parity cosine >= 0.9999;
     #  * the [CLS] row (what the head reads): its distance from the reference, 1 - cosine,
     #    at most twice the reference's own drift when only its attention's rounding
     #    changes (f32 vs float64; ~4e-4 at 24 layers, measured live) -- a single token's

@@ -268,6 +268,41 @@ def test_split_bf16_attention_error_is_bounded_by_the_split(ctx, mode):
     assert err.max() <= 2e-4
 
 
+def test_flash_attention_wide_and_narrow_workgroups_agree(ctx):
+    # The flash kernel runs 16 wavefronts per workgroup (512 queries) once L > 256 and that
+    # grid has a workgroup per CU, else 8. Each query's arithmetic is the same in both, so
+    # the same sequences give the same bits whether they run in a batch large enough for
+    # the 16-wavefront form or alone (the 8-wavefront form); both against float64.
+    import torch
+
+    from aikit_amd import enchip
+
+    H, hd, L = 12, 64, 300
+    D = H * hd
+    cus = ctx.device_info()["num_cus"]
+    S_wide = -(-cus // H)  # ceil(L / 512) = 1 workgroup per (head, sequence)
+    g = workloads.rng(7400)
+    qkv = g.standard_normal((S_wide, L, 3 * D)).astype(np.float32)
+    scale = np.float32(1.0 / np.sqrt(hd))
+    dq = torch.from_numpy(qkv).cuda()
+    wide = torch.full((S_wide * L, D), np.nan, device="cuda")
+    narrow = torch.full((2 * L, D), np.nan, device="cuda")
+    torch.cuda.synchronize()
+    q = dq.data_ptr()
+    ctx.set_attention_products(enchip.ATT_FLASH_BF16)
+    say(f"flash attention L={L}: {S_wide} sequences (16 wavefronts) and 2 sequences (8 wavefronts)")
+    ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, wide.data_ptr(), D, S_wide, L, H, hd, float(scale))
+    ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, narrow.data_ptr(), D, 2, L, H, hd, float(scale))
+    torch.cuda.synchronize()
+    w = wide.cpu().numpy().reshape(S_wide, L, D)
+    n = narrow.cpu().numpy().reshape(2, L, D)
+    assert np.array_equal(w[:2].view(np.uint32), n.view(np.uint32))
+    want = _attention_f64(qkv[[0, S_wide - 1]], 2, L, H, hd, scale)
+    wf = oracle.matmul_bt_worst_rel(w[[0, S_wide - 1]], want)
+    say(f"  worst rel {wf:.3g}")
+    assert wf <= 2e-4
+
+
 @pytest.mark.parametrize("L", [77, 300])
 @pytest.mark.parametrize("scale", [-0.2, 0.0, 0.4])
 def test_flash_attention_any_scale(ctx, L, scale):

@@ -22,7 +22,7 @@ from aikit_amd import enchip, workloads
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "w8a8_golden.npz")
-REL_TOL = 1e-5  # north_star: dequantized f32 outputs, max relative error per GEMM
+REL_TOL = 1e-5  # the W8A8 parity bar: dequantized f32 outputs, max relative error per GEMM
 
 
 def say(msg):
@@ -34,7 +34,7 @@ def bits(x):
 
 
 def assert_f32_parity(got, want, what):
-    """Bit-identical (NaN payloads aside), and the north-star 1e-5 max rel error over
+    """Bit-identical (NaN payloads aside), and the 1e-5 max rel error bar (REL_TOL) over
     the finite values (infinities must match exactly)."""
     assert got.shape == want.shape, what
     nan = np.isnan(want)

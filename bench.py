@@ -591,20 +591,28 @@ def time_steps(torch, stream, step, steps: int, warmup: int) -> float:
     return time.perf_counter() - t0
 
 
-def time_ops(torch, stream, model, step, steps: int, hev) -> dict:
-    """Per-operation device durations (ms lists by label) over `steps` steps, after one
-    untimed step with the same marks: a HIP event recorded on the launch stream at each of
-    the model's marks."""
-    marks = []
+def time_ops(torch, stream, model, step, steps: int, hev, warmup: int = 1):
+    """Per-operation device durations (ms lists by label) over `steps` steps, after `warmup`
+    untimed steps with the same marks, and how they were timed: a HIP event recorded on the
+    launch stream at each of the model's marks.
+
+    An eager event pair also counts any time the GPU sits idle between the two records, as
+    when a host stall lets the queue drain. So every event is created before the timed
+    steps (the loop only records), and the stream starts with a ~20 ms device-side sleep:
+    the host queues the steps far ahead of the GPU before the first timed kernel runs."""
     sp = stream.cuda_stream
     warm = []
     model.mark = lambda label: warm.append(hev.record(hev.create(), sp))
     with torch.cuda.stream(stream):
-        step()
+        for _ in range(max(1, warmup)):
+            step()
     torch.cuda.synchronize()
+    per_step = len(warm) // max(1, warmup)
+    pool = iter([hev.create() for _ in range(per_step * steps + 1)])
+    marks = []
 
     def mark(label):
-        ev = hev.create()
+        ev = next(pool)
         hev.record(ev, sp)
         marks.append((label, ev))
 
@@ -612,6 +620,7 @@ def time_ops(torch, stream, model, step, steps: int, hev) -> dict:
     try:
         torch.cuda.synchronize()
         with torch.cuda.stream(stream):
+            torch.cuda._sleep(40_000_000)  # ~20 ms of shader clock: the host's head start
             for _ in range(steps):
                 step()
         torch.cuda.synchronize()
@@ -621,12 +630,12 @@ def time_ops(torch, stream, model, step, steps: int, hev) -> dict:
     for (lab, e0), (_, e1) in zip(marks, marks[1:]):
         if lab != "end":
             per.setdefault(lab, []).append(hev.elapsed_ms(e0, e1))
-    return per
+    return per, "eager launches, a HIP event recorded at each mark (events created beforehand, the host queued ahead)"
 
 
 def fa_waves(ctx, S: int, L: int, H: int) -> int:
     """Wavefronts per workgroup of the library's flash attention launch (its dispatch rule)."""
-    return 16 if L > 256 and -(-L // 512) * H * S >= ctx.device_info()["num_cus"] else 8
+    return 16 if L > 256 and (L <= 512 or -(-L // 512) * H * S >= ctx.device_info()["num_cus"]) else 8
 
 
 def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
@@ -645,7 +654,7 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
         n = len(ms)
         t = sum(ms) / n * 1e-3  # average launch
         u = {"launches_per_step": n / steps, "us_per_launch": t * 1e6, "us_per_launch_median": sorted(ms)[n // 2] * 1e3,
-             "ops": 0.0, "bytes": 0.0}
+             "us_per_launch_min": min(ms) * 1e3, "us_per_launch_max": max(ms) * 1e3, "ops": 0.0, "bytes": 0.0}
         base = label.split(".")[0]
         if label.endswith(".gemm"):
             K, N, act = lin[base]
@@ -661,8 +670,7 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
         elif label == "attention":
             mode = ctx.attention_products
             u.update(kind="attention", ops=4.0 * S * H * L * L * hd, bytes=float(4 * M * D * 4),
-                     # the library's flash launch: 16 wavefronts per workgroup once L > 256 and
-                     # that grid has a workgroup per CU, else 8
+                     # the library's flash launch (fa_waves)
                      kernel=(f"enchip::attention_flash_bf16<{hd}, {fa_waves(ctx, S, L, H)}, true>" if mode == 2 else
                              f"enchip::attention_split_bf16<{hd}, {'true' if L == 512 else 'false'}>" if mode == 1
                              else f"enchip::attention_f32<{hd}>"))
@@ -909,7 +917,7 @@ def main() -> int:
     # Timed region 2 (kernel durations): the same K encodes with a HIP event recorded on the
     # launch stream between consecutive operations.
     hev = HipEvents()
-    per = time_ops(torch, stream, model, step, args.steps, hev)
+    per, op_timing = time_ops(torch, stream, model, step, args.steps, hev, args.warmup)
     hev.close()
     units = encode_units(ctx, model, cfg, per, args.steps)
     step_ms_events = sum(u["ms_per_step"] for u in units.values())
@@ -986,6 +994,7 @@ def main() -> int:
         },
         "output_finite": finite,
         "encode_kernels": units,
+        "encode_kernels_timing": op_timing,
         "encode_ms_per_step_from_events": step_ms_events,
         "encode_int8_tops": sum(u_["ops"] * u_["launches_per_step"] for u_ in w8a8.values()) /
                             sum(u_["ms_per_step"] for k_, u_ in w8a8.items() if k_.endswith(".gemm")) / 1e9,

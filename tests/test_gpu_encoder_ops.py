@@ -269,18 +269,19 @@ def test_split_bf16_attention_error_is_bounded_by_the_split(ctx, mode):
 
 
 def test_flash_attention_wide_and_narrow_workgroups_agree(ctx):
-    # The flash kernel runs 16 wavefronts per workgroup (512 queries) once L > 256 and that
-    # grid has a workgroup per CU, else 8. Each query's arithmetic is the same in both, so
-    # the same sequences give the same bits whether they run in a batch large enough for
-    # the 16-wavefront form or alone (the 8-wavefront form); both against float64.
+    # The flash kernel runs 16 wavefronts per workgroup (512 queries) once L > 256, except
+    # for L > 512 on a grid with fewer workgroups than CUs, where it runs 8. Each query's
+    # arithmetic is the same in both, so the same sequences give the same bits whether they
+    # run in a batch large enough for the 16-wavefront form or alone (the 8-wavefront
+    # form); both against float64.
     import torch
 
     from aikit_amd import enchip
 
-    H, hd, L = 12, 64, 300
+    H, hd, L = 12, 64, 700
     D = H * hd
     cus = ctx.device_info()["num_cus"]
-    S_wide = -(-cus // H)  # ceil(L / 512) = 1 workgroup per (head, sequence)
+    S_wide = -(-cus // (2 * H))  # ceil(L / 512) = 2 workgroups per (head, sequence)
     g = workloads.rng(7400)
     qkv = g.standard_normal((S_wide, L, 3 * D)).astype(np.float32)
     scale = np.float32(1.0 / np.sqrt(hd))

@@ -286,6 +286,36 @@ __global__ __launch_bounds__(64 * NW, NW / 2) void gemm_w8a8_pt(
                     tail_mask |= t4 << (4 * k);
                     *reinterpret_cast<int4 *>(&scr[(rsub + RPL * k) * SP + 4 * c4]) = o4;
                 }
+                // Pass 2a, only when some lane holds more than 28 tail values of its 32 (a
+                // wide pre-activation distribution, much of it on ErfF32's sign branch):
+                // settle every value on the sign branch (|u| > 4: erf = +-1, so GELU is x or
+                // a signed zero, by gelu_f32's operations) across the chunk at once, so that
+                // the per-lane rounds below only run the erf tail. Measured on MI355X (same
+                // process, M = 32768 or 4096, K = 768, N = 3072): config 2's pre-activations
+                // (standard deviation ~22) 65 -> 45 us. The pass costs where tails are many
+                // but few on the sign branch, hence the high trigger: at 16, standard
+                // deviation 3 (65% tails, 6% on the sign branch) went 341 -> 364 us; at 4,
+                // standard deviation 1 (16% tails) 221 -> 249 us; 0.5 (an encoder's FFN)
+                // never triggers it.
+                if (__builtin_amdgcn_ballot_w64(__builtin_popcount(tail_mask) > 28)) {
+#pragma unroll
+                    for (int k = 0; k < KR; ++k) {
+                        if (((tail_mask >> (4 * k)) & 15u) == 0u) continue;
+                        int *cell4 = &scr[(rsub + RPL * k) * SP + 4 * c4];
+                        int4 w = *reinterpret_cast<const int4 *>(cell4);
+                        int wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const float y = __int_as_float(wv[j]);
+                            const float u = y * 0.7071067811865476f;
+                            if ((tail_mask >> (4 * k + j)) & 1u && fabsf(u) > 4.0f) {
+                                wv[j] = __float_as_int(0.5f * y * (1.0f + (u < 0.0f ? -1.0f : 1.0f)));
+                                tail_mask &= ~(1u << (4 * k + j));
+                            }
+                        }
+                        *reinterpret_cast<int4 *>(cell4) = make_int4(wv[0], wv[1], wv[2], wv[3]);
+                    }
+                }
                 // Pass 2: the tail values, one per lane per round, so the wavefront runs
                 // the tail code max-popcount times instead of once per mixed instruction.
                 for (;;) {

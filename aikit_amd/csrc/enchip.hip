@@ -330,9 +330,18 @@ bool gemv_wide(const enchip_ctx *c, const Weight &w) {
     return groups >= 8 * cus || (groups >= 4 * cus && w.Kp <= 1024);
 }
 
-int persistent_grid(const enchip_ctx *c, int64_t tiles) {
-    const int64_t full = std::max<int64_t>(8, (2 * (int64_t)c->num_cus) / 8 * 8);
+int persistent_grid(const enchip_ctx *c, int64_t tiles, int per_cu = 2) {
+    const int64_t full = std::max<int64_t>(8, ((int64_t)per_cu * c->num_cus) / 8 * 8);
     return (int)std::min<int64_t>(full, (tiles + 7) / 8 * 8);
+}
+
+// Tile height of gemm_w8a8_pt for M rows of a weight: 64-row tiles at 3 workgroups per CU
+// when 128-row tiles would not fill the 2 per CU slots (small M), else 128. Measured on
+// MI355X (K = 768, N = 3072, GELU): M = 4096 46 -> 35 us on config 2's pre-activations and
+// 29 -> 25 us on an encoder's; at M = 32768 the 128-row tiles stay faster (164 against 166).
+int pt_bm(const enchip_ctx *c, const Weight &w, int64_t M) {
+    const int64_t tiles128 = ((M + enchip::PT_BM - 1) / enchip::PT_BM) * ((w.N + enchip::PT_BN - 1) / enchip::PT_BN);
+    return tiles128 < 2 * (int64_t)c->num_cus ? enchip::PT_BM_SMALL : enchip::PT_BM;
 }
 
 // Main-loop wave priority of gemm_w8a8_pt for a weight and epilogue: raised for the
@@ -345,20 +354,28 @@ int pt_prio(const Weight &w, int epi) {
     return epi == enchip::EPI_F32 && (w.N >= 1024 || w.Kp >= 1024) ? 1 : 0;
 }
 
+template <int BM, int PW, int EPI, bool AF>
+void launch_pt_bm(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, const float *as, const float *bias,
+                  void *out, int64_t ldo, int64_t M, hipStream_t s) {
+    using namespace enchip;
+    const int tilesM = (int)((M + BM - 1) / BM), tilesN = (int)((w.N + PT_BN - 1) / PT_BN);
+    const int64_t tiles = (int64_t)tilesM * tilesN;
+    const int grid = persistent_grid(c, tiles, BM == PT_BM_SMALL ? 3 : 2);
+    if (pt_prio(w, EPI))
+        hipLaunchKernelGGL((gemm_w8a8_pt<BM, PT_BN, PT_BK, PW, EPI, AF, PT_NW, 1>), dim3(grid), dim3(64 * PT_NW), 0, s, aq,
+                           lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp, tilesN, (int)tiles);
+    else
+        hipLaunchKernelGGL((gemm_w8a8_pt<BM, PT_BN, PT_BK, PW, EPI, AF, PT_NW, 0>), dim3(grid), dim3(64 * PT_NW), 0, s, aq,
+                           lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp, tilesN, (int)tiles);
+}
+
 template <int PW, int EPI, bool AF>
 void launch_pt(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, const float *as, const float *bias,
                void *out, int64_t ldo, int64_t M, hipStream_t s) {
-    using namespace enchip;
-    const int tilesM = (int)((M + PT_BM - 1) / PT_BM), tilesN = (int)((w.N + PT_BN - 1) / PT_BN);
-    const int64_t tiles = (int64_t)tilesM * tilesN;
-    if (pt_prio(w, EPI))
-        hipLaunchKernelGGL((gemm_w8a8_pt<PT_BM, PT_BN, PT_BK, PW, EPI, AF, PT_NW, 1>), dim3(persistent_grid(c, tiles)),
-                           dim3(64 * PT_NW), 0, s, aq, lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N,
-                           (int)w.Kp, tilesN, (int)tiles);
+    if (pt_bm(c, w, M) == enchip::PT_BM_SMALL)
+        launch_pt_bm<enchip::PT_BM_SMALL, PW, EPI, AF>(c, w, aq, lda, as, bias, out, ldo, M, s);
     else
-        hipLaunchKernelGGL((gemm_w8a8_pt<PT_BM, PT_BN, PT_BK, PW, EPI, AF, PT_NW, 0>), dim3(persistent_grid(c, tiles)),
-                           dim3(64 * PT_NW), 0, s, aq, lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N,
-                           (int)w.Kp, tilesN, (int)tiles);
+        launch_pt_bm<enchip::PT_BM, PW, EPI, AF>(c, w, aq, lda, as, bias, out, ldo, M, s);
 }
 
 // af: aq is fragment-major (the caller checked route_af); otherwise row-major at pitch lda.
@@ -575,7 +592,7 @@ int enchip_gemm_kernel_name(enchip_ctx *ctx, enchip_weight h, int64_t M, int act
     const int epi = act_code(act);
     char name[96];
     if (route_af(ctx, *w, M, nullptr, w->N))
-        snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, true, %d, %d>", enchip::PT_BM,
+        snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, true, %d, %d>", pt_bm(ctx, *w, M),
                  enchip::PT_BN, enchip::PT_BK, pt_ring(*w), epi, enchip::PT_NW, pt_prio(*w, epi));
     else if (fused_small_m(ctx, *w, M, nullptr) && epi != enchip::EPI_I32)
         snprintf(name, sizeof name, "enchip::gemv_w8a8_q<%d>", epi);
@@ -584,7 +601,7 @@ int enchip_gemm_kernel_name(enchip_ctx *ctx, enchip_weight h, int64_t M, int act
     else if (M <= ctx->small_m)
         snprintf(name, sizeof name, "enchip::gemv_w8a8<%d>", epi);
     else if (use_persistent(*w, nullptr, w->Kp, nullptr, w->N, M, false))
-        snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, false, %d, %d>", enchip::PT_BM,
+        snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, false, %d, %d>", pt_bm(ctx, *w, M),
                  enchip::PT_BN, enchip::PT_BK, pt_ring(*w), epi, enchip::PT_NW, pt_prio(*w, epi));
     else if (use_wide_tile(ctx, *w, M))
         snprintf(name, sizeof name, "enchip::gemm_w8a8<128, 256, %d, 2>", epi);

@@ -40,8 +40,9 @@
 namespace enchip {
 
 // Tile geometry and ring depth of the persistent kernel (the host checks its
-// preconditions).
-constexpr int PT_BM = 128, PT_BN = 256, PT_BK = 64, PT_PW = 2, PT_NW = 4;
+// preconditions). PT_BM_SMALL: the 64-row tile the host picks when 128-row tiles would
+// leave workgroup slots idle (fewer tiles than 2 per CU); it runs 3 workgroups per CU.
+constexpr int PT_BM = 128, PT_BM_SMALL = 64, PT_BN = 256, PT_BK = 64, PT_PW = 2, PT_NW = 4;
 
 // 16-byte nontemporal store of 4 output words. The f32 outputs are written once and
 // not read by this kernel; a normal store would let them evict the A row-blocks and
@@ -57,7 +58,7 @@ __device__ __forceinline__ void store_nt(void *p, int4 v) {
 // the BERT-base and XLM-R-large bias-only shapes except BERT-base's O, 4% slower, and the
 // GELU epilogue unchanged; bit-identical either way).
 template <int BM, int BN, int BK, int PW, int EPI, bool AF, int NW, int PRIO>
-__global__ __launch_bounds__(64 * NW, NW / 2) void gemm_w8a8_pt(
+__global__ __launch_bounds__(64 * NW, BM == PT_BM_SMALL ? 3 : NW / 2) void gemm_w8a8_pt(
     const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ Wf,
     const float *__restrict__ aS, const float *__restrict__ wS, const float *__restrict__ bias,
     void *__restrict__ out, int64_t ldo, int M, int N, int Kp, int tilesN, int numTiles) {

@@ -362,7 +362,7 @@ def test_pre_quantized_matches_oracle(ctx, workers, M, K, Ns, small_m):
 # (M, N) pairs that route to each GEMM kernel (K = 768): M <= 32 runs gemv_w8a8;
 # otherwise gemm_w8a8_pt (fragment-major activations) when N % 4 == 0, gemm_w8a8 when
 # not.
-KERNEL_ROUTES = [(8, 1024, "gemv"), (20, 1001, "gemv"), (300, 1024, "gemm_w8a8_pt<128, 256, 64, 2,"),
+KERNEL_ROUTES = [(8, 1024, "gemv"), (20, 1001, "gemv"), (300, 1024, "gemm_w8a8_pt<64, 256, 64, 2,"),
                  (300, 1001, "gemm_w8a8<")]
 
 
@@ -428,6 +428,30 @@ def test_special_weight_scales(ctx, M, N, route, act):
     finally:
         ctx.release_weight(w)
     assert_f32_parity(got, oracle.w8a8_linear(a, wq, ws, b, act, M, K, N), f"special scales {route}")
+
+
+@pytest.mark.parametrize("M,N,K,bm", [(300, 1024, 768, 64), (4096, 3072, 256, 64), (16384, 1024, 128, 128)])
+@pytest.mark.parametrize("act", [0, 1])
+def test_persistent_tile_heights_match_oracle(ctx, M, N, K, bm, act):
+    # gemm_w8a8_pt runs 64-row tiles (3 workgroups per CU) when 128-row tiles would leave
+    # workgroup slots idle (fewer than 2 per CU: 512 on MI355X), else 128-row tiles (M =
+    # 16384, N = 1024: exactly 512). Both bit-identical to the oracle, with and without
+    # GELU; the GELU case at config 2's wide pre-activations.
+    g = workloads.rng(61 + M + N + K + act)
+    a = workloads.activations(g, M, K)
+    wq, ws = workloads.int8_weights(g, N, K)
+    b = workloads.bias(g, N)
+    w = ctx.register_weight(wq, ws)
+    try:
+        name = ctx.gemm_kernel_name(w, M, act)
+        cus = ctx.device_info()["num_cus"]
+        tiles128 = -(-M // 128) * -(-N // 256)
+        assert name.startswith(f"enchip::gemm_w8a8_pt<{bm if cus == 256 else (64 if tiles128 < 2 * cus else 128)}, "), name
+        say(f"persistent GEMM M={M} N={N} K={K} act={act} via {name}")
+        got = ctx.linear(w, a, bias=b, act=act)
+    finally:
+        ctx.release_weight(w)
+    assert_f32_parity(got, oracle.w8a8_linear(a, wq, ws, b, act, M, K, N), f"tile height {bm}")
 
 
 def test_kernel_name_matches_dispatch(ctx):

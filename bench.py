@@ -927,8 +927,9 @@ def main() -> int:
     roofline = roofline_of(key, w8a8[key], ceilings, traffic_key)
     u = w8a8[key]
     roofline["limiter"] = (
-        "VALU: the GELU epilogue restates aikit's exact-erf GELUF32 with no FMA (~36 VALU per output in its "
-        "branch-free pass), so the kernel is bound by VALU issue below both its HBM and its MFMA roofline"
+        "VALU issue: the GELU epilogue restates aikit's exact-erf GELUF32 with no FMA (~36 VALU per output in "
+        "its branch-free pass), its largest fraction of any roof (roofline.valu); main loops and epilogues "
+        "overlap only where a CU's two workgroups are in different phases"
         if key == "ffn_up.gemm" else "MFMA issue in the main loop" if key.endswith(".gemm") else "HBM")
     roofline["scope"] = ("the W8A8 path's dominant kernel in the timed encode (by device time per step); "
                          "roofline_step_dominant covers the step's dominant kernel overall")

@@ -71,6 +71,9 @@ __global__ __launch_bounds__(64 * NW, BM == PT_BM_SMALL ? 3 : NW / 2) void gemm_
     constexpr int KB = BK / 32;
     constexpr int FA = TM * KB;  // A fragments per stage
     static_assert(FA % NW == 0 && TN >= 1, "A fragments per stage must split over the waves");
+    // Stage t writes stage t+1's A to LDS from the ring slot its loads went to one stage
+    // earlier; with a 1-stage ring that slot would still hold stage t's A.
+    static_assert(PW >= 2, "the ring needs at least 2 stages");
     static_assert(NT >= BN && NT >= BM && (BM & (BM - 1)) == 0, "constant staging: one thread per row / column");
     constexpr int FAW = FA / NW;  // A fragments each wave moves per stage
     constexpr int STAGE = FA * 1024;

@@ -402,6 +402,11 @@ def test_gelu_every_branch(ctx, M, N, route, spread):
     assert (u < 1).sum() > 0.01 * n and ((u >= 1) & (u <= 4)).sum() > 0.05 * n and (u > 4).sum() > 0.01 * n
     if spread > 10:
         assert (u > 4).sum() > 0.5 * n
+    else:
+        # over a quarter of the arguments off the series branch: a persistent-kernel chunk
+        # (32 rows x 64 columns per wavefront) then holds more tail values than its 512-cell
+        # list, so the per-lane rounds for the rest run too
+        assert (u >= 1).sum() > 0.4 * n
     assert_f32_parity(got, oracle.w8a8_linear(a, wq, ws, b, 1, M, K, N), f"GELU {route}")
 
 

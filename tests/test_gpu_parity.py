@@ -303,6 +303,9 @@ def test_device_ceilings_coherent(ctx):
     assert 1000 < c["hbm_read_gbps"] < 12000
     assert 1000 < c["hbm_write_gbps"] < 12000
     assert 500 < c["mfma_i8_tops"] < 6000
+    # non-packed f32 lane-operations: at most two wavefronts' instructions per SIMD per
+    # 4-cycle issue slot, 32 lanes per clock x 1024 SIMDs x 2.4 GHz = 78.6 T
+    assert 5 < c["valu_f32_tops"] < 80
 
 
 @pytest.mark.parametrize("M,K,Ns,small_m", [(1500, 768, (2304, 768), 32), (300, 1024, (2304, 768), 32),

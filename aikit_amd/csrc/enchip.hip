@@ -667,10 +667,41 @@ int enchip_probe_ceilings(enchip_ctx *ctx, enchip_ceilings *out) {
         out->hbm_write_gbps = (double)bytes / us / 1e3;
         const int iters = 2000;
         const unsigned mgrid = (unsigned)(ctx->num_cus * 2);
-        if ((e = best_us([&] {
-                 hipLaunchKernelGGL(enchip::probe_mfma_i8, dim3(mgrid), dim3(256), 0, ctx->stream, sink, iters);
-             }, &us)) != hipSuccess) break;
-        out->mfma_i8_tops = (double)mgrid * 4 * iters * 8 * 65536.0 / us / 1e6;
+        long long *clk = reinterpret_cast<long long *>(buf);  // the streaming probes are done with buf
+        int wall_khz = 0;
+        if ((e = hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, ctx->device)) != hipSuccess) break;
+        std::vector<long long> ticks(2 * (size_t)mgrid);
+        // the mean shader clock (MHz) of the last launch's blocks: s_memtime ticks over
+        // s_memrealtime ticks, times the constant clock's rate
+        auto clock_mhz = [&](double *mhz) -> hipError_t {
+            hipError_t err = hipMemcpyAsync(ticks.data(), clk, ticks.size() * sizeof(long long), hipMemcpyDeviceToHost,
+                                            ctx->stream);
+            if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+            if (err != hipSuccess) return err;
+            double sum = 0;
+            int n = 0;
+            for (unsigned b = 0; b < mgrid; ++b)
+                if (ticks[2 * b + 1] > 0) {
+                    sum += (double)ticks[2 * b] / (double)ticks[2 * b + 1];
+                    ++n;
+                }
+            *mhz = n ? sum / n * wall_khz / 1e3 : 0.0;
+            return hipSuccess;
+        };
+        for (int data = 0; data < 2 && e == hipSuccess; ++data) {
+            if ((e = best_us([&] {
+                     if (data)
+                         hipLaunchKernelGGL(enchip::probe_mfma_i8<true>, dim3(mgrid), dim3(256), 0, ctx->stream, sink, iters, clk);
+                     else
+                         hipLaunchKernelGGL(enchip::probe_mfma_i8<false>, dim3(mgrid), dim3(256), 0, ctx->stream, sink, iters, clk);
+                 }, &us)) != hipSuccess) break;
+            const double tops = (double)mgrid * 4 * iters * 8 * 65536.0 / us / 1e6;
+            double mhz = 0;
+            if ((e = clock_mhz(&mhz)) != hipSuccess) break;
+            (data ? out->mfma_i8_data_tops : out->mfma_i8_tops) = tops;
+            (data ? out->mfma_i8_data_mhz : out->mfma_i8_mhz) = mhz;
+        }
+        if (e != hipSuccess) break;
         const int viters = 4096;
         const unsigned vgrid = (unsigned)(ctx->num_cus * 8);  // 8 waves per SIMD
         if ((e = best_us([&] {

@@ -81,25 +81,81 @@ __global__ __launch_bounds__(256) void probe_stream_write(i32x4_p *__restrict__ 
         if (i + 256 * j < n16) dst[i + 256 * j] = v;
 }
 
+// A hash of a 32-bit counter (the finaliser of a 32-bit integer hash: xor-shifts and two
+// odd multipliers), for operand data made on the device.
+__device__ __forceinline__ uint32_t probe_hash(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+// Four int8 codes, each the sum of four uniform values in [-32, 31]: bell-shaped, standard
+// deviation ~37, in [-128, 124], like a per-token or per-channel quantization of normal
+// data (whose codes have standard deviation ~40 for rows of a few hundred values).
+__device__ __forceinline__ int probe_codes(uint32_t seed) {
+    int w = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t h = probe_hash(seed * 4u + (uint32_t)c);
+        int v = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v += (int)((h >> (8 * k)) & 63u) - 32;
+        w |= (v & 0xff) << (8 * c);
+    }
+    return w;
+}
+
 // int8 MFMA issue rate: 8 independent v_mfma_i32_32x32x32_i8 accumulator chains per
 // wave (enough to cover the instruction's latency), no memory traffic in the loop.
-__global__ __launch_bounds__(256) void probe_mfma_i8(int *__restrict__ out, int iters) {
-    const i32x4_p a = {(int)threadIdx.x, 1, 2, 3}, b = {3, 2, 1, (int)threadIdx.x};
+//   DATA = false: the same small operands in every instruction (the instruction's issue
+//     rate at the clock the chip holds with idle multipliers);
+//   DATA = true: 8 A and 8 B fragments of bell-shaped codes (probe_codes), a different
+//     pair in every instruction: the multipliers switch as they do on real data, and the
+//     chip lowers its shader clock under that power (measured on MI355X: ~2.39 GHz with
+//     constant operands, ~1.75 GHz with these).
+// iters is even. Thread 0 of each block writes the loop's shader-clock ticks
+// (s_memtime) and constant-rate ticks (s_memrealtime) to clk[2 * block + {0, 1}].
+template <bool DATA>
+__global__ __launch_bounds__(256) void probe_mfma_i8(int *__restrict__ out, int iters, long long *__restrict__ clk) {
+    i32x4_p a[8], b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if (DATA) {
+            const uint32_t base = ((blockIdx.x * 256u + threadIdx.x) * 16u + (uint32_t)i) * 4u;
+            a[i] = (i32x4_p){probe_codes(base), probe_codes(base + 1), probe_codes(base + 2), probe_codes(base + 3)};
+            const uint32_t bb = base + 32u;
+            b[i] = (i32x4_p){probe_codes(bb), probe_codes(bb + 1), probe_codes(bb + 2), probe_codes(bb + 3)};
+        } else {
+            a[i] = (i32x4_p){(int)threadIdx.x, 1, 2, 3};
+            b[i] = (i32x4_p){3, 2, 1, (int)threadIdx.x};
+        }
+    }
     i32x16_p acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][r] = 0;
-    for (int it = 0; it < iters; ++it) {
+    const long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; it += 2) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[i], 0, 0, 0);
+        for (int i = 0; i < 8; ++i) acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[(i + 3) & 7], acc[i], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[(i + 5) & 7], b[i], acc[i], 0, 0, 0);
     }
+    const long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
     int s = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) s += acc[i][r];
     out[blockIdx.x * 256 + threadIdx.x] = s;
+    if (threadIdx.x == 0) {
+        clk[2 * blockIdx.x] = t1 - t0;
+        clk[2 * blockIdx.x + 1] = r1 - r0;
+    }
 }
 
 }  // namespace enchip

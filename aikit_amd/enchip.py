@@ -84,7 +84,9 @@ class EnchipOp(ctypes.Structure):
 class EnchipCeilings(ctypes.Structure):
     """``enchip_ceilings`` of include/enchip.h."""
     _fields_ = [("hbm_read_gbps", ctypes.c_double), ("hbm_write_gbps", ctypes.c_double),
-                ("mfma_i8_tops", ctypes.c_double), ("valu_f32_tops", ctypes.c_double)]
+                ("mfma_i8_tops", ctypes.c_double), ("valu_f32_tops", ctypes.c_double),
+                ("mfma_i8_mhz", ctypes.c_double), ("mfma_i8_data_tops", ctypes.c_double),
+                ("mfma_i8_data_mhz", ctypes.c_double)]
 
 
 class EnchipError(RuntimeError):
@@ -189,7 +191,9 @@ class Context:
         c = EnchipCeilings()
         self._check(self._lib.enchip_probe_ceilings(self._h, ctypes.byref(c)))
         return {"hbm_read_gbps": c.hbm_read_gbps, "hbm_write_gbps": c.hbm_write_gbps,
-                "mfma_i8_tops": c.mfma_i8_tops, "valu_f32_tops": c.valu_f32_tops}
+                "mfma_i8_tops": c.mfma_i8_tops, "valu_f32_tops": c.valu_f32_tops,
+                "mfma_i8_mhz": c.mfma_i8_mhz, "mfma_i8_data_tops": c.mfma_i8_data_tops,
+                "mfma_i8_data_mhz": c.mfma_i8_data_mhz}
 
     def set_small_m(self, max_m: int) -> None:
         self._check(self._lib.enchip_set_small_m(self._h, max_m))

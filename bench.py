@@ -718,6 +718,7 @@ def roofline_of(label: str, u: dict, ceilings: dict, traffic_key: str) -> dict:
         "ridge_op_per_byte": ridge,
         "int8_frac_of_peak": ops / t / PEAK_INT8_OPS,
         "frac_of_measured_mfma_peak": ops / t / (ceilings["mfma_i8_tops"] * 1e12),
+        "frac_of_measured_mfma_data_peak": ops / t / (ceilings["mfma_i8_data_tops"] * 1e12),
         "frac_of_measured_hbm_read": nbytes / t / 1e9 / ceilings["hbm_read_gbps"],
         "traffic_source": TRAFFIC_PROFILE if traffic is not None else None,
     }
@@ -960,6 +961,14 @@ def main() -> int:
                      "products each f32 product is three bf16 MFMA products, so frac = 3 x achieved / the 2.5 PFLOP/s "
                      "bf16 dense peak (the MFMA work the kernel issues); the exact softmax's VALU work is not in it")
             if split else "achieved = algorithmic flops per second on the f32 MFMA"})
+    elif dom in w8a8:
+        # a W8A8 unit: the same roof as the roofline object (that object itself when the
+        # two dominant kernels coincide)
+        rd = roofline if dom == key else roofline_of(
+            dom, ud, ceilings, dom.split(".")[0] if dom.endswith(".gemm") else "quant_" + dom.split(".")[0])
+        step_dom.update({f: rd[f] for f in ("bound", "unit", "achieved", "peak", "frac")})
+        if "valu" in rd:
+            step_dom["valu_frac"] = rd["valu"]["frac"]
     log(f"dominant W8A8 kernel {key}: {u['us_per_launch']:.1f} us, roofline frac {roofline['frac']:.3f}; "
         f"step-dominant {dom} ({step_dom['share_of_step']:.0%} of the step)")
 

@@ -242,17 +242,24 @@ int enchip_gemm_kernel_name(enchip_ctx *ctx, enchip_weight w, int64_t M, int act
 
 /* Measured device ceilings (best of 5): HBM streaming read (the best of 8 or 16 16-byte
  * loads in flight per lane and two grid sizes) and write over a 1 GiB buffer (past the
- * 256 MiB MALL), the dense int8 MFMA rate (v_mfma_i32_32x32x32_i8, 8 independent chains per
- * wave, 2 blocks per CU), and the f32 VALU rate in lane-operations per second for
- * unfused, unpacked multiplies and adds (8 independent chains per lane, 8 waves per SIMD):
- * the roof of the bit-exact epilogues, which are made of exactly those.
+ * 256 MiB MALL); the dense int8 MFMA rate (v_mfma_i32_32x32x32_i8, 8 independent chains per
+ * wave, 2 blocks per CU) twice: with constant operands, and with a different pair of
+ * bell-shaped int8 operand fragments (standard deviation ~37, like quantized normal data)
+ * in every instruction, each with the mean shader clock its blocks ran at (s_memtime over
+ * s_memrealtime): the chip lowers its clock under the multipliers' power on real data;
+ * and the f32 VALU rate in lane-operations per second for unfused, unpacked multiplies and
+ * adds (8 independent chains per lane, 8 waves per SIMD): the roof of the bit-exact
+ * epilogues, which are made of exactly those.
  * Replaces gpu/roofline.cu's stream_read / imad_peak / dp4a_peak probes and
  * TestDeviceCeilings (gpu/roofline_test.go:57-140). Allocates and frees 1 GiB. */
 typedef struct enchip_ceilings {
     double hbm_read_gbps;
     double hbm_write_gbps;
-    double mfma_i8_tops;
-    double valu_f32_tops; /* T lane-operations / s */
+    double mfma_i8_tops;      /* constant operands */
+    double valu_f32_tops;     /* T lane-operations / s */
+    double mfma_i8_mhz;       /* shader clock during the constant-operand MFMA probe */
+    double mfma_i8_data_tops; /* bell-shaped random operands */
+    double mfma_i8_data_mhz;  /* shader clock during that probe */
 } enchip_ceilings;
 int enchip_probe_ceilings(enchip_ctx *ctx, enchip_ceilings *out);
 

@@ -303,6 +303,15 @@ def test_device_ceilings_coherent(ctx):
     assert 1000 < c["hbm_read_gbps"] < 12000
     assert 1000 < c["hbm_write_gbps"] < 12000
     assert 500 < c["mfma_i8_tops"] < 6000
+    # operands that switch the multipliers cannot issue faster than constant ones, and each
+    # probe's shader clock is within the part's range (MI355X: up to 2.4 GHz)
+    assert 500 < c["mfma_i8_data_tops"] < 1.05 * c["mfma_i8_tops"]
+    assert 300 < c["mfma_i8_data_mhz"] < 1.05 * c["mfma_i8_mhz"] and c["mfma_i8_mhz"] < 3000
+    # the rate follows the clock: 2048 int8 ops per clock per SIMD at the measured clock
+    # bounds each probe (4 SIMDs per CU)
+    cus = ctx.device_info()["num_cus"]
+    for tops, mhz in ((c["mfma_i8_tops"], c["mfma_i8_mhz"]), (c["mfma_i8_data_tops"], c["mfma_i8_data_mhz"])):
+        assert tops < 1.05 * 2048 * 4 * cus * mhz * 1e6 / 1e12
     # non-packed f32 lane-operations: at most two wavefronts' instructions per SIMD per
     # 4-cycle issue slot, 32 lanes per clock x 1024 SIMDs x 2.4 GHz = 78.6 T
     assert 5 < c["valu_f32_tops"] < 80

@@ -336,17 +336,23 @@ __global__ __launch_bounds__(64 * NW, BM == PT_BM_SMALL ? 3 : NW / 2) void gemm_
                 // whole libraries, bit-identical): FFN-up in the BERT-base encode 196 ->
                 // 186 us, config 2's linear 48 -> 45 us per call.
                 {
+                    // The prefix sum, bit-sliced: one ballot and one count of the lanes
+                    // below per bit of the count (0..32), all VALU and scalar work, where a
+                    // 6-step shuffle scan waits on a cross-lane LDS permute per step. Measured
+                    // on MI355X, bit-identical: pass 2 10.3K -> 8.3K cycles per tile and wave
+                    // on pre-activations of standard deviation 0.5; FFN-up in the BERT-base
+                    // encode 177-179 -> 174-175 us.
                     const int cnt = __builtin_popcount(tail_mask);
-                    int incl = cnt;
+                    int excl = 0, total = 0;
 #pragma unroll
-                    for (int d = 1; d < 64; d <<= 1) {
-                        const int y = __shfl_up(incl, d, 64);
-                        if (lane >= d) incl += y;
+                    for (int b = 0; b < 6; ++b) {
+                        const uint64_t bm = __builtin_amdgcn_ballot_w64((cnt >> b) & 1);
+                        excl += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u)) << b;
+                        total += __builtin_popcountll(bm) << b;
                     }
-                    const int total = __shfl(incl, 63, 64);
                     if (total != 0) {
                         auto slot = [&](int e) { return reinterpret_cast<uint16_t *>(&scr[(e >> 4) * SP + WN]) + (e & 15); };
-                        int pos = incl - cnt;
+                        int pos = excl;
                         uint32_t rest = 0u;
                         for (uint32_t m = tail_mask; m != 0u; m &= m - 1u, ++pos) {
                             const int b = __builtin_ctz(m);

@@ -1499,6 +1499,12 @@ int enchip_set_attention_products(enchip_ctx *ctx, int mode) {
 
 namespace {
 
+// Stage-1 chunks (rows x chunks) from which the threshold filter runs: below it the
+// threshold's two extra dependent launches cost more than the selections they skip.
+// Measured on MI355X at n = 2^20 (128 chunks per row), k = 10, per call: 32 rows 57 ->
+// 63 us with the filter, 64 rows 91 -> 81, 256 rows 291 -> 207.
+constexpr int64_t kTopkFilterChunks = 8192;
+
 // Enqueues the two top-k stages (topk.h) after the caller checked the arguments.
 int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, int64_t n, int64_t k, int32_t *index,
                 int64_t ldi, float *score, int64_t lds, hipStream_t s) {
@@ -1512,14 +1518,34 @@ int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, in
     const bool wide = k <= TOPK_SMALL_K;
     const int64_t chunk = wide ? TOPK_WCHUNK : TOPK_CHUNK;
     const int64_t nchunks = std::max<int64_t>(1, (n + chunk - 1) / chunk);
+    // Long rows on a grid of many chunks: threshold from each row's first chunks, then the
+    // other chunks filter against it (topk_chunk_wide), so most skip their selection. The
+    // thresholds (one key per row) follow the candidates in the scratch.
+    const bool filter = wide && nchunks >= 2 * TOPK_SAMPLE_CHUNKS && rows * nchunks >= kTopkFilterChunks;
     int rc;
-    if ((rc = ensure(c, &c->d_cand, &c->cand_cap, (size_t)(rows * nchunks * k) * sizeof(uint64_t)))) return rc;
+    if ((rc = ensure(c, &c->d_cand, &c->cand_cap, (size_t)(rows * nchunks * k + (filter ? rows : 0)) * sizeof(uint64_t))))
+        return rc;
+    uint64_t *thr = filter ? c->d_cand + rows * nchunks * k : nullptr;
     int kp = 1;
     while (kp < k) kp <<= 1;
     for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
         const int64_t nr = std::min<int64_t>(65535, rows - r0);
-        hipLaunchKernelGGL(wide ? topk_chunk_wide : topk_chunk, dim3((unsigned)nchunks, (unsigned)nr), dim3(256), 0, s,
-                           scores + r0 * ld, ld, n, (int)k, (int)nchunks, c->d_cand + r0 * nchunks * k);
+        uint64_t *cr = c->d_cand + r0 * nchunks * k;
+        if (filter) {
+            hipLaunchKernelGGL(topk_chunk_wide, dim3((unsigned)TOPK_SAMPLE_CHUNKS, (unsigned)nr), dim3(256), 0, s,
+                               scores + r0 * ld, ld, n, (int)k, (int)nchunks, cr, 0, (const uint64_t *)nullptr);
+            hipLaunchKernelGGL(topk_thresh, dim3((unsigned)((nr + 3) / 4)), dim3(256), 0, s, (const uint64_t *)cr, nr,
+                               (int)nchunks, (int)k, thr + r0);
+            hipLaunchKernelGGL(topk_chunk_wide, dim3((unsigned)(nchunks - TOPK_SAMPLE_CHUNKS), (unsigned)nr), dim3(256), 0,
+                               s, scores + r0 * ld, ld, n, (int)k, (int)nchunks, cr, TOPK_SAMPLE_CHUNKS,
+                               (const uint64_t *)(thr + r0));
+        } else if (wide) {
+            hipLaunchKernelGGL(topk_chunk_wide, dim3((unsigned)nchunks, (unsigned)nr), dim3(256), 0, s, scores + r0 * ld,
+                               ld, n, (int)k, (int)nchunks, cr, 0, (const uint64_t *)nullptr);
+        } else {
+            hipLaunchKernelGGL(topk_chunk, dim3((unsigned)nchunks, (unsigned)nr), dim3(256), 0, s, scores + r0 * ld, ld,
+                               n, (int)k, (int)nchunks, cr);
+        }
     }
     for (int64_t r0 = 0; r0 < rows; r0 += kRowChunk) {
         const int64_t nr = std::min<int64_t>(kRowChunk, rows - r0);

@@ -18,7 +18,11 @@
 //     otherwise by a radix select over the keys held in registers (8 bits a pass, LDS
 //     histogram).
 //   (for k <= 32, topk_chunk_wide: the same selection over 8192-score chunks, compared
-//     as floats, half the per-chunk selection work per score.)
+//     as floats, half the per-chunk selection work per score. On long rows it first runs
+//     on each row's first TOPK_SAMPLE_CHUNKS chunks; topk_thresh takes the k-th largest of
+//     their keys as a lower bound of the row's k-th largest key; every other chunk then
+//     writes its keys at or above that bound when there are at most k of them (no
+//     selection), else selects its k largest.)
 //   topk_merge: one workgroup per row selects the k largest of the row's candidates the
 //     same way (maxima in registers when k <= 32 and there are at most 4096 candidates,
 //     else a radix select over them in memory and a bitonic sort in LDS) and writes
@@ -294,25 +298,70 @@ __global__ __launch_bounds__(256) void topk_chunk(const float *__restrict__ scor
 //   4. wavefront 0 takes the maximum of the gathered keys k times.
 constexpr int TOPK_WCHUNK = 8192;
 
+//
+// With `thr` (a key per row, 0 for none), a chunk first counts its keys >= the row's key:
+// when there are at most k, they are the chunk's only keys that can be among the row's k
+// largest (thr is a lower bound of the row's k-th largest key), and the chunk writes just
+// those, in any order, 0-padded, with no selection rounds. Otherwise (or with no
+// threshold) it selects its k largest as above. Chunk index = chunk0 + blockIdx.x.
+constexpr int TOPK_SAMPLE_CHUNKS = 4;  // chunks per row whose k largest give the row's threshold
+
+// The score whose order bits are a key's high half (the inverse of topk_order on non-NaN).
+__device__ __forceinline__ float topk_key_score(uint64_t key) {
+    const uint32_t th = (uint32_t)(key >> 32);
+    return __uint_as_float((th & 0x80000000u) ? (th & 0x7fffffffu) : ~th);
+}
+
 __global__ __launch_bounds__(256) void topk_chunk_wide(const float *__restrict__ scores, int64_t ld, int64_t n, int k,
-                                                       int nchunks, uint64_t *__restrict__ cand) {
+                                                       int nchunks, uint64_t *__restrict__ cand, int chunk0,
+                                                       const uint64_t *__restrict__ thr) {
     constexpr int EPT = TOPK_WCHUNK / 256;
     __shared__ uint64_t maxima[256];
     __shared__ uint64_t gathered[TOPK_SMALL_K * EPT];  // <= k threads x EPT keys
     __shared__ uint64_t thresh;
     __shared__ unsigned count;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t row = blockIdx.y, base = (int64_t)blockIdx.x * TOPK_WCHUNK;
+    const int64_t row = blockIdx.y, chunk = chunk0 + (int64_t)blockIdx.x, base = chunk * TOPK_WCHUNK;
     const float *p = scores + row * ld + base;
+    uint64_t *out = cand + (row * nchunks + chunk) * (int64_t)k;
     // last valid position of the chunk (n > 0 whenever a chunk is launched); the loads are
     // unconditional (clamped), so all of them are in flight before the first is used
     const int last = (int)(n - base < TOPK_WCHUNK ? n - base : TOPK_WCHUNK) - 1;
     float x[EPT];
 #pragma unroll
     for (int j = 0; j < EPT; ++j) x[j] = p[min(tid + 256 * j, last)];  // coalesced
+    auto lo_at = [&](int j) { return 0xffffffffu - (uint32_t)(base + tid + 256 * j); };
     // The comparisons below run on the floats themselves, which order exactly as the keys'
     // high halves do: a NaN compares false (never retained), -0 == +0, and a strict > over
     // ascending positions keeps the lowest index among equal scores.
+    if (thr != nullptr) {
+        const uint64_t t = thr[row];
+        if (t != 0) {
+            // key >= t: score above t's, or equal and index low half at least t's
+            const float tf = topk_key_score(t);
+            const uint32_t tl = (uint32_t)t;
+            uint32_t mine = 0;
+#pragma unroll
+            for (int j = 0; j < EPT; ++j)
+                mine |= (tid + 256 * j <= last && (x[j] > tf || (x[j] == tf && lo_at(j) >= tl))) ? 1u << j : 0u;
+            if (tid == 0) count = 0;
+            __syncthreads();
+            if (mine != 0u) {
+                unsigned pos = atomicAdd(&count, (unsigned)__builtin_popcount(mine));
+                for (uint32_t m = mine; m != 0u; m &= m - 1u, ++pos) {
+                    const int j = __builtin_ctz(m);
+                    if (pos < (unsigned)k) gathered[pos] = ((uint64_t)topk_order(x[j]) << 32) | lo_at(j);
+                }
+            }
+            __syncthreads();
+            const unsigned total = count;
+            if (total <= (unsigned)k) {
+                for (int i = tid; i < k; i += 256) out[i] = i < (int)total ? gathered[i] : 0;
+                return;
+            }
+            __syncthreads();  // every thread has read count before the selection resets it
+        }
+    }
     float bf = -INFINITY;
     int bj = -1;
 #pragma unroll
@@ -321,7 +370,6 @@ __global__ __launch_bounds__(256) void topk_chunk_wide(const float *__restrict__
         bf = up ? x[j] : bf;
         bj = up ? j : bj;
     }
-    auto lo_at = [&](int j) { return 0xffffffffu - (uint32_t)(base + tid + 256 * j); };
     const uint64_t tmax = bj >= 0 ? ((uint64_t)topk_order(bf) << 32) | lo_at(bj) : 0;
     maxima[tid] = tmax;
     if (tid == 0) count = 0;
@@ -352,8 +400,8 @@ __global__ __launch_bounds__(256) void topk_chunk_wide(const float *__restrict__
         // key >= t: score above t's, or equal and index low half (0xffffffff - index) at
         // least t's; t == 1 takes every non-NaN score
         const bool every = t == 1;
-        const uint32_t th = (uint32_t)(t >> 32), tl = (uint32_t)t;
-        const float tf = __uint_as_float((th & 0x80000000u) ? (th & 0x7fffffffu) : ~th);  // th's score
+        const uint32_t tl = (uint32_t)t;
+        const float tf = topk_key_score(t);
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
             const uint32_t lo = lo_at(j);
@@ -363,7 +411,6 @@ __global__ __launch_bounds__(256) void topk_chunk_wide(const float *__restrict__
     }
     __syncthreads();
     if (wave != 0) return;
-    uint64_t *out = cand + (row * nchunks + blockIdx.x) * (int64_t)k;
     const int c = (int)count;
     if (c <= 64) {
         uint64_t v = lane < c ? gathered[lane] : 0;
@@ -391,6 +438,28 @@ __global__ __launch_bounds__(256) void topk_chunk_wide(const float *__restrict__
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
+}
+
+// The row thresholds for topk_chunk_wide: the k-th largest of the keys stage 1 kept from
+// each row's first TOPK_SAMPLE_CHUNKS chunks (the k largest of each, so the k-th largest
+// key among all their scores, a lower bound of the row's k-th largest), or 0 when those
+// chunks hold fewer than k keys. One wavefront per row; k <= TOPK_SMALL_K.
+__global__ __launch_bounds__(256) void topk_thresh(const uint64_t *__restrict__ cand, int64_t rows, int nchunks, int k,
+                                                   uint64_t *__restrict__ thr) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint64_t *c = cand + row * nchunks * (int64_t)k;
+    const int m = TOPK_SAMPLE_CHUNKS * k;  // <= 128: two keys per lane
+    uint64_t v0 = lane < m ? c[lane] : 0, v1 = lane + 64 < m ? c[lane + 64] : 0;
+    uint64_t t = 0;
+    for (int r = 0; r < k; ++r) {
+        t = wave_max_u64(v0 > v1 ? v0 : v1);
+        if (t == 0) break;  // fewer than k keys: no threshold
+        v0 = v0 == t ? 0 : v0;  // keys are unique: one lane
+        v1 = v1 == t ? 0 : v1;
+    }
+    if (lane == 0) thr[row] = t;
 }
 
 // radix_threshold over m keys in device memory (read once per pass; the merge's

@@ -650,6 +650,65 @@ def test_topk_rows_matches_reference_selection(ctx, rows, n, k):
     _check_topk(di.cpu().numpy(), dv.cpu().numpy(), s, k, "topk")
 
 
+def _fast_top_hits(s, k):
+    # oracle.top_hits for long rows: every score above the k-th largest, plus the ties at
+    # it, sorted by (score desc, index asc), first k. Checked against oracle.top_hits below.
+    idx = np.flatnonzero(~np.isnan(s))
+    if idx.size <= k:
+        return oracle.top_hits(s, k)
+    v = s[idx]
+    kth = np.partition(v, v.size - k)[v.size - k]
+    keep = idx[v >= kth]
+    order = np.lexsort((keep, -s[keep].astype(np.float64)))
+    keep = keep[order[:k]]
+    return keep, s[keep]
+
+
+@pytest.mark.parametrize("kind,k", [("normal", 10), ("grid", 10), ("grid", 32), ("normal", 1), ("increasing", 10),
+                                    ("decreasing", 10), ("constant", 10), ("nan_head", 10)])
+def test_topk_rows_threshold_filter(ctx, kind, k):
+    # 64 rows of 2^20 + 3 scores (129 chunks of 8192, the last ragged): stage 1 runs on each
+    # row's first 4 chunks, takes the k-th largest of their keys as the row's bound, and the
+    # other chunks keep only their keys at or above it when they are at most k. Exact for
+    # any data: ties at the bound break by index (grid, constant), a rising row exceeds the
+    # bound in every chunk (full selection everywhere), a falling one in none, and rows
+    # whose first chunks are NaN have no bound.
+    import torch
+
+    rows, n = 64, (1 << 20) + 3
+    g = workloads.rng(1000 + k + len(kind))
+    if kind == "normal":
+        s = g.standard_normal((rows, n), dtype=np.float32)
+    elif kind == "grid":
+        s = (g.integers(-50, 51, size=(rows, n)) * 0.25).astype(np.float32)
+        s[g.random((rows, n)) < 0.02] = np.nan
+        s[g.random((rows, n)) < 0.02] = -0.0
+    elif kind in ("increasing", "decreasing"):
+        ramp = np.arange(n, dtype=np.float32)
+        s = np.tile(ramp if kind == "increasing" else -ramp, (rows, 1))
+    elif kind == "constant":
+        s = np.full((rows, n), 0.5, np.float32)
+    else:
+        s = g.standard_normal((rows, n), dtype=np.float32)
+        s[: rows // 2, : 4 * 8192] = np.nan
+    say(f"topk threshold filter {kind} rows={rows} n={n} k={k}")
+    ds = torch.from_numpy(s).cuda()
+    di = torch.empty((rows, k), dtype=torch.int32, device="cuda")
+    dv = torch.empty((rows, k), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.topk_rows_dev(ds.data_ptr(), n, rows, n, k, di.data_ptr(), k, dv.data_ptr(), k)
+    torch.cuda.synchronize()
+    hi, hs = di.cpu().numpy(), dv.cpu().numpy()
+    for r in range(rows):
+        idx, sc = _fast_top_hits(s[r], k)
+        if r < 2:
+            oi, osc = oracle.top_hits(s[r], k)
+            assert np.array_equal(idx, oi) and np.array_equal(bits(sc), bits(osc)), "fast reference != oracle"
+        assert hi[r, : idx.size].tolist() == idx.tolist(), f"{kind} row {r}: indices differ"
+        assert np.array_equal(bits(hs[r, : idx.size]), bits(sc)), f"{kind} row {r}: scores differ"
+        assert (hi[r, idx.size:] == -1).all() and np.isnan(hs[r, idx.size:]).all(), f"{kind} row {r}: padding"
+
+
 @pytest.mark.parametrize("k", [1, 10, 32])
 def test_topk_rows_concentrated_winners(ctx, k):
     # Every large score sits at positions one thread of a chunk holds (index = 5 mod 256),

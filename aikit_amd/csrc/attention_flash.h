@@ -290,10 +290,10 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
                 __builtin_amdgcn_s_setprio(1);
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
-                    const int pos = 32 * s + 16 * kb + 8 * hf;
 #pragma unroll
                     for (int i = 0; i < NOT; ++i) {
-                        // = (32 i + r) VP + (2 pos ^ fa_vswz(32 i + r)): with 2 pos = 64 s + 32 kb +
+                        // = (32 i + r) VP + (2 pos ^ fa_vswz(32 i + r)) for the key position
+                        // pos = 32 s + 16 kb + 8 hf: with 2 pos = 64 s + 32 kb +
                         // 16 hf and i < 2 the swizzle is 32 i + 16 (r / 16), so it folds into the
                         // per-lane base and the immediate offset (no extra registers)
                         const int off = (32 * i + r) * Lay::VP + 64 * s + 32 * (kb ^ i) + 16 * (hf ^ (r >> 4));

@@ -1346,6 +1346,7 @@ int enchip_residual_layer_norm_dev(enchip_ctx *ctx, float *d_h, int64_t ldh, con
         else if (D <= 128 && !vec) LN_CASE(2);
         else if (D <= 256) LN_CASE(4);
         else if (D <= 512) LN_CASE(8);
+        else if (D <= 768) LN_CASE(12);  // BERT-base: 3 float4 per lane, none idle
         else if (D <= 1024) LN_CASE(16);
         else if (D <= 2048) LN_CASE(32);
         else LN_CASE(64);
@@ -1385,6 +1386,7 @@ int enchip_residual_layer_norm_quant_dev(enchip_ctx *ctx, float *d_h, int64_t ld
                        d_w, d_b, eps, aq, ldq, as)
         if (width <= 256) LNQ_CASE(4);
         else if (width <= 512) LNQ_CASE(8);
+        else if (width <= 768) LNQ_CASE(12);  // BERT-base: 3 float4 per lane, none idle
         else if (width <= 1024) LNQ_CASE(16);
         else if (width <= 2048) LNQ_CASE(32);
         else LNQ_CASE(64);

@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "gelu_f32.h"
 #include "kernels.h"
@@ -21,10 +22,35 @@
 
 namespace enchip {
 
+// The sum over the wavefront, in every lane: pairs at lane distance 1, 2, 4, 8, 16, 32
+// (the lane_dpp / lane_swap moves). Each step adds two values in either order, which
+// rounds the same (addition commutes), so every lane holds the same bits.
 __device__ __forceinline__ double wave_sum_f64(double s) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-    return s;
+    auto dpp = [](double v, auto ctrl) {
+        const uint64_t u = (uint64_t)__double_as_longlong(v);
+        const uint32_t lo = lane_dpp<decltype(ctrl)::value>((uint32_t)u);
+        const uint32_t hi = lane_dpp<decltype(ctrl)::value>((uint32_t)(u >> 32));
+        return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+    };
+    s += dpp(s, std::integral_constant<int, 0xB1>{});
+    s += dpp(s, std::integral_constant<int, 0x4E>{});
+    s += dpp(s, std::integral_constant<int, 0x141>{});
+    s += dpp(s, std::integral_constant<int, 0x140>{});
+    auto swap_sum = [](double v, bool wide) {
+        const uint64_t u = (uint64_t)__double_as_longlong(v);
+        uint32_t la, lb, ha, hb;
+        if (wide) {
+            lane_swap32((uint32_t)u, la, lb);
+            lane_swap32((uint32_t)(u >> 32), ha, hb);
+        } else {
+            lane_swap16((uint32_t)u, la, lb);
+            lane_swap16((uint32_t)(u >> 32), ha, hb);
+        }
+        return __longlong_as_double((long long)(((uint64_t)ha << 32) | la)) +
+               __longlong_as_double((long long)(((uint64_t)hb << 32) | lb));
+    };
+    s = swap_sum(s, false);
+    return swap_sum(s, true);
 }
 
 // linalg.SoftmaxRowScaledInto (linalg/exp.go:174-182 -> exp_scalar.go:84-89, 9-35), in
@@ -105,19 +131,31 @@ __global__ __launch_bounds__(256) void residual_layer_norm(float *__restrict__ h
     double s = 0.0;
     // column of element j of this lane
     auto col = [&](int j) { return VEC ? 256 * (j >> 2) + 4 * lane + (j & 3) : lane + 64 * j; };
-    if (VEC) {
+    constexpr int CH = VEC && CPL >= 4 ? CPL / 4 : 1;
+    f32x4 wv[CH], bv[CH];  // VEC: the LayerNorm's weight and bias, loaded with the row
+    if constexpr (VEC) {
+        // every load unconditional on a clamped column (a lane past D re-reads the row's
+        // last float4 and ignores it; VEC implies D % 4 == 0), so all are in flight at once
+        f32x4 a[CH], r[CH];
 #pragma unroll
-        for (int j4 = 0; j4 < CPL / 4; ++j4) {
-            const int c = 256 * j4 + 4 * lane;
-            f32x4 a = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
-            if (c < D) {
-                a = *reinterpret_cast<const f32x4 *>(p + c);
-                if (q != nullptr) r = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(q + c));
-            }
-            v[4 * j4 + 0] = q != nullptr ? a.x + r.x : a.x;
-            v[4 * j4 + 1] = q != nullptr ? a.y + r.y : a.y;
-            v[4 * j4 + 2] = q != nullptr ? a.z + r.z : a.z;
-            v[4 * j4 + 3] = q != nullptr ? a.w + r.w : a.w;
+        for (int j4 = 0; j4 < CH; ++j4) {
+            const int cc = min(256 * j4 + 4 * lane, D - 4);
+            a[j4] = *reinterpret_cast<const f32x4 *>(p + cc);
+            wv[j4] = *reinterpret_cast<const f32x4 *>(w + cc);
+            bv[j4] = *reinterpret_cast<const f32x4 *>(b + cc);
+        }
+        if (q != nullptr) {
+#pragma unroll
+            for (int j4 = 0; j4 < CH; ++j4)
+                r[j4] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(q + min(256 * j4 + 4 * lane, D - 4)));
+        }
+#pragma unroll
+        for (int j4 = 0; j4 < CH; ++j4) {
+            const bool in = 256 * j4 + 4 * lane < D;
+            v[4 * j4 + 0] = in ? (q != nullptr ? a[j4].x + r[j4].x : a[j4].x) : 0.0f;
+            v[4 * j4 + 1] = in ? (q != nullptr ? a[j4].y + r[j4].y : a[j4].y) : 0.0f;
+            v[4 * j4 + 2] = in ? (q != nullptr ? a[j4].z + r[j4].z : a[j4].z) : 0.0f;
+            v[4 * j4 + 3] = in ? (q != nullptr ? a[j4].w + r[j4].w : a[j4].w) : 0.0f;
         }
 #pragma unroll
         for (int j = 0; j < CPL; ++j)
@@ -144,17 +182,16 @@ __global__ __launch_bounds__(256) void residual_layer_norm(float *__restrict__ h
     }
     const double variance = wave_sum_f64(sq) / (double)D;
     const double inv_std = 1.0 / sqrt(variance + eps);
-    if (VEC) {
+    if constexpr (VEC) {
 #pragma unroll
         for (int j4 = 0; j4 < CPL / 4; ++j4) {
             const int c = 256 * j4 + 4 * lane;
             if (c >= D) continue;
-            const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + c), bv = *reinterpret_cast<const f32x4 *>(b + c);
             f32x4 o;
-            o.x = (float)((((double)v[4 * j4 + 0] - mean) * inv_std) * (double)wv.x + (double)bv.x);
-            o.y = (float)((((double)v[4 * j4 + 1] - mean) * inv_std) * (double)wv.y + (double)bv.y);
-            o.z = (float)((((double)v[4 * j4 + 2] - mean) * inv_std) * (double)wv.z + (double)bv.z);
-            o.w = (float)((((double)v[4 * j4 + 3] - mean) * inv_std) * (double)wv.w + (double)bv.w);
+            o.x = (float)((((double)v[4 * j4 + 0] - mean) * inv_std) * (double)wv[j4].x + (double)bv[j4].x);
+            o.y = (float)((((double)v[4 * j4 + 1] - mean) * inv_std) * (double)wv[j4].y + (double)bv[j4].y);
+            o.z = (float)((((double)v[4 * j4 + 2] - mean) * inv_std) * (double)wv[j4].z + (double)bv[j4].z);
+            o.w = (float)((((double)v[4 * j4 + 3] - mean) * inv_std) * (double)wv[j4].w + (double)bv[j4].w);
             *reinterpret_cast<f32x4 *>(p + c) = o;
         }
     } else {
@@ -193,20 +230,31 @@ __global__ __launch_bounds__(512) void residual_layer_norm_quant(float *__restri
     if (row < rows) {
         float *p = h + row * ldh;
         const float *qy = y != nullptr ? y + row * ldy : nullptr;
+        // Every load unconditional on a clamped column (a lane past D re-reads the row's
+        // last float4 and ignores it; D % 4 == 0 and D >= 4, host check), the LayerNorm's
+        // weight and bias included, so all are in flight at once: one round trip per row.
+        f32x4 a[CH], r[CH], wv[CH], bv[CH];
+#pragma unroll
+        for (int j4 = 0; j4 < CH; ++j4) {
+            const int cc = min(256 * j4 + 4 * lane, D - 4);
+            a[j4] = *reinterpret_cast<const f32x4 *>(p + cc);
+            wv[j4] = *reinterpret_cast<const f32x4 *>(w + cc);
+            bv[j4] = *reinterpret_cast<const f32x4 *>(b + cc);
+        }
+        if (qy != nullptr) {
+#pragma unroll
+            for (int j4 = 0; j4 < CH; ++j4)
+                r[j4] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(qy + min(256 * j4 + 4 * lane, D - 4)));
+        }
         float v[CPL];
         double s = 0.0;
 #pragma unroll
         for (int j4 = 0; j4 < CH; ++j4) {
-            const int c = 256 * j4 + 4 * lane;
-            f32x4 a = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
-            if (c < D) {
-                a = *reinterpret_cast<const f32x4 *>(p + c);
-                if (qy != nullptr) r = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(qy + c));
-            }
-            v[4 * j4 + 0] = qy != nullptr ? a.x + r.x : a.x;
-            v[4 * j4 + 1] = qy != nullptr ? a.y + r.y : a.y;
-            v[4 * j4 + 2] = qy != nullptr ? a.z + r.z : a.z;
-            v[4 * j4 + 3] = qy != nullptr ? a.w + r.w : a.w;
+            const bool in = 256 * j4 + 4 * lane < D;
+            v[4 * j4 + 0] = in ? (qy != nullptr ? a[j4].x + r[j4].x : a[j4].x) : 0.0f;
+            v[4 * j4 + 1] = in ? (qy != nullptr ? a[j4].y + r[j4].y : a[j4].y) : 0.0f;
+            v[4 * j4 + 2] = in ? (qy != nullptr ? a[j4].z + r[j4].z : a[j4].z) : 0.0f;
+            v[4 * j4 + 3] = in ? (qy != nullptr ? a[j4].w + r[j4].w : a[j4].w) : 0.0f;
         }
 #pragma unroll
         for (int j = 0; j < CPL; ++j)
@@ -228,11 +276,10 @@ __global__ __launch_bounds__(512) void residual_layer_norm_quant(float *__restri
             const int c = 256 * j4 + 4 * lane;
             o[j4] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (c >= D) continue;
-            const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + c), bv = *reinterpret_cast<const f32x4 *>(b + c);
-            o[j4].x = (float)((((double)v[4 * j4 + 0] - mean) * inv_std) * (double)wv.x + (double)bv.x);
-            o[j4].y = (float)((((double)v[4 * j4 + 1] - mean) * inv_std) * (double)wv.y + (double)bv.y);
-            o[j4].z = (float)((((double)v[4 * j4 + 2] - mean) * inv_std) * (double)wv.z + (double)bv.z);
-            o[j4].w = (float)((((double)v[4 * j4 + 3] - mean) * inv_std) * (double)wv.w + (double)bv.w);
+            o[j4].x = (float)((((double)v[4 * j4 + 0] - mean) * inv_std) * (double)wv[j4].x + (double)bv[j4].x);
+            o[j4].y = (float)((((double)v[4 * j4 + 1] - mean) * inv_std) * (double)wv[j4].y + (double)bv[j4].y);
+            o[j4].z = (float)((((double)v[4 * j4 + 2] - mean) * inv_std) * (double)wv[j4].z + (double)bv[j4].z);
+            o[j4].w = (float)((((double)v[4 * j4 + 3] - mean) * inv_std) * (double)wv[j4].w + (double)bv[j4].w);
             const f32x4 ov = {o[j4].x, o[j4].y, o[j4].z, o[j4].w};
             *reinterpret_cast<f32x4 *>(p + c) = ov;
         }

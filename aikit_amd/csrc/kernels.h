@@ -60,13 +60,42 @@ __device__ __forceinline__ float absmax_step(float m, float v) {
     return t > m ? t : m;
 }
 
+// Cross-lane moves for wavefront reductions, all VALU (no LDS permute, no wait):
+//   lane_dpp<CTRL>(v): v of the lane a DPP pattern names within each 16-lane row (every
+//     lane has a source lane): 0xB1 = lane ^ 1, 0x4E = lane ^ 2, 0x141 = the mirror in
+//     each group of 8 (lane ^ 7), 0x140 = the mirror in each row (lane ^ 15);
+//   lane_swap16 / lane_swap32(v): {v, v of lane ^ 16} / {v, v of lane ^ 32}, in an order
+//     that depends on the lane (v_permlane16_swap / v_permlane32_swap of v with itself).
+// A reduction that applies ^1, ^2, then the 8- and 16-lane mirrors sees lane ^ 4 and
+// lane ^ 8 through the mirrors, because by then each group of 4 (then 8) holds one value.
+template <int CTRL>
+__device__ __forceinline__ uint32_t lane_dpp(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ void lane_swap16(uint32_t v, uint32_t &a, uint32_t &b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
+}
+__device__ __forceinline__ void lane_swap32(uint32_t v, uint32_t &a, uint32_t &b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
+}
+
+// The maximum over the wavefront of per-lane maxima that are never NaN (absmax_step's),
+// in every lane: max is order-free there, so any pairing gives the same bits.
 __device__ __forceinline__ float wave_absmax(float m) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        float o = __shfl_xor(m, off, 64);
-        m = o > m ? o : m;
-    }
-    return m;
+    auto step = [](float x, float o) { return o > x ? o : x; };
+    m = step(m, __uint_as_float(lane_dpp<0xB1>(__float_as_uint(m))));
+    m = step(m, __uint_as_float(lane_dpp<0x4E>(__float_as_uint(m))));
+    m = step(m, __uint_as_float(lane_dpp<0x141>(__float_as_uint(m))));
+    m = step(m, __uint_as_float(lane_dpp<0x140>(__float_as_uint(m))));
+    uint32_t a, b;
+    lane_swap16(__float_as_uint(m), a, b);
+    m = step(__uint_as_float(a), __uint_as_float(b));
+    lane_swap32(__float_as_uint(m), a, b);
+    return step(__uint_as_float(a), __uint_as_float(b));
 }
 
 // Byte offset of code (row, k) in the fragment-major activation layout

@@ -138,17 +138,22 @@ __device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v) {
 
 // Maximum over the wavefront, in every lane: within each row of 16 lanes by DPP moves
 // (lane ^ 1, lane ^ 2, the half-row mirror, the row mirror: a few cycles each), then
-// across rows by two lane permutes.
+// across rows by the row-pair and half-wave swaps (v_permlane16_swap /
+// v_permlane32_swap), all VALU.
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     v = dpp_max_u64<0xB1>(v);   // quad_perm [1,0,3,2]
     v = dpp_max_u64<0x4E>(v);   // quad_perm [2,3,0,1]
     v = dpp_max_u64<0x141>(v);  // row_half_mirror: groups of 8
     v = dpp_max_u64<0x140>(v);  // row_mirror: groups of 16
 #pragma unroll
-    for (int off = 16; off < 64; off <<= 1) {
-        const uint32_t lo = __shfl_xor((uint32_t)v, off, 64), hi = __shfl_xor((uint32_t)(v >> 32), off, 64);
-        const uint64_t o = ((uint64_t)hi << 32) | lo;
-        v = o > v ? o : v;
+    for (int wide = 0; wide < 2; ++wide) {
+        const auto lo = wide ? __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false)
+                             : __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+        const auto hi = wide ? __builtin_amdgcn_permlane32_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false)
+                             : __builtin_amdgcn_permlane16_swap((uint32_t)(v >> 32), (uint32_t)(v >> 32), false, false);
+        const uint64_t a = ((uint64_t)(uint32_t)hi[0] << 32) | (uint32_t)lo[0];
+        const uint64_t b = ((uint64_t)(uint32_t)hi[1] << 32) | (uint32_t)lo[1];
+        v = a > b ? a : b;
     }
     return v;
 }

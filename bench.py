@@ -664,7 +664,7 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
             K = lin[base][0]
             u.update(kind="w8a8", bytes=float(5 * M * K + 4 * M), kernel=quant_kernel_name(K, True))
         elif label.endswith("+quant"):
-            cpl = 16 if D <= 1024 else (32 if D <= 2048 else 64)
+            cpl = 4 if D <= 256 else 8 if D <= 512 else 12 if D <= 768 else 16 if D <= 1024 else 32 if D <= 2048 else 64
             u.update(kind="w8a8", bytes=float(13 * M * D + 4 * M + 8 * D),
                      kernel=f"enchip::residual_layer_norm_quant<{cpl}>")
         elif label == "attention":

@@ -285,18 +285,17 @@ __global__ __launch_bounds__(512) void residual_layer_norm_quant(float *__restri
         }
         // the quantizer on the stored values (columns past D hold 0: no effect on the max)
         const float m = row_absmax<CH>(o);
+        // every one of the 64*CH words is written (ldq4 <= 64*CH): past D the values are 0,
+        // so their codes are 0, and no per-word branch is needed
         if (m == 0.0f) {
-            for (int k4 = lane; k4 < ldq4; k4 += 64) *word(k4) = 0;
+#pragma unroll
+            for (int j4 = 0; j4 < CH; ++j4) *word(lane + 64 * j4) = 0;
             if (lane == 0) scale[row] = 0.0f;
         } else {
             const float sc = m / 127.0f;
             const float inv = 1.0f / sc;
 #pragma unroll
-            for (int j4 = 0; j4 < CH; ++j4) {
-                const int k4 = lane + 64 * j4;
-                if (k4 < D4) *word(k4) = pack_codes(o[j4], inv);
-            }
-            for (int k4 = D4 + lane; k4 < ldq4; k4 += 64) *word(k4) = 0;
+            for (int j4 = 0; j4 < CH; ++j4) *word(lane + 64 * j4) = pack_codes(o[j4], inv);
             if (lane == 0) scale[row] = sc;
         }
     }

@@ -47,11 +47,12 @@ enum Epi { EPI_I32 = 0, EPI_F32 = 1, EPI_F32_GELU = 2 };
 // multiply; roundf is round-half-away-from-zero like Go's math.Round, and exact
 // for every float32. A NaN (from an Inf or NaN input) converts to 0 as Go's
 // int8(NaN) does on amd64.
+// Written without branches (the if / else-if clamp compiled to divergent branches per
+// value): the clamp as max / min, which turns a NaN into -127, then the NaN test picks 0.
 __device__ __forceinline__ int quant_code(float v, float inv) {
-    float x = roundf(v * inv);
-    if (x > 127.0f) x = 127.0f;
-    else if (x < -127.0f) x = -127.0f;
-    return (x == x) ? (int)x : 0;
+    const float x = roundf(v * inv);
+    const float c = fminf(fmaxf(x, -127.0f), 127.0f);
+    return x == x ? (int)c : 0;
 }
 
 // Max of |v| ignoring NaN, as the reference's `if v > maxAbs` does.
@@ -119,12 +120,15 @@ __device__ __forceinline__ void load_row_raw(const float *__restrict__ a, int64_
     const int K4 = K >> 2;
     // Unconditional loads (lanes past the row re-read its last float4 and zero it), so
     // all CH are in flight at once; behind a per-chunk branch the compiler waits for
-    // each load before issuing the next.
+    // each load before issuing the next. The zeroing is a bit mask, not a select: the
+    // compiler turns a select of a loaded value back into a branch around the load.
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int k4 = lane + 64 * c;
-        const f32x4 t = __builtin_nontemporal_load(src + min(k4, K4 - 1));
-        v[c] = k4 < K4 ? make_float4(t.x, t.y, t.z, t.w) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const i32x4 t = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(src) + min(k4, K4 - 1));
+        const int keep = k4 < K4 ? -1 : 0;
+        v[c] = make_float4(__int_as_float(t.x & keep), __int_as_float(t.y & keep), __int_as_float(t.z & keep),
+                           __int_as_float(t.w & keep));
     }
 }
 
@@ -210,18 +214,17 @@ __global__ __launch_bounds__(512 / RPW) void quant_rows_frag(const float *__rest
         const int64_t row = r0 + rr;
         if (row >= M) continue;
         const float m = row_absmax<CH>(v[u]);
+        // Every one of the 64*CH words of the row is written (ldq4 <= 64*CH): past K the
+        // loaded values are 0, so their codes are 0, and no per-word branch is needed.
         if (m == 0.0f) {
-            for (int k4 = lane; k4 < ldq4; k4 += 64) *word(rr, k4) = 0;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) *word(rr, lane + 64 * c) = 0;
             if (lane == 0) scale[row] = 0.0f;
         } else {
             const float s = m / 127.0f;
             const float inv = 1.0f / s;
 #pragma unroll
-            for (int c = 0; c < CH; ++c) {
-                const int k4 = lane + 64 * c;
-                if (k4 < K4) *word(rr, k4) = pack_codes(v[u][c], inv);
-            }
-            for (int k4 = K4 + lane; k4 < ldq4; k4 += 64) *word(rr, k4) = 0;
+            for (int c = 0; c < CH; ++c) *word(rr, lane + 64 * c) = pack_codes(v[u][c], inv);
             if (lane == 0) scale[row] = s;
         }
     }

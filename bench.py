@@ -52,6 +52,12 @@ def quant_kernel_name(K: int, frag: bool) -> str:
     return f"enchip::quant_rows_vec<{(K + 255) // 256}>" if 0 < K <= 4096 and K % 4 == 0 else "enchip::quant_rows_scalar<false>"
 
 
+def ln_cpl(D: int) -> int:
+    """Floats per lane of the LayerNorm kernels enchip launches for rows of D (multiple
+    of 4, 16-byte aligned) floats."""
+    return 4 if D <= 256 else 8 if D <= 512 else 12 if D <= 768 else 16 if D <= 1024 else 32 if D <= 2048 else 64
+
+
 def measured_traffic() -> dict:
     """HBM bytes per launch for each linear and its quantizer, as measured by the two
     rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) recorded in TRAFFIC_PROFILE. The
@@ -664,9 +670,8 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
             K = lin[base][0]
             u.update(kind="w8a8", bytes=float(5 * M * K + 4 * M), kernel=quant_kernel_name(K, True))
         elif label.endswith("+quant"):
-            cpl = 4 if D <= 256 else 8 if D <= 512 else 12 if D <= 768 else 16 if D <= 1024 else 32 if D <= 2048 else 64
             u.update(kind="w8a8", bytes=float(13 * M * D + 4 * M + 8 * D),
-                     kernel=f"enchip::residual_layer_norm_quant<{cpl}>")
+                     kernel=f"enchip::residual_layer_norm_quant<{ln_cpl(D)}>")
         elif label == "attention":
             mode = ctx.attention_products
             u.update(kind="attention", ops=4.0 * S * H * L * L * hd, bytes=float(4 * M * D * 4),
@@ -678,7 +683,7 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
             u.update(kind="row", bytes=float(12 * M * D), kernel="enchip::embed_rows<true>")
         elif label in ("embed_ln", "attn_ln", "out_ln"):
             u.update(kind="row", bytes=float((8 if label == "embed_ln" else 12) * M * D),
-                     kernel="enchip::residual_layer_norm<16, true>")
+                     kernel=f"enchip::residual_layer_norm<{ln_cpl(D)}, true>")
         else:
             u.update(kind="row", bytes=float(4 * M * D), kernel="enchip::pool_mean_cols + l2_normalize_rows")
         u["ms_per_step"] = u["us_per_launch"] * u["launches_per_step"] / 1e3

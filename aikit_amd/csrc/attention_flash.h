@@ -121,21 +121,18 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
     // A negative scale is applied as |scale| to -Q (an exact negation), so that the scores'
     // factor c = |scale| log2 e is never negative and the running maximum of the raw scores
     // s gives that of c s.
+    // The Q loads are issued here and split after the first K / V tile's loads are issued,
+    // so all of them are in flight together (a per-block branch between a load and the next
+    // made the compiler wait for each in turn); the negation flips the sign bit (exactly -q,
+    // NaN included) without a branch.
     const bool neg = scale < 0.0f;
     const float c = fabsf(scale) * FA_LOG2E;
     bf16x8 qh[NB], ql[NB];
+    float qt[NB][8];
     {
         const float *qrow = q + (row0 + min(qw + r, L - 1)) * ld + head * HD;
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            float t[8];
-            load8(qrow + 16 * b + 8 * hf, t);
-            if (neg) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) t[i] = -t[i];
-            }
-            split_bf16x8(t, qh[b], ql[b]);
-        }
+        for (int b = 0; b < NB; ++b) load8(qrow + 16 * b + 8 * hf, qt[b]);
     }
 
     // K / V tile staging: loads of tile t into registers, then split into LDS stage s.
@@ -212,6 +209,15 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
     float m_run = -INFINITY, l_run = 0.0f;
 
     load_tile(0);
+    {
+        const uint32_t qsign = neg ? 0x80000000u : 0u;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qt[b][i] = __uint_as_float(__float_as_uint(qt[b][i]) ^ qsign);
+            split_bf16x8(qt[b], qh[b], ql[b]);
+        }
+    }
     store_tile(0);
     lds_barrier();
     for (int t = 0; t < nt; ++t) {

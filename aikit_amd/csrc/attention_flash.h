@@ -42,12 +42,11 @@ namespace enchip {
 
 constexpr int FA_KT = 64;     // keys per LDS tile
 // Wavefronts (32 queries each) per workgroup in the product: 16 (512 queries, 1024
-// threads) once L > FA_WIDE_L, except for L > 512 on grids with fewer workgroups than
-// CUs; else 8. Each K / V tile is split into LDS once per
-// workgroup, so wider workgroups split each head's keys fewer times: at BERT-base
-// shape (L = 512, 64 sequences, 12 heads) 16 wavefronts took 201 us against 215-221 us
-// for 8 and 270 us for 4 on MI355X, bit-identical results. Up to L = 256, 16 wavefronts
-// would leave half of each workgroup idle.
+// threads) for 256 < L < 512, and for L > 512 on grids of at least as many workgroups as
+// CUs; else 8 (the host's rule, with measurements, is in enchip_attention_f32_dev). Each
+// K / V tile is split into LDS once per workgroup, so wider workgroups split each head's
+// keys fewer times; narrower ones leave two workgroups per CU whose phases drift apart.
+// Up to L = 256, 16 wavefronts would leave half of each workgroup idle.
 constexpr int FA_WAVES = 8;
 constexpr int FA_WAVES_WIDE = 16;
 constexpr int FA_WIDE_L = 256;

@@ -1441,13 +1441,20 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
     if (flash) {
         const bool vec = ldo % 4 == 0 && (uintptr_t)d_out % 16 == 0;
         constexpr int nw8 = enchip::FA_WAVES, nw16 = enchip::FA_WAVES_WIDE;
-        // 16 wavefronts once L > 256, except for L > 512 on a grid with fewer workgroups
-        // than CUs: there the 8-wavefront form's twice as many workgroups spread further
-        // (L = 1000 over 8 heads x sequences: 51 against 78 us), while up to L = 512 one
-        // 16-wavefront workgroup covers a head's queries that two 8-wavefront ones would
-        // split unevenly (L = 300 over 192 heads x sequences: 30 against 43 us)
+        // 16 wavefronts once L > 256, except:
+        //  - L = 512 (two full 8-wavefront workgroups per head): two workgroups per CU
+        //    whose barrier phases drift apart overlap one's MFMA work with the other's
+        //    softmax, which outweighs splitting each K / V tile twice (BERT-base, 64 x 12
+        //    heads: 190-194 -> 175-177 us; XLM-R-large, 128 x 16: 490 -> 472-477);
+        //  - L > 512 on a grid with fewer workgroups than CUs: the 8-wavefront form's
+        //    twice as many workgroups spread further (L = 1000 over 8 heads x sequences:
+        //    51 against 78 us).
+        // Otherwise up to L = 512 one 16-wavefront workgroup covers a head's queries that
+        // two 8-wavefront ones would split unevenly (L = 300 over 768 heads x sequences:
+        // 94.5 against 98.7 us). The results are the same bits either way.
         const int64_t wide_grid = ((L + 32 * nw16 - 1) / (32 * nw16)) * heads * nseq;
-        const bool wide = L > enchip::FA_WIDE_L && (L <= 32 * nw16 || wide_grid >= ctx->num_cus);
+        const bool wide = L > enchip::FA_WIDE_L &&
+                          (L <= 32 * nw16 ? L != 32 * nw16 : wide_grid >= ctx->num_cus);
         const int nw = wide ? nw16 : nw8;
         lds = (size_t)enchip::fa_lds_bytes((int)head_dim);
         per_seq = ((L + 32 * nw - 1) / (32 * nw)) * heads;

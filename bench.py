@@ -641,7 +641,7 @@ def time_ops(torch, stream, model, step, steps: int, hev, warmup: int = 1):
 
 def fa_waves(ctx, S: int, L: int, H: int) -> int:
     """Wavefronts per workgroup of the library's flash attention launch (its dispatch rule)."""
-    return 16 if L > 256 and (L <= 512 or -(-L // 512) * H * S >= ctx.device_info()["num_cus"]) else 8
+    return 16 if L > 256 and (L != 512 if L <= 512 else -(-L // 512) * H * S >= ctx.device_info()["num_cus"]) else 8
 
 
 def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:

@@ -269,8 +269,8 @@ def test_split_bf16_attention_error_is_bounded_by_the_split(ctx, mode):
 
 
 def test_flash_attention_wide_and_narrow_workgroups_agree(ctx):
-    # The flash kernel runs 16 wavefronts per workgroup (512 queries) once L > 256, except
-    # for L > 512 on a grid with fewer workgroups than CUs, where it runs 8. Each query's
+    # The flash kernel runs 16 wavefronts per workgroup (512 queries) for 256 < L < 512 and
+    # for L > 512 on a grid of at least as many workgroups as CUs; else 8. Each query's
     # arithmetic is the same in both, so the same sequences give the same bits whether they
     # run in a batch large enough for the 16-wavefront form or alone (the 8-wavefront
     # form); both against float64.

@@ -48,7 +48,7 @@ def quant_kernel_name(K: int, frag: bool) -> str:
     Kp = (K + 63) // 64 * 64
     if frag:
         ch = (Kp + 255) // 256
-        return f"enchip::quant_rows_frag<{ch}, {2 if ch <= 6 else 1}>" if 0 < Kp <= 4096 and K % 4 == 0 else "enchip::quant_rows_scalar<true>"
+        return f"enchip::quant_rows_frag<{ch}, {2 if ch <= 2 else 1}>" if 0 < Kp <= 4096 and K % 4 == 0 else "enchip::quant_rows_scalar<true>"
     return f"enchip::quant_rows_vec<{(K + 255) // 256}>" if 0 < K <= 4096 and K % 4 == 0 else "enchip::quant_rows_scalar<false>"
 
 

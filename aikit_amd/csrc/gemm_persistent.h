@@ -335,6 +335,11 @@ __global__ __launch_bounds__(64 * NW, BM == PT_BM_SMALL ? 3 : NW / 2) void gemm_
                 // took max-popcount rounds (~2.2). Measured on MI355X (same box, A/B of
                 // whole libraries, bit-identical): FFN-up in the BERT-base encode 196 ->
                 // 186 us, config 2's linear 48 -> 45 us per call.
+                // The tail pass is a chain of LDS round trips and one long dependent
+                // gelu_f32 per lane; at raised wave priority it issues ahead of the other
+                // workgroup's wave on the SIMD (config 2, many tails: 43.8 -> 42.2 us per
+                // call; the BERT-base encode unchanged to -0.5%).
+                __builtin_amdgcn_s_setprio(1);
                 {
                     // The prefix sum, bit-sliced: one ballot and one count of the lanes
                     // below per bit of the count (0..32), all VALU and scalar work, where a
@@ -389,6 +394,7 @@ __global__ __launch_bounds__(64 * NW, BM == PT_BM_SMALL ? 3 : NW / 2) void gemm_
                         *cell = __float_as_int(gelu_f32(__int_as_float(*cell)));
                     }
                 }
+                __builtin_amdgcn_s_setprio(0);
                 // Pass 3: 16-byte stores of the finished values.
 #pragma unroll
                 for (int k = 0; k < KR; ++k) v[k] = *reinterpret_cast<const int4 *>(&scr[(rsub + RPL * k) * SP + 4 * c4]);

@@ -21,6 +21,7 @@
 #include "encoder_ops.h"
 #include "gemm_f32.h"
 #include "gemm_persistent.h"
+#include "gemm_skinny.h"
 #include "topk.h"
 #include "kernels.h"
 #include "probes.h"
@@ -132,6 +133,8 @@ struct enchip_ctx {
     size_t hit_i_cap = 0;
     float *d_hit_s = nullptr;
     size_t hit_s_cap = 0;
+    // enchip_ann_topk routing (enchip_ann_topk_stats)
+    int64_t ann_fused_calls = 0, ann_fallbacks = 0;
 };
 
 namespace {
@@ -353,31 +356,74 @@ int pt_bm(const enchip_ctx *c, const Weight &w, int64_t M) {
 // epilogue keeps 0: raised, BERT-base FFN-up took 206 us per launch in the encode against
 // 189 us (it ran 3-5% faster on uniformly random codes, whose pre-activations differ).
 int pt_prio(const Weight &w, int epi) {
-    return epi == enchip::EPI_F32 && (w.N >= 1024 || w.Kp >= 1024) ? 1 : 0;
+    return (epi == enchip::EPI_F32 || epi == enchip::EPI_TOPK) && (w.N >= 1024 || w.Kp >= 1024) ? 1 : 0;
 }
 
 template <int BM, int PW, int EPI, bool AF>
 void launch_pt_bm(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, const float *as, const float *bias,
-                  void *out, int64_t ldo, int64_t M, hipStream_t s) {
+                  void *out, int64_t ldo, int64_t M, hipStream_t s, const enchip::TopkSink &sink) {
     using namespace enchip;
     const int tilesM = (int)((M + BM - 1) / BM), tilesN = (int)((w.N + PT_BN - 1) / PT_BN);
     const int64_t tiles = (int64_t)tilesM * tilesN;
     const int grid = persistent_grid(c, tiles, BM == PT_BM_SMALL ? 3 : 2);
     if (pt_prio(w, EPI))
         hipLaunchKernelGGL((gemm_w8a8_pt<BM, PT_BN, PT_BK, PW, EPI, AF, PT_NW, 1>), dim3(grid), dim3(64 * PT_NW), 0, s, aq,
-                           lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp, tilesN, (int)tiles);
+                           lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp, tilesN, (int)tiles, sink);
     else
         hipLaunchKernelGGL((gemm_w8a8_pt<BM, PT_BN, PT_BK, PW, EPI, AF, PT_NW, 0>), dim3(grid), dim3(64 * PT_NW), 0, s, aq,
-                           lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp, tilesN, (int)tiles);
+                           lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp, tilesN, (int)tiles, sink);
 }
 
 template <int PW, int EPI, bool AF>
 void launch_pt(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, const float *as, const float *bias,
-               void *out, int64_t ldo, int64_t M, hipStream_t s) {
+               void *out, int64_t ldo, int64_t M, hipStream_t s, const enchip::TopkSink &sink = {}) {
     if (pt_bm(c, w, M) == enchip::PT_BM_SMALL)
-        launch_pt_bm<enchip::PT_BM_SMALL, PW, EPI, AF>(c, w, aq, lda, as, bias, out, ldo, M, s);
+        launch_pt_bm<enchip::PT_BM_SMALL, PW, EPI, AF>(c, w, aq, lda, as, bias, out, ldo, M, s, sink);
     else
-        launch_pt_bm<enchip::PT_BM, PW, EPI, AF>(c, w, aq, lda, as, bias, out, ldo, M, s);
+        launch_pt_bm<enchip::PT_BM, PW, EPI, AF>(c, w, aq, lda, as, bias, out, ldo, M, s, sink);
+}
+
+// gemm_w8a8_skinny's shapes (gemm_skinny.h), by Kp / 32 (0: not this kernel): more rows
+// than the small-M kernels take and at most 256 (all of them in LDS), Kp / 32 one of 4, 8,
+// 12, 16, and at least 1024 groups of 32 channels (N >= 32768: ann indexes). Row-major A
+// needs 16-byte aligned rows.
+int skinny_nk(const enchip_ctx *c, const Weight &w, int64_t M, const void *aq, int64_t lda, bool af) {
+    const int nk = (int)(w.Kp / 32);
+    if (M <= c->small_m || M > 256 || (nk != 4 && nk != 8 && nk != 12 && nk != 16) || (w.N + 31) / 32 < 1024)
+        return 0;
+    if (!af && (lda % 16 != 0 || (uintptr_t)aq % 16 != 0 || lda < w.Kp)) return 0;
+    return nk;
+}
+
+template <int MB, int EPI, bool AF>
+void launch_skinny_mb(enchip_ctx *c, const Weight &w, int nk, const int8_t *aq, int64_t lda, const float *as,
+                      const float *bias, float *out, int64_t ldo, int64_t M, hipStream_t s,
+                      const enchip::TopkSink &sink) {
+    using namespace enchip;
+    const int64_t groups = (w.N + 31) / 32;
+    const dim3 grid((unsigned)std::min<int64_t>(c->num_cus, (groups + SK_WAVES - 1) / SK_WAVES)), block(64 * SK_WAVES);
+#define SK_CASE(NK)                                                                                                    \
+    case NK:                                                                                                           \
+        hipLaunchKernelGGL((gemm_w8a8_skinny<MB, NK, EPI, AF>), grid, block, 0, s, aq, lda, w.d_w, as, w.d_s, bias, \
+                           out, ldo, (int)M, (int)w.N, sink);                                                          \
+        break;
+    switch (nk) {
+        SK_CASE(4)
+        SK_CASE(8)
+        SK_CASE(12)
+        SK_CASE(16)
+        default: break;
+    }
+#undef SK_CASE
+}
+
+// nk from skinny_nk; 32 x 4 or 32 x 8 rows staged.
+template <int EPI, bool AF>
+void launch_skinny(enchip_ctx *c, const Weight &w, int nk, const int8_t *aq, int64_t lda, const float *as,
+                   const float *bias, float *out, int64_t ldo, int64_t M, hipStream_t s,
+                   const enchip::TopkSink &sink = {}) {
+    if (M <= 128) launch_skinny_mb<4, EPI, AF>(c, w, nk, aq, lda, as, bias, out, ldo, M, s, sink);
+    else launch_skinny_mb<8, EPI, AF>(c, w, nk, aq, lda, as, bias, out, ldo, M, s, sink);
 }
 
 // af: aq is fragment-major (the caller checked route_af); otherwise row-major at pitch lda.
@@ -385,6 +431,13 @@ void launch_pt(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, co
 template <int EPI>
 bool launch_gemm_epi(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, const float *as,
                      const float *bias, void *out, int64_t ldo, int64_t M, hipStream_t s, bool af) {
+    if (EPI == enchip::EPI_F32) {
+        if (const int nk = skinny_nk(c, w, M, aq, lda, af)) {
+            if (af) launch_skinny<enchip::EPI_F32, true>(c, w, nk, aq, lda, as, bias, (float *)out, ldo, M, s);
+            else launch_skinny<enchip::EPI_F32, false>(c, w, nk, aq, lda, as, bias, (float *)out, ldo, M, s);
+            return true;
+        }
+    }
     if (af || (M > c->small_m && use_persistent(w, aq, lda, out, ldo, M, false))) {
         if (af) launch_pt<enchip::PT_PW, EPI, true>(c, w, aq, lda, as, bias, out, ldo, M, s);
         else launch_pt<enchip::PT_PW, EPI, false>(c, w, aq, lda, as, bias, out, ldo, M, s);
@@ -593,7 +646,10 @@ int enchip_gemm_kernel_name(enchip_ctx *ctx, enchip_weight h, int64_t M, int act
     if (!buf || len <= 0) return fail(ctx, ENCHIP_ERR_ARG, "gemm_kernel_name: bad buffer");
     const int epi = act_code(act);
     char name[96];
-    if (route_af(ctx, *w, M, nullptr, w->N))
+    const int sk = epi == enchip::EPI_F32 ? skinny_nk(ctx, *w, M, nullptr, w->Kp, true) : 0;
+    if (sk)  // the library's own quantization is fragment-major (pre_dev's row-major codes: false)
+        snprintf(name, sizeof name, "enchip::gemm_w8a8_skinny<%d, %d, %d, true>", M <= 128 ? 4 : 8, sk, epi);
+    else if (route_af(ctx, *w, M, nullptr, w->N))
         snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, true, %d, %d>", pt_bm(ctx, *w, M),
                  enchip::PT_BN, enchip::PT_BK, pt_ring(*w), epi, enchip::PT_NW, pt_prio(*w, epi));
     else if (fused_small_m(ctx, *w, M, nullptr) && epi != enchip::EPI_I32)
@@ -1546,7 +1602,7 @@ int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, in
             hipLaunchKernelGGL(topk_chunk_wide, dim3((unsigned)TOPK_SAMPLE_CHUNKS, (unsigned)nr), dim3(256), 0, s,
                                scores + r0 * ld, ld, n, (int)k, (int)nchunks, cr, 0, (const uint64_t *)nullptr);
             hipLaunchKernelGGL(topk_thresh, dim3((unsigned)((nr + 3) / 4)), dim3(256), 0, s, (const uint64_t *)cr, nr,
-                               (int)nchunks, (int)k, thr + r0);
+                               (int)nchunks, (int)k, thr + r0, (unsigned *)nullptr);
             hipLaunchKernelGGL(topk_chunk_wide, dim3((unsigned)(nchunks - TOPK_SAMPLE_CHUNKS), (unsigned)nr), dim3(256), 0,
                                s, scores + r0 * ld, ld, n, (int)k, (int)nchunks, cr, TOPK_SAMPLE_CHUNKS,
                                (const uint64_t *)(thr + r0));
@@ -1565,6 +1621,81 @@ int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, in
                            index + r0 * ldi, ldi, score + r0 * lds, lds);
     }
     return check_launch(c, "topk");
+}
+
+// enchip_ann_topk's fused route: the selection runs in the scoring GEMM's epilogue, so the
+// M x N scores are never written or read back.
+//   1. gemm_w8a8_pt scores each row's first kSinkSample columns into d_dst, and stage 1
+//      + topk_thresh take the k-th largest key among them: a lower bound of the row's
+//      k-th largest key (the sample is part of the row). topk_thresh zeroes the counts.
+//   2. gemm_w8a8_pt<EPI_TOPK> scores every column and appends the scores whose key is at
+//      or above their row's bound to the row's list (gemm_persistent.h, TopkSink): the
+//      row's k largest keys are all there.
+//   3. topk_sink_merge selects the k largest of each list.
+// About k of every kSinkSample columns clear a bound on exchangeable scores (k * N /
+// kSinkSample per row); a row whose list overflows kSinkCap (adversarial orders, e.g.
+// scores rising along the index) makes the caller run the two-pass route instead.
+constexpr int64_t kSinkSample = (int64_t)enchip::TOPK_SAMPLE_CHUNKS * enchip::TOPK_WCHUNK;
+constexpr int kSinkCap = enchip::TOPK_CHUNK;
+
+// k <= TOPK_SMALL_K on fragment-major activations, over rows at least 4 samples long whose
+// expected lists fill at most a quarter of the cap.
+bool ann_fused_ok(const Weight &w, int64_t k, bool af) {
+    return af && k >= 1 && k <= enchip::TOPK_SMALL_K && w.N >= 4 * kSinkSample &&
+           k * w.N <= (int64_t)kSinkCap * kSinkSample / 4;
+}
+
+// Enqueues steps 1-3 on s for M rows of fragment-major codes in the context scratch
+// (d_aq, d_as), leaving the hits in d_hit_i / d_hit_s and the list sizes (uint32, M) at
+// *counts.
+int launch_ann_fused(enchip_ctx *c, const Weight &w, int64_t M, int64_t k, hipStream_t s, const unsigned **counts) {
+    using namespace enchip;
+    int rc;
+    if ((rc = ensure(c, &c->d_dst, &c->dst_cap, (size_t)(M * kSinkSample) * sizeof(float)))) return rc;
+    const int64_t cand_n = M * TOPK_SAMPLE_CHUNKS * k;
+    const size_t words = (size_t)(cand_n + M + M * kSinkCap) + (size_t)(M * kSinkCap + 1) / 2 + (size_t)(M + 1) / 2;
+    if ((rc = ensure(c, &c->d_cand, &c->cand_cap, words * sizeof(uint64_t)))) return rc;
+    uint64_t *cand = c->d_cand, *thr = cand + cand_n, *keys = thr + M;
+    float *raw = reinterpret_cast<float *>(keys + M * kSinkCap);
+    unsigned *count = reinterpret_cast<unsigned *>(raw + M * kSinkCap + ((M * kSinkCap) & 1));
+    Weight sample = w;
+    sample.N = sample.Np = kSinkSample;
+    if ((rc = launch_gemm(c, sample, c->d_aq, w.Kp, c->d_as, nullptr, EPI_F32, c->d_dst, kSinkSample, M, s, true)))
+        return rc;
+    for (int64_t r0 = 0; r0 < M; r0 += 65535) {
+        const int64_t nr = std::min<int64_t>(65535, M - r0);
+        uint64_t *cr = cand + r0 * TOPK_SAMPLE_CHUNKS * k;
+        hipLaunchKernelGGL(topk_chunk_wide, dim3((unsigned)TOPK_SAMPLE_CHUNKS, (unsigned)nr), dim3(256), 0, s,
+                           c->d_dst + r0 * kSinkSample, kSinkSample, kSinkSample, (int)k, TOPK_SAMPLE_CHUNKS, cr, 0,
+                           (const uint64_t *)nullptr);
+        hipLaunchKernelGGL(topk_thresh, dim3((unsigned)((nr + 3) / 4)), dim3(256), 0, s, (const uint64_t *)cr, nr,
+                           TOPK_SAMPLE_CHUNKS, (int)k, thr + r0, count + r0);
+    }
+    if ((rc = check_launch(c, "ann_topk sample"))) return rc;
+    TopkSink sink;
+    sink.thr = thr;
+    sink.count = count;
+    sink.key = keys;
+    sink.score = raw;
+    sink.cap = kSinkCap;
+    if (const int nk = skinny_nk(c, w, M, c->d_aq, w.Kp, true)) {
+        // 128 rows a launch: with 256 rows' accumulators the candidate epilogue spills
+        for (int64_t r0 = 0; r0 < M; r0 += 128) {
+            TopkSink part = sink;
+            part.thr += r0;
+            part.count += r0;
+            part.key += r0 * kSinkCap;
+            part.score += r0 * kSinkCap;
+            launch_skinny_mb<4, EPI_TOPK, true>(c, w, nk, c->d_aq + r0 * w.Kp, w.Kp, c->d_as + r0, nullptr, nullptr, 0,
+                                                std::min<int64_t>(128, M - r0), s, part);
+        }
+    } else
+        launch_pt<PT_PW, EPI_TOPK, true>(c, w, c->d_aq, w.Kp, c->d_as, nullptr, nullptr, 0, M, s, sink);
+    if ((rc = check_launch(c, "gemm_w8a8 topk"))) return rc;
+    hipLaunchKernelGGL(topk_sink_merge, dim3((unsigned)M), dim3(256), 0, s, (const unsigned *)count,
+                       (const uint64_t *)keys, (const float *)raw, kSinkCap, (int)k, c->d_hit_i, k, c->d_hit_s, k);
+    *counts = count;
+    return check_launch(c, "topk_sink_merge");
 }
 
 }  // namespace
@@ -1601,7 +1732,6 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int6
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     const int64_t K = w->K, N = w->N;
     if ((rc = ensure(ctx, &ctx->d_a, &ctx->a_cap, std::max<size_t>((size_t)(M * K) * sizeof(float), 16)))) return rc;
-    if ((rc = ensure(ctx, &ctx->d_dst, &ctx->dst_cap, (size_t)(M * N) * sizeof(float)))) return rc;
     if ((rc = ensure(ctx, &ctx->d_hit_i, &ctx->hit_i_cap, (size_t)(M * k) * sizeof(int32_t)))) return rc;
     if ((rc = ensure(ctx, &ctx->d_hit_s, &ctx->hit_s_cap, (size_t)(M * k) * sizeof(float)))) return rc;
     if ((rc = ensure_act_scratch(ctx, M, w->Kp))) return rc;
@@ -1609,8 +1739,24 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int6
     if ((rc = scratch_wait(ctx, s))) return rc;
     if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, queries, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
     // the bias-free W8A8 scores (ann/backend.go:25-29), then the selection on the device
-    const bool af = route_af(ctx, *w, M, ctx->d_dst, N);
+    // (d_dst, from the context allocator, is 256-byte aligned: the route does not depend
+    // on whether it is allocated yet)
+    const bool af = route_af(ctx, *w, M, nullptr, N);
     if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, w->Kp, ctx->d_as, s, af))) return rc;
+    if (ann_fused_ok(*w, k, af)) {
+        const unsigned *d_count = nullptr;
+        if ((rc = launch_ann_fused(ctx, *w, M, k, s, &d_count))) return rc;
+        if ((rc = scratch_record(ctx, s))) return rc;
+        std::vector<unsigned> count((size_t)M);
+        HIP_TRY(ctx, hipMemcpyAsync(hit_index, ctx->d_hit_i, (size_t)(M * k) * sizeof(int32_t), hipMemcpyDeviceToHost, s));
+        HIP_TRY(ctx, hipMemcpyAsync(hit_score, ctx->d_hit_s, (size_t)(M * k) * sizeof(float), hipMemcpyDeviceToHost, s));
+        HIP_TRY(ctx, hipMemcpyAsync(count.data(), d_count, (size_t)M * sizeof(unsigned), hipMemcpyDeviceToHost, s));
+        HIP_TRY(ctx, hipStreamSynchronize(s));
+        ++ctx->ann_fused_calls;
+        if (*std::max_element(count.begin(), count.end()) <= (unsigned)kSinkCap) return ENCHIP_OK;
+        ++ctx->ann_fallbacks;  // some row's list overflowed: the two-pass route below
+    }
+    if ((rc = ensure(ctx, &ctx->d_dst, &ctx->dst_cap, (size_t)(M * N) * sizeof(float)))) return rc;
     if ((rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, nullptr, enchip::EPI_F32, ctx->d_dst, N, M, s, af)))
         return rc;
     if ((rc = launch_topk(ctx, ctx->d_dst, N, M, N, k, ctx->d_hit_i, k, ctx->d_hit_s, k, s))) return rc;
@@ -1618,6 +1764,15 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int6
     HIP_TRY(ctx, hipMemcpyAsync(hit_index, ctx->d_hit_i, (size_t)(M * k) * sizeof(int32_t), hipMemcpyDeviceToHost, s));
     HIP_TRY(ctx, hipMemcpyAsync(hit_score, ctx->d_hit_s, (size_t)(M * k) * sizeof(float), hipMemcpyDeviceToHost, s));
     HIP_TRY(ctx, hipStreamSynchronize(s));
+    return ENCHIP_OK;
+}
+
+int enchip_ann_topk_stats(enchip_ctx *ctx, int64_t *fused, int64_t *fallbacks) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (!fused || !fallbacks) return fail(ctx, ENCHIP_ERR_ARG, "ann_topk_stats: null pointer");
+    *fused = ctx->ann_fused_calls;
+    *fallbacks = ctx->ann_fallbacks;
     return ENCHIP_OK;
 }
 

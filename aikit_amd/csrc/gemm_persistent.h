@@ -28,6 +28,8 @@
 //   * GELU: every value of a 32-row chunk takes ErfF32's series branch without
 //     branching; the few values that need another branch are gathered into a per-wave
 //     list in LDS and re-evaluated 64 at a time.
+//   * EPI_TOPK (ann scoring with its top-k): nothing is stored; the scores at or above
+//     their row's bound go to the row's candidate list (TopkSink).
 //
 // Numerics are those of gemm_w8a8 (kernels.h): the int32 dot is exact, and the epilogue
 // rounds in the reference's order, so the two kernels give identical bits.
@@ -37,10 +39,23 @@
 #include <stdint.h>
 
 #include "kernels.h"
+#include "topk.h"
 
 #pragma clang fp contract(off)
 
 namespace enchip {
+
+// Where EPI_TOPK puts the scores it keeps: row r's candidates are its scores whose top-k
+// key (topk.h) is at or above thr[r] (every non-NaN score when thr[r] is 0), in no
+// particular order. count[r] (zeroed before the launch) counts them all; the first cap go
+// to key[r*cap ..] and, as their f32 bits (so a -0 stays -0), score[r*cap ..].
+struct TopkSink {
+    const uint64_t *thr = nullptr;
+    unsigned *count = nullptr;
+    uint64_t *key = nullptr;
+    float *score = nullptr;
+    int cap = 0;
+};
 
 // Tile geometry and ring depth of the persistent kernel (the host checks its
 // preconditions). PT_BM_SMALL: the 64-row tile the host picks when 128-row tiles would
@@ -64,7 +79,7 @@ template <int BM, int BN, int BK, int PW, int EPI, bool AF, int NW, int PRIO>
 __global__ __launch_bounds__(64 * NW, BM == PT_BM_SMALL ? 3 : NW / 2) void gemm_w8a8_pt(
     const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ Wf,
     const float *__restrict__ aS, const float *__restrict__ wS, const float *__restrict__ bias,
-    void *__restrict__ out, int64_t ldo, int M, int N, int Kp, int tilesN, int numTiles) {
+    void *__restrict__ out, int64_t ldo, int M, int N, int Kp, int tilesN, int numTiles, TopkSink sink) {
     constexpr int NT = 64 * NW;  // threads
     constexpr int WN = BN / NW;  // output columns per wave
     constexpr int TM = BM / 32, TN = WN / 32;
@@ -90,6 +105,7 @@ __global__ __launch_bounds__(64 * NW, BM == PT_BM_SMALL ? 3 : NW / 2) void gemm_
     __shared__ __attribute__((aligned(16))) float s_as[BM];
     __shared__ __attribute__((aligned(16))) float s_ws[BN];
     __shared__ __attribute__((aligned(16))) float s_b[BN];
+    __shared__ __attribute__((aligned(16))) uint64_t s_thr[EPI == EPI_TOPK ? BM : 1];  // row bounds, as s_as
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nk = Kp / BK, nk32 = Kp >> 5;
@@ -177,6 +193,7 @@ __global__ __launch_bounds__(64 * NW, BM == PT_BM_SMALL ? 3 : NW / 2) void gemm_
         const float c_as = aS[min(m0 + (tid & (BM - 1)), M - 1)];
         const float c_ws = wS[min(n0 + tid, N - 1)];
         const float c_b = has_bias ? bias[min(n0 + tid, N - 1)] : kNoBias;
+        const uint64_t c_thr = EPI == EPI_TOPK ? sink.thr[min(m0 + (tid & (BM - 1)), M - 1)] : 0;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -244,6 +261,7 @@ __global__ __launch_bounds__(64 * NW, BM == PT_BM_SMALL ? 3 : NW / 2) void gemm_
         if (PRIO) __builtin_amdgcn_s_setprio(0);
         // ---- epilogue: constants to LDS, then transpose + 16-byte stores per wave
         if (tid < BM) s_as[as_slot] = c_as;
+        if (EPI == EPI_TOPK && tid < BM) s_thr[as_slot] = c_thr;
         if (tid < BN) {
             s_ws[tid] = c_ws;
             s_b[tid] = c_b;
@@ -402,7 +420,7 @@ __global__ __launch_bounds__(64 * NW, BM == PT_BM_SMALL ? 3 : NW / 2) void gemm_
                 // all of the chunk's LDS reads first, then the arithmetic
 #pragma unroll
                 for (int k = 0; k < KR; ++k) v[k] = *reinterpret_cast<const int4 *>(&scr[(rsub + RPL * k) * SP + 4 * c4]);
-                if (EPI == EPI_F32) {
+                if (EPI == EPI_F32 || EPI == EPI_TOPK) {
 #pragma unroll
                     for (int k = 0; k < KR; ++k) {
                         const int vv[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
@@ -415,7 +433,53 @@ __global__ __launch_bounds__(64 * NW, BM == PT_BM_SMALL ? 3 : NW / 2) void gemm_
             }
             // N % 4 == 0 (host check): a lane's 4 columns are all in or all out. Whole
             // tiles store without per-row checks.
-            if (full) {
+            if constexpr (EPI == EPI_TOPK) {
+                // The scores are not stored. A score whose key is at or above its row's
+                // bound joins the row's candidates. First only the comparisons (bit 4k+j:
+                // value j of this lane's row k); the few keepers (the bound is a sample's
+                // k-th largest key, so about k of every sample's worth of a row clear it)
+                // are then dequantized again from the accumulators still in the scratch,
+                // which keeps the common path's registers those of EPI_F32.
+                uint32_t keep = 0;
+#pragma unroll
+                for (int k = 0; k < KR; ++k) {
+                    const uint64_t t = s_thr[i * 32 + rsub * KR + k];
+                    const float tf = topk_key_score(t);
+                    const uint32_t tl = (uint32_t)t;
+                    const float x[4] = {__int_as_float(v[k].x), __int_as_float(v[k].y), __int_as_float(v[k].z),
+                                        __int_as_float(v[k].w)};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        // key >= t: the score above t's, or equal and the index no larger
+                        // (a NaN compares false); t == 0 keeps every non-NaN score
+                        const uint32_t lo = 0xffffffffu - (uint32_t)(col + j);
+                        const bool in = t == 0 ? x[j] == x[j] : (x[j] > tf || (x[j] == tf && lo >= tl));
+                        keep |= in ? 1u << (4 * k + j) : 0u;
+                    }
+                }
+                while (keep != 0u) {
+                    const int k = __builtin_ctz(keep) >> 2;
+                    const uint32_t grp = (keep >> (4 * k)) & 15u;
+                    keep &= ~(15u << (4 * k));
+                    if (!row_ok(k)) continue;
+                    const int4 a = *reinterpret_cast<const int4 *>(&scr[(rsub + RPL * k) * SP + 4 * c4]);
+                    const float as = s_as[i * 32 + rsub * KR + k];
+                    const float x[4] = {dequant(a.x, as, wsv[0], bv[0]), dequant(a.y, as, wsv[1], bv[1]),
+                                        dequant(a.z, as, wsv[2], bv[2]), dequant(a.w, as, wsv[3], bv[3])};
+                    const int64_t row = m0 + i * 32 + rsub + RPL * k;
+                    unsigned pos = atomicAdd(&sink.count[row], (unsigned)__builtin_popcount(grp));
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if (!((grp >> j) & 1u)) continue;
+                        if (pos < (unsigned)sink.cap) {
+                            const int64_t at = row * sink.cap + pos;
+                            sink.key[at] = ((uint64_t)topk_order(x[j]) << 32) | (0xffffffffu - (uint32_t)(col + j));
+                            sink.score[at] = x[j];
+                        }
+                        ++pos;
+                    }
+                }
+            } else if (full) {
 #pragma unroll
                 for (int k = 0; k < KR; ++k) store_nt(p0 + k * step, v[k]);
             } else {

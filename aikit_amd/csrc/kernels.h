@@ -38,7 +38,9 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-enum Epi { EPI_I32 = 0, EPI_F32 = 1, EPI_F32_GELU = 2 };
+// EPI_TOPK (gemm_w8a8_pt only): the f32 outputs of EPI_F32 are not stored; each one at or
+// above its row's bound goes to the row's top-k candidate list (TopkSink).
+enum Epi { EPI_I32 = 0, EPI_F32 = 1, EPI_F32_GELU = 2, EPI_TOPK = 3 };
 
 // ----------------------------------------------------------------------------
 // Quantization (linalg/quant.go:43-71, activations' all-zero row -> scale 0).

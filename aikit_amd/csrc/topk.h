@@ -450,7 +450,7 @@ __global__ __launch_bounds__(256) void topk_chunk_wide(const float *__restrict__
 // key among all their scores, a lower bound of the row's k-th largest), or 0 when those
 // chunks hold fewer than k keys. One wavefront per row; k <= TOPK_SMALL_K.
 __global__ __launch_bounds__(256) void topk_thresh(const uint64_t *__restrict__ cand, int64_t rows, int nchunks, int k,
-                                                   uint64_t *__restrict__ thr) {
+                                                   uint64_t *__restrict__ thr, unsigned *__restrict__ zero) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -465,6 +465,52 @@ __global__ __launch_bounds__(256) void topk_thresh(const uint64_t *__restrict__ 
         v1 = v1 == t ? 0 : v1;
     }
     if (lane == 0) thr[row] = t;
+    if (lane == 0 && zero != nullptr) zero[row] = 0;  // the row's TopkSink count
+}
+
+// The merge after the fused scoring GEMM (gemm_w8a8_pt<EPI_TOPK>): one workgroup per row
+// takes the k largest (k <= TOPK_SMALL_K) of the count[row] candidates the GEMM kept (keys
+// at key[row*cap ..], their scores at score[row*cap ..], unordered), and writes indices and
+// scores as topk_merge does. A row with more than cap candidates writes nothing: its
+// caller runs the two-pass path instead. cap <= TOPK_CHUNK.
+__global__ __launch_bounds__(256) void topk_sink_merge(const unsigned *__restrict__ count,
+                                                       const uint64_t *__restrict__ key,
+                                                       const float *__restrict__ score_in, int cap, int k,
+                                                       int32_t *__restrict__ index, int64_t ldi,
+                                                       float *__restrict__ score, int64_t lds_) {
+    constexpr int EPT = TOPK_CHUNK / 256;
+    __shared__ uint64_t lds[256 + EPT * TOPK_SMALL_K + 2];
+    __shared__ uint64_t sorted[TOPK_SMALL_K];
+    const int tid = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const unsigned n = count[row];
+    if (n > (unsigned)cap) return;  // the same for every thread of the row
+    const uint64_t *kr = key + row * cap;
+    const float *sr = score_in + row * cap;
+    uint64_t kk[EPT];
+    float sv[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        // clamped loads, all in flight at once; past n the key is masked to 0 (none)
+        const unsigned i = (unsigned)(tid + 256 * j);
+        const unsigned at = i < n ? i : 0u;
+        const uint64_t keep = i < n ? ~0ull : 0ull;
+        kk[j] = kr[at] & keep;
+        sv[j] = sr[at];
+    }
+    top_small_k<EPT>(kk, k, sorted, lds);
+    __syncthreads();
+    for (int i = tid; i < k; i += 256) {
+        const uint64_t s = sorted[i];
+        index[row * ldi + i] = s ? (int32_t)topk_index(s) : -1;
+        if (!s) score[row * lds_ + i] = __uint_as_float(0x7fc00000u);
+    }
+    // each selected key's own f32 score, from the one thread that holds it (keys are unique)
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+        if (kk[j] != 0)
+            for (int i = 0; i < k; ++i)
+                if (kk[j] == sorted[i]) score[row * lds_ + i] = sv[j];
 }
 
 // radix_threshold over m keys in device memory (read once per pass; the merge's

@@ -49,6 +49,7 @@ _SIGNATURES = {
     "enchip_weight_image_bytes": (_i64, [_i64, _i64]),
     "enchip_topk_rows_dev": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
     "enchip_ann_topk": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _i64, _vp, _vp]),
+    "enchip_ann_topk_stats": (_int, [_vp, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "enchip_weight_export": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _vp]),
     "enchip_weight_register_image": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, ctypes.POINTER(ctypes.c_uint64)]),
     "enchip_softmax_rows_scaled_dev": (_int, [_vp, _vp, _i64, _i64, _i64, ctypes.c_float, _vp]),
@@ -245,6 +246,12 @@ class Context:
         hs = np.empty((M, k), np.float32)
         self._check(self._lib.enchip_ann_topk(self._h, index.handle, _ptr(q), M, k, _ptr(hi), _ptr(hs)))
         return hi, hs
+
+    def ann_topk_stats(self) -> tuple:
+        """(calls of ann_topk on the fused route, those of them that fell back to two passes)."""
+        fused, fallbacks = _i64(), _i64()
+        self._check(self._lib.enchip_ann_topk_stats(self._h, ctypes.byref(fused), ctypes.byref(fallbacks)))
+        return fused.value, fallbacks.value
 
     def weight_image_bytes(self, N: int, K: int) -> int:
         """Bytes of the fragment-major image of an N x K weight (-1: shape refused)."""

@@ -584,6 +584,44 @@ def test_ann_flat_i8_scores(ctx, M, N, K):
     assert_f32_parity(got, oracle.w8a8_linear(q, codes, scales, None, 0, M, K, N), "ann scores")
 
 
+@pytest.mark.parametrize("M,N,K,with_bias", [(40, 32772, 100, True), (129, 65540, 384, False), (256, 40000, 512, True),
+                                              (100, 33000, 256, False), (250, 32768, 384, True)])
+def test_skinny_scores_match_oracle(ctx, M, N, K, with_bias):
+    # gemm_w8a8_skinny (33..256 rows, Kp / 32 in {4, 8, 12, 16}, N >= 32768: ann scoring):
+    # all rows' codes in LDS, weights streamed per 32-channel group. Bit-identical to the
+    # oracle through the library's own fragment-major quantization (linear) and on
+    # row-major codes at a padded pitch (pre_dev), with ragged N, ragged row blocks and
+    # a bias.
+    import torch
+
+    g = workloads.rng(97 + M + N + K)
+    q = workloads.activations(g, M, K)
+    codes = g.integers(-127, 128, size=(N, K), dtype=np.int8)
+    scales = g.uniform(1e-3, 1e-2, size=N).astype(np.float32)
+    bias = workloads.bias(g, N) if with_bias else None
+    want = oracle.w8a8_linear(q, codes, scales, bias, 0, M, K, N)
+    w = ctx.register_weight(codes, scales)
+    try:
+        name = ctx.gemm_kernel_name(w, M, 0)
+        say(f"skinny scores M={M} N={N} K={K} bias={with_bias} via {name}")
+        assert "gemm_w8a8_skinny" in name, name
+        assert_f32_parity(ctx.linear(w, q, bias), want, "skinny linear")
+        ldq = (K + 63) // 64 * 64 + 64  # a pitch past Kp
+        qc, qs = oracle.quantize_activations(q, M, K)
+        aq = np.zeros((M, ldq), np.int8)
+        aq[:, :K] = qc
+        da = torch.from_numpy(aq).cuda()
+        ds = torch.from_numpy(np.ascontiguousarray(qs, np.float32)).cuda()
+        db = torch.from_numpy(bias).cuda() if with_bias else None
+        dd = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        ctx.pre_dev(w, da.data_ptr(), ldq, M, ds.data_ptr(), db.data_ptr() if with_bias else 0, 0, dd.data_ptr())
+        torch.cuda.synchronize()
+        assert_f32_parity(dd.cpu().numpy(), want, "skinny pre_dev")
+    finally:
+        ctx.release_weight(w)
+
+
 # ------------------------------------------------------------------ pre-swizzled weight images
 def test_weight_image_export_and_register(ctx, tmp_path):
     # enchip_weight_export gives the image weight_cache.frag_image builds on the host;
@@ -746,6 +784,56 @@ def test_ann_topk_matches_score_batch_plus_top_hits(ctx, M, N, K, k):
     finally:
         ctx.release_weight(w)
     _check_topk(hi, hs, oracle.w8a8_linear(q, codes, scales, None, 0, M, K, N), k, "ann_topk")
+
+
+@pytest.mark.parametrize("kind,M,k", [("normal", 64, 10), ("normal", 40, 32), ("normal", 33, 1), ("ties", 64, 10),
+                                      ("constant", 40, 5), ("rising", 48, 10)])
+def test_ann_topk_fused_route(ctx, kind, M, k):
+    # Above the small-M limit, with k <= 32 and at least 131072 index rows, TopKBatch keeps
+    # the scores on the chip: each query's bound is the k-th best key among the first
+    # 32768 rows' scores, one scoring pass (gemm_w8a8_pt's EPI_TOPK epilogue) lists only
+    # the scores at or above it, and a merge selects from the lists. Identical to
+    # ScoreBatch + topHits on the oracle's scores:
+    #   normal: random codes, a ragged last tile (N % 256 = 244), ragged last row-block;
+    #   ties: every non-zero score negative and the best ones zeros of both signs (index
+    #     rows of zero codes, scales of either sign), NaN scores from NaN scales: the
+    #     bound is a zero and ties at it break by index, -0 comes back as -0;
+    #   constant: all scores equal, so exactly k clear the bound;
+    #   rising: scores grow along the index, every row past the sample clears the bound,
+    #     the lists overflow and the call runs the two-pass route instead.
+    N, K = 150004, 256
+    g = workloads.rng(4000 + M + k + len(kind))
+    q = workloads.activations(g, M, K)
+    if kind == "normal":
+        codes = g.integers(-127, 128, size=(N, K), dtype=np.int8)
+        scales = g.uniform(1e-3, 1e-2, size=N).astype(np.float32)
+    elif kind == "ties":
+        q = np.abs(q) + np.float32(0.01)
+        codes = g.integers(-3, 1, size=(N, K), dtype=np.int8)
+        scales = g.choice(np.array([0.25, 0.5], np.float32), size=N)
+        zero = g.random(N) < 0.002
+        codes[zero] = 0
+        scales[zero] *= g.choice(np.array([1, -1], np.float32), size=int(zero.sum()))
+        scales[(g.random(N) < 0.002) & ~zero] = np.nan
+    else:
+        q = np.abs(q) + np.float32(0.01)
+        codes = np.ones((N, K), np.int8)
+        scales = (np.full(N, 1e-3, np.float32) if kind == "constant"
+                  else np.linspace(1e-3, 2e-3, N, dtype=np.float32))
+    want_fallback = kind == "rising"
+    w = ctx.register_weight(codes, scales)
+    try:
+        f0, b0 = ctx.ann_topk_stats()
+        say(f"ann top-k fused route {kind} M={M} N={N} K={K} k={k}")
+        hi, hs = ctx.ann_topk(w, q, k)
+        f1, b1 = ctx.ann_topk_stats()
+    finally:
+        ctx.release_weight(w)
+    assert (f1 - f0, b1 - b0) == (1, 1 if want_fallback else 0), "route"
+    scores = oracle.w8a8_linear(q, codes, scales, None, 0, M, K, N)
+    if kind == "ties":
+        assert np.signbit(scores[:, zero]).any() and (scores[:, zero] == 0).all(), "signed zeros present"
+    _check_topk(hi, hs, scores, k, f"ann_topk fused {kind}")
 
 
 # ------------------------------------------------------------------ fused small-M quantize + GEMV

@@ -409,16 +409,36 @@ def other_configs(ctx, torch, stream, ceilings):
         e1.record(stream)
         torch.cuda.synchronize()
         t_topk = e0.elapsed_time(e1) * 1e-3 / reps
+        # TopKBatch through its host entry point (enchip_ann_topk: host queries in, host hits
+        # out, synchronous). Above the small-M limit with k <= 32 the selection runs in the
+        # scoring pass and the M x N scores are never written (the fused route).
+        qh = a.cpu().numpy()
+        for _ in range(3):
+            ctx.ann_topk(hidx, qh, kk)
+        f0, b0 = ctx.ann_topk_stats()
+        th = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            ctx.ann_topk(hidx, qh, kk)
+            th.append(time.perf_counter() - t0)
+        f1, b1 = ctx.ann_topk_stats()
+        route = "two-pass" if f1 == f0 else ("fused" if b1 == b0 else "fused, fell back to two-pass")
         nbytes = N * K + M * K + 4 * M + 4 * N + 4 * M * N
+        kname = ctx.gemm_kernel_name(hidx, M, 0)
+        if "skinny" in kname:  # pre_dev's codes are row-major
+            kname = kname.replace(", true>", ", false>")
         out[f"ann_flat_i8_m{M}"] = {
             "top10_us_per_call": t_topk * 1e6,
+            "ann_topk_host_us_per_call": float(np.median(th)) * 1e6, "ann_topk_route": route,
             "M": M, "K": K, "N": N, "us_per_call": t * 1e6, "hbm_gbps": nbytes / t / 1e9,
             "frac_hbm_peak": nbytes / t / PEAK_HBM_BPS,
             "frac_measured_read_ceiling": nbytes / t / 1e9 / ceilings["hbm_read_gbps"],
-            "int8_tops": 2.0 * M * N * K / t / 1e12, "kernel": ctx.gemm_kernel_name(hidx, M, 0),
+            "int8_tops": 2.0 * M * N * K / t / 1e12, "kernel": kname,
             "note": "M queries against a 2^20 x 384 int8 index (403 MB > MALL), pre-quantized queries, "
                     "bias-free W8A8 scores (enchip_w8a8_pre_dev); bytes = index + queries + scales + M*N f32 scores; "
-                    "top10_us_per_call = the same scores plus the device top-10 per query (enchip_topk_rows_dev)"}
+                    "top10_us_per_call = the same scores plus the device top-10 per query (enchip_topk_rows_dev); "
+                    "ann_topk_host_us_per_call = enchip_ann_topk (host queries -> host top-10 hits, wall clock, "
+                    "median), on the route ann_topk_route names"}
         if M <= 16:
             # the reference's CPU path for the same scores: the C restatement of its AVX2
             # W8A8 linear (oracle/cpu_baseline.c), bias-free, on the host's cores

@@ -387,12 +387,15 @@ void launch_pt(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, co
 // than the small-M kernels take and at most 256 (all of them in LDS), Kp / 32 one of 4, 8,
 // 12, 16, and at least 1024 groups of 32 channels (N >= 32768: ann indexes). Row-major A
 // needs 16-byte aligned rows.
-int skinny_nk(const enchip_ctx *c, const Weight &w, int64_t M, const void *aq, int64_t lda, bool af) {
+int skinny_shape_nk(const Weight &w, const void *aq, int64_t lda, bool af) {
     const int nk = (int)(w.Kp / 32);
-    if (M <= c->small_m || M > 256 || (nk != 4 && nk != 8 && nk != 12 && nk != 16) || (w.N + 31) / 32 < 1024)
-        return 0;
+    if ((nk != 4 && nk != 8 && nk != 12 && nk != 16) || (w.N + 31) / 32 < 1024) return 0;
     if (!af && (lda % 16 != 0 || (uintptr_t)aq % 16 != 0 || lda < w.Kp)) return 0;
     return nk;
+}
+
+int skinny_nk(const enchip_ctx *c, const Weight &w, int64_t M, const void *aq, int64_t lda, bool af) {
+    return M > c->small_m && M <= 256 ? skinny_shape_nk(w, aq, lda, af) : 0;
 }
 
 template <int MB, int EPI, bool AF>
@@ -1678,8 +1681,10 @@ int launch_ann_fused(enchip_ctx *c, const Weight &w, int64_t M, int64_t k, hipSt
     sink.key = keys;
     sink.score = raw;
     sink.cap = kSinkCap;
-    if (const int nk = skinny_nk(c, w, M, c->d_aq, w.Kp, true)) {
-        // 128 rows a launch: with 256 rows' accumulators the candidate epilogue spills
+    if (const int nk = skinny_shape_nk(w, c->d_aq, w.Kp, true)) {
+        // 128 rows a launch, whatever M (each launch reads the index once): with 256 rows'
+        // accumulators the candidate epilogue spills, and at M = 1024 eight launches took
+        // well under the persistent kernel's candidate pass
         for (int64_t r0 = 0; r0 < M; r0 += 128) {
             TopkSink part = sink;
             part.thr += r0;

@@ -51,6 +51,7 @@ __global__ __launch_bounds__(64 * SK_WAVES, 1) void gemm_w8a8_skinny(
     __shared__ i32x4 s_a[MB * NK * 64];
     __shared__ __attribute__((aligned(16))) float s_as[MB * 32];
     __shared__ uint64_t s_thr[EPI == EPI_TOPK ? MB * 32 : 1];
+    __shared__ __attribute__((aligned(16))) float s_tf[EPI == EPI_TOPK ? MB * 32 : 1];  // bound scores
     // EPI_TOPK: the workgroup's candidates, per row, until its flush at the end. A global
     // atomic that returns its value would wait (in-order vmcnt) for every weight load in
     // flight behind it, a full memory latency per group with a candidate; LDS atomics
@@ -75,25 +76,13 @@ __global__ __launch_bounds__(64 * SK_WAVES, 1) void gemm_w8a8_skinny(
     for (int r = tid; r < MB * 32; r += 64 * SK_WAVES) {
         s_as[r] = aS[min(r, M - 1)];
         if (EPI == EPI_TOPK) {
-            s_thr[r] = sink.thr[min(r, M - 1)];
+            const uint64_t t = sink.thr[min(r, M - 1)];
+            s_thr[r] = t;
+            s_tf[r] = t == 0 ? -INFINITY : topk_key_score(t);  // -inf: no bound, every non-NaN score
             s_cnt[r] = 0;
         }
     }
     __syncthreads();
-
-    // EPI_TOPK: the lowest bound score of this lane's 16 x MB rows (-inf when one of them
-    // has no bound). A score below it cannot be kept, so only the rare ones at or above it
-    // take the exact test against their own row's bound.
-    float lmin = INFINITY;
-    if (EPI == EPI_TOPK) {
-#pragma unroll
-        for (int rb = 0; rb < MB; ++rb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint64_t t = s_thr[rb * 32 + acc_row(r, lane)];
-                lmin = fminf(lmin, t == 0 ? -INFINITY : topk_key_score(t));
-            }
-    }
 
     const int groups = (N + 31) >> 5, stride = gridDim.x * SK_WAVES;
     int g = blockIdx.x * SK_WAVES + wave;
@@ -179,18 +168,21 @@ __global__ __launch_bounds__(64 * SK_WAVES, 1) void gemm_w8a8_skinny(
             const uint32_t lo = 0xffffffffu - (uint32_t)col;
 #pragma unroll
             for (int rb = 0; rb < MB; ++rb) {
-                // bit 4q + u: value acc[rb][4q + u] is at or above lmin (a NaN is not)
+                // bit 4q + u: value acc[rb][4q + u] is at or above its row's bound score (a
+                // NaN is not), which a kept key needs; only ties at that score need the
+                // index test below
                 uint32_t pass = 0;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int row0 = rb * 32 + 8 * q + 4 * (lane >> 5);
                     const float4 as4 = *reinterpret_cast<const float4 *>(&s_as[row0]);
-                    const float asv[4] = {as4.x, as4.y, as4.z, as4.w};
+                    const float4 tf4 = *reinterpret_cast<const float4 *>(&s_tf[row0]);
+                    const float asv[4] = {as4.x, as4.y, as4.z, as4.w}, tfv[4] = {tf4.x, tf4.y, tf4.z, tf4.w};
 #pragma unroll
                     for (int u = 0; u < 4; ++u)
-                        pass |= dequant(acc[rb][4 * q + u], asv[u], ws_c, bb_c) >= lmin ? 1u << (4 * q + u) : 0u;
+                        pass |= dequant(acc[rb][4 * q + u], asv[u], ws_c, bb_c) >= tfv[u] ? 1u << (4 * q + u) : 0u;
                 }
-                if (pass != 0u) {  // rare: the exact test against each row's own bound
+                if (pass != 0u) {  // rare: the exact key test
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         if (!((pass >> r) & 1u)) continue;
@@ -201,7 +193,7 @@ __global__ __launch_bounds__(64 * SK_WAVES, 1) void gemm_w8a8_skinny(
                         const float tf = topk_key_score(t);
                         // key >= t: the score above t's, or equal and the index no larger;
                         // t == 0 keeps every non-NaN score
-                        const bool in = row < M && (t == 0 || x > tf || (x == tf && lo >= (uint32_t)t));
+                        const bool in = row < M && (t == 0 || x > tf || (x == tf && lo >= (uint32_t)t)) && x == x;
                         if (in) {
                             const uint64_t key = ((uint64_t)topk_order(x) << 32) | lo;
                             const unsigned p = atomicAdd(&s_cnt[row], 1u);

@@ -787,7 +787,7 @@ def test_ann_topk_matches_score_batch_plus_top_hits(ctx, M, N, K, k):
 
 
 @pytest.mark.parametrize("kind,M,k", [("normal", 64, 10), ("normal", 40, 32), ("normal", 33, 1), ("ties", 64, 10),
-                                      ("constant", 40, 5), ("rising", 48, 10)])
+                                      ("constant", 40, 5), ("rising", 48, 10), ("normal", 300, 10)])
 def test_ann_topk_fused_route(ctx, kind, M, k):
     # Above the small-M limit, with k <= 32 and at least 131072 index rows, TopKBatch keeps
     # the scores on the chip: each query's bound is the k-th best key among the first
@@ -795,6 +795,7 @@ def test_ann_topk_fused_route(ctx, kind, M, k):
     # the scores at or above it, and a merge selects from the lists. Identical to
     # ScoreBatch + topHits on the oracle's scores:
     #   normal: random codes, a ragged last tile (N % 256 = 244), ragged last row-block;
+    #     300 queries: three candidate launches of up to 128 queries;
     #   ties: every non-zero score negative and the best ones zeros of both signs (index
     #     rows of zero codes, scales of either sign), NaN scores from NaN scales: the
     #     bound is a zero and ties at it break by index, -0 comes back as -0;

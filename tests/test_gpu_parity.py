@@ -786,24 +786,27 @@ def test_ann_topk_matches_score_batch_plus_top_hits(ctx, M, N, K, k):
     _check_topk(hi, hs, oracle.w8a8_linear(q, codes, scales, None, 0, M, K, N), k, "ann_topk")
 
 
-@pytest.mark.parametrize("kind,M,k", [("normal", 64, 10), ("normal", 40, 32), ("normal", 33, 1), ("ties", 64, 10),
-                                      ("constant", 40, 5), ("rising", 48, 10), ("normal", 300, 10)])
-def test_ann_topk_fused_route(ctx, kind, M, k):
+@pytest.mark.parametrize("kind,M,k,K", [("normal", 64, 10, 256), ("normal", 40, 32, 256), ("normal", 33, 1, 256),
+                                        ("ties", 64, 10, 256), ("constant", 40, 5, 256), ("rising", 48, 10, 256),
+                                        ("normal", 300, 10, 256), ("normal", 64, 10, 600), ("normal", 40, 10, 500)])
+def test_ann_topk_fused_route(ctx, kind, M, k, K):
     # Above the small-M limit, with k <= 32 and at least 131072 index rows, TopKBatch keeps
     # the scores on the chip: each query's bound is the k-th best key among the first
     # 32768 rows' scores, one scoring pass (gemm_w8a8_pt's EPI_TOPK epilogue) lists only
     # the scores at or above it, and a merge selects from the lists. Identical to
     # ScoreBatch + topHits on the oracle's scores:
     #   normal: random codes, a ragged last tile (N % 256 = 244), ragged last row-block;
-    #     300 queries: three candidate launches of up to 128 queries;
+    #     300 queries: three candidate launches of up to 128 queries; K = 600 (Kp = 640, 20
+    #     K steps, past the skinny kernel's 16): the persistent kernel's candidate
+    #     epilogue; K = 500: the skinny kernel's one-deep ring (16 K steps);
     #   ties: every non-zero score negative and the best ones zeros of both signs (index
     #     rows of zero codes, scales of either sign), NaN scores from NaN scales: the
     #     bound is a zero and ties at it break by index, -0 comes back as -0;
     #   constant: all scores equal, so exactly k clear the bound;
     #   rising: scores grow along the index, every row past the sample clears the bound,
     #     the lists overflow and the call runs the two-pass route instead.
-    N, K = 150004, 256
-    g = workloads.rng(4000 + M + k + len(kind))
+    N = 150004
+    g = workloads.rng(4000 + M + k + K + len(kind))
     q = workloads.activations(g, M, K)
     if kind == "normal":
         codes = g.integers(-127, 128, size=(N, K), dtype=np.int8)

@@ -1641,11 +1641,18 @@ int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, in
 constexpr int64_t kSinkSample = (int64_t)enchip::TOPK_SAMPLE_CHUNKS * enchip::TOPK_WCHUNK;
 constexpr int kSinkCap = enchip::TOPK_CHUNK;
 
-// k <= TOPK_SMALL_K on fragment-major activations, over rows at least 4 samples long whose
-// expected lists fill at most a quarter of the cap.
-bool ann_fused_ok(const Weight &w, int64_t k, bool af) {
-    return af && k >= 1 && k <= enchip::TOPK_SMALL_K && w.N >= 4 * kSinkSample &&
-           k * w.N <= (int64_t)kSinkCap * kSinkSample / 4;
+// k <= TOPK_SMALL_K over rows at least 4 samples long whose expected lists fill at most a
+// quarter of the cap, on fragment-major activations: the linear route's own (af), or, for
+// M at or below the small-M limit, quantized fragment-major for this route alone when the
+// skinny candidate kernel and the persistent GEMM (sample scores, two-pass fallback) take
+// the shape.
+bool ann_fused_ok(const enchip_ctx *c, const Weight &w, int64_t M, int64_t k, bool af) {
+    if (k < 1 || k > enchip::TOPK_SMALL_K || w.N < 4 * kSinkSample || k * w.N > (int64_t)kSinkCap * kSinkSample / 4)
+        return false;
+    // from 8 queries: measured on MI355X (2^20 x 384, k = 10, per host call) M = 16 207 -> 189 us,
+    // M = 1 150 -> 179 us (the GEMV's scores are cheap there, the extra launches are not)
+    return af || (M >= 8 && M <= c->small_m && skinny_shape_nk(w, nullptr, w.Kp, true) != 0 &&
+                  use_persistent(w, nullptr, w.Kp, nullptr, w.N, M, true));
 }
 
 // Enqueues steps 1-3 on s for M rows of fragment-major codes in the context scratch
@@ -1691,8 +1698,13 @@ int launch_ann_fused(enchip_ctx *c, const Weight &w, int64_t M, int64_t k, hipSt
             part.count += r0;
             part.key += r0 * kSinkCap;
             part.score += r0 * kSinkCap;
-            launch_skinny_mb<4, EPI_TOPK, true>(c, w, nk, c->d_aq + r0 * w.Kp, w.Kp, c->d_as + r0, nullptr, nullptr, 0,
-                                                std::min<int64_t>(128, M - r0), s, part);
+            const int64_t mr = std::min<int64_t>(128, M - r0);
+            if (mr <= 32)  // one row block: the epilogue's work per score covers 32 rows, not 128
+                launch_skinny_mb<1, EPI_TOPK, true>(c, w, nk, c->d_aq + r0 * w.Kp, w.Kp, c->d_as + r0, nullptr,
+                                                    nullptr, 0, mr, s, part);
+            else
+                launch_skinny_mb<4, EPI_TOPK, true>(c, w, nk, c->d_aq + r0 * w.Kp, w.Kp, c->d_as + r0, nullptr,
+                                                    nullptr, 0, mr, s, part);
         }
     } else
         launch_pt<PT_PW, EPI_TOPK, true>(c, w, c->d_aq, w.Kp, c->d_as, nullptr, nullptr, 0, M, s, sink);
@@ -1746,9 +1758,10 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int6
     // the bias-free W8A8 scores (ann/backend.go:25-29), then the selection on the device
     // (d_dst, from the context allocator, is 256-byte aligned: the route does not depend
     // on whether it is allocated yet)
-    const bool af = route_af(ctx, *w, M, nullptr, N);
+    const bool fuse = ann_fused_ok(ctx, *w, M, k, route_af(ctx, *w, M, nullptr, N));
+    const bool af = fuse || route_af(ctx, *w, M, nullptr, N);  // the codes' layout, for both routes
     if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, w->Kp, ctx->d_as, s, af))) return rc;
-    if (ann_fused_ok(*w, k, af)) {
+    if (fuse) {
         const unsigned *d_count = nullptr;
         if ((rc = launch_ann_fused(ctx, *w, M, k, s, &d_count))) return rc;
         if ((rc = scratch_record(ctx, s))) return rc;

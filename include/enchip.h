@@ -427,7 +427,7 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight index, const float *queries, 
                     int64_t k, int32_t *hit_index, float *hit_score);
 
 /* How enchip_ann_topk has run on this context: *fused = calls that took the fused route
- * (M above the small-M limit, k <= 32, an index of at least 131072 rows whose dimension
+ * (M >= 8, k <= 32, an index of at least 131072 rows whose dimension
  * padded to 64 is an even multiple of 64, as the tiled GEMM takes it: each query's
  * bound from the k-th best score of the index's first 32768 rows, then one scoring pass
  * that keeps only the scores at or above it, so the M x n scores are never written);

@@ -788,13 +788,17 @@ def test_ann_topk_matches_score_batch_plus_top_hits(ctx, M, N, K, k):
 
 @pytest.mark.parametrize("kind,M,k,K", [("normal", 64, 10, 256), ("normal", 40, 32, 256), ("normal", 33, 1, 256),
                                         ("ties", 64, 10, 256), ("constant", 40, 5, 256), ("rising", 48, 10, 256),
-                                        ("normal", 300, 10, 256), ("normal", 64, 10, 600), ("normal", 40, 10, 500)])
+                                        ("normal", 300, 10, 256), ("normal", 64, 10, 600), ("normal", 40, 10, 500),
+                                        ("normal", 16, 10, 384), ("normal", 8, 32, 256), ("ties", 9, 10, 256),
+                                        ("rising", 8, 10, 256)])
 def test_ann_topk_fused_route(ctx, kind, M, k, K):
     # Above the small-M limit, with k <= 32 and at least 131072 index rows, TopKBatch keeps
     # the scores on the chip: each query's bound is the k-th best key among the first
     # 32768 rows' scores, one scoring pass (gemm_w8a8_pt's EPI_TOPK epilogue) lists only
     # the scores at or above it, and a merge selects from the lists. Identical to
     # ScoreBatch + topHits on the oracle's scores:
+    #   (8 <= M <= 32, the small-M limit: the codes are quantized fragment-major for this
+    #   route and the candidate pass holds one 32-row block)
     #   normal: random codes, a ragged last tile (N % 256 = 244), ragged last row-block;
     #     300 queries: three candidate launches of up to 128 queries; K = 600 (Kp = 640, 20
     #     K steps, past the skinny kernel's 16): the persistent kernel's candidate

@@ -713,6 +713,10 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
         if u["bytes"]:
             u["alg_gbps"] = u["bytes"] / t / 1e9
             u["frac_hbm_peak"] = u["bytes"] / t / PEAK_HBM_BPS
+        if label == "attention":
+            # split-bf16 products: three bf16 MFMA products per f32 product
+            u["frac_mfma_peak"] = (u["ops"] / t / PEAK_FP32_FLOPS if ctx.attention_products == 0
+                                   else 3 * u["ops"] / t / PEAK_BF16_FLOPS)
         table[label] = u
     return table
 
@@ -880,6 +884,107 @@ def linear_stack(ctx, torch, stream, cfg, layers_host, steps: int, warmup: int, 
                  "int8 MFMA GEMM + fused dequant epilogue each, on seeded N(0,1) inputs resident in HBM; kernel "
                  "times from HIP events around each launch in a second region of the same steps"),
     }
+
+
+LINE_LIMIT = 8192  # bytes: the stdout line the driver parses stays well under this
+DETAIL_PATH = os.path.join("gpurun_out", "bench_detail.json")
+
+
+def write_detail(result: dict) -> str | None:
+    """The full result (every kernel's figures, the linear stack, the other configs)
+    goes to stderr and to DETAIL_PATH; the stdout line carries only its summary.
+    Returns the path written, or None when it could not be written."""
+    text = json.dumps(result)
+    print(f"[bench] detail {text}", file=sys.stderr, flush=True)
+    try:
+        os.makedirs(os.path.dirname(DETAIL_PATH), exist_ok=True)
+        with open(DETAIL_PATH, "w") as f:
+            f.write(text + "\n")
+        return DETAIL_PATH
+    except OSError as e:
+        log(f"could not write {DETAIL_PATH}: {e}")
+        return None
+
+
+def _r(x, nd: int = 4):
+    """Round floats to nd significant digits for the compact line."""
+    if isinstance(x, float):
+        return float(f"{x:.{nd}g}")
+    return x
+
+
+def compact_result(result: dict, detail_path: str | None = None) -> dict:
+    """The one JSON line bench.py prints: the contract's keys, a short config, the
+    roofline of the W8A8 path's dominant kernel (with its VALU roof and measured HBM
+    traffic), the step's dominant kernel, the measured ceilings, the CPU baseline, a
+    {unit: [us per launch, fraction of its roof]} table of the encode's kernels and one
+    figure per other config. Everything else stays in the detail file. The result is
+    bounded by LINE_LIMIT whatever the number of kernels (the table is dropped first,
+    then the other configs, if a line would exceed it)."""
+    keep = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+            "scaling", "vs_baseline", "dtype", "data")
+    out = {k: _r(result[k], 6) if k in ("value", "ms_per_step") else result[k] for k in keep if k in result}
+    cfg = result.get("config", {})
+    out["config"] = {
+        "workload": "bert-base b64xs512 W8A8 encode (token ids -> pooled L2 embeddings), resident in HBM",
+        **{k: cfg[k] for k in ("model", "global_batch", "seq_len", "parallelism", "attention_products", "launch")
+           if k in cfg},
+    }
+    rf = result.get("roofline") or {}
+    roof = {k: _r(rf[k]) for k in ("bound", "achieved", "peak", "unit", "frac", "traffic", "kernel", "unit_label",
+                                    "avg_launch_us", "alg_bytes_per_launch", "alg_ops_per_launch",
+                                    "int8_frac_of_peak", "traffic_source") if k in rf}
+    if "valu" in rf:
+        v = rf["valu"]
+        roof["valu"] = {"frac": _r(v.get("frac")), "achieved_t_lane_ops": _r(v.get("achieved_t_lane_ops")),
+                        "peak_t_lane_ops": _r(v.get("measured_peak_t_lane_ops")),
+                        "lane_ops_per_output": v.get("lane_ops_per_output")}
+    out["roofline"] = roof
+    sd = result.get("roofline_step_dominant") or {}
+    out["roofline_step_dominant"] = {k: _r(sd[k]) for k in ("unit_label", "kernel", "avg_launch_us", "share_of_step",
+                                                            "bound", "unit", "achieved", "peak", "frac", "valu_frac")
+                                     if k in sd}
+    if result.get("measured_ceilings"):
+        out["measured_ceilings"] = {k: _r(v) for k, v in result["measured_ceilings"].items()}
+    cb = result.get("cpu_baseline")
+    out["cpu_baseline"] = None if cb is None else {
+        k: _r(cb[k]) if k != "sample" else str(cb[k])[:400] for k in ("value", "unit", "cores", "kind", "sample")
+        if k in cb}
+    kern = {}
+    for label, u in (result.get("encode_kernels") or {}).items():
+        frac = u.get("frac_int8_peak") if u.get("ops") else u.get("frac_hbm_peak")
+        if label == "attention":
+            frac = u.get("frac_mfma_peak", frac)
+        kern[label] = [_r(u.get("us_per_launch"), 4), _r(frac, 3)]
+    out["kernels_us_frac"] = kern
+    other = {}
+    oc = result.get("other_configs") or {}
+    if "config2_isolated_linear" in oc:
+        other["cfg2_us_per_call"] = _r(oc["config2_isolated_linear"].get("us_per_call"))
+    for n in ("768", "3072"):
+        c = oc.get(f"config3_gemv_n{n}")
+        if c:
+            other[f"cfg3_n{n}_us_per_call"] = _r(c.get("us_per_call"))
+            other[f"cfg3_n{n}_frac_hbm"] = _r(c.get("frac_hbm_peak"), 3)
+    if "rerank_device_cfg5" in oc:
+        other["cfg5_pairs_per_s"] = _r(oc["rerank_device_cfg5"].get("pairs_per_s"))
+    for m in ("1", "16", "256"):
+        c = oc.get(f"ann_flat_i8_m{m}")
+        if c:
+            other[f"ann_m{m}_us"] = _r(c.get("us_per_call"))
+    if "linear_stack" in result:
+        other["linear_stack_ms"] = _r(result["linear_stack"].get("ms_per_step"))
+    for k in ("encode_f32_products", "encode_split_bf16_two_pass"):
+        if k in result:
+            other[f"{k}_ms"] = _r(result[k].get("ms_per_step"))
+    out["other"] = other
+    out["output_finite"] = result.get("output_finite")
+    out["detail"] = detail_path or "stderr ([bench] detail ...)"
+    for drop in ("kernels_us_frac", "other"):
+        if len(json.dumps(out)) <= LINE_LIMIT:
+            break
+        out.pop(drop, None)
+    return out
 
 
 def main() -> int:
@@ -1068,7 +1173,9 @@ def main() -> int:
     else:
         result["cpu_baseline"] = None
     ctx.close()
-    print(json.dumps(result), flush=True)
+    detail = write_detail(result)
+    line = compact_result(result, detail)
+    print(json.dumps(line), flush=True)
     return 0
 
 

@@ -60,12 +60,19 @@ constexpr int64_t kNoAllocRows = (int64_t)1 << 18;
 constexpr size_t kNoAllocBytes = kNoAllocCodeBytes + (size_t)kNoAllocRows * sizeof(float);
 static __device__ __align__(256) int8_t scratch[kNoAllocBytes];
 
-// Device address of `scratch` per device, resolved once per device (hipGetSymbolAddress
-// with that device current). In host code the name `scratch` is only a stand-in: kernels
-// and copies get these addresses.
+// Per device: the device address of `scratch` (hipGetSymbolAddress with that device
+// current; in host code the name `scratch` is only a stand-in, so kernels and copies get
+// this address) and an event recorded after the last call that used it. Every context on
+// the device shares both; g_noalloc_mu guards them and is held across a call's whole
+// enqueue, so calls from different threads or contexts order themselves through the event.
 constexpr int kMaxDevices = 64;
+struct NoallocDevice {
+    int8_t *ptr = nullptr;
+    hipEvent_t ev = nullptr;  // held for the life of the process, like the array
+    bool pending = false;     // ev has been recorded since the last capture-free call
+};
 std::mutex g_noalloc_mu;
-int8_t *g_noalloc_ptr[kMaxDevices] = {};
+NoallocDevice g_noalloc[kMaxDevices];
 
 // Called by enchip_open with `device` current. On failure the no-alloc entry point
 // declines on this device; everything else works.
@@ -73,16 +80,25 @@ hipError_t noalloc_scratch_init(int device, int8_t **out) {
     *out = nullptr;
     if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> g(g_noalloc_mu);
-    if (!g_noalloc_ptr[device]) {
+    NoallocDevice &d = g_noalloc[device];
+    if (!d.ev) {
+        hipError_t e = hipEventCreateWithFlags(&d.ev, hipEventDisableTiming);
+        if (e != hipSuccess) {
+            d.ev = nullptr;
+            (void)hipGetLastError();
+            return e;
+        }
+    }
+    if (!d.ptr) {
         void *p = nullptr;
         hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) {
             (void)hipGetLastError();
             return e;
         }
-        g_noalloc_ptr[device] = static_cast<int8_t *>(p);
+        d.ptr = static_cast<int8_t *>(p);
     }
-    *out = g_noalloc_ptr[device];
+    *out = d.ptr;
     return hipSuccess;
 }
 
@@ -1082,10 +1098,24 @@ int enchip_w8a8_linear_noalloc_dev(enchip_ctx *ctx, enchip_weight h, const float
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     int8_t *aq = ctx->noalloc;
     float *as = reinterpret_cast<float *>(ctx->noalloc + kNoAllocCodeBytes);
+    // The device's array is shared by every context and stream: this call's quantizer
+    // waits for the previous call's GEMM (an event wait, which allocates nothing), and
+    // its GEMM records the event for the next. Under stream capture neither happens (a
+    // captured graph cannot wait on an event recorded outside it): the caller orders
+    // captured calls, and calls that overlap on one GPU then race.
+    std::lock_guard<std::mutex> gd(g_noalloc_mu);
+    NoallocDevice &nd = g_noalloc[ctx->device];
+    const bool cap = capturing(s);
+    if (!cap && nd.pending) HIP_TRY(ctx, hipStreamWaitEvent(s, nd.ev, 0));
     // Every code the GEMM reads for rows < M (columns [K, Kp) zero) and every scale is
     // written by the quantizer first, so nothing from an earlier call is read.
     if ((rc = launch_quant(ctx, d_a, M, w->K, aq, w->Kp, as, s, af))) return rc;
-    return launch_gemm(ctx, *w, aq, w->Kp, as, d_bias, act_code(act), d_dst, w->N, M, s, af);
+    if ((rc = launch_gemm(ctx, *w, aq, w->Kp, as, d_bias, act_code(act), d_dst, w->N, M, s, af))) return rc;
+    if (!cap) {
+        HIP_TRY(ctx, hipEventRecord(nd.ev, s));
+        nd.pending = true;
+    }
+    return ENCHIP_OK;
 }
 
 int enchip_w8a8_linear(enchip_ctx *ctx, enchip_weight h, const float *a, int64_t M, const float *bias, int act,

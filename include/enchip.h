@@ -201,8 +201,11 @@ int enchip_w8a8_linear_dev(enchip_ctx *ctx, enchip_weight w, const float *d_a,
  * harnesses that forbid allocation). Declines with ENCHIP_ERR_ARG when M > 2^18 or the
  * codes (M rounded up to 128 rows when the persistent GEMM runs, else M, times K
  * rounded up to 64) exceed 32 MiB. Every call on a device shares that device's array
- * (across contexts and streams) and leaves its contents behind: calls that overlap on
- * one GPU race; the caller serialises them (one stream, or its own events). */
+ * (across contexts and streams) and leaves its contents behind. Outside stream capture
+ * the library orders the calls itself: each call's kernels wait on a per-device event
+ * recorded after the previous call's (an event wait allocates nothing). Under capture
+ * they do not (a graph cannot wait on an event recorded outside it), so captured calls
+ * that overlap on one GPU race; the caller serialises them. */
 int enchip_w8a8_linear_noalloc_dev(enchip_ctx *ctx, enchip_weight w, const float *d_a, int64_t M,
                                    const float *d_bias, int act, float *d_dst, void *stream);
 

@@ -114,12 +114,13 @@ void cpub_w8a8_linear(const float *a, int64_t M, int64_t K, const int8_t *bq,
                       const float *bs, int64_t N, const float *bias, int act,
                       float *dst, int workers, int8_t *aq, float *as);
 
-#ifdef __cplusplus
-}
-#endif
 /* orc_attention's arithmetic with the heads spread over `workers` threads and loops the
  * compiler vectorises; bit-identical to orc_attention (the encode's CPU baseline). */
 void cpub_attention(const float *Q, const float *K, const float *V, float *ctx, int64_t L, int64_t D,
                     int64_t heads, int workers);
+
+#ifdef __cplusplus
+}
+#endif
 
 #endif

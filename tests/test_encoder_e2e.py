@@ -462,9 +462,11 @@ def test_config5_full_depth_device_rerank(ctx, xlmr_large_full, mode):
     #    at most twice the reference's own drift when only its attention's rounding
     #    changes (f32 vs float64; ~4e-4 at 24 layers, measured live) -- a single token's
     #    state cannot agree more closely than the composition agrees with itself;
-    #  * the device head on the device's own [CLS] row within 1e-5, and the logit within
-    #    the bound the [CLS] difference allows (tanh is 1-Lipschitz, so
-    #    |dlogit| <= |cw| |Wp|_2 |dCLS|).
+    #  * the device head on the device's own [CLS] row within 1e-5;
+    #  * the device logit against the reference's within twice what the reference's own
+    #    [CLS] drift allows its logit (tanh is 1-Lipschitz, so a [CLS] change d moves the
+    #    logit by at most |cw| |Wp|_2 |d|): a fixed bar set by the reference alone, not
+    #    by the device's own [CLS] error.
     import torch
 
     from aikit_amd.bert_dev import DeviceBert
@@ -494,12 +496,14 @@ def test_config5_full_depth_device_rerank(ctx, xlmr_large_full, mode):
     cos = _cos(ref_cls, dev_cls)
     self_cos = _cos(ref_cls, ref64[0])
     head_err = abs(got - _head_logit(dev_cls, head))
-    bound = (np.linalg.norm(head["cw"].astype(np.float64)) * np.linalg.norm(head["pw"].astype(np.float64), 2) *
-             np.linalg.norm(dev_cls.astype(np.float64) - ref_cls))
     ref_logit = _head_logit(ref_cls, head)
+    self_drift = abs(_head_logit(ref64[0], head) - ref_logit)
+    lip = np.linalg.norm(head["cw"].astype(np.float64)) * np.linalg.norm(head["pw"].astype(np.float64), 2)
+    bar = 2 * lip * np.linalg.norm(ref64[0].astype(np.float64) - ref_cls) + 1e-5
     say(f"  pooled cosine {pooled_cos:.9f}; [CLS] cosine {cos:.9f} (reference vs itself with float64 attention "
-        f"{self_cos:.9f}); logit {got:.6f} vs {ref_logit:.6f} (bound {bound:.3g}); head error {head_err:.3g}")
+        f"{self_cos:.9f}); logit {got:.6f} vs {ref_logit:.6f} (reference's own logit drift {self_drift:.3g}, bar "
+        f"{bar:.3g}); head error {head_err:.3g}")
     assert pooled_cos >= COS_MIN
     assert 1 - cos <= 2 * (1 - self_cos)
     assert head_err <= 1e-5
-    assert abs(got - ref_logit) <= bound + 1e-5
+    assert abs(got - ref_logit) <= bar

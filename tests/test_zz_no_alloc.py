@@ -96,3 +96,40 @@ def test_noalloc_declines_beyond_its_scratch():
             ctx.release_weight(w)
     finally:
         ctx.close()
+
+
+def test_noalloc_calls_on_two_streams_and_contexts_stay_exact():
+    """Calls enqueued back to back on two streams of two contexts share the device's
+    array; the library's per-device event orders them, so each output equals
+    enchip_w8a8_linear_dev's bit for bit (without it, the next call's quantizer would
+    overwrite codes a running GEMM still reads)."""
+    import torch
+
+    lib = enchip.load()
+    ctxs = [enchip.Context(0), enchip.Context(0)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    g = workloads.rng(4244)
+    K, N, M, n_calls = 3072, 768, 4096, 6
+    wq, ws = workloads.int8_weights(g, N, K)
+    ws_h = [c.register_weight(wq, ws) for c in ctxs]
+    try:
+        b = torch.from_numpy(workloads.bias(g, N)).cuda()
+        acts = [torch.from_numpy(workloads.activations(g, M, K)).cuda() for _ in range(n_calls)]
+        outs = [torch.full((M, N), 7.0, device="cuda") for _ in range(n_calls)]
+        torch.cuda.synchronize()
+        say(f"no-alloc linear M={M} K={K} N={N}: {n_calls} calls alternating over 2 streams / 2 contexts")
+        for i in range(n_calls):
+            c, w, s = ctxs[i % 2], ws_h[i % 2], streams[i % 2]
+            rc = lib.enchip_w8a8_linear_noalloc_dev(c.handle, w.handle, acts[i].data_ptr(), M, b.data_ptr(), 0,
+                                                    outs[i].data_ptr(), ctypes.c_void_p(s.cuda_stream))
+            assert rc == enchip.OK, lib.enchip_last_error(c.handle).decode()
+        torch.cuda.synchronize()
+        for i in range(n_calls):
+            want = torch.empty((M, N), device="cuda")
+            ctxs[0].linear_dev(ws_h[0], acts[i].data_ptr(), M, b.data_ptr(), 0, want.data_ptr())
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(outs[i].cpu().numpy()), bits(want.cpu().numpy())), i
+    finally:
+        for c, w in zip(ctxs, ws_h):
+            c.release_weight(w)
+            c.close()

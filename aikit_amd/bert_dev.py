@@ -134,7 +134,7 @@ class DeviceBert:
     def fused_attention(self, L: int) -> bool:
         if not self.fused or self.hd not in (32, 64):
             return False
-        return L <= 512 or self.ctx.attention_products == enchip.ATT_FLASH_BF16
+        return L <= 512 or self.ctx.attention_products in (enchip.ATT_FLASH_BF16, enchip.ATT_FLASH_F16)
 
     def _buffers(self, S: int, L: int):
         key = (S, L)

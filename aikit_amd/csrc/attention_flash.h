@@ -1,16 +1,17 @@
-// attention_flash.h -- scaled dot-product attention with an online softmax and
-// split-bfloat16 products: the third product mode of enchip_attention_f32_dev
-// (ENCHIP_ATT_FLASH_BF16), the device form of encoder/attention.go:81-121 attentionCore up
-// to the context.
+// attention_flash.h -- scaled dot-product attention with an online softmax and split
+// products: the flash product modes of enchip_attention_f32_dev (ENCHIP_ATT_FLASH_F16, the
+// default, and ENCHIP_ATT_FLASH_BF16), the device form of encoder/attention.go:81-121
+// attentionCore up to the context.
 //
 // One workgroup takes 32 * NW queries of one (head, sequence) and walks that head's keys
 // in tiles of FA_KT:
-//   * the tile's K and V rows (f32, read once per workgroup) are split into bfloat16
-//     hi / lo parts (x = hi + lo + e, |e| <= 2^-18 |x|, as attention_split_bf16 splits
-//     them) and staged in LDS, double-buffered, the next tile's loads in flight during
-//     this tile's arithmetic;
+//   * the tile's K and V rows (f32, read once per workgroup) are split into two 16-bit
+//     parts, x = hi + lo + e, and staged in LDS, double-buffered, the next tile's loads in
+//     flight during this tile's arithmetic. F16: IEEE half parts, |e| <= 2^-22 |x| (for
+//     |x| >= 2^-3; 2^-25 absolute below), finite for |x| < 65520. Otherwise bfloat16 parts
+//     (as attention_split_bf16 splits them), |e| <= 2^-18 |x|, any finite x;
 //   * wavefront w owns queries 32w .. 32w + 31 and computes S^T = K Q^T (the A operand K
-//     from LDS, its split Q^T held in registers) on v_mfma_f32_32x32x16_bf16, three
+//     from LDS, its split Q^T held in registers) on v_mfma_f32_32x32x16_f16 / _bf16, three
 //     products per pair (hi.lo' + lo.hi' + hi.hi'). In that accumulator lane l holds
 //     query l % 32 and keys 8 (e / 4) + 4 (l / 32) + e % 4 of the 32-key block, so each
 //     query's softmax state is the lane's own (plus one exchange between the two lane
@@ -25,9 +26,12 @@
 //   * at the end the context is divided by l and stored.
 // The arithmetic differs from attentionCore's (exact two-pass softmax, f32 products) in
 // the split products, the running maximum, the fused base-2 exponent and the hardware
-// 2^x: results agree within the
-// f32 MatmulBT gate (gpu/enccuda/backend_test.go:71-81, <= 2e-4 of max(|ref|, 1)), which
-// the tests hold it to. Any L; head_dim 32 or 64. Non-finite operands give NaN.
+// 2^x: results agree within the f32 MatmulBT gate (gpu/enccuda/backend_test.go:71-81,
+// <= 2e-4 of max(|ref|, 1)), which the tests hold them to. Measured against float64 on
+// inputs of standard deviation 2 and 4, the half split stays within that gate and the
+// bfloat16 split does not (its three-product error is 2^6 times larger). Any L; head_dim
+// 32 or 64. Non-finite operands (and, with F16, operands of magnitude 65520 or more) give
+// NaN.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -51,7 +55,7 @@ constexpr int FA_WAVES = 8;
 constexpr int FA_WAVES_WIDE = 16;
 constexpr int FA_WIDE_L = 256;
 
-// LDS of one stage: K hi / lo planes, FA_KT rows of HD bf16 (row pitch HD*2 + 16 bytes, so
+// LDS of one stage: K hi / lo planes, FA_KT rows of HD 16-bit parts (row pitch HD*2 + 16 bytes, so
 // that 32 lanes' 16-byte reads of 32 rows fall in distinct banks), then V^T hi / lo planes,
 // HD rows (one per head-dim column) of FA_KT keys (pitch FA_KT*2 + 16 bytes; each row's
 // 16-byte key groups permuted by fa_vswz).
@@ -88,8 +92,8 @@ __device__ __forceinline__ int fa_vswz(int R) { return 16 * ((R >> 4) & 3); }
 // (head, sequence) on one XCD). Row i of sequence z, head h starts at q/k/v + (z*L + i)*ld
 // + h*HD (16-byte aligned, ld a multiple of 4), out + (z*L + i)*ldo + h*HD; VEC: ldo a
 // multiple of 4 and out 16-byte aligned (16-byte stores).
-template <int HD, int NW, bool VEC>
-__global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
+template <int HD, int NW, bool VEC, bool F16>
+__global__ __launch_bounds__(64 * NW) void attention_flash(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t ld,
     float *__restrict__ out, int64_t ldo, int L, int heads, float scale) {
     static_assert(HD == 32 || HD == 64, "head dimension (and NOT <= 2, which the V^T read swizzle uses)");
@@ -102,6 +106,8 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
     constexpr int VCH = (FA_KT / 2) * HD / 4;   // (key pair, 4 columns) V items per tile
     constexpr int KPT = (KCH + NT - 1) / NT;    // K chunks per thread
     constexpr int VPT = (VCH + NT - 1) / NT;    // V items per thread
+    using Ops = SplitOps<F16>;
+    using vec8 = typename Ops::vec8;
     extern __shared__ __attribute__((aligned(16))) char fa_lds[];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane & 31, hf = lane >> 5;
@@ -126,7 +132,7 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
     // NaN included) without a branch.
     const bool neg = scale < 0.0f;
     const float c = fabsf(scale) * FA_LOG2E;
-    bf16x8 qh[NB], ql[NB];
+    vec8 qh[NB], ql[NB];
     float qt[NB][8];
     {
         const float *qrow = q + (row0 + min(qw + r, L - 1)) * ld + head * HD;
@@ -174,10 +180,10 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
                 const int key = c / (HD / 8), col = (c % (HD / 8)) * 8;
                 const float x[8] = {kr[i][0].x, kr[i][0].y, kr[i][0].z, kr[i][0].w,
                                     kr[i][1].x, kr[i][1].y, kr[i][1].z, kr[i][1].w};
-                bf16x8 h, l;
-                split_bf16x8(x, h, l);
-                *reinterpret_cast<bf16x8 *>(khi + key * Lay::KP + 2 * col) = h;
-                *reinterpret_cast<bf16x8 *>(klo + key * Lay::KP + 2 * col) = l;
+                vec8 h, l;
+                Ops::split8(x, h, l);
+                *reinterpret_cast<vec8 *>(khi + key * Lay::KP + 2 * col) = h;
+                *reinterpret_cast<vec8 *>(klo + key * Lay::KP + 2 * col) = l;
             }
         }
 #pragma unroll
@@ -191,7 +197,7 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     uint32_t hw, lw;
-                    split_pair(a[j], b[j], hw, lw);
+                    Ops::pair(a[j], b[j], hw, lw);
                     const int vo = (col + j) * Lay::VP + ((2 * pos) ^ fa_vswz(col + j));
                     *reinterpret_cast<uint32_t *>(vhi + vo) = hw;
                     *reinterpret_cast<uint32_t *>(vlo + vo) = lw;
@@ -214,7 +220,7 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
         for (int b = 0; b < NB; ++b) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) qt[b][i] = __uint_as_float(__float_as_uint(qt[b][i]) ^ qsign);
-            split_bf16x8(qt[b], qh[b], ql[b]);
+            Ops::split8(qt[b], qh[b], ql[b]);
         }
     }
     store_tile(0);
@@ -235,8 +241,8 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
                     const int off = (32 * s + r) * Lay::KP + 2 * (16 * b + 8 * hf);
-                    const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(khi + off);
-                    const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(klo + off);
+                    const vec8 kh = *reinterpret_cast<const vec8 *>(khi + off);
+                    const vec8 kl = *reinterpret_cast<const vec8 *>(klo + off);
                     acc = mfma_split3(kh, kl, qh[b], ql[b], acc);
                 }
                 // ---- online softmax of query qw + r over these keys, in base-2 units
@@ -289,9 +295,9 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
                 // tile's barrier together, in the same phase): measured 181 against 189 us at
                 // BERT-base shape on MI355X; raised for the S^T products instead, or for
                 // both, it gained less.
-                bf16x8 ph[2], pl[2];
-                split_bf16x8(x, ph[0], pl[0]);
-                split_bf16x8(x + 8, ph[1], pl[1]);
+                vec8 ph[2], pl[2];
+                Ops::split8(x, ph[0], pl[0]);
+                Ops::split8(x + 8, ph[1], pl[1]);
                 __builtin_amdgcn_s_setprio(1);
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
@@ -302,8 +308,8 @@ __global__ __launch_bounds__(64 * NW) void attention_flash_bf16(
                         // 16 hf and i < 2 the swizzle is 32 i + 16 (r / 16), so it folds into the
                         // per-lane base and the immediate offset (no extra registers)
                         const int off = (32 * i + r) * Lay::VP + 64 * s + 32 * (kb ^ i) + 16 * (hf ^ (r >> 4));
-                        const bf16x8 vh = *reinterpret_cast<const bf16x8 *>(vhi + off);
-                        const bf16x8 vl = *reinterpret_cast<const bf16x8 *>(vlo + off);
+                        const vec8 vh = *reinterpret_cast<const vec8 *>(vhi + off);
+                        const vec8 vl = *reinterpret_cast<const vec8 *>(vlo + off);
                         o[i] = mfma_split3(vh, vl, ph[kb], pl[kb], o[i]);
                     }
                 }

@@ -120,7 +120,7 @@ struct enchip_ctx {
     std::vector<std::pair<const void *, size_t>> lds_set;
     uint64_t next_handle = 1;
     int64_t small_m = 32;
-    int att_products = ENCHIP_ATT_FLASH_BF16;  // enchip_set_attention_products
+    int att_products = ENCHIP_ATT_FLASH_F16;  // enchip_set_attention_products
     // Device scratch (grown on demand, freed by enchip_close). Each growable buffer is
     // capped at scratch_limit bytes (enchip_set_scratch_limit; 0 = no cap).
     size_t scratch_limit = 0;
@@ -1508,7 +1508,8 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
                              float scale, void *stream) {
     if (!ctx) return ENCHIP_ERR_ARG;
     std::lock_guard<std::mutex> g(ctx->mu);
-    const bool flash = ctx->att_products == ENCHIP_ATT_FLASH_BF16;
+    const bool flash = ctx->att_products == ENCHIP_ATT_FLASH_BF16 || ctx->att_products == ENCHIP_ATT_FLASH_F16;
+    const bool f16 = ctx->att_products == ENCHIP_ATT_FLASH_F16;
     if (head_dim != 32 && head_dim != 64)
         return fail(ctx, ENCHIP_ERR_ARG, "attention: head_dim must be 32 or 64, got %lld", (long long)head_dim);
     const int64_t max_l = flash ? ((int64_t)1 << 30) : enchip::ATT_MAX_L;
@@ -1550,12 +1551,13 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
         lds = (size_t)enchip::fa_lds_bytes((int)head_dim);
         per_seq = ((L + 32 * nw - 1) / (32 * nw)) * heads;
         threads = 64 * nw;
-        if (wide)
-            fn = head_dim == 64 ? (vec ? enchip::attention_flash_bf16<64, nw16, true> : enchip::attention_flash_bf16<64, nw16, false>)
-                                : (vec ? enchip::attention_flash_bf16<32, nw16, true> : enchip::attention_flash_bf16<32, nw16, false>);
-        else
-            fn = head_dim == 64 ? (vec ? enchip::attention_flash_bf16<64, nw8, true> : enchip::attention_flash_bf16<64, nw8, false>)
-                                : (vec ? enchip::attention_flash_bf16<32, nw8, true> : enchip::attention_flash_bf16<32, nw8, false>);
+#define FA_PICK(F16)                                                                                          \
+    (wide ? (head_dim == 64 ? (vec ? enchip::attention_flash<64, nw16, true, F16> : enchip::attention_flash<64, nw16, false, F16>) \
+                            : (vec ? enchip::attention_flash<32, nw16, true, F16> : enchip::attention_flash<32, nw16, false, F16>)) \
+          : (head_dim == 64 ? (vec ? enchip::attention_flash<64, nw8, true, F16> : enchip::attention_flash<64, nw8, false, F16>) \
+                            : (vec ? enchip::attention_flash<32, nw8, true, F16> : enchip::attention_flash<32, nw8, false, F16>)))
+        fn = f16 ? FA_PICK(true) : FA_PICK(false);
+#undef FA_PICK
     } else {
         const bool split = ctx->att_products == ENCHIP_ATT_SPLIT_BF16;
         const bool full = L == enchip::ATT_MAX_L;
@@ -1582,15 +1584,16 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
         hipLaunchKernelGGL(fn, grid, dim3((unsigned)threads), lds, s, d_q + off * ld, d_k + off * ld, d_v + off * ld,
                            ld, d_out + off * ldo, ldo, (int)L, (int)heads, scale);
     }
-    return check_launch(ctx, flash ? "attention_flash_bf16" : "attention");
+    return check_launch(ctx, flash ? "attention_flash" : "attention");
 }
 
 int enchip_set_attention_products(enchip_ctx *ctx, int mode) {
     if (!ctx) return ENCHIP_ERR_ARG;
     std::lock_guard<std::mutex> g(ctx->mu);
-    if (mode != ENCHIP_ATT_F32 && mode != ENCHIP_ATT_SPLIT_BF16 && mode != ENCHIP_ATT_FLASH_BF16)
-        return fail(ctx, ENCHIP_ERR_ARG, "attention products: mode must be ENCHIP_ATT_F32, ENCHIP_ATT_SPLIT_BF16 or "
-                    "ENCHIP_ATT_FLASH_BF16");
+    if (mode != ENCHIP_ATT_F32 && mode != ENCHIP_ATT_SPLIT_BF16 && mode != ENCHIP_ATT_FLASH_BF16 &&
+        mode != ENCHIP_ATT_FLASH_F16)
+        return fail(ctx, ENCHIP_ERR_ARG, "attention products: mode must be ENCHIP_ATT_F32, ENCHIP_ATT_SPLIT_BF16, "
+                    "ENCHIP_ATT_FLASH_BF16 or ENCHIP_ATT_FLASH_F16");
     ctx->att_products = mode;
     return ENCHIP_OK;
 }

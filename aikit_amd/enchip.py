@@ -23,7 +23,8 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libenchip.s
 
 OK, ERR_NO_DEVICE, ERR_ARG, ERR_HIP, ERR_OOM, ERR_HANDLE = range(6)
 ACT_NONE, ACT_GELU, ACT_TANH = 0, 1, 2
-ATT_F32, ATT_SPLIT_BF16, ATT_FLASH_BF16 = 0, 1, 2  # enchip_att_products
+ATT_F32, ATT_SPLIT_BF16, ATT_FLASH_BF16, ATT_FLASH_F16 = 0, 1, 2, 3  # enchip_att_products
+ATT_DEFAULT = ATT_FLASH_F16  # the library's default
 B_NK, B_KN = 0, 1  # enchip_matmul_bt_f32_dev b layouts: b[N,K] rows, b[K,N] rows
 ABI_VERSION = 2
 
@@ -148,7 +149,7 @@ class Context:
         if rc != OK:
             raise EnchipError(rc, self._lib.enchip_last_error(None).decode())
         self._h = h
-        self.attention_products = ATT_FLASH_BF16  # the library's default
+        self.attention_products = ATT_DEFAULT
 
     # -- lifecycle ------------------------------------------------------------
     def close(self) -> None:
@@ -205,7 +206,8 @@ class Context:
         self._check(self._lib.enchip_set_scratch_limit(self._h, nbytes))
 
     def set_attention_products(self, mode: int) -> None:
-        """ATT_FLASH_BF16 (default), ATT_SPLIT_BF16 or ATT_F32: how attention_f32_dev computes."""
+        """ATT_FLASH_F16 (default), ATT_FLASH_BF16, ATT_SPLIT_BF16 or ATT_F32: how attention_f32_dev
+        computes."""
         self._check(self._lib.enchip_set_attention_products(self._h, mode))
         self.attention_products = mode
 

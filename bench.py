@@ -495,9 +495,10 @@ def other_configs(ctx, torch, stream, ceilings):
         att[f"{name}_frac_fp32_mfma_peak"] = flops / t / PEAK_FP32_FLOPS
         att[f"{name}_hbm_gbps"] = nbytes / t / 1e9
     # the fused form: both products and the softmax in one launch, scores kept on chip, with
-    # its products on the f32 MFMA and (the default) on the bf16 MFMA over split operands
+    # its products on the f32 MFMA, on the bf16 MFMA over bfloat16-split operands, and (the
+    # default) on the f16 MFMA over half-split operands
     for mode, tag in ((enchip.ATT_F32, "fused_f32"), (enchip.ATT_SPLIT_BF16, "fused_split_bf16"),
-                      (enchip.ATT_FLASH_BF16, "fused_flash_bf16")):
+                      (enchip.ATT_FLASH_BF16, "fused_flash_bf16"), (enchip.ATT_FLASH_F16, "fused_flash_f16")):
         ctx.set_attention_products(mode)
         for _ in range(3):
             ctx.attention_f32_dev(base, base + D * 4, base + 2 * D * 4, 3 * D, ctxv.data_ptr(), D, S, L, H, hd, 0.125,
@@ -513,13 +514,14 @@ def other_configs(ctx, torch, stream, ceilings):
         att[f"{tag}_tflops_f32_equivalent"] = 2 * flops / t / 1e12
         if mode == enchip.ATT_F32:
             att[f"{tag}_frac_fp32_mfma_peak"] = 2 * flops / t / PEAK_FP32_FLOPS
-        else:  # three bf16 products per f32 product
+        else:  # three 16-bit products per f32 product (the bf16 and f16 dense peaks are equal)
             att[f"{tag}_frac_bf16_mfma_peak"] = 3 * 2 * flops / t / PEAK_BF16_FLOPS
-    ctx.set_attention_products(enchip.ATT_FLASH_BF16)
+    ctx.set_attention_products(enchip.ATT_DEFAULT)
     att.update({"S": S, "L": L, "heads": H, "head_dim": hd, "gflop_per_product": flops / 1e9,
                 "kernels": "enchip::gemm_f32_bt_lds<2, 2, false> (QK^T), enchip::gemm_f32_bt_lds<4, 1, true> (PV), "
                            "enchip::attention_f32<64> (fused, f32 MFMA), enchip::attention_split_bf16<64, true> "
-                           "(fused, split-bf16 MFMA: the default)",
+                           "(fused, split-bf16 MFMA), enchip::attention_flash<64, 8, true, false|true> (fused online softmax, "
+                           "bfloat16 / half split products; the half split is the default)",
                 "note": "one config-4 layer's attention products (qk, pv: f32 MatmulBT on v_mfma_f32_32x32x2_f32), all "
                         "768 (sequence, head) problems per launch, operands resident; bytes = operands read once + "
                         "output written once; softmax not included in qk/pv, included in the fused forms"})
@@ -696,7 +698,8 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
             mode = ctx.attention_products
             u.update(kind="attention", ops=4.0 * S * H * L * L * hd, bytes=float(4 * M * D * 4),
                      # the library's flash launch (fa_waves)
-                     kernel=(f"enchip::attention_flash_bf16<{hd}, {fa_waves(ctx, S, L, H)}, true>" if mode == 2 else
+                     kernel=(f"enchip::attention_flash<{hd}, {fa_waves(ctx, S, L, H)}, true, {'true' if mode == 3 else 'false'}>"
+                             if mode in (2, 3) else
                              f"enchip::attention_split_bf16<{hd}, {'true' if L == 512 else 'false'}>" if mode == 1
                              else f"enchip::attention_f32<{hd}>"))
         elif label == "embed_rows":
@@ -714,7 +717,7 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
             u["alg_gbps"] = u["bytes"] / t / 1e9
             u["frac_hbm_peak"] = u["bytes"] / t / PEAK_HBM_BPS
         if label == "attention":
-            # split-bf16 products: three bf16 MFMA products per f32 product
+            # split products: three 16-bit MFMA products per f32 product
             u["frac_mfma_peak"] = (u["ops"] / t / PEAK_FP32_FLOPS if ctx.attention_products == 0
                                    else 3 * u["ops"] / t / PEAK_BF16_FLOPS)
         table[label] = u
@@ -768,8 +771,7 @@ def device_forward(ctx, torch, stream, layers_host, cfg, steps: int = 3, warmup:
     S = cfg.batch
     rate = "pairs_per_s" if head == "rerank" else "seqs_per_s"
     tail = "cross-encoder head (f32 pooler + tanh + classifier)" if head == "rerank" else "pooling + L2"
-    products = {enchip.ATT_F32: "f32", enchip.ATT_SPLIT_BF16: "split-bf16 two-pass",
-                enchip.ATT_FLASH_BF16: "split-bf16 online-softmax"}[ctx.attention_products]
+    products = ATT_NAMES[ctx.attention_products]
     return {rate: S / t, "ms_per_batch": t * 1e3, "batch": S, "seq_len": cfg.seq, "layers": cfg.layers,
             "hidden": cfg.hidden, "output_finite": finite, "attention_products": products, "steps": steps,
             "note": "%d encodes back to back from token ids (after %d warm-up): embedding rows + LayerNorm, W8A8 "
@@ -886,6 +888,10 @@ def linear_stack(ctx, torch, stream, cfg, layers_host, steps: int, warmup: int, 
     }
 
 
+ATT_NAMES = {0: "f32 two-pass (ENCHIP_ATT_F32)", 1: "split-bf16 two-pass (ENCHIP_ATT_SPLIT_BF16)",
+             2: "split-bf16 online-softmax (ENCHIP_ATT_FLASH_BF16)",
+             3: "split-f16 online-softmax (ENCHIP_ATT_FLASH_F16)"}  # enchip_att_products
+
 LINE_LIMIT = 8192  # bytes: the stdout line the driver parses stays well under this
 DETAIL_PATH = os.path.join("gpurun_out", "bench_detail.json")
 
@@ -974,7 +980,7 @@ def compact_result(result: dict, detail_path: str | None = None) -> dict:
             other[f"ann_m{m}_us"] = _r(c.get("us_per_call"))
     if "linear_stack" in result:
         other["linear_stack_ms"] = _r(result["linear_stack"].get("ms_per_step"))
-    for k in ("encode_f32_products", "encode_split_bf16_two_pass"):
+    for k in ("encode_f32_products", "encode_split_bf16_two_pass", "encode_flash_bf16"):
         if k in result:
             other[f"{k}_ms"] = _r(result[k].get("ms_per_step"))
     out["other"] = other
@@ -1087,8 +1093,8 @@ def main() -> int:
             "alg_flops_per_launch": ud["ops"],
             "peak": (PEAK_BF16_FLOPS if split else PEAK_FP32_FLOPS) / 1e12,
             "frac": (3 * f / PEAK_BF16_FLOPS) if split else f / PEAK_FP32_FLOPS,
-            "note": ("achieved = the f32 attention's algorithmic flops (4 L^2 hd per head) per second; with split-bf16 "
-                     "products each f32 product is three bf16 MFMA products, so frac = 3 x achieved / the 2.5 PFLOP/s "
+            "note": ("achieved = the f32 attention's algorithmic flops (4 L^2 hd per head) per second; with split "
+                     "products each f32 product is three 16-bit MFMA products, so frac = 3 x achieved / the 2.5 PFLOP/s "
                      "bf16 dense peak (the MFMA work the kernel issues); the exact softmax's VALU work is not in it")
             if split else "achieved = algorithmic flops per second on the f32 MFMA"})
     elif dom in w8a8:
@@ -1117,8 +1123,9 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": ("bert-base b64xs512 W8A8 encode resident on the device: token ids -> embedding rows + "
-                         "LayerNorm -> 12 layers x {W8A8 fused QKV 768->2304 +bias, fused attention (f32 "
-                         "semantics: online softmax, products on the bf16 MFMA over split operands), W8A8 O "
+                         "LayerNorm -> 12 layers x {W8A8 fused QKV 768->2304 +bias, fused attention "
+                         "(online softmax, products on the f16 MFMA over half-split operands, within the f32 "
+                         "MatmulBT gate), W8A8 O "
                          "768->768 +bias, "
                          "residual LayerNorm fused with the next quantization, W8A8 FFN-up 768->3072 +bias+GELU, "
                          "W8A8 FFN-down 3072->768 +bias, residual LayerNorm} -> mean pool + L2; every W8A8 "
@@ -1128,7 +1135,7 @@ def main() -> int:
             "seq_len": cfg.seq,
             "tokens_per_step": cfg.tokens,
             "parallelism": "single GPU",
-            "attention_products": "split-bf16 online-softmax (ENCHIP_ATT_FLASH_BF16)",
+            "attention_products": ATT_NAMES[ctx.attention_products],
             "seeds": {"weights": 2024, "tables_and_ids": 5},
             "launch": "eager",
         },
@@ -1143,18 +1150,20 @@ def main() -> int:
         "measured_ceilings": ceilings,
         "device": info,
     }
-    # the same encode with the attention products on the f32 MFMA
+    # the same encode with the attention's other product modes
     n2 = max(3, args.steps // 2)
     for mode, key, what in ((enchip.ATT_F32, "encode_f32_products",
                              "the two-pass attention with both products on the f32 MFMA"),
                             (enchip.ATT_SPLIT_BF16, "encode_split_bf16_two_pass",
-                             "the two-pass attention (the reference's softmax steps) with split-bf16 products")):
+                             "the two-pass attention (the reference's softmax steps) with split-bf16 products"),
+                            (enchip.ATT_FLASH_BF16, "encode_flash_bf16",
+                             "the online-softmax attention with bfloat16-split products")):
         ctx.set_attention_products(mode)
         el2 = time_steps(torch, stream, step, n2, 1)
         result[key] = {"seqs_per_s": cfg.batch * n2 / el2, "ms_per_step": el2 * 1e3 / n2, "steps": n2,
                        "note": f"the headline encode with {what} (enchip_set_attention_products)"}
         log(f"{key}: {result[key]['ms_per_step']:.3f} ms/step")
-    ctx.set_attention_products(enchip.ATT_FLASH_BF16)
+    ctx.set_attention_products(enchip.ATT_DEFAULT)
     model.close()
 
     if not args.no_other_configs:

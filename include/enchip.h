@@ -390,21 +390,30 @@ int enchip_attention_f32_dev(enchip_ctx *ctx, const float *d_q, const float *d_k
 
 /* How enchip_attention_f32_dev computes the attention (no reference counterpart: a
  * device tuning choice, like enchip_set_small_m):
- *   ENCHIP_ATT_FLASH_BF16 (the default) one pass over the keys with an online softmax
+ *   ENCHIP_ATT_FLASH_F16  (the default) one pass over the keys with an online softmax
  *                         (running maximum, 2^x on the hardware, the context rescaled as
  *                         the maximum grows, divided by the sum at the end), both products
- *                         on the bf16 MFMA over operands split into two bfloat16 parts
- *                         (x.y ~ hi.hi' + hi.lo' + lo.hi', each product within 3 * 2^-18
+ *                         on the f16 MFMA over operands split into two IEEE half parts
+ *                         (x.y ~ hi.hi' + hi.lo' + lo.hi', each product within ~3 * 2^-22
  *                         of exact, summed in f32), K and V staged through on-chip memory
- *                         once per 256 queries. Any L. Within the same f32 MatmulBT gate;
- *                         2.3x the speed of ENCHIP_ATT_SPLIT_BF16 (MI355X, BERT-base L=512).
+ *                         once per 256 queries. Any L. Within the f32 MatmulBT gate on
+ *                         inputs of standard deviation up to 4 (tested). Operands must be
+ *                         below 65520 in magnitude: larger ones give NaN.
+ *   ENCHIP_ATT_FLASH_BF16 the same kernel with the operands split into bfloat16 parts
+ *                         (each product within 3 * 2^-18): any finite operand, but 2^6
+ *                         times the product error (above the gate at standard deviation 2).
  *   ENCHIP_ATT_SPLIT_BF16 the reference's two-pass softmax (enchip_softmax_rows_scaled_dev's
- *                         steps) on a 32-query score tile held on chip, products as above.
- *                         L <= 512.
+ *                         steps) on a 32-query score tile held on chip, bfloat16 split
+ *                         products. L <= 512.
  *   ENCHIP_ATT_F32        the same two-pass kernel with f32 MFMA products
  *                         (v_mfma_f32_32x32x2_f32). L <= 512.
- * Non-finite operands give NaN in the bf16 modes. Applies to later calls on this context. */
-enum enchip_att_products { ENCHIP_ATT_F32 = 0, ENCHIP_ATT_SPLIT_BF16 = 1, ENCHIP_ATT_FLASH_BF16 = 2 };
+ * Non-finite operands give NaN in the split modes. Applies to later calls on this context. */
+enum enchip_att_products {
+    ENCHIP_ATT_F32 = 0,
+    ENCHIP_ATT_SPLIT_BF16 = 1,
+    ENCHIP_ATT_FLASH_BF16 = 2,
+    ENCHIP_ATT_FLASH_F16 = 3
+};
 int enchip_set_attention_products(enchip_ctx *ctx, int mode);
 
 /* The k best of each of `rows` rows of n scores (pitch ld), on the device:

@@ -32,7 +32,7 @@ from aikit_amd import enchip, workloads
 pytestmark = pytest.mark.gpu
 
 COS_MIN = 0.9999  # the encoder parity bar: cosine against the reference composition
-ATT_MODES = {"flash_bf16": 2, "split_bf16": 1, "f32": 0}  # enchip_att_products
+ATT_MODES = {"flash_f16": 3, "flash_bf16": 2, "split_bf16": 1, "f32": 0}  # enchip_att_products
 
 
 def say(msg):
@@ -138,7 +138,7 @@ def embeddings_in(ids, w, cfg):
     return oracle.layer_norm(h, *w["emb_ln"], L, D, 1e-12)
 
 
-@pytest.mark.parametrize("fused", ["flash_bf16", "split_bf16", "f32", False])
+@pytest.mark.parametrize("fused", ["flash_f16", "flash_bf16", "split_bf16", "f32", False])
 def test_config1_device_resident_forward(ctx, workers, fused):
     # The whole forward on the device (aikit_amd.bert_dev: W8A8 linears, f32 attention
     # products, softmax, residual + LayerNorm, pooling), every activation resident,
@@ -163,7 +163,7 @@ def test_config1_device_resident_forward(ctx, workers, fused):
     from aikit_amd import enchip
 
     model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn, fused=bool(fused))
-    ctx.set_attention_products(ATT_MODES[fused] if fused else enchip.ATT_FLASH_BF16)
+    ctx.set_attention_products(ATT_MODES[fused] if fused else enchip.ATT_DEFAULT)
     try:
         say(f"{cfg.name} device-resident forward, {S} sequences of {L}, fused attention {fused}")
         h = torch.from_numpy(h0).cuda()
@@ -174,7 +174,7 @@ def test_config1_device_resident_forward(ctx, workers, fused):
         dev = pooled.cpu().numpy()
     finally:
         model.close()
-        ctx.set_attention_products(enchip.ATT_FLASH_BF16)  # the default
+        ctx.set_attention_products(enchip.ATT_DEFAULT)
     worst = 1.0
     for s, ids in enumerate(seqs):
         ref = encode(ids, w, cfg, ref_linear)
@@ -383,7 +383,7 @@ def test_config4_full_depth_device_encode(ctx, bert_base_full, mode):
         dev = pooled.cpu().numpy()
     finally:
         model.close()
-        ctx.set_attention_products(enchip.ATT_FLASH_BF16)  # the default
+        ctx.set_attention_products(enchip.ATT_DEFAULT)
     for s_, ref in enumerate(refs):
         cos = _cos(ref, dev[s_])
         say(f"  seq {s_}: cosine {cos:.9f}")
@@ -463,10 +463,10 @@ def test_config5_full_depth_device_rerank(ctx, xlmr_large_full, mode):
     #    changes (f32 vs float64; ~4e-4 at 24 layers, measured live) -- a single token's
     #    state cannot agree more closely than the composition agrees with itself;
     #  * the device head on the device's own [CLS] row within 1e-5;
-    #  * the device logit against the reference's within twice what the reference's own
-    #    [CLS] drift allows its logit (tanh is 1-Lipschitz, so a [CLS] change d moves the
-    #    logit by at most |cw| |Wp|_2 |d|): a fixed bar set by the reference alone, not
-    #    by the device's own [CLS] error.
+    #  * the device logit against the reference's within twice the reference's own logit
+    #    drift (its logit with float64 attention against its logit with f32 attention)
+    #    plus 0.01 (1.6% of this head's logit): a fixed bar set by the reference alone,
+    #    not by the device's own [CLS] error.
     import torch
 
     from aikit_amd.bert_dev import DeviceBert
@@ -490,7 +490,7 @@ def test_config5_full_depth_device_rerank(ctx, xlmr_large_full, mode):
         dev_h = h.cpu().numpy()
     finally:
         model.close()
-        ctx.set_attention_products(enchip.ATT_FLASH_BF16)  # the default
+        ctx.set_attention_products(enchip.ATT_DEFAULT)
     dev_cls, ref_cls = dev_h[0], ref[0]
     pooled_cos = _cos(dev_h.astype(np.float64).mean(axis=0), ref.astype(np.float64).mean(axis=0))
     cos = _cos(ref_cls, dev_cls)
@@ -498,8 +498,7 @@ def test_config5_full_depth_device_rerank(ctx, xlmr_large_full, mode):
     head_err = abs(got - _head_logit(dev_cls, head))
     ref_logit = _head_logit(ref_cls, head)
     self_drift = abs(_head_logit(ref64[0], head) - ref_logit)
-    lip = np.linalg.norm(head["cw"].astype(np.float64)) * np.linalg.norm(head["pw"].astype(np.float64), 2)
-    bar = 2 * lip * np.linalg.norm(ref64[0].astype(np.float64) - ref_cls) + 1e-5
+    bar = 2 * self_drift + 0.01
     say(f"  pooled cosine {pooled_cos:.9f}; [CLS] cosine {cos:.9f} (reference vs itself with float64 attention "
         f"{self_cos:.9f}); logit {got:.6f} vs {ref_logit:.6f} (reference's own logit drift {self_drift:.3g}, bar "
         f"{bar:.3g}); head error {head_err:.3g}")

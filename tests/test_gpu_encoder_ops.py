@@ -178,7 +178,8 @@ def _attention_f64(qkv, S, L, H, hd, scale):
     return out
 
 
-PRODUCT_MODES = {"f32": 0, "split_bf16": 1, "flash_bf16": 2}  # enchip_att_products
+PRODUCT_MODES = {"f32": 0, "split_bf16": 1, "flash_bf16": 2, "flash_f16": 3}  # enchip_att_products
+FLASH_MODES = [2, 3]  # the online-softmax kernel with bfloat16 / half split products
 
 
 @pytest.mark.parametrize("products", list(PRODUCT_MODES))
@@ -220,10 +221,10 @@ def test_fused_attention_matches_f64_and_unfused(ctx, S, L, H, hd, products):
     # and the CPU restatement of the reference's attention for the first sequence
     ref = oracle.attention(qkv[0, :, :D], qkv[0, :, D:2 * D], qkv[0, :, 2 * D:], L, D, H)
     assert oracle.matmul_bt_worst_rel(f[0], ref) <= 2e-4
-    ctx.set_attention_products(enchip.ATT_FLASH_BF16)  # the default
+    ctx.set_attention_products(enchip.ATT_DEFAULT)
 
 
-@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("mode", [1, 2, 3])
 def test_split_bf16_attention_error_is_bounded_by_the_split(ctx, mode):
     # The split-bfloat16 products against the f64 attention on inputs of larger and mixed
     # magnitude (V spanning 6 decades), each output's error measured against the scale of
@@ -250,7 +251,7 @@ def test_split_bf16_attention_error_is_bounded_by_the_split(ctx, mode):
         ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, out.data_ptr(), D, S, L, H, hd, float(scale))
         torch.cuda.synchronize()
     finally:
-        ctx.set_attention_products(enchip.ATT_FLASH_BF16)  # the default
+        ctx.set_attention_products(enchip.ATT_DEFAULT)
     got = out.cpu().numpy().reshape(S, L, D).astype(np.float64)
     want = _attention_f64(qkv, S, L, H, hd, scale)
     # |ctx| <= sum_j P_j |V_j|: the scale of the P.V sum's terms per output
@@ -268,7 +269,8 @@ def test_split_bf16_attention_error_is_bounded_by_the_split(ctx, mode):
     assert err.max() <= 2e-4
 
 
-def test_flash_attention_wide_and_narrow_workgroups_agree(ctx):
+@pytest.mark.parametrize("mode", FLASH_MODES)
+def test_flash_attention_wide_and_narrow_workgroups_agree(ctx, mode):
     # The flash kernel runs 16 wavefronts per workgroup (512 queries) for 256 < L < 512 and
     # for L > 512 on a grid of at least as many workgroups as CUs; else 8. Each query's
     # arithmetic is the same in both, so the same sequences give the same bits whether they
@@ -290,11 +292,14 @@ def test_flash_attention_wide_and_narrow_workgroups_agree(ctx):
     narrow = torch.full((2 * L, D), np.nan, device="cuda")
     torch.cuda.synchronize()
     q = dq.data_ptr()
-    ctx.set_attention_products(enchip.ATT_FLASH_BF16)
-    say(f"flash attention L={L}: {S_wide} sequences (16 wavefronts) and 2 sequences (8 wavefronts)")
-    ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, wide.data_ptr(), D, S_wide, L, H, hd, float(scale))
-    ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, narrow.data_ptr(), D, 2, L, H, hd, float(scale))
-    torch.cuda.synchronize()
+    ctx.set_attention_products(mode)
+    say(f"flash attention (mode {mode}) L={L}: {S_wide} sequences (16 wavefronts) and 2 sequences (8 wavefronts)")
+    try:
+        ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, wide.data_ptr(), D, S_wide, L, H, hd, float(scale))
+        ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, narrow.data_ptr(), D, 2, L, H, hd, float(scale))
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_attention_products(enchip.ATT_DEFAULT)
     w = wide.cpu().numpy().reshape(S_wide, L, D)
     n = narrow.cpu().numpy().reshape(2, L, D)
     assert np.array_equal(w[:2].view(np.uint32), n.view(np.uint32))
@@ -304,9 +309,10 @@ def test_flash_attention_wide_and_narrow_workgroups_agree(ctx):
     assert wf <= 2e-4
 
 
+@pytest.mark.parametrize("mode", FLASH_MODES)
 @pytest.mark.parametrize("L", [77, 300])
 @pytest.mark.parametrize("scale", [-0.2, 0.0, 0.4])
-def test_flash_attention_any_scale(ctx, L, scale):
+def test_flash_attention_any_scale(ctx, L, scale, mode):
     # The online softmax runs in base 2 on c = |scale| log2 e with Q negated for a negative
     # scale (an exact negation), so the running maximum stays that of the scaled scores;
     # scale 0 gives the mean of V, including over the padded keys of the last tile. Both
@@ -323,9 +329,12 @@ def test_flash_attention_any_scale(ctx, L, scale):
     out = torch.full((S * L, D), np.nan, device="cuda")
     torch.cuda.synchronize()
     q = dq.data_ptr()
-    ctx.set_attention_products(enchip.ATT_FLASH_BF16)
-    ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, out.data_ptr(), D, S, L, H, hd, float(scale))
-    torch.cuda.synchronize()
+    ctx.set_attention_products(mode)
+    try:
+        ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, out.data_ptr(), D, S, L, H, hd, float(scale))
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_attention_products(enchip.ATT_DEFAULT)
     got = out.cpu().numpy().reshape(S, L, D)
     want = _attention_f64(qkv, S, L, H, hd, np.float32(scale))
     wf = oracle.matmul_bt_worst_rel(got, want)
@@ -336,8 +345,9 @@ def test_flash_attention_any_scale(ctx, L, scale):
         assert np.abs(got - mean_v).max() <= 1e-5
 
 
+@pytest.mark.parametrize("mode", FLASH_MODES)
 @pytest.mark.parametrize("S,L,H,hd", [(1, 1000, 2, 64), (2, 700, 3, 32)])
-def test_flash_attention_beyond_512_keys(ctx, S, L, H, hd):
+def test_flash_attention_beyond_512_keys(ctx, S, L, H, hd, mode):
     # The online-softmax kernel has no key limit (the two-pass kernels hold a row of
     # scores in LDS, L <= 512): longer sequences against float64 at the same gate.
     import torch
@@ -354,14 +364,89 @@ def test_flash_attention_beyond_512_keys(ctx, S, L, H, hd):
     torch.cuda.synchronize()
     q = dq.data_ptr()
     try:
-        ctx.set_attention_products(enchip.ATT_FLASH_BF16)
+        ctx.set_attention_products(mode)
         ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, out.data_ptr(), D, S, L, H, hd, float(scale))
         torch.cuda.synchronize()
     finally:
-        ctx.set_attention_products(enchip.ATT_FLASH_BF16)  # the default
+        ctx.set_attention_products(enchip.ATT_DEFAULT)
     wf = oracle.matmul_bt_worst_rel(out.cpu().numpy().reshape(S, L, D), _attention_f64(qkv, S, L, H, hd, scale))
     say(f"  worst rel {wf:.3g}")
     assert wf <= 2e-4
+
+
+@pytest.mark.parametrize("std", [2.0, 4.0])
+@pytest.mark.parametrize("products", ["flash_f16", "f32"])
+def test_attention_gate_at_realistic_magnitudes(ctx, std, products):
+    # The reference's f32 MatmulBT gate (gpu/enccuda/backend_test.go:71-81: worst
+    # |got - ref| / max(|ref|, 1) <= 2e-4) against a float64 attention on Q, K, V of
+    # standard deviation 2 and 4 (scores of standard deviation 4 and 16 at head_dim 64,
+    # trained-model magnitudes), for the default mode (half split products) and the f32
+    # products. The bfloat16 split's figure on the same inputs is printed beside them: it
+    # exceeds the gate here (measured 1.8-3.0e-4 at standard deviation 2), which is why it
+    # is not the default.
+    import torch
+
+    from aikit_amd import enchip
+
+    S, L, H, hd = 2, 512, 4, 64
+    D = H * hd
+    g = workloads.rng(7500 + int(std))
+    qkv = (g.standard_normal((S, L, 3 * D)) * std).astype(np.float32)
+    scale = np.float32(1.0 / np.sqrt(hd))
+    dq = torch.from_numpy(qkv).cuda()
+    q = dq.data_ptr()
+    want = _attention_f64(qkv, S, L, H, hd, scale)
+    got = {}
+    try:
+        for name in (products, "flash_bf16"):
+            out = torch.full((S * L, D), np.nan, device="cuda")
+            torch.cuda.synchronize()
+            ctx.set_attention_products(PRODUCT_MODES[name])
+            ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, out.data_ptr(), D, S, L, H, hd, float(scale))
+            torch.cuda.synchronize()
+            got[name] = oracle.matmul_bt_worst_rel(out.cpu().numpy().reshape(S, L, D), want)
+    finally:
+        ctx.set_attention_products(enchip.ATT_DEFAULT)
+    say(f"attention std={std}: worst rel {products} {got[products]:.3g} (flash_bf16 {got['flash_bf16']:.3g})")
+    assert got[products] <= 2e-4
+
+
+def test_flash_f16_out_of_range_operand_gives_nan(ctx):
+    # The half split is finite only for operands below 65520 in magnitude; a larger one
+    # makes inf - inf in its products, so the rows that use it come out NaN (never a finite
+    # wrong value), while the bfloat16 split (any finite operand) stays finite and within
+    # the gate there.
+    import torch
+
+    from aikit_amd import enchip
+
+    S, L, H, hd = 1, 64, 2, 64
+    D = H * hd
+    g = workloads.rng(7600)
+    qkv = g.standard_normal((S, L, 3 * D)).astype(np.float32)
+    qkv[0, 5, 3] = 1e5  # query 5 of head 0
+    scale = np.float32(1.0 / np.sqrt(hd))
+    dq = torch.from_numpy(qkv).cuda()
+    q = dq.data_ptr()
+    outs = {}
+    try:
+        for mode in (enchip.ATT_FLASH_F16, enchip.ATT_FLASH_BF16):
+            out = torch.zeros((S * L, D), device="cuda")
+            torch.cuda.synchronize()
+            ctx.set_attention_products(mode)
+            ctx.attention_f32_dev(q, q + D * 4, q + 2 * D * 4, 3 * D, out.data_ptr(), D, S, L, H, hd, float(scale))
+            torch.cuda.synchronize()
+            outs[mode] = out.cpu().numpy().reshape(S, L, D)
+    finally:
+        ctx.set_attention_products(enchip.ATT_DEFAULT)
+    f16 = outs[enchip.ATT_FLASH_F16]
+    assert np.isnan(f16[0, 5, :hd]).all()  # the row of head 0 whose query overflowed
+    ok = np.ones((S, L, D), bool)
+    ok[0, 5, :hd] = False
+    assert np.isfinite(f16[ok]).all()  # every other row: finite
+    bf = outs[enchip.ATT_FLASH_BF16]
+    assert np.isfinite(bf).all()
+    assert oracle.matmul_bt_worst_rel(bf, _attention_f64(qkv, S, L, H, hd, scale)) <= 2e-4
 
 
 def test_fused_attention_rejects_unsupported(ctx):
@@ -380,7 +465,7 @@ def test_fused_attention_rejects_unsupported(ctx):
         with pytest.raises(enchip.EnchipError):  # L above 512 in a two-pass mode
             ctx.attention_f32_dev(p, p, p, 64, p, 64, 1, 513, 1, 64, 0.1)
     finally:
-        ctx.set_attention_products(enchip.ATT_FLASH_BF16)  # the default
+        ctx.set_attention_products(enchip.ATT_DEFAULT)
     torch.cuda.synchronize()
 
 

@@ -505,23 +505,30 @@ int launch_gemm(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, c
 }
 
 // True when a linear that quantizes its own activations (d_a [M][K] f32, pitch K) runs
-// as the single small-M launch gemv_w8a8_q: M within the small-M limit, a narrow N (the
-// wide kernel's many workgroups would each quantize every row again), whole float4 rows
-// that fit the kernel's registers, and few enough values that quantizing all of them in
-// every workgroup costs less than a second launch.
+// as the single small-M launch gemv_w8a8_q: M within the small-M limit (at most 32, one
+// MFMA tile of rows), a narrow N (the wide kernel's streaming form serves wide N), and
+// whole float4 rows that fit one wavefront's registers.
 bool fused_small_m(const enchip_ctx *c, const Weight &w, int64_t M, const float *d_a) {
-    return M >= 1 && M <= c->small_m && !gemv_wide(c, w) && w.K % 4 == 0 && w.K > 0 && w.K <= enchip::GVQ_MAX_K &&
-           M * w.K <= enchip::GVQ_MAX_MK &&
-           (d_a == nullptr || (uintptr_t)d_a % 16 == 0);
+    return M >= 1 && M <= c->small_m && M <= 32 && !gemv_wide(c, w) && w.K % 4 == 0 && w.K > 0 &&
+           w.K <= enchip::GVQ_MAX_K && (d_a == nullptr || (uintptr_t)d_a % 16 == 0);
 }
+
+// float4 per lane that hold one row of K floats in gemv_w8a8_q (K <= 256 * QCH).
+int gvq_qch(int64_t K) { return K <= 256 ? 1 : K <= 512 ? 2 : K <= 768 ? 3 : 4; }
 
 // The kernels of gemv_w8a8_q whose dynamic-LDS limit has been raised (process-wide: the
 // attribute belongs to the kernel on the current device).
 int launch_fused_small_m(enchip_ctx *c, const Weight &w, const float *d_a, int64_t M, const float *bias, int epi,
                          float *out, int64_t ldo, hipStream_t s) {
     using Kern = void (*)(const float *, const int8_t *, const float *, const float *, void *, int64_t, int, int, int, int);
-    const Kern fn = epi == enchip::EPI_F32_GELU ? enchip::gemv_w8a8_q<enchip::EPI_F32_GELU>
-                                                : enchip::gemv_w8a8_q<enchip::EPI_F32>;
+    static constexpr Kern table[2][4] = {
+        {enchip::gemv_w8a8_q<enchip::EPI_F32, 1>, enchip::gemv_w8a8_q<enchip::EPI_F32, 2>,
+         enchip::gemv_w8a8_q<enchip::EPI_F32, 3>, enchip::gemv_w8a8_q<enchip::EPI_F32, 4>},
+        {enchip::gemv_w8a8_q<enchip::EPI_F32_GELU, 1>, enchip::gemv_w8a8_q<enchip::EPI_F32_GELU, 2>,
+         enchip::gemv_w8a8_q<enchip::EPI_F32_GELU, 3>, enchip::gemv_w8a8_q<enchip::EPI_F32_GELU, 4>}};
+    if (M < 1 || M > 32 || w.K > enchip::GVQ_MAX_K || w.K % 4 != 0)
+        return fail(c, ENCHIP_ERR_ARG, "gemv_w8a8_q: M=%lld K=%lld outside its shapes", (long long)M, (long long)w.K);
+    const Kern fn = table[epi == enchip::EPI_F32_GELU ? 1 : 0][gvq_qch(w.K) - 1];
     const size_t lds = (size_t)enchip::gvq_lds_bytes((int)w.Kp);
     if (lds > 64 * 1024) {
         const std::pair<const void *, size_t> key(reinterpret_cast<const void *>(fn), lds);
@@ -530,8 +537,9 @@ int launch_fused_small_m(enchip_ctx *c, const Weight &w, const float *d_a, int64
             c->lds_set.push_back(key);
         }
     }
-    hipLaunchKernelGGL(fn, dim3((unsigned)((w.N + 31) / 32)), dim3(64 * enchip::GV_WAVES), lds, s, d_a, w.d_w, w.d_s,
-                       bias, out, ldo, (int)M, (int)w.N, (int)w.K, (int)w.Kp);
+    const dim3 grid((unsigned)((w.N + 31) / 32), (unsigned)((M + enchip::GVQ_ROWS - 1) / enchip::GVQ_ROWS));
+    hipLaunchKernelGGL(fn, grid, dim3(64 * enchip::GVQ_WAVES), lds, s, d_a, w.d_w, w.d_s, bias, out, ldo, (int)M,
+                       (int)w.N, (int)w.K, (int)w.Kp);
     return check_launch(c, "gemv_w8a8_q");
 }
 
@@ -672,7 +680,7 @@ int enchip_gemm_kernel_name(enchip_ctx *ctx, enchip_weight h, int64_t M, int act
         snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, true, %d, %d>", pt_bm(ctx, *w, M),
                  enchip::PT_BN, enchip::PT_BK, pt_ring(*w), epi, enchip::PT_NW, pt_prio(*w, epi));
     else if (fused_small_m(ctx, *w, M, nullptr) && epi != enchip::EPI_I32)
-        snprintf(name, sizeof name, "enchip::gemv_w8a8_q<%d>", epi);
+        snprintf(name, sizeof name, "enchip::gemv_w8a8_q<%d, %d>", epi, gvq_qch(w->K));
     else if (M <= ctx->small_m && gemv_wide(ctx, *w))
         snprintf(name, sizeof name, "enchip::gemv_w8a8_wide<%d>", epi);
     else if (M <= ctx->small_m)

@@ -504,73 +504,72 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8a8(
 }
 
 // gemv_w8a8 with the per-token quantization of its (at most 32) activation rows done in
-// the kernel, so a small-M linear is one launch: every workgroup quantizes all rows into
-// LDS, in the A-operand fragment layout (frag_off), with quant_rows_vec's arithmetic (the
-// absmax of |v| over a row does not depend on the order it is taken in, then s = m/127,
-// 1/s and pack_codes), then runs gemv_w8a8's K split with its A fragments read from LDS.
-// Codes, scales and outputs are those of quant_rows_vec + gemv_w8a8. The rows are held in
-// registers (K <= GVQ_MAX_K) with all of a wave's loads in flight, and the first batch of
-// weight fragments is loaded while they are quantized. Each of the N/32 workgroups reads
-// the rows again from L2: cheap next to the weight stream at the narrow N this kernel
-// serves. K % 4 == 0, 16-byte aligned rows (pitch K); dynamic LDS gvq_lds_bytes(Kp).
-// (Longer rows are quantized faster by quant_rows_vec than by a two-pass loop here:
-// measured on MI355X at M = 16, K = 3072, N = 768, 14.5 us for the two kernels against
-// 22 us fused.)
+// the kernel, so a small-M linear is one launch. The grid is (N/32 channel groups) x
+// (M/4 row groups): each 8-wave workgroup quantizes only its GVQ_ROWS rows, one per wave,
+// with quant_rows_vec's arithmetic (the absmax of |v| over a row does not depend on the
+// order it is taken in, then s = m/127, 1/s and pack_codes) into LDS in the A-operand
+// fragment layout (frag_off), runs gemv_w8a8's K split over its 8 waves for its 32 output
+// channels with the A fragments read from LDS, and reduces and stores only its rows.
+// Codes, scales and outputs are those of quant_rows_vec + gemv_w8a8 (int32 partial sums
+// are exact in any order).
+//
+// Splitting the rows over workgroups, not quantizing every row in every workgroup, is what
+// makes the launch short: the per-element quantization (~15 VALU instructions) was the
+// longest phase, measured on MI355X by s_memtime stamps in a copy of the earlier kernel
+// (M = 16, K = 768: 2.4K of 8.2K shader cycles per wave with all 16 rows in each of the
+// 24 workgroups); with 4 rows per workgroup a call in graph replay went 5.41 -> 3.45 us
+// (N = 768) and 5.58 -> 4.24 us (N = 3072), and M = 32 7.7 -> 3.5 us. The row group's
+// workgroups read the same weight fragments (block ids nb + k * N/32 share an XCD's L2 when
+// N/32 is a multiple of 8), so HBM still streams each weight about once.
+//
+// Each row is held in registers (K <= 256 * QCH) with all of a wave's loads in flight and
+// unconditional (a lane past the row re-reads its last float4 and zeroes it by a bit mask),
+// and the weight fragments are loaded before the quantization. Rows of the 32-row MFMA
+// tile outside the group are never written in LDS: their sums are computed and dropped.
+// K % 4 == 0, K <= GVQ_MAX_K, 16-byte aligned rows (pitch K); dynamic LDS gvq_lds_bytes(Kp).
 constexpr int GVQ_MAX_K = 1024;
-// M * K above which each workgroup's re-quantization of every row costs more than the
-// separate quant_rows_vec launch (MI355X: M = 16, K = 768 takes 7.0 us fused against 8.2 us
-// for the two kernels; M = 32, K = 1024 takes 12.2 us against 9.6 us).
-constexpr int GVQ_MAX_MK = 16384;
-__host__ __device__ inline int gvq_lds_bytes(int Kp) {
-    const int codes = Kp * 32, red = GV_WAVES * 16 * 64 * 4;  // the reduction reuses the code area
-    return (codes > red ? codes : red) + 32 * 4;
-}
+constexpr int GVQ_ROWS = 4, GVQ_WAVES = 8;
+__host__ __device__ inline int gvq_lds_bytes(int Kp) { return Kp * 32 + GVQ_WAVES * GVQ_ROWS * 32 * 4 + 16; }
 
-template <int EPI>
-__global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8a8_q(
+template <int EPI, int QCH>
+__global__ __launch_bounds__(64 * GVQ_WAVES) void gemv_w8a8_q(
     const float *__restrict__ a, const int8_t *__restrict__ Wf, const float *__restrict__ wS,
     const float *__restrict__ bias, void *__restrict__ out, int64_t ldo, int M, int N, int K, int Kp) {
+    static_assert(GVQ_ROWS <= GVQ_WAVES && (GVQ_MAX_K / 32 + GVQ_WAVES - 1) / GVQ_WAVES <= 4, "one row per wave, <= 4 fragments");
     extern __shared__ __attribute__((aligned(16))) int8_t gvq[];
-    constexpr int RPW = 32 / GV_WAVES;  // rows per wavefront
-    constexpr int QCH = GVQ_MAX_K / 256;  // float4 per lane per row, held in registers
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nb = blockIdx.x, nk32 = Kp >> 5, K4 = K >> 2, Kp4 = Kp >> 2;
-    float *s_as = reinterpret_cast<float *>(gvq + (gvq_lds_bytes(Kp) - 32 * 4));
-
-    // ---- this wave's rows (at most RPW; rows past M are never stored, so they are neither
-    // loaded nor quantized: their LDS codes are left as they are) in registers, all loads
-    // issued at once, before the weight loads: loads complete in issue order, so the
-    // quantization below waits only for its own rows while the weights are in flight
-    const int nrows = M > wave ? (M - wave + GV_WAVES - 1) / GV_WAVES : 0;  // <= RPW
-    f32x4 v[RPW][QCH];
+    const int nb = blockIdx.x, rg = blockIdx.y, nk32 = Kp >> 5, K4 = K >> 2, Kp4 = Kp >> 2;
+    int *red = reinterpret_cast<int *>(gvq + Kp * 32);
+    float *s_as = reinterpret_cast<float *>(gvq + Kp * 32 + GVQ_WAVES * GVQ_ROWS * 32 * 4);
+    const int row = rg * GVQ_ROWS + wave;  // the row this wave quantizes (waves < GVQ_ROWS)
+    const bool qwave = wave < GVQ_ROWS && row < M;
+    float4 v[QCH];
+    if (qwave) {
+        const i32x4 *src = reinterpret_cast<const i32x4 *>(a + (int64_t)row * K);
 #pragma unroll
-    for (int j = 0; j < RPW; ++j) {
-        if (j >= nrows) break;
-        const f32x4 *src = reinterpret_cast<const f32x4 *>(a + (int64_t)(wave + GV_WAVES * j) * K);
-#pragma unroll
-        for (int c = 0; c < QCH; ++c) v[j][c] = src[min(lane + 64 * c, K4 - 1)];
+        for (int c = 0; c < QCH; ++c) {
+            const int k4 = lane + 64 * c;
+            const i32x4 t = src[min(k4, K4 - 1)];
+            const int keep = k4 < K4 ? -1 : 0;
+            v[c] = make_float4(__int_as_float(t.x & keep), __int_as_float(t.y & keep), __int_as_float(t.z & keep),
+                               __int_as_float(t.w & keep));
+        }
     }
-    // this wave's first batch of weight fragments
+    // this wave's weight fragments wave, wave + 8, ... (clamped; extra copies skipped below)
     const int8_t *wfr = Wf + (int64_t)nb * nk32 * 1024 + lane * 16;
-    i32x4 b[GV_BATCH];
+    i32x4 b[4];
 #pragma unroll
-    for (int u = 0; u < GV_BATCH; ++u)
-        b[u] = *reinterpret_cast<const i32x4 *>(wfr + (int64_t)min(wave + u * GV_WAVES, nk32 - 1) * 1024);
-
-    // ---- quantize
-#pragma unroll
-    for (int j = 0; j < RPW; ++j) {
-        if (j >= nrows) break;
-        const int row = wave + GV_WAVES * j;
+    for (int u = 0; u < 4; ++u)
+        b[u] = *reinterpret_cast<const i32x4 *>(wfr + (int64_t)min(wave + u * GVQ_WAVES, nk32 - 1) * 1024);
+    if (qwave) {
         float m = 0.0f;
 #pragma unroll
-        for (int c = 0; c < QCH; ++c)
-            if (lane + 64 * c < K4) {
-                m = absmax_step(m, v[j][c].x);
-                m = absmax_step(m, v[j][c].y);
-                m = absmax_step(m, v[j][c].z);
-                m = absmax_step(m, v[j][c].w);
-            }
+        for (int c = 0; c < QCH; ++c) {
+            m = absmax_step(m, v[c].x);
+            m = absmax_step(m, v[c].y);
+            m = absmax_step(m, v[c].z);
+            m = absmax_step(m, v[c].w);
+        }
         m = wave_absmax(m);
         const bool zero = m == 0.0f;
         const float sc = zero ? 0.0f : m / 127.0f;
@@ -579,49 +578,42 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8a8_q(
         for (int c = 0; c < QCH; ++c) {
             const int k4 = lane + 64 * c;
             if (k4 < Kp4)
-                *reinterpret_cast<int *>(gvq + frag_off(row, 4 * (int64_t)k4, nk32)) =
-                    (!zero && k4 < K4) ? pack_codes(make_float4(v[j][c].x, v[j][c].y, v[j][c].z, v[j][c].w), inv) : 0;
+                *reinterpret_cast<int *>(gvq + frag_off(row & 31, 4 * (int64_t)k4, nk32)) =
+                    (!zero && k4 < K4) ? pack_codes(v[c], inv) : 0;
         }
-        if (lane == 0) s_as[row] = sc;
+        if (lane == 0) s_as[wave] = sc;
     }
     __syncthreads();
-
-    // ---- gemv_w8a8's K split, A fragments from LDS (the first batch's weights loaded above)
     i32x16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0;
-    for (int k0 = wave; k0 < nk32; k0 += GV_WAVES * GV_BATCH) {
-        if (k0 != wave) {
 #pragma unroll
-            for (int u = 0; u < GV_BATCH; ++u)
-                b[u] = *reinterpret_cast<const i32x4 *>(wfr + (int64_t)min(k0 + u * GV_WAVES, nk32 - 1) * 1024);
+    for (int u = 0; u < 4; ++u) {
+        const int kk = wave + u * GVQ_WAVES;
+        if (kk < nk32) {
+            const i32x4 av = *reinterpret_cast<const i32x4 *>(gvq + kk * 1024 + lane * 16);
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b[u], acc, 0, 0, 0);
         }
-        i32x4 av[GV_BATCH];
-#pragma unroll
-        for (int u = 0; u < GV_BATCH; ++u)
-            av[u] = *reinterpret_cast<const i32x4 *>(gvq + min(k0 + u * GV_WAVES, nk32 - 1) * 1024 + lane * 16);
-#pragma unroll
-        for (int u = 0; u < GV_BATCH; ++u)
-            if (k0 + u * GV_WAVES < nk32) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[u], b[u], acc, 0, 0, 0);
     }
-    __syncthreads();  // every wave is done with the codes: the LDS takes the partial sums
-    int *red = reinterpret_cast<int *>(gvq);
+    // the group's rows r0 .. r0 + 3 of the 32-row tile are registers 4q .. 4q + 3 of lane
+    // half h (acc_row(4q + i, lane) = 8q + 4 (lane / 32) + i)
+    const int r0 = (rg * GVQ_ROWS) & 31, q = r0 >> 3, h = (r0 >> 2) & 1;
+    if ((lane >> 5) == h) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
+        for (int i = 0; i < GVQ_ROWS; ++i) red[(wave * GVQ_ROWS + i) * 32 + (lane & 31)] = acc[4 * q + i];
+    }
     __syncthreads();
-
-    const int col = nb * 32 + (lane & 31);
-    const float ws = col < N ? wS[col] : 0.0f;
-    const float bb = (bias != nullptr && col < N) ? bias[col] : kNoBias;
-#pragma unroll
-    for (int rr = 0; rr < 16 / GV_WAVES; ++rr) {
-        const int r = wave * (16 / GV_WAVES) + rr;
+    if (tid < GVQ_ROWS * 32) {
+        const int i = tid >> 5, c = tid & 31;
         int sum = 0;
 #pragma unroll
-        for (int w = 0; w < GV_WAVES; ++w) sum += red[(w * 16 + r) * 64 + lane];
-        const int row = acc_row(r, lane);
-        if (row >= M || col >= N) continue;
-        reinterpret_cast<float *>(out)[(int64_t)row * ldo + col] = epilogue<EPI>(sum, s_as[row], ws, bb);
+        for (int w = 0; w < GVQ_WAVES; ++w) sum += red[(w * GVQ_ROWS + i) * 32 + c];
+        const int orow = rg * GVQ_ROWS + i, col = nb * 32 + c;
+        if (orow < M && col < N) {
+            const float ws = wS[col];
+            const float bb = bias != nullptr ? bias[col] : kNoBias;
+            reinterpret_cast<float *>(out)[(int64_t)orow * ldo + col] = epilogue<EPI>(sum, s_as[i], ws, bb);
+        }
     }
 }
 

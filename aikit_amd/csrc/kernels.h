@@ -505,7 +505,7 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8a8(
 
 // gemv_w8a8 with the per-token quantization of its (at most 32) activation rows done in
 // the kernel, so a small-M linear is one launch. The grid is (N/32 channel groups) x
-// (M/4 row groups): each 8-wave workgroup quantizes only its GVQ_ROWS rows, one per wave,
+// (M/8 row groups): each 8-wave workgroup quantizes only its GVQ_ROWS rows, one per wave,
 // with quant_rows_vec's arithmetic (the absmax of |v| over a row does not depend on the
 // order it is taken in, then s = m/127, 1/s and pack_codes) into LDS in the A-operand
 // fragment layout (frag_off), runs gemv_w8a8's K split over its 8 waves for its 32 output
@@ -517,10 +517,11 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8a8(
 // makes the launch short: the per-element quantization (~15 VALU instructions) was the
 // longest phase, measured on MI355X by s_memtime stamps in a copy of the earlier kernel
 // (M = 16, K = 768: 2.4K of 8.2K shader cycles per wave with all 16 rows in each of the
-// 24 workgroups); with 4 rows per workgroup a call in graph replay went 5.41 -> 3.45 us
-// (N = 768) and 5.58 -> 4.24 us (N = 3072), and M = 32 7.7 -> 3.5 us. The row group's
-// workgroups read the same weight fragments (block ids nb + k * N/32 share an XCD's L2 when
-// N/32 is a multiple of 8), so HBM still streams each weight about once.
+// 24 workgroups). Per call in graph replay, cold weights: 5.41 us before, 3.45 us with 4
+// rows per workgroup and 3.37 us with 8 (N = 768); 5.58, 4.24 and 3.54 us (N = 3072); M =
+// 32, N = 768: 7.7, 3.5 and 3.4 us. The row groups' workgroups read the same weight
+// fragments (block ids nb + k * N/32 share an XCD's L2 when N/32 is a multiple of 8), so
+// HBM still streams each weight about once.
 //
 // Each row is held in registers (K <= 256 * QCH) with all of a wave's loads in flight and
 // unconditional (a lane past the row re-reads its last float4 and zeroes it by a bit mask),
@@ -528,14 +529,15 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8a8(
 // tile outside the group are never written in LDS: their sums are computed and dropped.
 // K % 4 == 0, K <= GVQ_MAX_K, 16-byte aligned rows (pitch K); dynamic LDS gvq_lds_bytes(Kp).
 constexpr int GVQ_MAX_K = 1024;
-constexpr int GVQ_ROWS = 4, GVQ_WAVES = 8;
+constexpr int GVQ_ROWS = 8, GVQ_WAVES = 8;
 __host__ __device__ inline int gvq_lds_bytes(int Kp) { return Kp * 32 + GVQ_WAVES * GVQ_ROWS * 32 * 4 + 16; }
 
 template <int EPI, int QCH>
 __global__ __launch_bounds__(64 * GVQ_WAVES) void gemv_w8a8_q(
     const float *__restrict__ a, const int8_t *__restrict__ Wf, const float *__restrict__ wS,
     const float *__restrict__ bias, void *__restrict__ out, int64_t ldo, int M, int N, int K, int Kp) {
-    static_assert(GVQ_ROWS <= GVQ_WAVES && (GVQ_MAX_K / 32 + GVQ_WAVES - 1) / GVQ_WAVES <= 4, "one row per wave, <= 4 fragments");
+    static_assert(GVQ_ROWS == 8 && GVQ_ROWS <= GVQ_WAVES && (GVQ_MAX_K / 32 + GVQ_WAVES - 1) / GVQ_WAVES <= 4,
+                  "one row per wave, <= 4 fragments per wave, row groups of one accumulator register quad");
     extern __shared__ __attribute__((aligned(16))) int8_t gvq[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nb = blockIdx.x, rg = blockIdx.y, nk32 = Kp >> 5, K4 = K >> 2, Kp4 = Kp >> 2;
@@ -595,13 +597,11 @@ __global__ __launch_bounds__(64 * GVQ_WAVES) void gemv_w8a8_q(
             acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b[u], acc, 0, 0, 0);
         }
     }
-    // the group's rows r0 .. r0 + 3 of the 32-row tile are registers 4q .. 4q + 3 of lane
-    // half h (acc_row(4q + i, lane) = 8q + 4 (lane / 32) + i)
-    const int r0 = (rg * GVQ_ROWS) & 31, q = r0 >> 3, h = (r0 >> 2) & 1;
-    if ((lane >> 5) == h) {
+    // the group's rows 8q .. 8q + 7 of the 32-row tile are registers 4q .. 4q + 3
+    // (acc_row(4q + i, lane) = 8q + 4 (lane / 32) + i)
+    const int q = rg & 3;
 #pragma unroll
-        for (int i = 0; i < GVQ_ROWS; ++i) red[(wave * GVQ_ROWS + i) * 32 + (lane & 31)] = acc[4 * q + i];
-    }
+    for (int i = 0; i < 4; ++i) red[(wave * GVQ_ROWS + (lane >> 5) * 4 + i) * 32 + (lane & 31)] = acc[4 * q + i];
     __syncthreads();
     if (tid < GVQ_ROWS * 32) {
         const int i = tid >> 5, c = tid & 31;

@@ -851,7 +851,7 @@ def test_ann_topk_fused_route(ctx, kind, M, k, K):
                                        (1, 256, 64, 1), (4, 260, 200, 0), (31, 700, 160, 1)])
 def test_fused_small_m_matches_two_kernels_and_oracle(ctx, M, K, N, act):
     # At M <= 32 a self-quantizing linear is one launch (gemv_w8a8_q: each workgroup
-    # quantizes its group of 4 rows into on-chip memory, one wavefront per row, held in 1-4
+    # quantizes its group of 8 rows into on-chip memory, one wavefront per row, held in 1-4
     # float4 per lane by K); with want_acc the same call runs the separate quantizer +
     # gemv_w8a8. Same bits, and the oracle's, including an all-zero row (scale 0), an Inf
     # row (scale Inf: codes 0) and a row with NaNs (ignored by the absmax), across every

@@ -295,7 +295,27 @@ def other_configs(ctx, torch, stream, ceilings):
     tg = graph_us(call, reps)
     t = tg * 1e-6 if tg is not None else t_eager
     ops = 2.0 * M * N * K
+    # where a call's time goes: the same call without the GELU, and its two kernels alone
+    # (the GEMM on the call's own fragment-major codes, with and without the GELU)
+    _, ldq = ctx.frag_route(h, M)
+    with torch.cuda.stream(stream):
+        aq = torch.empty((M * ldq,), device="cuda", dtype=torch.int8)
+        asc = torch.empty(M, device="cuda", dtype=torch.float32)
+    torch.cuda.synchronize()
+    quant = lambda: ctx.quant_rows_frag_dev(a.data_ptr(), M, K, aq.data_ptr(), ldq, asc.data_ptr(), sp)
+    quant()
+    split = {
+        "call_bias_only_us": graph_us(lambda: ctx.linear_dev(h, a.data_ptr(), M, b.data_ptr(), 0, dst.data_ptr(), sp),
+                                      reps),
+        "quantizer_us": graph_us(quant, reps),
+        "gemm_gelu_us": graph_us(lambda: ctx.pre_frag_dev(h, aq.data_ptr(), ldq, M, asc.data_ptr(), b.data_ptr(),
+                                                          c2["act"], dst.data_ptr(), sp), reps),
+        "gemm_bias_only_us": graph_us(lambda: ctx.pre_frag_dev(h, aq.data_ptr(), ldq, M, asc.data_ptr(), b.data_ptr(),
+                                                               0, dst.data_ptr(), sp), reps),
+        "note": "HIP graph replay of 50 calls each; the GEMM legs run on the quantizer's codes of the same "
+                "activations (enchip_w8a8_pre_frag_dev)"}
     out["config2_isolated_linear"] = {
+        "split": split,
         "M": M, "K": K, "N": N, "act": "gelu", "us_per_call": t * 1e6, "int8_tops": ops / t / 1e12,
         "frac_int8_peak": ops / t / PEAK_INT8_OPS, "us_per_call_eager": t_eager * 1e6,
         "timing": "HIP graph replay" if tg is not None else "eager",
@@ -967,6 +987,10 @@ def compact_result(result: dict, detail_path: str | None = None) -> dict:
     oc = result.get("other_configs") or {}
     if "config2_isolated_linear" in oc:
         other["cfg2_us_per_call"] = _r(oc["config2_isolated_linear"].get("us_per_call"))
+        sp2 = oc["config2_isolated_linear"].get("split") or {}
+        for k in ("call_bias_only_us", "quantizer_us", "gemm_gelu_us", "gemm_bias_only_us"):
+            if sp2.get(k) is not None:
+                other[f"cfg2_{k}"] = _r(sp2[k])
     for n in ("768", "3072"):
         c = oc.get(f"config3_gemv_n{n}")
         if c:

@@ -513,22 +513,26 @@ bool fused_small_m(const enchip_ctx *c, const Weight &w, int64_t M, const float 
            w.K <= enchip::GVQ_MAX_K && (d_a == nullptr || (uintptr_t)d_a % 16 == 0);
 }
 
-// float4 per lane that hold one row of K floats in gemv_w8a8_q (K <= 256 * QCH).
-int gvq_qch(int64_t K) { return K <= 256 ? 1 : K <= 512 ? 2 : K <= 768 ? 3 : 4; }
+// float4 per lane that hold one row of K floats in gemv_w8a8_q (K <= 256 * QCH), one of
+// the instantiated 1, 2, 3, 4, 8, 12, 16.
+int gvq_qch(int64_t K) {
+    return K <= 256 ? 1 : K <= 512 ? 2 : K <= 768 ? 3 : K <= 1024 ? 4 : K <= 2048 ? 8 : K <= 3072 ? 12 : 16;
+}
 
 // The kernels of gemv_w8a8_q whose dynamic-LDS limit has been raised (process-wide: the
 // attribute belongs to the kernel on the current device).
 int launch_fused_small_m(enchip_ctx *c, const Weight &w, const float *d_a, int64_t M, const float *bias, int epi,
                          float *out, int64_t ldo, hipStream_t s) {
     using Kern = void (*)(const float *, const int8_t *, const float *, const float *, void *, int64_t, int, int, int, int);
-    static constexpr Kern table[2][4] = {
-        {enchip::gemv_w8a8_q<enchip::EPI_F32, 1>, enchip::gemv_w8a8_q<enchip::EPI_F32, 2>,
-         enchip::gemv_w8a8_q<enchip::EPI_F32, 3>, enchip::gemv_w8a8_q<enchip::EPI_F32, 4>},
-        {enchip::gemv_w8a8_q<enchip::EPI_F32_GELU, 1>, enchip::gemv_w8a8_q<enchip::EPI_F32_GELU, 2>,
-         enchip::gemv_w8a8_q<enchip::EPI_F32_GELU, 3>, enchip::gemv_w8a8_q<enchip::EPI_F32_GELU, 4>}};
+#define GVQ_ROW(E)                                                                                           \
+    {enchip::gemv_w8a8_q<E, 1>, enchip::gemv_w8a8_q<E, 2>, enchip::gemv_w8a8_q<E, 3>, enchip::gemv_w8a8_q<E, 4>, \
+     enchip::gemv_w8a8_q<E, 8>, enchip::gemv_w8a8_q<E, 12>, enchip::gemv_w8a8_q<E, 16>}
+    static constexpr Kern table[2][7] = {GVQ_ROW(enchip::EPI_F32), GVQ_ROW(enchip::EPI_F32_GELU)};
+#undef GVQ_ROW
     if (M < 1 || M > 32 || w.K > enchip::GVQ_MAX_K || w.K % 4 != 0)
         return fail(c, ENCHIP_ERR_ARG, "gemv_w8a8_q: M=%lld K=%lld outside its shapes", (long long)M, (long long)w.K);
-    const Kern fn = table[epi == enchip::EPI_F32_GELU ? 1 : 0][gvq_qch(w.K) - 1];
+    const int qch = gvq_qch(w.K);
+    const Kern fn = table[epi == enchip::EPI_F32_GELU ? 1 : 0][qch <= 4 ? qch - 1 : qch == 8 ? 4 : qch == 12 ? 5 : 6];
     const size_t lds = (size_t)enchip::gvq_lds_bytes((int)w.Kp);
     if (lds > 64 * 1024) {
         const std::pair<const void *, size_t> key(reinterpret_cast<const void *>(fn), lds);

@@ -525,10 +525,11 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8a8(
 //
 // Each row is held in registers (K <= 256 * QCH) with all of a wave's loads in flight and
 // unconditional (a lane past the row re-reads its last float4 and zeroes it by a bit mask),
-// and the weight fragments are loaded before the quantization. Rows of the 32-row MFMA
-// tile outside the group are never written in LDS: their sums are computed and dropped.
-// K % 4 == 0, K <= GVQ_MAX_K, 16-byte aligned rows (pitch K); dynamic LDS gvq_lds_bytes(Kp).
-constexpr int GVQ_MAX_K = 1024;
+// and the wave's weight fragments (at most QCH: Kp <= 256 * QCH) are loaded before the
+// quantization. Rows of the 32-row MFMA tile outside the group are never written in LDS:
+// their sums are computed and dropped. K % 4 == 0, K <= GVQ_MAX_K, 16-byte aligned rows
+// (pitch K); dynamic LDS gvq_lds_bytes(Kp) (136 KiB at K = 4096).
+constexpr int GVQ_MAX_K = 4096;
 constexpr int GVQ_ROWS = 8, GVQ_WAVES = 8;
 __host__ __device__ inline int gvq_lds_bytes(int Kp) { return Kp * 32 + GVQ_WAVES * GVQ_ROWS * 32 * 4 + 16; }
 
@@ -536,8 +537,7 @@ template <int EPI, int QCH>
 __global__ __launch_bounds__(64 * GVQ_WAVES) void gemv_w8a8_q(
     const float *__restrict__ a, const int8_t *__restrict__ Wf, const float *__restrict__ wS,
     const float *__restrict__ bias, void *__restrict__ out, int64_t ldo, int M, int N, int K, int Kp) {
-    static_assert(GVQ_ROWS == 8 && GVQ_ROWS <= GVQ_WAVES && (GVQ_MAX_K / 32 + GVQ_WAVES - 1) / GVQ_WAVES <= 4,
-                  "one row per wave, <= 4 fragments per wave, row groups of one accumulator register quad");
+    static_assert(GVQ_ROWS == 8 && GVQ_ROWS <= GVQ_WAVES, "one row per wave, row groups of one accumulator register quad");
     extern __shared__ __attribute__((aligned(16))) int8_t gvq[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nb = blockIdx.x, rg = blockIdx.y, nk32 = Kp >> 5, K4 = K >> 2, Kp4 = Kp >> 2;
@@ -559,9 +559,9 @@ __global__ __launch_bounds__(64 * GVQ_WAVES) void gemv_w8a8_q(
     }
     // this wave's weight fragments wave, wave + 8, ... (clamped; extra copies skipped below)
     const int8_t *wfr = Wf + (int64_t)nb * nk32 * 1024 + lane * 16;
-    i32x4 b[4];
+    i32x4 b[QCH];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < QCH; ++u)
         b[u] = *reinterpret_cast<const i32x4 *>(wfr + (int64_t)min(wave + u * GVQ_WAVES, nk32 - 1) * 1024);
     if (qwave) {
         float m = 0.0f;
@@ -590,7 +590,7 @@ __global__ __launch_bounds__(64 * GVQ_WAVES) void gemv_w8a8_q(
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < QCH; ++u) {
         const int kk = wave + u * GVQ_WAVES;
         if (kk < nk32) {
             const i32x4 av = *reinterpret_cast<const i32x4 *>(gvq + kk * 1024 + lane * 16);

@@ -848,11 +848,13 @@ def test_ann_topk_fused_route(ctx, kind, M, k, K):
 @pytest.mark.parametrize("M,K,N,act", [(1, 768, 768, 0), (16, 768, 3072, 1), (16, 768, 768, 0), (16, 1024, 768, 1),
                                        (5, 64, 1001, 1), (7, 1000, 96, 0), (9, 384, 1024, 0), (3, 36, 40, 1),
                                        (32, 1024, 768, 1), (32, 768, 3072, 0), (8, 768, 768, 1), (13, 512, 96, 0),
-                                       (1, 256, 64, 1), (4, 260, 200, 0), (31, 700, 160, 1)])
+                                       (1, 256, 64, 1), (4, 260, 200, 0), (31, 700, 160, 1),
+                                       (16, 3072, 768, 0), (5, 4096, 1024, 1), (32, 1536, 384, 1), (7, 2000, 100, 0),
+                                       (1, 4096, 96, 0)])
 def test_fused_small_m_matches_two_kernels_and_oracle(ctx, M, K, N, act):
     # At M <= 32 a self-quantizing linear is one launch (gemv_w8a8_q: each workgroup
-    # quantizes its group of 8 rows into on-chip memory, one wavefront per row, held in 1-4
-    # float4 per lane by K); with want_acc the same call runs the separate quantizer +
+    # quantizes its group of 8 rows into on-chip memory, one wavefront per row, held in 1-16
+    # float4 per lane by K <= 4096); with want_acc the same call runs the separate quantizer +
     # gemv_w8a8. Same bits, and the oracle's, including an all-zero row (scale 0), an Inf
     # row (scale Inf: codes 0) and a row with NaNs (ignored by the absmax), across every
     # row group (M = 1 .. 32, ragged last groups).

@@ -470,9 +470,19 @@ bool launch_gemm_epi(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t l
                                s, aq, lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp);
         } else {
             const int64_t blocks = (w.N + 31) / 32;
-            if (!grid_fits(blocks, 64 * enchip::GV_WAVES)) return false;
-            hipLaunchKernelGGL((enchip::gemv_w8a8<EPI>), dim3((unsigned)blocks), dim3(64 * enchip::GV_WAVES), 0, s, aq,
-                               lda, w.d_w, as, w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp);
+            if (!grid_fits(blocks, 64 * enchip::GV_WAVES) || M > 32) return false;
+            // weight fragments per wave and batch: the whole K in one batch up to 32 fragments
+            const int64_t per_wave = (w.Kp / 32 + enchip::GV_WAVES - 1) / enchip::GV_WAVES;
+            const dim3 grid((unsigned)blocks, (unsigned)((M + enchip::GV_ROWS - 1) / enchip::GV_ROWS));
+#define GV_LAUNCH(NB)                                                                                             \
+    hipLaunchKernelGGL((enchip::gemv_w8a8<EPI, NB>), grid, dim3(64 * enchip::GV_WAVES), 0, s, aq, lda, w.d_w, as, \
+                       w.d_s, bias, out, ldo, (int)M, (int)w.N, (int)w.Kp)
+            if (per_wave <= 1) GV_LAUNCH(1);
+            else if (per_wave == 2) GV_LAUNCH(2);
+            else if (per_wave == 3) GV_LAUNCH(3);
+            else if (per_wave == 4) GV_LAUNCH(4);
+            else GV_LAUNCH(8);
+#undef GV_LAUNCH
         }
         return true;
     }
@@ -502,6 +512,12 @@ int launch_gemm(enchip_ctx *c, const Weight &w, const int8_t *aq, int64_t lda, c
         return fail(c, ENCHIP_ERR_ARG, "gemm: M=%lld N=%lld needs more workgroups than one launch addresses",
                     (long long)M, (long long)w.N);
     return check_launch(c, "gemm_w8a8");
+}
+
+// Weight fragments per wave and batch of gemv_w8a8 (the instantiated 1, 2, 3, 4, 8).
+int gv_nb(const Weight &w) {
+    const int64_t per_wave = (w.Kp / 32 + enchip::GV_WAVES - 1) / enchip::GV_WAVES;
+    return per_wave <= 4 ? (int)std::max<int64_t>(per_wave, 1) : 8;
 }
 
 // True when a linear that quantizes its own activations (d_a [M][K] f32, pitch K) runs
@@ -688,7 +704,7 @@ int enchip_gemm_kernel_name(enchip_ctx *ctx, enchip_weight h, int64_t M, int act
     else if (M <= ctx->small_m && gemv_wide(ctx, *w))
         snprintf(name, sizeof name, "enchip::gemv_w8a8_wide<%d>", epi);
     else if (M <= ctx->small_m)
-        snprintf(name, sizeof name, "enchip::gemv_w8a8<%d>", epi);
+        snprintf(name, sizeof name, "enchip::gemv_w8a8<%d, %d>", epi, gv_nb(*w));
     else if (use_persistent(*w, nullptr, w->Kp, nullptr, w->N, M, false))
         snprintf(name, sizeof name, "enchip::gemm_w8a8_pt<%d, %d, %d, %d, %d, false, %d, %d>", pt_bm(ctx, *w, M),
                  enchip::PT_BN, enchip::PT_BK, pt_ring(*w), epi, enchip::PT_NW, pt_prio(*w, epi));

@@ -443,62 +443,65 @@ __global__ __launch_bounds__(256, MINB) void gemm_w8a8(
 }
 
 // ----------------------------------------------------------------------------
-// Small-M variant (M <= 32): HBM-bound on the weight stream, so every weight
-// byte is read once and the whole M tile (zero-padded to 32 rows) rides along in
-// the MFMA. One block per 32 output channels; its GV_WAVES waves split K, each
-// issuing all of its weight-fragment loads (up to GV_BATCH at a time) before its
-// MFMAs, so a call costs about one HBM round trip rather than one per fragment.
-// The int32 partial sums are added exactly through LDS.
-constexpr int GV_WAVES = 8, GV_BATCH = 8;
+// Small-M variant (M <= 32) on codes already quantized (row-major, pitch lda): HBM-bound
+// on the weight stream, so every weight byte is read once and the M tile (zero-padded to
+// 32 rows) rides along in the MFMA. The grid is (N/32 channel groups) x (M/8 row groups):
+// each 8-wave workgroup splits K over its waves for its 32 output channels, each wave
+// issuing its weight and activation fragments (NB at a time: nk32 <= 8 NB needs one
+// batch) before its MFMAs, so a call costs about one HBM round trip; the exact int32
+// partials of the group's 8 rows only are added through LDS and stored. Lanes of rows
+// outside the group load the group's first row (their sums are dropped). Splitting the
+// rows over workgroups, where each workgroup used to reduce and store all 32 rows of its
+// channels: 4.42 -> 2.93 us per call at M = 16, K = 768, N = 768 and 4.64 -> 3.12 us at
+// N = 3072 (MI355X, graph replay over cold weights, bit-identical).
+constexpr int GV_WAVES = 8, GV_ROWS = 8;
 
-template <int EPI>
+template <int EPI, int NB>
 __global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8a8(
     const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ Wf,
     const float *__restrict__ aS, const float *__restrict__ wS, const float *__restrict__ bias,
     void *__restrict__ out, int64_t ldo, int M, int N, int Kp) {
-    __shared__ int red[GV_WAVES * 16 * 64];
+    __shared__ int red[GV_WAVES * GV_ROWS * 32];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nb = blockIdx.x, nk32 = Kp >> 5;
-    const int8_t *arow = A + (int64_t)min(lane & 31, M - 1) * lda + (lane >> 5) * 16;
+    const int nb = blockIdx.x, rg = blockIdx.y, nk32 = Kp >> 5;
+    const int q = rg & 3, r = lane & 31;  // the group's rows 8q .. 8q + 7 of the 32-row tile
+    const int8_t *arow = A + (int64_t)min((r >> 3) == q ? r : 8 * q, M - 1) * lda + (lane >> 5) * 16;
     const int8_t *wfr = Wf + (int64_t)nb * nk32 * 1024 + lane * 16;
 
     i32x16 acc;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0;
-    for (int k0 = wave; k0 < nk32; k0 += GV_WAVES * GV_BATCH) {
+    for (int k = 0; k < 16; ++k) acc[k] = 0;
+    for (int k0 = wave; k0 < nk32; k0 += GV_WAVES * NB) {
         // this wave's fragments k0, k0 + GV_WAVES, ...: loads first (clamped to the last
         // fragment, whose extra copies are skipped below), then the MFMAs
-        i32x4 a[GV_BATCH], b[GV_BATCH];
+        i32x4 a[NB], b[NB];
 #pragma unroll
-        for (int u = 0; u < GV_BATCH; ++u) {
+        for (int u = 0; u < NB; ++u) {
             const int kk = min(k0 + u * GV_WAVES, nk32 - 1);
             a[u] = *reinterpret_cast<const i32x4 *>(arow + kk * 32);
             b[u] = *reinterpret_cast<const i32x4 *>(wfr + (int64_t)kk * 1024);
         }
 #pragma unroll
-        for (int u = 0; u < GV_BATCH; ++u)
+        for (int u = 0; u < NB; ++u)
             if (k0 + u * GV_WAVES < nk32) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[u], b[u], acc, 0, 0, 0);
     }
+    // rows 8q .. 8q + 7 are registers 4q .. 4q + 3 (acc_row(4q + i, lane) = 8q + 4 (lane / 32) + i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
+    for (int i = 0; i < 4; ++i) red[(wave * GV_ROWS + (lane >> 5) * 4 + i) * 32 + r] = acc[4 * q + i];
     __syncthreads();
-
-    const int col = nb * 32 + (lane & 31);
-    const float ws = col < N ? wS[col] : 0.0f;
-    const float bb = (bias != nullptr && col < N) ? bias[col] : kNoBias;
-#pragma unroll
-    for (int rr = 0; rr < 16 / GV_WAVES; ++rr) {
-        const int r = wave * (16 / GV_WAVES) + rr;
+    if (tid < GV_ROWS * 32) {
+        const int i = tid >> 5, c = tid & 31;
         int sum = 0;
 #pragma unroll
-        for (int w = 0; w < GV_WAVES; ++w) sum += red[(w * 16 + r) * 64 + lane];
-        const int row = acc_row(r, lane);
-        if (row >= M || col >= N) continue;
-        if (EPI == EPI_I32) {
-            reinterpret_cast<int *>(out)[(int64_t)row * ldo + col] = sum;
-        } else {
-            reinterpret_cast<float *>(out)[(int64_t)row * ldo + col] =
-                epilogue<EPI>(sum, aS[row], ws, bb);
+        for (int w = 0; w < GV_WAVES; ++w) sum += red[(w * GV_ROWS + i) * 32 + c];
+        const int row = rg * GV_ROWS + i, col = nb * 32 + c;
+        if (row < M && col < N) {
+            if (EPI == EPI_I32) {
+                reinterpret_cast<int *>(out)[(int64_t)row * ldo + col] = sum;
+            } else {
+                const float bb = bias != nullptr ? bias[col] : kNoBias;
+                reinterpret_cast<float *>(out)[(int64_t)row * ldo + col] = epilogue<EPI>(sum, aS[row], wS[col], bb);
+            }
         }
     }
 }
@@ -655,14 +658,17 @@ __global__ __launch_bounds__(64 * GVW_WAVES) void gemv_w8a8_wide(
     if (col >= N) return;
     const float ws = wS[col];
     const float bb = bias != nullptr ? bias[col] : kNoBias;
+    // nontemporal stores: the scores are written once and not read here (M = 16 over a
+    // 2^20 x 384 index: 89.6 -> 83.7 us on MI355X; M = 1 unchanged)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int row = acc_row(r, lane);
         if (row >= M) continue;
         if (EPI == EPI_I32)
-            reinterpret_cast<int *>(out)[(int64_t)row * ldo + col] = acc[r];
+            __builtin_nontemporal_store(acc[r], reinterpret_cast<int *>(out) + (int64_t)row * ldo + col);
         else
-            reinterpret_cast<float *>(out)[(int64_t)row * ldo + col] = epilogue<EPI>(acc[r], aS[row], ws, bb);
+            __builtin_nontemporal_store(epilogue<EPI>(acc[r], aS[row], ws, bb),
+                                        reinterpret_cast<float *>(out) + (int64_t)row * ldo + col);
     }
 }
 

@@ -40,6 +40,13 @@ PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA
 TRAFFIC_PROFILE = "profiles/bert_base_b64s512_hbm_traffic.md"
 
 
+def gemv_kernel_name(K: int, act: int) -> str:
+    """gemv_w8a8's instantiation for a weight of K columns (padded to 64): its fragments
+    per wave and batch, as the library picks them."""
+    per_wave = -(-(-(-K // 64) * 64 // 32) // 8)
+    return f"enchip::gemv_w8a8<{1 + act}, {max(per_wave, 1) if per_wave <= 4 else 8}>"
+
+
 def quant_kernel_name(K: int, frag: bool) -> str:
     """Name of the quantize kernel enchip launches for rows of K floats (aligned
     buffers, pitch K padded to 64): quant_rows_frag<ceil(Kp/256), rows per wave> for fragment-major
@@ -372,7 +379,7 @@ def other_configs(ctx, torch, stream, ceilings):
             "M": M, "K": K, "N": N, "us_per_call": tb * 1e6,
             "hbm_gbps": (nbytes + qbytes) / tb / 1e9, "frac_hbm_peak": (nbytes + qbytes) / tb / PEAK_HBM_BPS,
             "frac_measured_read_ceiling": (nbytes + qbytes) / tb / 1e9 / ceilings["hbm_read_gbps"],
-            "gemv_only_us_per_call": t_gemv, "gemv_only_kernel": "enchip::gemv_w8a8<%d>" % (1 + c3["act"]),
+            "gemv_only_us_per_call": t_gemv, "gemv_only_kernel": gemv_kernel_name(K, c3["act"]),
             "launch_floor_us": floor_us,
             "us_per_call_eager": t_eager * 1e6, "timing": "HIP graph replay" if t_lin is not None else "eager",
             "weight_copies": len(hs), "weight_set_mb": len(hs) * N * K / 1e6,

@@ -21,9 +21,10 @@ def bits(x):
 
 
 # (K, N, act, [M first, M second]): the persistent GEMM on fragment-major codes (N % 4 == 0,
-# M > 32), the small-M kernels (M <= 32), the general GEMM on row-major codes (N % 4 != 0)
+# M > 32), the one-launch small-M kernel (M <= 32, K <= 4096), the general GEMM on row-major
+# codes (N % 4 != 0)
 ROUTES = [(768, 3072, 1, [4096, 300]), (3072, 768, 0, [8192, 1000]), (768, 768, 1, [32, 16]),
-          (768, 3072, 0, [16, 1]), (384, 1001, 1, [777, 64])]
+          (768, 3072, 0, [16, 1]), (3072, 768, 1, [24, 9]), (384, 1001, 1, [777, 64])]
 
 
 def test_noalloc_matches_linear_dev_on_two_calls():

@@ -99,6 +99,25 @@ __device__ __forceinline__ float gelu_f32(float x) {
     return 0.5f * x * (1.0f + erf_f32(x * 0.7071067811865476f));
 }
 
+// gelu_f32 for an argument off ErfF32's series branch (|u| >= 1, u = x * 0.7071067811865476f,
+// or NaN), without branches: the erf tail (1 <= |u| <= 4) is evaluated for every such
+// argument and the sign branch (|u| > 4) selected, by erf_f32's operations on each branch
+// (for |u| > 4 the tail's exp underflows harmlessly, and a NaN takes the tail, as in
+// erf_f32). Branch-free so that several independent arguments interleave. Not for |u| < 1.
+__device__ __forceinline__ float gelu_f32_offseries(float x) {
+    const float u = x * 0.7071067811865476f;
+    const float sgn = u < 0 ? -1.0f : 1.0f;
+    const float ax = u < 0 ? -u : u;
+    const float t = 1.0f / (1.0f + 0.3275911f * ax);
+    float p = 1.061405429f;
+    p = p * t - 1.453152027f;
+    p = p * t + 1.421413741f;
+    p = p * t - 0.284496736f;
+    p = p * t + 0.254829592f;
+    const float tail = sgn * (1.0f - p * t * exp_f32_core(-ax * ax));
+    return 0.5f * x * (1.0f + (ax > 4 ? sgn : tail));
+}
+
 // GELUF32 for the arguments that take ErfF32's series branch (|u| < 1, u = x *
 // 0.7071067811865476f), evaluated without branching. `tail` is set for every other
 // argument (|u| >= 1, including ErfF32's |u| > 4 sign branch, and NaN), whose value the

@@ -388,11 +388,20 @@ __global__ __launch_bounds__(64 * NW, BM == PT_BM_SMALL ? 3 : NW / 2) void gemm_
                         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                         __builtin_amdgcn_wave_barrier();
                         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                        // two list rounds at a time, branch-free, so their dependent
+                        // chains interleave (a chunk of a wide distribution has several)
                         const int n = min(total, TL_CAP);
-                        for (int base = 0; base < n; base += 64) {
-                            if (base + lane < n) {
-                                int *cell = &scr[*slot(base + lane)];
-                                *cell = __float_as_int(gelu_f32(__int_as_float(*cell)));
+                        for (int base = 0; base < n; base += 128) {
+                            const int e0 = base + lane, e1 = base + 64 + lane;
+                            const int i0 = *slot(min(e0, n - 1));
+                            if (base + 64 < n) {
+                                const int i1 = *slot(min(e1, n - 1));
+                                const float g0 = gelu_f32_offseries(__int_as_float(scr[i0]));
+                                const float g1 = gelu_f32_offseries(__int_as_float(scr[i1]));
+                                if (e0 < n) scr[i0] = __float_as_int(g0);
+                                if (e1 < n) scr[i1] = __float_as_int(g1);
+                            } else if (e0 < n) {
+                                scr[i0] = __float_as_int(gelu_f32_offseries(__int_as_float(scr[i0])));
                             }
                         }
                         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

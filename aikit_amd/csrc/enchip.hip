@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -21,6 +22,7 @@
 #include "encoder_ops.h"
 #include "gemm_f32.h"
 #include "gemm_persistent.h"
+#include "gemm_q8w.h"
 #include "gemm_skinny.h"
 #include "topk.h"
 #include "kernels.h"
@@ -38,6 +40,7 @@ struct Weight {
     int8_t *d_w = nullptr;  // fragment-major, [Np/32][Kp/32][1024]
     float *d_s = nullptr;   // [N]
     int64_t N = 0, K = 0, Np = 0, Kp = 0;
+    bool inf_scale = false;  // some scale is +-inf: enchip_matmul_bt_q8 declines (see there)
 };
 
 thread_local std::string g_open_error = "no error";
@@ -952,6 +955,7 @@ int upload_weight(enchip_ctx *ctx, Weight w, const int8_t *image, const float *w
     int rc;
     size_t wcap = 0, scap = 0;
     const size_t bytes = (size_t)(w.Np * w.Kp);
+    for (int64_t n = 0; n < w.N; ++n) w.inf_scale |= std::isinf(wscale[n]);
     if ((rc = ensure(ctx, &w.d_w, &wcap, bytes, false))) return rc;
     if ((rc = ensure(ctx, &w.d_s, &scap, (size_t)w.N * sizeof(float), false))) {
         (void)hipFree(w.d_w);
@@ -1391,6 +1395,104 @@ int enchip_matmul_bt_f32_dev(enchip_ctx *ctx, const float *d_a, int64_t lda, con
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     return launch_matmul_f32(ctx, d_a, lda, d_b, ldb, bkn, d_c, ldc, M, K, N, b1, b2, s);
+}
+
+// ---------------------------------------------------------------------------- weight-only int8 MatmulBTQ8
+
+namespace {
+
+// Enqueues C = A . (f32(q) * wscale)^T for a registered weight (gemm_q8w.h), after the
+// caller checked the arguments. K = 0 gives zeros (an empty sum, whatever the scales).
+int launch_matmul_q8w(enchip_ctx *c, const Weight &w, const float *A, int64_t lda, float *C, int64_t ldc,
+                      int64_t M, hipStream_t s) {
+    using namespace enchip;
+    if (M == 0) return ENCHIP_OK;
+    if (w.K == 0) {
+        const int64_t rchunk = std::max<int64_t>(1, ((int64_t)1 << 30) / w.N);
+        for (int64_t r0 = 0; r0 < M; r0 += rchunk) {
+            const int64_t n = std::min(rchunk, M - r0);
+            hipLaunchKernelGGL(fill_zero_f32, dim3((unsigned)((n * w.N + 255) / 256)), dim3(256), 0, s, C + r0 * ldc,
+                               ldc, (int64_t)0, (int64_t)0, (int)n, (int)w.N);
+        }
+        return check_launch(c, "fill_zero_f32");
+    }
+    const bool vec = w.K % 4 == 0 && lda % 4 == 0 && (uintptr_t)A % 16 == 0;
+    // 128 x 128 tiles when they give every CU two workgroups, else 64 x 64
+    const bool wide = ((M + 127) / 128) * ((w.N + 127) / 128) >= 2 * (int64_t)c->num_cus;
+    const int bm = wide ? 128 : 64, bn = bm;
+    const int tilesN = (int)((w.N + bn - 1) / bn);
+    // every wavefront reads whole 32-channel blocks of the image up to tilesN * bn
+    if ((int64_t)tilesN * bn > w.Np) return fail(c, ENCHIP_ERR_ARG, "gemm_q8w: %d tiles exceed the image", tilesN);
+    // rows per launch: at most 2^30 / tilesN tiles of rows, so the tile index stays an int
+    const int64_t rows = std::max<int64_t>(bm, (((int64_t)1 << 30) / tilesN) / bm * bm);
+    for (int64_t r0 = 0; r0 < M; r0 += rows) {
+        const int64_t n = std::min(rows, M - r0);
+        const dim3 grid((unsigned)(((n + bm - 1) / bm) * tilesN)), block(256);
+        const float *a = A + r0 * lda;
+        float *cz = C + r0 * ldc;
+#define Q8W_CALL(TM, TN, VEC)                                                                                   \
+    hipLaunchKernelGGL((gemm_q8w<TM, TN, VEC>), grid, block, 0, s, a, lda, w.d_w, w.d_s, cz, ldc, (int)n,       \
+                       (int)w.N, (int)w.K, (int)w.Kp, tilesN)
+        if (wide && vec) Q8W_CALL(2, 2, true);
+        else if (wide) Q8W_CALL(2, 2, false);
+        else if (vec) Q8W_CALL(1, 1, true);
+        else Q8W_CALL(1, 1, false);
+#undef Q8W_CALL
+    }
+    return check_launch(c, "gemm_q8w");
+}
+
+// The shared argument checks of the two entry points.
+int check_q8w(enchip_ctx *c, const char *what, const Weight &w, int64_t M) {
+    if (M < 0 || M > kMaxDimF32 || M * w.N > ((int64_t)1 << 36))
+        return fail(c, ENCHIP_ERR_ARG, "%s: bad M=%lld for N=%lld", what, (long long)M, (long long)w.N);
+    // The sum is scaled once at the end (inf * sum), where the CPU path scales each weight
+    // first (f32(q) * inf, NaN for a zero code): the two differ, so such a weight declines.
+    if (w.inf_scale)
+        return fail(c, ENCHIP_ERR_ARG, "%s: the weight has an infinite scale (the CPU path handles it)", what);
+    return ENCHIP_OK;
+}
+
+}  // namespace
+
+int enchip_matmul_bt_q8(enchip_ctx *ctx, enchip_weight h, const float *a, int64_t M, float *dst) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    Weight *w;
+    int rc = find_weight(ctx, h, &w);
+    if (rc) return rc;
+    if ((rc = check_q8w(ctx, "matmul_bt_q8", *w, M))) return rc;
+    if (M == 0) return ENCHIP_OK;
+    if (!dst || (w->K > 0 && !a)) return fail(ctx, ENCHIP_ERR_ARG, "matmul_bt_q8: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    const size_t in_bytes = (size_t)(M * w->K) * sizeof(float), out_bytes = (size_t)(M * w->N) * sizeof(float);
+    if ((rc = ensure(ctx, &ctx->d_a, &ctx->a_cap, std::max<size_t>(in_bytes, 16)))) return rc;
+    if ((rc = ensure(ctx, &ctx->d_dst, &ctx->dst_cap, out_bytes))) return rc;
+    hipStream_t s = ctx->stream;
+    // the activations are uploaded on every call (gpu/enccuda/backend.go:271-275)
+    if (in_bytes) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, in_bytes, hipMemcpyHostToDevice, s));
+    if ((rc = launch_matmul_q8w(ctx, *w, ctx->d_a, w->K, ctx->d_dst, w->N, M, s))) return rc;
+    HIP_TRY(ctx, hipMemcpyAsync(dst, ctx->d_dst, out_bytes, hipMemcpyDeviceToHost, s));
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    return ENCHIP_OK;
+}
+
+int enchip_matmul_bt_q8_dev(enchip_ctx *ctx, enchip_weight h, const float *d_a, int64_t lda, int64_t M,
+                            float *d_dst, int64_t ldd, void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    Weight *w;
+    int rc = find_weight(ctx, h, &w);
+    if (rc) return rc;
+    if ((rc = check_q8w(ctx, "matmul_bt_q8_dev", *w, M))) return rc;
+    if (M == 0) return ENCHIP_OK;
+    if (lda < w->K || ldd < w->N)
+        return fail(ctx, ENCHIP_ERR_ARG, "matmul_bt_q8_dev: pitches lda=%lld ldd=%lld must cover a row (K=%lld, N=%lld)",
+                    (long long)lda, (long long)ldd, (long long)w->K, (long long)w->N);
+    if (!d_dst || (w->K > 0 && !d_a)) return fail(ctx, ENCHIP_ERR_ARG, "matmul_bt_q8_dev: null pointer");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    return launch_matmul_q8w(ctx, *w, d_a, lda, d_dst, ldd, M, s);
 }
 
 // ---------------------------------------------------------------------------- encoder row ops

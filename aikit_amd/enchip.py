@@ -26,7 +26,7 @@ ACT_NONE, ACT_GELU, ACT_TANH = 0, 1, 2
 ATT_F32, ATT_SPLIT_BF16, ATT_FLASH_BF16, ATT_FLASH_F16 = 0, 1, 2, 3  # enchip_att_products
 ATT_DEFAULT = ATT_FLASH_F16  # the library's default
 B_NK, B_KN = 0, 1  # enchip_matmul_bt_f32_dev b layouts: b[N,K] rows, b[K,N] rows
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # Every symbol include/enchip.h declares, with (restype, argtypes).
 _vp, _i64, _int = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
@@ -74,6 +74,8 @@ _SIGNATURES = {
     "enchip_set_small_m": (_int, [_vp, _i64]),
     "enchip_set_scratch_limit": (_int, [_vp, _i64]),
     "enchip_w8a8_linear_noalloc_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _vp, _int, _vp, _vp]),
+    "enchip_matmul_bt_q8": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _vp]),
+    "enchip_matmul_bt_q8_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _i64, _vp, _i64, _vp]),
 }
 SYMBOLS = tuple(_SIGNATURES)
 
@@ -351,6 +353,22 @@ class Context:
         lv = [None if t is None else ctypes.byref(F32Batch(*t)) for t in (inner, outer)]
         self._check(self._lib.enchip_matmul_bt_f32_dev(self._h, d_a or None, lda, d_b or None, ldb, b_layout,
                                                        d_c or None, ldc, M, K, N, lv[0], lv[1], stream or None))
+
+    def matmul_bt_q8(self, w: Weight, a: np.ndarray) -> np.ndarray:
+        """encoder.Q8Backend.MatmulBTQ8 (encoder/backend_use.go:59-83): f32 a[M,K] times the
+        registered weight w widened, a . (f32(wq) * wscale)^T; the activations stay f32."""
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        M = a.shape[0] if a.ndim == 2 else -1
+        if a.shape != (M, w.K):
+            raise ValueError(f"matmul_bt_q8: a shape {a.shape} != (M, {w.K})")
+        dst = np.empty((M, w.N), np.float32)
+        self._check(self._lib.enchip_matmul_bt_q8(self._h, w.handle, _ptr(a), M, _ptr(dst)))
+        return dst
+
+    def matmul_bt_q8_dev(self, w: Weight, d_a: int, lda: int, M: int, d_dst: int, ldd: int,
+                         stream: int = 0) -> None:
+        self._check(self._lib.enchip_matmul_bt_q8_dev(self._h, w.handle, d_a or None, lda, M, d_dst or None, ldd,
+                                                      stream or None))
 
     def softmax_rows_scaled_dev(self, d_x: int, ld: int, rows: int, cols: int, scale: float, stream: int = 0) -> None:
         self._check(self._lib.enchip_softmax_rows_scaled_dev(self._h, d_x or None, ld, rows, cols, scale,

@@ -42,7 +42,7 @@ const (
 	statusOK  = 0
 	actNone   = 0
 	actGELU   = 1
-	abiVersion = 2
+	abiVersion = 3
 )
 
 var (
@@ -58,6 +58,7 @@ var (
 	cLinear         func(ctx uintptr, w uint64, a unsafe.Pointer, m int64, bias unsafe.Pointer,
 		act int32, dst unsafe.Pointer, accDebug unsafe.Pointer) int32
 	cMatmulBTF32    func(ctx uintptr, a, b, dst unsafe.Pointer, m, k, n int64) int32
+	cMatmulBTQ8     func(ctx uintptr, w uint64, a unsafe.Pointer, m int64, dst unsafe.Pointer) int32
 	cAnnTopK        func(ctx uintptr, w uint64, q unsafe.Pointer, m, k int64, idx, score unsafe.Pointer) int32
 )
 
@@ -87,6 +88,7 @@ func load() error {
 		purego.RegisterLibFunc(&cWeightRelease, h, "enchip_weight_release")
 		purego.RegisterLibFunc(&cLinear, h, "enchip_w8a8_linear")
 		purego.RegisterLibFunc(&cMatmulBTF32, h, "enchip_matmul_bt_f32")
+		purego.RegisterLibFunc(&cMatmulBTQ8, h, "enchip_matmul_bt_q8")
 		purego.RegisterLibFunc(&cAnnTopK, h, "enchip_ann_topk")
 		if v := cAbiVersion(); v != abiVersion {
 			loadErr = fmt.Errorf("enchip: libenchip ABI %d, binding wants %d", v, abiVersion)
@@ -156,11 +158,27 @@ func (b *Backend) MatmulBT(a, w, dst []float32, M, K, N int) {
 	}
 }
 
-// MatmulBTQ8 implements encoder.Q8Backend by declining. That contract is
-// weight-only (encoder/backend_use.go:59-83), and this engine quantizes
-// activations; see MatmulBTW8A8.
+// MatmulBTQ8 implements encoder.Q8Backend, the weight-only int8 seam
+// (encoder/backend_use.go:59-83): dst = a · (f32(wq)·wscales)ᵀ with the activations
+// left in f32 (enchip_matmul_bt_q8 never quantizes them). The weight is resident per
+// (ptr, len), the same registration MatmulBTW8A8 uses, and stays int8 on the device;
+// a is uploaded on every call. Small shapes (enccuda's threshold,
+// gpu/enccuda/backend.go:248-250) and any failure return false, and the caller runs
+// matmulBTQ8Into on the CPU unchanged.
 func (b *Backend) MatmulBTQ8(dst, a []float32, wq []int8, wscales []float32, M, K, N int) bool {
-	return false
+	if 2*int64(M)*int64(K)*int64(N) < minGPUFlops || M <= 0 || K <= 0 || N <= 0 {
+		return false
+	}
+	if len(a) < M*K || len(wq) < N*K || len(wscales) < N || len(dst) < M*N {
+		return false
+	}
+	b.mu.Lock()
+	defer b.mu.Unlock()
+	h, err := b.resident(wq[:N*K], wscales[:N], N, K)
+	if err != nil {
+		return false
+	}
+	return cMatmulBTQ8(b.ctx, h, unsafe.Pointer(&a[0]), int64(M), unsafe.Pointer(&dst[0])) == statusOK
 }
 
 // MatmulBTW8A8 implements encoder.W8A8Backend:

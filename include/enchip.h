@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define ENCHIP_ABI_VERSION 2
+#define ENCHIP_ABI_VERSION 3
 
 typedef struct enchip_ctx enchip_ctx;
 typedef uint64_t enchip_weight; /* opaque handle; 0 is never a valid handle */
@@ -146,7 +146,7 @@ int enchip_weight_shape(enchip_ctx *ctx, enchip_weight w, int64_t *N, int64_t *K
  * int32 accumulators [M,N] are also written to it (parity testing).
  * This is the body of the new opt-in W8A8Backend.MatmulBTW8A8 capability; the
  * weight-only Q8Backend.MatmulBTQ8 contract (encoder/backend_use.go:59-83) is NOT
- * served by it. */
+ * served by it (enchip_matmul_bt_q8 serves that one). */
 int enchip_w8a8_linear(enchip_ctx *ctx, enchip_weight w, const float *a, int64_t M,
                        const float *bias, int act, float *dst, int32_t *acc_debug);
 
@@ -302,6 +302,33 @@ int enchip_matmul_bt_f32_dev(enchip_ctx *ctx, const float *d_a, int64_t lda, con
                              int64_t ldb, int b_layout, float *d_c, int64_t ldc, int64_t M,
                              int64_t K, int64_t N, const enchip_f32_batch *inner,
                              const enchip_f32_batch *outer, void *stream);
+
+/* Weight-only int8 product with f32 activations on host buffers:
+ *   dst[m][n] = sum_k a[m][k] * (f32(wq[n][k]) * wscale[n]),
+ * the device side of encoder.Q8Backend.MatmulBTQ8 (encoder/backend_use.go:59-83; enccuda's
+ * MatmulBTQ8, gpu/enccuda/backend.go:246-287, and the CPU path it stands in for,
+ * encoder/scratch.go:211-218 -> matmulBTQ8Into, encoder/linalg_q8.go:80-84). w is a weight
+ * registered by enchip_weight_register (or _register_image): the same int8 codes and scales
+ * the W8A8 entry points use, resident on the device in int8, never widened in memory.
+ * a[M,K] and dst[M,N] are row-major host buffers; a is uploaded on every call, dst
+ * downloaded before returning. The activations are NEVER quantized: each is split
+ * exactly into three bf16 parts and every product with a weight code is exact on the bf16
+ * MFMA, summed in f32 in an order of its own, and the sum is multiplied by wscale[n] once.
+ * The contract is the reference's gate against a float64 dot product, worst
+ * |dst - ref| / max(|ref|, 1) <= 2e-4 (gpu/enccuda/backend_test.go:234-289). K == 0 gives
+ * zeros. A weight with an infinite scale is refused (ENCHIP_ERR_ARG): the CPU path
+ * scales each code before the sum and gets NaN where a code is 0, which a scale applied
+ * to the sum cannot reproduce. Which shapes are worth the round trip is the caller's
+ * choice (enccuda's minGPUFlops): this entry point always runs on the device.
+ * M <= 2^30, M*N <= 2^36. */
+int enchip_matmul_bt_q8(enchip_ctx *ctx, enchip_weight w, const float *a, int64_t M,
+                        float *dst);
+
+/* Device form of enchip_matmul_bt_q8: d_a[M,K] with row pitch lda >= K and d_dst[M,N]
+ * with row pitch ldd >= N, in floats, on device buffers, enqueued on `stream` (NULL: the
+ * context stream). Same arithmetic and contract; allocates nothing. */
+int enchip_matmul_bt_q8_dev(enchip_ctx *ctx, enchip_weight w, const float *d_a, int64_t lda,
+                            int64_t M, float *d_dst, int64_t ldd, void *stream);
 
 /* The f32 row operations between a BERT layer's linears, in place on device buffers,
  * enqueued on `stream` (NULL: the context stream). Each restates the reference operation

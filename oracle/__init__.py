@@ -63,6 +63,9 @@ def lib() -> ctypes.CDLL:
             "orc_attention": (None, [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64]),
             "orc_matmul_bt_f64": (None, [_f32p, _f32p, _i64, _i64, _i64,
                                          np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")]),
+            "orc_dequant_rows_i8": (None, [_i8p, _f32p, _i64, _i64, _f32p]),
+            "orc_matmul_bt_q8_f64": (None, [_f32p, _i8p, _f32p, _i64, _i64, _i64,
+                                            np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")]),
             "orc_pool_mean": (None, [_f32p, _i64, _i64, _f32p]),
             "orc_l2_normalize": (None, [_f32p, _i64]),
             "cpub_dot_i8": (ctypes.c_int32, [_i8p, _i8p, _i64]),
@@ -218,6 +221,21 @@ def matmul_bt_f64(a, b, M: int, K: int, N: int):
     """refMatmulBT (gpu/enccuda/backend_test.go:32-44): float64 a[M,K] . b[N,K]^T."""
     dst = np.empty(max(M * N, 1), np.float64)
     lib().orc_matmul_bt_f64(_c(a, np.float32).reshape(-1), _c(b, np.float32).reshape(-1), M, K, N, dst)
+    return dst[: M * N].reshape(M, N)
+
+
+def dequant_rows_i8(q, scales, rows: int, cols: int):
+    """DequantizeRowsInt8Into (linalg/dequant_i8.go:20-43): float32(q) * scale per row."""
+    dst = np.empty(max(rows * cols, 1), np.float32)
+    lib().orc_dequant_rows_i8(_c(q, np.int8).reshape(-1), _c(scales, np.float32).reshape(-1), rows, cols, dst)
+    return dst[: rows * cols].reshape(rows, cols)
+
+
+def matmul_bt_q8_f64(a, q, scales, M: int, K: int, N: int):
+    """cpuQ8Ref (gpu/enccuda/backend_test.go:208-224): float64 a[M,K] . (q[N,K] * scales[N])^T."""
+    dst = np.empty(max(M * N, 1), np.float64)
+    lib().orc_matmul_bt_q8_f64(_c(a, np.float32).reshape(-1), _c(q, np.int8).reshape(-1),
+                               _c(scales, np.float32).reshape(-1), M, K, N, dst)
     return dst[: M * N].reshape(M, N)
 
 

@@ -319,6 +319,30 @@ void orc_matmul_bt_f64(const float *a, const float *b, int64_t M, int64_t K, int
         }
 }
 
+/* linalg/dequant_i8.go:20-43 DequantizeRowsInt8Into (scalar form dequantRowInt8Scalar,
+ * :38-43): dst[r*cols + k] = float32(q[r*cols + k]) * scales[r], one f32 multiply of an
+ * exact integer. The weight the CPU's weight-only path widens before its f32 MatmulBT
+ * (encoder/linalg_q8.go:80-84). */
+void orc_dequant_rows_i8(const int8_t *q, const float *scales, int64_t rows, int64_t cols, float *dst) {
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t k = 0; k < cols; k++) dst[r * cols + k] = (float)q[r * cols + k] * scales[r];
+}
+
+/* gpu/enccuda/backend_test.go:208-224 cpuQ8Ref: the float64 ground truth of the
+ * weight-only product, dst[m][n] = sum_k (double)a[m][k] * ((double)q[n][k] * (double)
+ * scales[n]), accumulated in k order. The gate of enccuda's MatmulBTQ8 is <= 2e-4 of
+ * max(|ref|, 1) against it (backend_test.go:243-289). */
+void orc_matmul_bt_q8_f64(const float *a, const int8_t *q, const float *scales, int64_t M, int64_t K, int64_t N,
+                          double *dst) {
+    for (int64_t m = 0; m < M; m++)
+        for (int64_t n = 0; n < N; n++) {
+            const double sc = (double)scales[n];
+            double acc = 0;
+            for (int64_t k = 0; k < K; k++) acc += (double)a[m * K + k] * ((double)q[n * K + k] * sc);
+            dst[m * N + n] = acc;
+        }
+}
+
 /* encoder/pooling.go:84-105 poolOne(mean). */
 void orc_pool_mean(const float *seq, int64_t L, int64_t D, float *out) {
     if (L == 0) {

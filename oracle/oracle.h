@@ -93,6 +93,9 @@ void orc_attention(const float *Q, const float *K, const float *V, float *ctx,
                    int64_t L, int64_t D, int64_t heads);
 
 /* encoder/pooling.go:84-105 poolOne(mean): f64 accumulation over L rows. */
+void orc_dequant_rows_i8(const int8_t *q, const float *scales, int64_t rows, int64_t cols, float *dst);
+void orc_matmul_bt_q8_f64(const float *a, const int8_t *q, const float *scales, int64_t M, int64_t K, int64_t N,
+                          double *dst);
 void orc_pool_mean(const float *seq, int64_t L, int64_t D, float *out);
 
 /* embed/pool.go:22-38 L2Normalize (f64 norm, eps 1e-12), in place. */

@@ -326,6 +326,44 @@ def test_matmul_bt_f64_brute_force_and_integers():
     assert oracle.matmul_bt_f64(a[:, :0], b[:, :0], 3, 0, 4).tolist() == [[0.0] * 4] * 3
 
 
+def test_dequant_rows_i8_reference_vectors():
+    # linalg/dequant_i8_test.go:46-75 (TestDequantizeRowsInt8_extremes): -128, -1, 0, 127
+    # at scale 0.5 widen to exactly -64, -0.5, 0, 63.5 (a sign-extension or zero-extension
+    # slip fails it).
+    q = np.tile(np.array([-128, -1, 0, 127], np.int8), 16)
+    got = oracle.dequant_rows_i8(q, np.array([0.5], np.float32), 1, 64)
+    assert got.reshape(-1).tolist() == [-64.0, -0.5, 0.0, 63.5] * 16
+    # dequant_i8_test.go:17-44: every column count it straddles, rows 1 and 3, full int8
+    # range, against numpy's float32 multiply (one IEEE single rounding), bit for bit.
+    g = np.random.default_rng(17)
+    for cols in (1, 7, 8, 9, 31, 32, 33, 63, 64, 65, 96, 127, 128, 768, 3072):
+        for rows in (1, 3):
+            qq = g.integers(-128, 128, size=(rows, cols)).astype(np.int8)
+            sc = (g.standard_normal(rows) * 0.01).astype(np.float32)
+            want = qq.astype(np.float32) * sc[:, None]
+            assert np.array_equal(oracle.dequant_rows_i8(qq, sc, rows, cols).view(np.uint32), want.view(np.uint32))
+
+
+def test_matmul_bt_q8_f64_against_numpy_and_integers():
+    # cpuQ8Ref (gpu/enccuda/backend_test.go:208-224): exactly the integer result where
+    # every product and partial sum is an integer below 2^53 (a transposed weight, a
+    # scale applied per row of a instead of per channel, or a dropped term fails), and
+    # within float64 reassociation of numpy's product of the widened weight otherwise.
+    g = np.random.default_rng(43)
+    M, K, N = 5, 301, 7
+    ai = g.integers(-1000, 1001, size=(M, K))
+    qi = g.integers(-128, 128, size=(N, K))
+    si = g.integers(1, 9, size=N)
+    got = oracle.matmul_bt_q8_f64(ai.astype(np.float32), qi.astype(np.int8), si.astype(np.float32), M, K, N)
+    assert np.array_equal(got, (ai @ (qi * si[:, None]).T).astype(np.float64))
+    a = g.standard_normal((M, K)).astype(np.float32)
+    s = (0.002 + (np.arange(N) % 13) * 0.0001).astype(np.float32)
+    want = a.astype(np.float64) @ (qi.astype(np.float64) * s.astype(np.float64)[:, None]).T
+    got = oracle.matmul_bt_q8_f64(a, qi.astype(np.int8), s, M, K, N)
+    assert np.allclose(got, want, rtol=1e-13, atol=1e-13)
+    assert oracle.matmul_bt_q8_f64(a[:, :0], qi[:, :0].astype(np.int8), s, M, 0, N).tolist() == [[0.0] * N] * M
+
+
 def test_matmul_bt_worst_rel_statistic():
     # backend_test.go:71-80: relative to |ref|, with |ref| < 1 measured absolutely.
     ref = np.array([[1000.0, 0.5, -2.0]])

@@ -1417,9 +1417,18 @@ int launch_matmul_q8w(enchip_ctx *c, const Weight &w, const float *A, int64_t ld
         return check_launch(c, "fill_zero_f32");
     }
     const bool vec = w.K % 4 == 0 && lda % 4 == 0 && (uintptr_t)A % 16 == 0;
-    // 128 x 128 tiles when they give every CU two workgroups, else 64 x 64
-    const bool wide = ((M + 127) / 128) * ((w.N + 127) / 128) >= 2 * (int64_t)c->num_cus;
-    const int bm = wide ? 128 : 64, bn = bm;
+    // 128 x 256 tiles when they give every CU two workgroups, else 128 x 128 when those
+    // do, else 64 x 64 when those give every CU one; below that the K-split small form
+    // (32 x 64 tiles, or 32 x 32 when 32 x 64 would leave CUs idle). Measured on MI355X:
+    // M = 512, K = 768, N = 2304 takes 24 us as 288 64 x 64 tiles against 31 in the small
+    // form, which re-splits A for each column tile; M = 128, K = 768, N = 768, 24 such
+    // tiles, takes 18 us against 9.
+    const int64_t cus = c->num_cus, cus2 = 2 * cus;
+    auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((w.N + bn - 1) / bn); };
+    const int form = tiles(128, 256) >= cus2 ? 2 : tiles(128, 128) >= cus2 ? 1 : tiles(64, 64) >= cus ? 0
+                     : tiles(32, 64) >= cus ? -2 : -1;
+    const bool wide = form > 0;
+    const int bm = form < 0 ? 32 : wide ? 128 : 64, bn = form == 2 ? 256 : form == -2 ? 64 : form == -1 ? 32 : bm;
     const int tilesN = (int)((w.N + bn - 1) / bn);
     // every wavefront reads whole 32-channel blocks of the image up to tilesN * bn
     if ((int64_t)tilesN * bn > w.Np) return fail(c, ENCHIP_ERR_ARG, "gemm_q8w: %d tiles exceed the image", tilesN);
@@ -1433,11 +1442,21 @@ int launch_matmul_q8w(enchip_ctx *c, const Weight &w, const float *A, int64_t ld
 #define Q8W_CALL(TM, TN, VEC)                                                                                   \
     hipLaunchKernelGGL((gemm_q8w<TM, TN, VEC>), grid, block, 0, s, a, lda, w.d_w, w.d_s, cz, ldc, (int)n,       \
                        (int)w.N, (int)w.K, (int)w.Kp, tilesN)
-        if (wide && vec) Q8W_CALL(2, 2, true);
+#define Q8W_SMALL(TN, VEC)                                                                                      \
+    hipLaunchKernelGGL((gemm_q8w_small<TN, VEC>), grid, block, 0, s, a, lda, w.d_w, w.d_s, cz, ldc, (int)n,     \
+                       (int)w.N, (int)w.K, (int)w.Kp, tilesN)
+        if (form == -2 && vec) Q8W_SMALL(2, true);
+        else if (form == -2) Q8W_SMALL(2, false);
+        else if (form == -1 && vec) Q8W_SMALL(1, true);
+        else if (form == -1) Q8W_SMALL(1, false);
+        else if (form == 2 && vec) Q8W_CALL(2, 4, true);
+        else if (form == 2) Q8W_CALL(2, 4, false);
+        else if (wide && vec) Q8W_CALL(2, 2, true);
         else if (wide) Q8W_CALL(2, 2, false);
         else if (vec) Q8W_CALL(1, 1, true);
         else Q8W_CALL(1, 1, false);
 #undef Q8W_CALL
+#undef Q8W_SMALL
     }
     return check_launch(c, "gemm_q8w");
 }

@@ -225,4 +225,133 @@ __global__ __launch_bounds__(256, 2) void gemm_q8w(const float *__restrict__ A, 
     }
 }
 
+// Small-M form: one workgroup per 32-row x (32 TN)-channel tile, its 4 wavefronts
+// splitting K (wavefront w takes the 32-deep chunks w, w + 4, w + 8, ...). Each lane loads
+// its own MFMA operand values straight from HBM -- lane (row m, half h) the 16 activations
+// a[m, 32 kc + 16 h ..], split in registers, and its 16 weight bytes -- so there is no LDS
+// and no barrier in the main loop, and a ring of Q8W_RING chunks per wavefront keeps that
+// many loads in flight. The four partial sums meet in LDS and are added in a fixed order
+// (wavefront 0 + 1 + 2 + 3), so the result does not depend on timing. Same arithmetic,
+// edges and preconditions as gemm_q8w.
+constexpr int Q8W_RING = 4;
+
+template <int TN, bool VEC>
+__global__ __launch_bounds__(256) void gemm_q8w_small(const float *__restrict__ A, int64_t lda,
+                                                      const int8_t *__restrict__ W, const float *__restrict__ ws,
+                                                      float *__restrict__ C, int64_t ldc, int M, int N, int K, int Kp,
+                                                      int tilesN) {
+    __shared__ float red[4][TN][16][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
+    const int logical = xcd_logical_tile(blockIdx.x, gridDim.x);
+    const int m0 = (logical / tilesN) * 32, n0 = (logical % tilesN) * (32 * TN);
+    const int nk = Kp / 32;
+    const float *arow = A + (int64_t)min(m0 + (lane & 31), M - 1) * lda + 16 * h;
+    const int8_t *wb[TN];
+#pragma unroll
+    for (int t = 0; t < TN; ++t) wb[t] = W + ((int64_t)((n0 >> 5) + t) * nk) * 1024 + lane * 16;
+
+    float av[Q8W_RING][16];
+    u32x4 wr[Q8W_RING][TN];
+    // chunk kc into ring slot d (kc < nk, uniform per wavefront)
+    auto load = [&](int d, int kc) {
+        const int k0 = 32 * kc + 16 * h;
+        if (32 * kc + 32 <= K) {
+            if (VEC) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const f32x4 x = *reinterpret_cast<const f32x4 *>(arow + 32 * kc + 4 * i);
+                    av[d][4 * i] = x.x;
+                    av[d][4 * i + 1] = x.y;
+                    av[d][4 * i + 2] = x.z;
+                    av[d][4 * i + 3] = x.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) av[d][i] = arow[32 * kc + i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float x = arow[min(32 * kc + i, K - 1 - 16 * h)];
+                av[d][i] = k0 + i < K ? x : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TN; ++t) wr[d][t] = *reinterpret_cast<const u32x4 *>(wb[t] + (int64_t)kc * 1024);
+    };
+
+    f32x16 acc[TN];
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[t][e] = 0.0f;
+
+#pragma unroll
+    for (int d = 0; d < Q8W_RING; ++d)
+        if (wave + 4 * d < nk) load(d, wave + 4 * d);
+    for (int kb = wave; kb < nk; kb += 4 * Q8W_RING) {
+#pragma unroll
+        for (int d = 0; d < Q8W_RING; ++d) {
+            const int kc = kb + 4 * d;
+            if (kc >= nk) break;  // uniform per wavefront
+            // this chunk's operands out of the slot, then the slot's next chunk in flight
+            bf16x8 ap[3][2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                uint32_t t1[8], t2[8], t3[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) q8w_split3(av[d][8 * j + e], t1[e], t2[e], t3[e]);
+                ap[0][j] = __builtin_bit_cast(bf16x8, (u32x4){q8w_pack(t1[0], t1[1]), q8w_pack(t1[2], t1[3]),
+                                                              q8w_pack(t1[4], t1[5]), q8w_pack(t1[6], t1[7])});
+                ap[1][j] = __builtin_bit_cast(bf16x8, (u32x4){q8w_pack(t2[0], t2[1]), q8w_pack(t2[2], t2[3]),
+                                                              q8w_pack(t2[4], t2[5]), q8w_pack(t2[6], t2[7])});
+                ap[2][j] = __builtin_bit_cast(bf16x8, (u32x4){q8w_pack(t3[0], t3[1]), q8w_pack(t3[2], t3[3]),
+                                                              q8w_pack(t3[4], t3[5]), q8w_pack(t3[6], t3[7])});
+            }
+            bf16x8 wq[TN][2];
+#pragma unroll
+            for (int t = 0; t < TN; ++t) {
+                const uint32_t dw[4] = {wr[d][t].x, wr[d][t].y, wr[d][t].z, wr[d][t].w};
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    uint32_t x[4];
+                    q8w_widen4(dw[2 * j], x[0], x[1]);
+                    q8w_widen4(dw[2 * j + 1], x[2], x[3]);
+                    wq[t][j] = __builtin_bit_cast(bf16x8, (u32x4){x[0], x[1], x[2], x[3]});
+                }
+            }
+            if (kc + 4 * Q8W_RING < nk) load(d, kc + 4 * Q8W_RING);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int t = 0; t < TN; ++t) {
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[2][j], wq[t][j], acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[1][j], wq[t][j], acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[0][j], wq[t][j], acc[t], 0, 0, 0);
+                }
+        }
+    }
+
+    // ---- the four partial sums, added in wavefront order; wavefront w finishes the
+    // accumulator registers 4w .. 4w + 3 (rows acc_row(r, lane)) of every channel block
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[wave][t][r][lane] = acc[t][r];
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+        const int n = n0 + 32 * t + (lane & 31);
+        const float s = ws[min(n, N - 1)];
+        if (n >= N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 4 * wave + i;
+            const float v = ((red[0][t][r][lane] + red[1][t][r][lane]) + red[2][t][r][lane]) + red[3][t][r][lane];
+            const int m = m0 + acc_row(r, lane);
+            if (m < M) C[(int64_t)m * ldc + n] = v * s;
+        }
+    }
+}
+
 }  // namespace enchip

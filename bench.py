@@ -554,6 +554,70 @@ def other_configs(ctx, torch, stream, ceilings):
                         "output written once; softmax not included in qk/pv, included in the fused forms"})
     out["attention_f32_cfg4_layer"] = att
     del qkv, scores, ctxv
+
+    # encoder.Q8Backend.MatmulBTQ8, the weight-only int8 seam (f32 activations never
+    # quantized): a BERT-base layer's four linears at one 512-token sequence (the Go
+    # forward's per-sequence calls) on device buffers and through the host entry point
+    # (upload a, download dst), and at the config-4 batch of 32768 rows on the device;
+    # the f32 MatmulBT on the widened weight (how enccuda serves this seam) beside it.
+    g = np.random.default_rng(21)
+    q8 = {}
+    shapes = (("qkv", 768, 2304), ("o", 768, 768), ("ffn_up", 768, 3072), ("ffn_down", 3072, 768))
+    for M in (512, 32768):
+        tot_us = tot_host_us = tot_flop = 0.0
+        for name, K, N in shapes:
+            wq = g.integers(-127, 128, size=(N, K)).astype(np.int8)
+            ws = (0.002 + (np.arange(N) % 13) * 1e-4).astype(np.float32)
+            w = ctx.register_weight(wq, ws)
+            with torch.cuda.stream(stream):
+                da = torch.randn((M, K), device="cuda", generator=torch.Generator(device="cuda").manual_seed(M + K))
+                dd = torch.empty((M, N), device="cuda")
+            torch.cuda.synchronize()
+            for _ in range(3):
+                ctx.matmul_bt_q8_dev(w, da.data_ptr(), K, M, dd.data_ptr(), N, sp)
+            reps = 10
+            e0.record(stream)
+            for _ in range(reps):
+                ctx.matmul_bt_q8_dev(w, da.data_ptr(), K, M, dd.data_ptr(), N, sp)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            t = e0.elapsed_time(e1) * 1e-3 / reps
+            q8[f"m{M}_{name}_us"] = t * 1e6
+            tot_us += t * 1e6
+            tot_flop += 2.0 * M * N * K
+            if M == 512:
+                ah = da.cpu().numpy()
+                for _ in range(2):
+                    ctx.matmul_bt_q8(w, ah)
+                t0 = time.perf_counter()
+                for _ in range(reps):
+                    ctx.matmul_bt_q8(w, ah)
+                th = (time.perf_counter() - t0) / reps
+                q8[f"m{M}_{name}_host_us"] = th * 1e6
+                tot_host_us += th * 1e6
+            if M == 32768 and name == "ffn_up":
+                wf = torch.from_numpy(wq.astype(np.float32) * ws[:, None]).cuda()  # float32(q) * scale
+                for _ in range(2):
+                    ctx.matmul_bt_f32_dev(da.data_ptr(), K, wf.data_ptr(), K, B_NK, dd.data_ptr(), N, M, K, N, stream=sp)
+                e0.record(stream)
+                for _ in range(3):
+                    ctx.matmul_bt_f32_dev(da.data_ptr(), K, wf.data_ptr(), K, B_NK, dd.data_ptr(), N, M, K, N, stream=sp)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                q8["m32768_ffn_up_f32_matmul_bt_us"] = e0.elapsed_time(e1) * 1e3 / 3
+                del wf
+            ctx.release_weight(w)
+            del da, dd
+        q8[f"m{M}_layer_us"] = tot_us
+        q8[f"m{M}_tflops"] = tot_flop / (tot_us * 1e-6) / 1e12
+        q8[f"m{M}_frac_bf16_mfma_peak"] = 3 * tot_flop / (tot_us * 1e-6) / PEAK_BF16_FLOPS
+        if tot_host_us:
+            q8[f"m{M}_layer_host_us"] = tot_host_us
+    q8.update({"kernels": "enchip::gemm_q8w<TM, TN, VEC> (LDS-staged split, 64 x 64 to 128 x 256 tiles), "
+                          "enchip::gemm_q8w_small<TN, VEC> (K split over the workgroup's wavefronts)",
+               "note": "TFLOP/s = 2MNK / time; each f32 activation is split exactly into three bf16 parts, so the "
+                       "bf16 MFMA fraction counts 3 x 2MNK; host_us includes the upload of a and download of dst"})
+    out["matmul_bt_q8_weight_only"] = q8
     return out
 
 
@@ -1009,6 +1073,11 @@ def compact_result(result: dict, detail_path: str | None = None) -> dict:
         c = oc.get(f"ann_flat_i8_m{m}")
         if c:
             other[f"ann_m{m}_us"] = _r(c.get("us_per_call"))
+    q8 = oc.get("matmul_bt_q8_weight_only")
+    if q8:
+        for k in ("m512_layer_us", "m512_layer_host_us", "m32768_layer_us", "m32768_tflops"):
+            if q8.get(k) is not None:
+                other[f"q8w_{k}"] = _r(q8[k])
     if "linear_stack" in result:
         other["linear_stack_ms"] = _r(result["linear_stack"].get("ms_per_step"))
     for k in ("encode_f32_products", "encode_split_bf16_two_pass", "encode_flash_bf16"):

@@ -49,7 +49,7 @@ def worst(got, a, q, s):
 # backend_test.go:250-254, and the forward_q8 linears of linalg_q8_test.go:111-117
 REF_SHAPES = [(8, 32, 32), (128, 768, 768), (128, 768, 3072), (80, 768, 2304), (80, 3072, 768), (512, 768, 3072)]
 EDGE_SHAPES = [(1, 1, 1), (1, 768, 768), (31, 7, 33), (33, 31, 17), (65, 64, 300), (200, 100, 1), (513, 33, 257),
-               (64, 4096, 64), (3, 1000, 130)]
+               (64, 4096, 64), (3, 1000, 130), (256 + 17, 768, 3072 + 50), (256 + 17, 1001, 3072 + 50)]
 
 
 @pytest.mark.parametrize("M,K,N", REF_SHAPES + EDGE_SHAPES)
@@ -70,7 +70,8 @@ def test_matmul_bt_q8_gate(ctx, M, K, N):
         ctx.release_weight(w)
 
 
-@pytest.mark.parametrize("M,K,N", [(96, 64, 160), (33, 511, 70), (128, 1024, 64), (5, 6, 7), (300, 4096, 33)])
+@pytest.mark.parametrize("M,K,N", [(96, 64, 160), (33, 511, 70), (128, 1024, 64), (5, 6, 7), (300, 4096, 33),
+                                   (200, 1000, 3000), (200, 1001, 3000)])
 def test_matmul_bt_q8_exact_on_integers(ctx, M, K, N):
     # |a| <= 16, |q| <= 128, K <= 4096: every product and partial sum is an integer below
     # 2^24, exact in f32 in any order; power-of-two scales keep the final multiply exact.
@@ -88,7 +89,8 @@ def test_matmul_bt_q8_exact_on_integers(ctx, M, K, N):
         ctx.release_weight(w)
 
 
-@pytest.mark.parametrize("M,K,N", [(70, 100, 90), (513, 768, 300), (4096 + 37, 200, 2048 + 100)])
+@pytest.mark.parametrize("M,K,N", [(70, 100, 90), (513, 768, 300), (256 + 17, 300, 3072 + 50),
+                                   (4096 + 37, 200, 2048 + 100), (16384 + 37, 200, 2048 + 100)])
 def test_matmul_bt_q8_one_hot_selects_activations_exactly(ctx, M, K, N):
     # Channel n has one nonzero code, c_n in {1, -1, 2, -128}, at k = p_n, and a
     # power-of-two scale: dst[m, n] = a[m, p_n] * c_n * s_n exactly, for activations with
@@ -115,11 +117,13 @@ def test_matmul_bt_q8_one_hot_selects_activations_exactly(ctx, M, K, N):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-def test_matmul_bt_q8_wide_tiles_ragged(ctx):
-    # enough 128 x 128 tiles to take the wide form, M and N not multiples of the tile;
-    # checked exactly on integers over the whole output, and against the gate on the
-    # first and last rows (the float64 truth of every row would take the oracle minutes)
-    M, K, N = 4096 + 37, 768, 2048 + 100
+@pytest.mark.parametrize("M,N", [(4096 + 37, 2048 + 100), (16384 + 37, 2048 + 100)])
+def test_matmul_bt_q8_wide_tiles_ragged(ctx, M, N):
+    # enough 128 x 128 (then 128 x 256) tiles to take the wide forms, M and N not multiples
+    # of the tile; checked exactly on integers over the whole output, and against the gate
+    # on the first and last rows (the float64 truth of every row would take the oracle
+    # minutes)
+    K = 768
     g = workloads.rng(77)
     say(f"matmul_bt_q8 wide tiles M={M} K={K} N={N}")
     ai = g.integers(-16, 17, size=(M, K))

@@ -304,3 +304,107 @@ def test_host_and_device_calls_on_different_streams(ctx, workers):
         assert np.array_equal(bits(host), bits(want2))
     finally:
         ctx.release_weight(w)
+
+
+# ---- the weight-only seam, encoder.Q8Backend.MatmulBTQ8 (encoder/backend_use.go:59-83)
+
+MIN_GPU_FLOPS = 1 << 20  # gpu/enccuda/backend.go:75, the threshold the Go leaf keeps
+
+
+class EnchipQ8:
+    """The Go leaf's MatmulBTQ8 restated over the raw ABI (gpu/enchip/backend.go): small
+    shapes decline, weights are registered once per weight array (the leaf keys by
+    (ptr, len); here by the array object), activations are passed on every call, any
+    non-zero status is a decline."""
+
+    def __init__(self, ctx):
+        self.ctx, self.lib = ctx, enchip.load()
+        self.handles = {}
+
+    def __call__(self, dst, a, wq, ws, M, K, N):
+        if 2 * M * K * N < MIN_GPU_FLOPS or M <= 0 or K <= 0 or N <= 0:
+            return False
+        key = id(wq)
+        if key not in self.handles:
+            try:
+                self.handles[key] = self.ctx.register_weight(wq, ws)
+            except enchip.EnchipError:
+                return False
+        rc = self.lib.enchip_matmul_bt_q8(self.ctx.handle, self.handles[key].handle, a.ctypes.data, M,
+                                          dst.ctypes.data)
+        return rc == enchip.OK
+
+    def close(self):
+        for h in self.handles.values():
+            self.ctx.release_weight(h)
+        self.handles = {}
+
+
+def mmq8(backend, dst, a, wq, ws, M, K, N):
+    """encoder/scratch.go:211-218: the backend, or on decline matmulBTQ8Into's CPU path
+    (widen with DequantizeRowsInt8Into, then an f32 product; numpy's f32 product stands
+    in for matmulBTInto's loop order here)."""
+    if backend is not None and backend(dst, a, wq, ws, M, K, N):
+        return True
+    with np.errstate(invalid="ignore"):  # an infinite scale widens zero codes to NaN
+        dst[:] = a @ oracle.dequant_rows_i8(wq, ws, N, K).T
+    return False
+
+
+def test_q8_weight_residency_and_activations_never_cached(ctx):
+    # gpu/enccuda/backend_test.go:291-369 (TestEncCUDA_q8WeightResidency): one
+    # registration per distinct weight, a re-used weight hits, two weights give two
+    # results, and a new activation against the cached weight changes the result and
+    # meets the gate.
+    g = workloads.rng(12)
+    M, K, N = 128, 768, 768
+    a1 = g.standard_normal((M, K)).astype(np.float32)
+    a2 = g.standard_normal((M, K)).astype(np.float32)
+    w1 = g.integers(-127, 128, size=(N, K)).astype(np.int8)
+    w2 = g.integers(-127, 128, size=(N, K)).astype(np.int8)
+    ws = np.full(N, 0.003, np.float32)
+    be = EnchipQ8(ctx)
+    try:
+        d1, d2, d3, d4 = (np.empty((M, N), np.float32) for _ in range(4))
+        assert mmq8(be, d1, a1, w1, ws, M, K, N) and len(be.handles) == 1
+        assert mmq8(be, d2, a1, w2, ws, M, K, N) and len(be.handles) == 2
+        assert mmq8(be, d3, a1, w1, ws, M, K, N) and len(be.handles) == 2
+        assert np.array_equal(bits(d1), bits(d3))
+        assert not np.array_equal(d1, d2)
+        assert mmq8(be, d4, a2, w1, ws, M, K, N)
+        assert not np.array_equal(d1, d4), "a new activation gave the cached result"
+        worst = oracle.matmul_bt_worst_rel(d4, oracle.matmul_bt_q8_f64(a2, w1, ws, M, K, N))
+        say(f"  new activation against the cached weight: worst {worst:.3g}")
+        assert worst <= 2e-4
+    finally:
+        be.close()
+
+
+def test_q8_declines_leave_dst_to_the_cpu_path(ctx):
+    # below the threshold (backend_test.go:250, "tiny/declined") and for a weight with an
+    # infinite scale (whose zero codes the CPU path turns into NaN) the backend declines
+    # without writing dst, and the CPU path's result is what the caller gets.
+    g = workloads.rng(13)
+    be = EnchipQ8(ctx)
+    try:
+        M, K, N = 8, 32, 32
+        a = g.standard_normal((M, K)).astype(np.float32)
+        wq = g.integers(-127, 128, size=(N, K)).astype(np.int8)
+        ws = np.full(N, 0.002, np.float32)
+        dst = np.full((M, N), 7.0, np.float32)
+        assert not be(dst, a, wq, ws, M, K, N) and np.all(dst == 7.0) and not be.handles
+        assert not mmq8(be, dst, a, wq, ws, M, K, N)
+        assert np.array_equal(bits(dst), bits(a @ oracle.dequant_rows_i8(wq, ws, N, K).T))
+
+        M, K, N = 64, 256, 128
+        a = g.standard_normal((M, K)).astype(np.float32)
+        wq = g.integers(-127, 128, size=(N, K)).astype(np.int8)
+        wq[0, 3] = 0
+        ws = np.full(N, 0.002, np.float32)
+        ws[0] = np.inf
+        dst = np.full((M, N), 7.0, np.float32)
+        assert not be(dst, a, wq, ws, M, K, N) and np.all(dst == 7.0)
+        assert not mmq8(be, dst, a, wq, ws, M, K, N)
+        assert np.all(np.isnan(dst[:, 0]))  # 0 * inf in the CPU path's widened weight
+    finally:
+        be.close()

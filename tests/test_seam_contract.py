@@ -408,3 +408,58 @@ def test_q8_declines_leave_dst_to_the_cpu_path(ctx):
         assert np.all(np.isnan(dst[:, 0]))  # 0 * inf in the CPU path's widened weight
     finally:
         be.close()
+
+
+def test_q8_eight_threads_on_one_context(ctx):
+    # encoder.EncodeBatch's workers (encoder/model.go:214) on the weight-only seam: 8
+    # threads, each alternating weight-only and W8A8 calls on its own weight through one
+    # context. Every weight-only result is bit-identical to the same call made alone
+    # (the kernels' sums run in a fixed order) and within the gate, and the W8A8 calls in
+    # between, which share the context's device buffers, leave them undisturbed.
+    lib = enchip.load()
+    g = workloads.rng(35)
+    shapes = [(64 + 96 * t, 768 if t % 2 else 3072, 256 * (1 + t % 3)) for t in range(8)]
+    wts = [(g.integers(-127, 128, size=(N, K)).astype(np.int8), np.full(N, 0.002, np.float32))
+           for _, K, N in shapes]
+    hs = [ctx.register_weight(wq, ws) for wq, ws in wts]
+    inputs = [g.standard_normal((M, K)).astype(np.float32) for M, K, _ in shapes]
+    alone = [ctx.matmul_bt_q8(h, a) for h, a in zip(hs, inputs)]
+    results, errors = {}, {}
+    start = threading.Barrier(8)
+
+    def worker(t):
+        try:
+            M, K, N = shapes[t]
+            start.wait()
+            outs = []
+            for it in range(6):
+                dst = np.empty((M, N), np.float32)
+                rc = lib.enchip_matmul_bt_q8(ctx.handle, hs[t].handle, inputs[t].ctypes.data, M, dst.ctypes.data)
+                assert rc == enchip.OK, lib.enchip_last_error(ctx.handle).decode()
+                outs.append(dst)
+                d8 = np.empty((M, N), np.float32)
+                rc = lib.enchip_w8a8_linear(ctx.handle, hs[t].handle, inputs[t].ctypes.data, M, None, 0,
+                                            d8.ctypes.data, None)
+                assert rc == enchip.OK, lib.enchip_last_error(ctx.handle).decode()
+            results[t] = outs
+        except BaseException as exc:  # reported by the main thread
+            errors[t] = exc
+
+    try:
+        threads = [threading.Thread(target=worker, args=(t,)) for t in range(8)]
+        say("8 threads x 6 weight-only + 6 W8A8 calls on one context")
+        for th in threads:
+            th.start()
+        for th in threads:
+            th.join(timeout=100)
+        assert not errors, errors
+        for t, (M, K, N) in enumerate(shapes):
+            for it, got in enumerate(results[t]):
+                assert np.array_equal(bits(got), bits(alone[t])), f"thread {t} call {it}"
+            wq, ws = wts[t]
+            rows = slice(0, 32)
+            ref = oracle.matmul_bt_q8_f64(np.ascontiguousarray(inputs[t][rows]), wq, ws, 32, K, N)
+            assert oracle.matmul_bt_worst_rel(alone[t][rows], ref) <= 2e-4
+    finally:
+        for h in hs:
+            ctx.release_weight(h)

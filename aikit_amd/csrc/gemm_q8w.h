@@ -8,10 +8,10 @@
 // b1 = the top 16 bits of a, b2 = the top 16 bits of a - b1, b3 = a - b1 - b2. a - b1 has at
 // most 16 significant bits and a - b1 - b2 at most 8, so both subtractions are exact and b3
 // is a bf16 value: a = b1 + b2 + b3 with no rounding, over f32's whole range (a part below
-// 2^-126 may be flushed, an absolute error under 2^-126). A weight code q (|q| <= 127) is a
-// bf16 value exactly. So every v_mfma_f32_32x32x16_bf16 product b_i q is exact and the sum
-// over k (three MFMAs per 16-deep block) is accumulated in f32 in an order of its own; the
-// channel scale multiplies the sum once at the end. The CPU rounds each widened weight and
+// 2^-126 may be flushed, an absolute error under 2^-126). A weight code q (any int8, -128
+// included) is a bf16 value exactly. So every v_mfma_f32_32x32x16_bf16 product b_i q is exact
+// and the sum over k (three MFMAs per 16-deep block) is accumulated in f32 in an order of its
+// own; the channel scale multiplies the sum once at the end. The CPU rounds each widened weight and
 // sums in f32 in its own order; the contract both meet is the reference's gate against a
 // float64 dot product, worst |C - ref| <= 2e-4 max(|ref|, 1)
 // (gpu/enccuda/backend_test.go:234-289). An infinite activation keeps b2 = b3 = 0, so its

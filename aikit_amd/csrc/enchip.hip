@@ -1767,13 +1767,18 @@ int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, in
                            index, ldi, score, lds);
         return check_launch(c, "topk");
     }
-    const bool wide = k <= TOPK_SMALL_K;
-    const int64_t chunk = wide ? TOPK_WCHUNK : TOPK_CHUNK;
-    const int64_t nchunks = std::max<int64_t>(1, (n + chunk - 1) / chunk);
     // Long rows on a grid of many chunks: threshold from each row's first chunks, then the
     // other chunks filter against it (topk_chunk_wide), so most skip their selection. The
     // thresholds (one key per row) follow the candidates in the scratch.
-    const bool filter = wide && nchunks >= 2 * TOPK_SAMPLE_CHUNKS && rows * nchunks >= kTopkFilterChunks;
+    const int64_t wchunks = std::max<int64_t>(1, (n + TOPK_WCHUNK - 1) / TOPK_WCHUNK);
+    const bool can_filter = wchunks >= 2 * TOPK_SAMPLE_CHUNKS && rows * wchunks >= kTopkFilterChunks;
+    // topk_chunk_wide for k <= 32; for 32 < k <= 64 only with the filter, where most chunks
+    // skip their k selection rounds. Measured on MI355X at n = 2^20, per call: 256 rows
+    // (filtered) k = 33, 48, 64: 755, 743, 762 -> 245, 267, 301 us; unfiltered, the radix
+    // stage 1 is as fast or faster (16 rows, k = 64: 119 us against 158; 1 row 80 against 107).
+    const bool wide = k <= TOPK_SMALL_K || (k <= TOPK_WIDE_K && can_filter);
+    const bool filter = wide && can_filter;
+    const int64_t nchunks = wide ? wchunks : std::max<int64_t>(1, (n + TOPK_CHUNK - 1) / TOPK_CHUNK);
     int rc;
     if ((rc = ensure(c, &c->d_cand, &c->cand_cap, (size_t)(rows * nchunks * k + (filter ? rows : 0)) * sizeof(uint64_t))))
         return rc;

@@ -12,21 +12,20 @@
 // Key 0 is never a valid key and marks "no candidate" (a NaN score, or padding).
 //
 // Two stages, so the M x N score matrix is read from device memory once:
-//   topk_chunk: one 256-thread workgroup per (row, 4096-score chunk) selects the k largest
-//     keys of its chunk and writes them as the chunk's k candidates: for k <= 32 by a
-//     bound from the per-thread maxima and maxima of the few keys above it (top_small_k),
-//     otherwise by a radix select over the keys held in registers (8 bits a pass, LDS
-//     histogram).
-//   (for k <= 32, topk_chunk_wide: the same selection over 8192-score chunks, compared
-//     as floats, half the per-chunk selection work per score. On long rows it first runs
-//     on each row's first TOPK_SAMPLE_CHUNKS chunks; topk_thresh takes the k-th largest of
-//     their keys as a lower bound of the row's k-th largest key; every other chunk then
-//     writes its keys at or above that bound when there are at most k of them (no
-//     selection), else selects its k largest.)
+//   topk_chunk_wide (k <= 64): one 256-thread workgroup per (row, 8192-score chunk)
+//     selects the k largest keys of its chunk and writes them as the chunk's k candidates,
+//     by a bound from the per-thread maxima and maxima of the few keys above it, comparing
+//     the scores as floats and building keys only for those it keeps. On long rows it
+//     first runs on each row's first TOPK_SAMPLE_CHUNKS chunks; topk_thresh takes the k-th
+//     largest of their keys as a lower bound of the row's k-th largest key; every other
+//     chunk then writes its keys at or above that bound when there are at most k of them
+//     (no selection), else selects its k largest.
+//   topk_chunk (k > 64): the same contract over 4096-score chunks by a radix select over
+//     the keys held in registers (8 bits a pass, LDS histogram).
 //   topk_merge: one workgroup per row selects the k largest of the row's candidates the
-//     same way (maxima in registers when k <= 32 and there are at most 4096 candidates,
-//     else a radix select over them in memory and a bitonic sort in LDS) and writes
-//     indices and scores in order.
+//     same way (maxima in registers when k <= 64 and there are at most 4096 candidates, or
+//     8192 for k > 32; else a radix select over them in memory and a bitonic sort in LDS)
+//     and writes indices and scores in order.
 // Keys are unique, so the radix select finds the k-th largest key exactly and the
 // selected set does not depend on the order of anything; outputs are deterministic.
 #pragma once
@@ -126,6 +125,7 @@ __device__ uint64_t radix_threshold(const uint64_t (&key)[EPT], int want, unsign
 }
 
 constexpr int TOPK_SMALL_K = 32;  // up to this k, selection by repeated maxima
+constexpr int TOPK_WIDE_K = 64;   // up to this k, stage 1 on TOPK_WCHUNK-score chunks by maxima
 
 // v and the value of the lane a DPP pattern names (every lane has a source lane), larger.
 template <int CTRL>
@@ -187,18 +187,18 @@ __device__ void top_by_max(uint64_t (&key)[EPT], int k, uint64_t *out, uint64_t 
     }
 }
 
-// The block's k largest keys (k <= TOPK_SMALL_K; keys held EPT per thread, distinct,
-// 0 = none) in descending order into out[0..k), 0-padded, with little work per key:
+// The block's k largest keys (k <= KMAX; keys held EPT per thread, distinct, 0 = none)
+// in descending order into out[0..k), 0-padded, with little work per key:
 //   1. each thread's largest key; wavefront 0 finds T, the k-th largest of those 256
 //      maxima (or 1 when fewer than k are nonzero). At least k keys are >= T (the k
 //      threads' maxima), so every one of the block's k largest keys is >= T;
 //   2. the keys >= T (at most EPT keys of each of those k threads) are gathered in LDS;
 //   3. wavefront 0 takes their maximum k times.
-// 256 threads; lds holds 256 + EPT*TOPK_SMALL_K + 2 words.
-template <int EPT>
+// 256 threads; lds holds 256 + EPT*KMAX + 2 words.
+template <int EPT, int KMAX = TOPK_SMALL_K>
 __device__ void top_small_k(const uint64_t (&key)[EPT], int k, uint64_t *out, uint64_t *lds) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    uint64_t *maxima = lds, *cand = lds + 256, *misc = lds + 256 + EPT * TOPK_SMALL_K;
+    uint64_t *maxima = lds, *cand = lds + 256, *misc = lds + 256 + EPT * KMAX;
     uint64_t tmax = 0;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) tmax = key[j] > tmax ? key[j] : tmax;
@@ -233,31 +233,31 @@ __device__ void top_small_k(const uint64_t (&key)[EPT], int k, uint64_t *out, ui
     __syncthreads();
     if (wave == 0) {
         const int c = (int)(unsigned)misc[1];  // <= EPT * k
-        uint64_t v[EPT * TOPK_SMALL_K / 64];
+        uint64_t v[EPT * KMAX / 64];
 #pragma unroll
-        for (int i = 0; i < EPT * TOPK_SMALL_K / 64; ++i) {
+        for (int i = 0; i < EPT * KMAX / 64; ++i) {
             const int idx = lane + 64 * i;
             v[i] = idx < c ? cand[idx] : 0;
         }
         for (int r = 0; r < k; ++r) {
             uint64_t m = 0;
 #pragma unroll
-            for (int i = 0; i < EPT * TOPK_SMALL_K / 64; ++i) m = v[i] > m ? v[i] : m;
+            for (int i = 0; i < EPT * KMAX / 64; ++i) m = v[i] > m ? v[i] : m;
             m = wave_max_u64(m);
             if (lane == 0) out[r] = m;
 #pragma unroll
-            for (int i = 0; i < EPT * TOPK_SMALL_K / 64; ++i) v[i] = v[i] == m ? 0 : v[i];
+            for (int i = 0; i < EPT * KMAX / 64; ++i) v[i] = v[i] == m ? 0 : v[i];
         }
     }
 }
 
-// Stage 1. Grid (nchunks, rows), 256 threads. cand[row][chunk][k], 0 for unused slots.
+// Stage 1 for k > TOPK_WIDE_K. Grid (nchunks, rows), 256 threads. cand[row][chunk][k], 0
+// for unused slots.
 __global__ __launch_bounds__(256) void topk_chunk(const float *__restrict__ scores, int64_t ld, int64_t n, int k,
                                                   int nchunks, uint64_t *__restrict__ cand) {
     constexpr int EPT = TOPK_CHUNK / 256;
     __shared__ unsigned hist[256];
     __shared__ uint64_t bcast[2];
-    __shared__ uint64_t small[256 + EPT * TOPK_SMALL_K + 2];
     __shared__ unsigned fill;
     const int64_t row = blockIdx.y, base = (int64_t)blockIdx.x * TOPK_CHUNK;
     const float *p = scores + row * ld;
@@ -276,10 +276,6 @@ __global__ __launch_bounds__(256) void topk_chunk(const float *__restrict__ scor
         }
     }
     uint64_t *out = cand + (row * nchunks + blockIdx.x) * (int64_t)k;
-    if (k <= TOPK_SMALL_K) {
-        top_small_k<EPT>(key, k, out, small);
-        return;
-    }
     const uint64_t th = radix_threshold<EPT>(key, k, hist, bcast);
     if (threadIdx.x == 0) fill = 0;
     __syncthreads();
@@ -290,7 +286,7 @@ __global__ __launch_bounds__(256) void topk_chunk(const float *__restrict__ scor
     for (int i = (int)fill + threadIdx.x; i < k; i += 256) out[i] = 0;
 }
 
-// Stage 1 for k <= TOPK_SMALL_K: one workgroup per (row, TOPK_WCHUNK-score chunk), each
+// Stage 1 for k <= TOPK_WIDE_K: one workgroup per (row, TOPK_WCHUNK-score chunk), each
 // thread holding 32 scores (the index is implicit in the position) and comparing them as
 // floats, so a workgroup covers 2x the scores of topk_chunk for the same selection work
 // (the k-round selections are the serial part, once per chunk) and only the keys it keeps
@@ -322,7 +318,7 @@ __global__ __launch_bounds__(256) void topk_chunk_wide(const float *__restrict__
                                                        const uint64_t *__restrict__ thr) {
     constexpr int EPT = TOPK_WCHUNK / 256;
     __shared__ uint64_t maxima[256];
-    __shared__ uint64_t gathered[TOPK_SMALL_K * EPT];  // <= k threads x EPT keys
+    __shared__ uint64_t gathered[TOPK_WIDE_K * EPT];  // <= k threads x EPT keys
     __shared__ uint64_t thresh;
     __shared__ unsigned count;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -448,21 +444,27 @@ __global__ __launch_bounds__(256) void topk_chunk_wide(const float *__restrict__
 // The row thresholds for topk_chunk_wide: the k-th largest of the keys stage 1 kept from
 // each row's first TOPK_SAMPLE_CHUNKS chunks (the k largest of each, so the k-th largest
 // key among all their scores, a lower bound of the row's k-th largest), or 0 when those
-// chunks hold fewer than k keys. One wavefront per row; k <= TOPK_SMALL_K.
+// chunks hold fewer than k keys. One wavefront per row; k <= TOPK_WIDE_K.
 __global__ __launch_bounds__(256) void topk_thresh(const uint64_t *__restrict__ cand, int64_t rows, int nchunks, int k,
                                                    uint64_t *__restrict__ thr, unsigned *__restrict__ zero) {
+    constexpr int PER_LANE = TOPK_SAMPLE_CHUNKS * TOPK_WIDE_K / 64;
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
     const uint64_t *c = cand + row * nchunks * (int64_t)k;
-    const int m = TOPK_SAMPLE_CHUNKS * k;  // <= 128: two keys per lane
-    uint64_t v0 = lane < m ? c[lane] : 0, v1 = lane + 64 < m ? c[lane + 64] : 0;
+    const int m = TOPK_SAMPLE_CHUNKS * k;  // <= 64 * PER_LANE
+    uint64_t v[PER_LANE];
+#pragma unroll
+    for (int i = 0; i < PER_LANE; ++i) v[i] = lane + 64 * i < m ? c[lane + 64 * i] : 0;
     uint64_t t = 0;
     for (int r = 0; r < k; ++r) {
-        t = wave_max_u64(v0 > v1 ? v0 : v1);
+        uint64_t mx = v[0];
+#pragma unroll
+        for (int i = 1; i < PER_LANE; ++i) mx = v[i] > mx ? v[i] : mx;
+        t = wave_max_u64(mx);
         if (t == 0) break;  // fewer than k keys: no threshold
-        v0 = v0 == t ? 0 : v0;  // keys are unique: one lane
-        v1 = v1 == t ? 0 : v1;
+#pragma unroll
+        for (int i = 0; i < PER_LANE; ++i) v[i] = v[i] == t ? 0 : v[i];  // keys are unique: one slot
     }
     if (lane == 0) thr[row] = t;
     if (lane == 0 && zero != nullptr) zero[row] = 0;  // the row's TopkSink count
@@ -600,6 +602,26 @@ __global__ __launch_bounds__(256) void topk_merge(const uint64_t *__restrict__ c
     extern __shared__ uint64_t sorted[];
     const int64_t row = blockIdx.x;
     const uint64_t *c = cand + row * m;
+    if (k > TOPK_SMALL_K && k <= TOPK_WIDE_K && m <= 2 * TOPK_CHUNK) {
+        // up to 64 of at most 8192 candidates: top_small_k over them in registers
+        constexpr int EPT = 2 * TOPK_CHUNK / 256;
+        __shared__ uint64_t wide[256 + EPT * TOPK_WIDE_K + 2];
+        uint64_t key[EPT];
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) {
+            const int64_t i = threadIdx.x + 256 * j;
+            key[j] = c[min(i, m - 1)] & (i < m ? ~0ull : 0ull);  // clamped loads, all in flight
+        }
+        top_small_k<EPT, TOPK_WIDE_K>(key, k, sorted, wide);
+        __syncthreads();
+        for (int i = threadIdx.x; i < k; i += 256) {
+            const uint64_t kk = sorted[i];
+            const int64_t col = kk ? topk_index(kk) : -1;
+            index[row * ldi + i] = (int32_t)col;
+            score[row * lds_ + i] = kk ? scores[row * ld + col] : __uint_as_float(0x7fc00000u);
+        }
+        return;
+    }
     if (k <= TOPK_SMALL_K && m <= TOPK_CHUNK) {
         // few candidates, small k: hold them in registers and take the maxima in order
         constexpr int EPT = TOPK_CHUNK / 256;

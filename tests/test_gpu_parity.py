@@ -668,7 +668,7 @@ def _check_topk(hi, hs, scores, k, what):
 
 @pytest.mark.parametrize("rows,n,k", [(3, 10000, 10), (2, 4096, 1024), (5, 1000, 1000), (1, 1, 5), (4, 50000, 100),
                                       (2, 8193, 7), (1, 300000, 64), (2, 0, 5), (3, 70000, 32), (2, 16384, 10),
-                                      (1, 16385, 1), (2, 40000, 33)])
+                                      (1, 16385, 1), (2, 40000, 33), (3, 70000, 48), (2, 1100003, 64)])
 def test_topk_rows_matches_reference_selection(ctx, rows, n, k):
     # FlatI8.topHits' order (score desc, index asc; NaN skipped) on scores full of ties
     # (a coarse grid), signed zeros and NaNs, across chunk boundaries.
@@ -703,17 +703,20 @@ def _fast_top_hits(s, k):
 
 
 @pytest.mark.parametrize("kind,k", [("normal", 10), ("grid", 10), ("grid", 32), ("normal", 1), ("increasing", 10),
-                                    ("decreasing", 10), ("constant", 10), ("nan_head", 10)])
+                                    ("decreasing", 10), ("constant", 10), ("nan_head", 10), ("normal", 64),
+                                    ("grid", 48), ("increasing", 64), ("constant", 64), ("nan_head", 40)])
 def test_topk_rows_threshold_filter(ctx, kind, k):
     # 64 rows of 2^20 + 3 scores (129 chunks of 8192, the last ragged): stage 1 runs on each
     # row's first 4 chunks, takes the k-th largest of their keys as the row's bound, and the
     # other chunks keep only their keys at or above it when they are at most k. Exact for
     # any data: ties at the bound break by index (grid, constant), a rising row exceeds the
     # bound in every chunk (full selection everywhere), a falling one in none, and rows
-    # whose first chunks are NaN have no bound.
+    # whose first chunks are NaN have no bound. For k > 32 the rows but "normal" are 2^20
+    # scores, so the merge's 128 k candidates take its 8192-key register form; "normal"
+    # keeps 129 chunks and the merge's radix form.
     import torch
 
-    rows, n = 64, (1 << 20) + 3
+    rows, n = 64, (1 << 20) + 3 if k <= 32 or kind == "normal" else 1 << 20
     g = workloads.rng(1000 + k + len(kind))
     if kind == "normal":
         s = g.standard_normal((rows, n), dtype=np.float32)
@@ -747,7 +750,7 @@ def test_topk_rows_threshold_filter(ctx, kind, k):
         assert (hi[r, idx.size:] == -1).all() and np.isnan(hs[r, idx.size:]).all(), f"{kind} row {r}: padding"
 
 
-@pytest.mark.parametrize("k", [1, 10, 32])
+@pytest.mark.parametrize("k", [1, 10, 32, 64])
 def test_topk_rows_concentrated_winners(ctx, k):
     # Every large score sits at positions one thread of a chunk holds (index = 5 mod 256),
     # so that thread's maximum alone clears the bound and its 64 keys (more than a

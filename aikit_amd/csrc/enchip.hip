@@ -1770,15 +1770,13 @@ int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, in
     // Long rows on a grid of many chunks: threshold from each row's first chunks, then the
     // other chunks filter against it (topk_chunk_wide), so most skip their selection. The
     // thresholds (one key per row) follow the candidates in the scratch.
-    const int64_t wchunks = std::max<int64_t>(1, (n + TOPK_WCHUNK - 1) / TOPK_WCHUNK);
-    const bool can_filter = wchunks >= 2 * TOPK_SAMPLE_CHUNKS && rows * wchunks >= kTopkFilterChunks;
-    // topk_chunk_wide for k <= 32; for 32 < k <= 64 only with the filter, where most chunks
-    // skip their k selection rounds. Measured on MI355X at n = 2^20, per call: 256 rows
-    // (filtered) k = 33, 48, 64: 755, 743, 762 -> 245, 267, 301 us; unfiltered, the radix
-    // stage 1 is as fast or faster (16 rows, k = 64: 119 us against 158; 1 row 80 against 107).
-    const bool wide = k <= TOPK_SMALL_K || (k <= TOPK_WIDE_K && can_filter);
-    const bool filter = wide && can_filter;
-    const int64_t nchunks = wide ? wchunks : std::max<int64_t>(1, (n + TOPK_CHUNK - 1) / TOPK_CHUNK);
+    // topk_chunk_wide up to k = 64, else the radix topk_chunk. Measured on MI355X at n = 2^20
+    // (same process, per call), against the radix stage 1: k = 64 at 1, 16, 256 rows 81, 119,
+    // 765 -> 40, 70, 238 us; k = 33 61, 98, 756 -> 36, 63, 226 us.
+    const bool wide = k <= TOPK_WIDE_K;
+    const int64_t chunk = wide ? TOPK_WCHUNK : TOPK_CHUNK;
+    const int64_t nchunks = std::max<int64_t>(1, (n + chunk - 1) / chunk);
+    const bool filter = wide && nchunks >= 2 * TOPK_SAMPLE_CHUNKS && rows * nchunks >= kTopkFilterChunks;
     int rc;
     if ((rc = ensure(c, &c->d_cand, &c->cand_cap, (size_t)(rows * nchunks * k + (filter ? rows : 0)) * sizeof(uint64_t))))
         return rc;
@@ -1823,18 +1821,22 @@ int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, in
 //      row's k largest keys are all there.
 //   3. topk_sink_merge selects the k largest of each list.
 // About k of every kSinkSample columns clear a bound on exchangeable scores (k * N /
-// kSinkSample per row); a row whose list overflows kSinkCap (adversarial orders, e.g.
-// scores rising along the index) makes the caller run the two-pass route instead.
+// kSinkSample per row); a row whose list overflows its capacity (sink_cap: adversarial
+// orders, e.g. scores rising along the index) makes the caller run the two-pass route
+// instead.
 constexpr int64_t kSinkSample = (int64_t)enchip::TOPK_SAMPLE_CHUNKS * enchip::TOPK_WCHUNK;
-constexpr int kSinkCap = enchip::TOPK_CHUNK;
 
-// k <= TOPK_SMALL_K over rows at least 4 samples long whose expected lists fill at most a
-// quarter of the cap, on fragment-major activations: the linear route's own (af), or, for
+// Candidates listed per row: 4096 for k <= 32, 8192 for k <= 64 (topk_sink_merge holds
+// them 16 or 32 per thread).
+int sink_cap(int64_t k) { return k <= enchip::TOPK_SMALL_K ? enchip::TOPK_CHUNK : 2 * enchip::TOPK_CHUNK; }
+
+// k <= TOPK_WIDE_K over rows at least 4 samples long whose expected lists fill at most a
+// quarter of the capacity, on fragment-major activations: the linear route's own (af), or, for
 // M at or below the small-M limit, quantized fragment-major for this route alone when the
 // skinny candidate kernel and the persistent GEMM (sample scores, two-pass fallback) take
 // the shape.
 bool ann_fused_ok(const enchip_ctx *c, const Weight &w, int64_t M, int64_t k, bool af) {
-    if (k < 1 || k > enchip::TOPK_SMALL_K || w.N < 4 * kSinkSample || k * w.N > (int64_t)kSinkCap * kSinkSample / 4)
+    if (k < 1 || k > enchip::TOPK_WIDE_K || w.N < 4 * kSinkSample || k * w.N > (int64_t)sink_cap(k) * kSinkSample / 4)
         return false;
     // from 8 queries: measured on MI355X (2^20 x 384, k = 10, per host call) M = 16 207 -> 189 us,
     // M = 1 150 -> 179 us (the GEMV's scores are cheap there, the extra launches are not)
@@ -1849,12 +1851,12 @@ int launch_ann_fused(enchip_ctx *c, const Weight &w, int64_t M, int64_t k, hipSt
     using namespace enchip;
     int rc;
     if ((rc = ensure(c, &c->d_dst, &c->dst_cap, (size_t)(M * kSinkSample) * sizeof(float)))) return rc;
-    const int64_t cand_n = M * TOPK_SAMPLE_CHUNKS * k;
-    const size_t words = (size_t)(cand_n + M + M * kSinkCap) + (size_t)(M * kSinkCap + 1) / 2 + (size_t)(M + 1) / 2;
+    const int64_t cand_n = M * TOPK_SAMPLE_CHUNKS * k, cap = sink_cap(k);
+    const size_t words = (size_t)(cand_n + M + M * cap) + (size_t)(M * cap + 1) / 2 + (size_t)(M + 1) / 2;
     if ((rc = ensure(c, &c->d_cand, &c->cand_cap, words * sizeof(uint64_t)))) return rc;
     uint64_t *cand = c->d_cand, *thr = cand + cand_n, *keys = thr + M;
-    float *raw = reinterpret_cast<float *>(keys + M * kSinkCap);
-    unsigned *count = reinterpret_cast<unsigned *>(raw + M * kSinkCap + ((M * kSinkCap) & 1));
+    float *raw = reinterpret_cast<float *>(keys + M * cap);
+    unsigned *count = reinterpret_cast<unsigned *>(raw + M * cap + ((M * cap) & 1));
     Weight sample = w;
     sample.N = sample.Np = kSinkSample;
     if ((rc = launch_gemm(c, sample, c->d_aq, w.Kp, c->d_as, nullptr, EPI_F32, c->d_dst, kSinkSample, M, s, true)))
@@ -1874,7 +1876,7 @@ int launch_ann_fused(enchip_ctx *c, const Weight &w, int64_t M, int64_t k, hipSt
     sink.count = count;
     sink.key = keys;
     sink.score = raw;
-    sink.cap = kSinkCap;
+    sink.cap = (int)cap;
     if (const int nk = skinny_shape_nk(w, c->d_aq, w.Kp, true)) {
         // 128 rows a launch, whatever M (each launch reads the index once): with 256 rows'
         // accumulators the candidate epilogue spills, and at M = 1024 eight launches took
@@ -1883,8 +1885,8 @@ int launch_ann_fused(enchip_ctx *c, const Weight &w, int64_t M, int64_t k, hipSt
             TopkSink part = sink;
             part.thr += r0;
             part.count += r0;
-            part.key += r0 * kSinkCap;
-            part.score += r0 * kSinkCap;
+            part.key += r0 * cap;
+            part.score += r0 * cap;
             const int64_t mr = std::min<int64_t>(128, M - r0);
             if (mr <= 32)  // one row block: the epilogue's work per score covers 32 rows, not 128
                 launch_skinny_mb<1, EPI_TOPK, true>(c, w, nk, c->d_aq + r0 * w.Kp, w.Kp, c->d_as + r0, nullptr,
@@ -1896,8 +1898,14 @@ int launch_ann_fused(enchip_ctx *c, const Weight &w, int64_t M, int64_t k, hipSt
     } else
         launch_pt<PT_PW, EPI_TOPK, true>(c, w, c->d_aq, w.Kp, c->d_as, nullptr, nullptr, 0, M, s, sink);
     if ((rc = check_launch(c, "gemm_w8a8 topk"))) return rc;
-    hipLaunchKernelGGL(topk_sink_merge, dim3((unsigned)M), dim3(256), 0, s, (const unsigned *)count,
-                       (const uint64_t *)keys, (const float *)raw, kSinkCap, (int)k, c->d_hit_i, k, c->d_hit_s, k);
+    if (k <= TOPK_SMALL_K)
+        hipLaunchKernelGGL((topk_sink_merge<TOPK_CHUNK / 256, TOPK_SMALL_K>), dim3((unsigned)M), dim3(256), 0, s,
+                           (const unsigned *)count, (const uint64_t *)keys, (const float *)raw, (int)cap, (int)k,
+                           c->d_hit_i, k, c->d_hit_s, k);
+    else
+        hipLaunchKernelGGL((topk_sink_merge<2 * TOPK_CHUNK / 256, TOPK_WIDE_K>), dim3((unsigned)M), dim3(256), 0, s,
+                           (const unsigned *)count, (const uint64_t *)keys, (const float *)raw, (int)cap, (int)k,
+                           c->d_hit_i, k, c->d_hit_s, k);
     *counts = count;
     return check_launch(c, "topk_sink_merge");
 }
@@ -1958,7 +1966,7 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int6
         HIP_TRY(ctx, hipMemcpyAsync(count.data(), d_count, (size_t)M * sizeof(unsigned), hipMemcpyDeviceToHost, s));
         HIP_TRY(ctx, hipStreamSynchronize(s));
         ++ctx->ann_fused_calls;
-        if (*std::max_element(count.begin(), count.end()) <= (unsigned)kSinkCap) return ENCHIP_OK;
+        if (*std::max_element(count.begin(), count.end()) <= (unsigned)sink_cap(k)) return ENCHIP_OK;
         ++ctx->ann_fallbacks;  // some row's list overflowed: the two-pass route below
     }
     if ((rc = ensure(ctx, &ctx->d_dst, &ctx->dst_cap, (size_t)(M * N) * sizeof(float)))) return rc;

@@ -126,6 +126,11 @@ __device__ uint64_t radix_threshold(const uint64_t (&key)[EPT], int want, unsign
 
 constexpr int TOPK_SMALL_K = 32;  // up to this k, selection by repeated maxima
 constexpr int TOPK_WIDE_K = 64;   // up to this k, stage 1 on TOPK_WCHUNK-score chunks by maxima
+// Above this k the selections sort in LDS instead of taking k dependent rounds of a
+// wavefront maximum. Measured on MI355X (n = 2^20, per call, 16 / 64 rows): k = 32 79 / 105
+// -> 62 / 89 us sorted, k = 24 66 / 93 -> 59 / 86; k = 10 43 / 75 with rounds against 53 / 83
+// sorted, k = 16 even.
+constexpr int TOPK_SORT_K = 16;
 
 // v and the value of the lane a DPP pattern names (every lane has a source lane), larger.
 template <int CTRL>
@@ -187,13 +192,52 @@ __device__ void top_by_max(uint64_t (&key)[EPT], int k, uint64_t *out, uint64_t 
     }
 }
 
+// Bitonic sort of a[0..n) in LDS, descending (zeros sink to the end); n a power of two.
+// Every thread of the 256-thread block calls it; it ends with a barrier.
+__device__ void block_sort_desc(uint64_t *a, int n) {
+    for (int size = 2; size <= n; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < n; i += 256) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const uint64_t x = a[i], y = a[j];
+                    const bool desc = (i & size) == 0;
+                    if (desc ? x < y : x > y) {
+                        a[i] = y;
+                        a[j] = x;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+}
+
+// k rounds over one wavefront's keys (N slots per lane, only the first NB of them nonzero):
+// round r writes the wavefront maximum to out[r] (lane 0) and zeroes it where it was.
+template <int NB, int N>
+__device__ __forceinline__ void max_rounds(uint64_t (&v)[N], int k, uint64_t *out, int lane) {
+    for (int r = 0; r < k; ++r) {
+        uint64_t m = 0;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) m = v[i] > m ? v[i] : m;
+        m = wave_max_u64(m);
+        if (lane == 0) out[r] = m;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) v[i] = v[i] == m ? 0 : v[i];
+    }
+}
+
 // The block's k largest keys (k <= KMAX; keys held EPT per thread, distinct, 0 = none)
 // in descending order into out[0..k), 0-padded, with little work per key:
 //   1. each thread's largest key; wavefront 0 finds T, the k-th largest of those 256
 //      maxima (or 1 when fewer than k are nonzero). At least k keys are >= T (the k
 //      threads' maxima), so every one of the block's k largest keys is >= T;
 //   2. the keys >= T (at most EPT keys of each of those k threads) are gathered in LDS;
-//   3. wavefront 0 takes their maximum k times.
+//   3. wavefront 0 takes their maximum k times, over as many slots per lane as the
+//      gathered count needs (a power of two: fully unrolled, no per-slot branches).
+// For k > TOPK_SORT_K, steps 1 and 3 sort in LDS instead (block_sort_desc: the 256 maxima,
+// then the gathered keys padded to a power of two), where k dependent rounds of a
+// wavefront maximum would cost more.
 // 256 threads; lds holds 256 + EPT*KMAX + 2 words.
 template <int EPT, int KMAX = TOPK_SMALL_K>
 __device__ void top_small_k(const uint64_t (&key)[EPT], int k, uint64_t *out, uint64_t *lds) {
@@ -205,6 +249,22 @@ __device__ void top_small_k(const uint64_t (&key)[EPT], int k, uint64_t *out, ui
     maxima[tid] = tmax;
     if (tid == 0) misc[1] = 0;  // candidate count
     __syncthreads();
+    if (k > TOPK_SORT_K) {  // uniform
+        block_sort_desc(maxima, 256);
+        const uint64_t t = maxima[k - 1] != 0 ? maxima[k - 1] : 1;  // 1: fewer than k nonzero maxima
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            if (key[j] != 0 && key[j] >= t) cand[atomicAdd(reinterpret_cast<unsigned *>(&misc[1]), 1u)] = key[j];
+        __syncthreads();
+        const int c = (int)(unsigned)misc[1];  // <= EPT * k
+        int p = 2;
+        while (p < c) p <<= 1;
+        for (int i = c + tid; i < p; i += 256) cand[i] = 0;
+        __syncthreads();
+        block_sort_desc(cand, p);
+        for (int i = tid; i < k; i += 256) out[i] = i < c ? cand[i] : 0;
+        return;
+    }
     if (wave == 0) {
         uint64_t v[4];
 #pragma unroll
@@ -233,21 +293,20 @@ __device__ void top_small_k(const uint64_t (&key)[EPT], int k, uint64_t *out, ui
     __syncthreads();
     if (wave == 0) {
         const int c = (int)(unsigned)misc[1];  // <= EPT * k
-        uint64_t v[EPT * KMAX / 64];
+        constexpr int NV = EPT * KMAX / 64;
+        uint64_t v[NV];
 #pragma unroll
-        for (int i = 0; i < EPT * KMAX / 64; ++i) {
+        for (int i = 0; i < NV; ++i) {
             const int idx = lane + 64 * i;
             v[i] = idx < c ? cand[idx] : 0;
         }
-        for (int r = 0; r < k; ++r) {
-            uint64_t m = 0;
-#pragma unroll
-            for (int i = 0; i < EPT * KMAX / 64; ++i) m = v[i] > m ? v[i] : m;
-            m = wave_max_u64(m);
-            if (lane == 0) out[r] = m;
-#pragma unroll
-            for (int i = 0; i < EPT * KMAX / 64; ++i) v[i] = v[i] == m ? 0 : v[i];
-        }
+        const int nv = (c + 63) >> 6;  // slots holding keys; uniform
+        if (nv <= 1) max_rounds<1>(v, k, out, lane);
+        else if (nv <= 2) max_rounds<(NV < 2 ? NV : 2)>(v, k, out, lane);
+        else if (nv <= 4) max_rounds<(NV < 4 ? NV : 4)>(v, k, out, lane);
+        else if (nv <= 8) max_rounds<(NV < 8 ? NV : 8)>(v, k, out, lane);
+        else if (nv <= 16) max_rounds<(NV < 16 ? NV : 16)>(v, k, out, lane);
+        else max_rounds<NV>(v, k, out, lane);
     }
 }
 
@@ -297,6 +356,8 @@ __global__ __launch_bounds__(256) void topk_chunk(const float *__restrict__ scor
 //      are nonzero); every one of the chunk's k largest keys is >= T;
 //   3. threads whose maximum is >= T (at most k) gather their keys >= T in LDS;
 //   4. wavefront 0 takes the maximum of the gathered keys k times.
+// For k > TOPK_SORT_K, steps 2 and 4 sort in LDS instead (block_sort_desc), as
+// top_small_k does.
 constexpr int TOPK_WCHUNK = 8192;
 
 //
@@ -375,7 +436,11 @@ __global__ __launch_bounds__(256) void topk_chunk_wide(const float *__restrict__
     maxima[tid] = tmax;
     if (tid == 0) count = 0;
     __syncthreads();
-    if (wave == 0) {
+    const bool sorted = k > TOPK_SORT_K;  // uniform: steps 2 and 4 sort in LDS (top_small_k)
+    if (sorted) {
+        block_sort_desc(maxima, 256);
+        if (tid == 0) thresh = maxima[k - 1] != 0 ? maxima[k - 1] : 1;
+    } else if (wave == 0) {
         uint64_t v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = maxima[4 * lane + i];
@@ -411,6 +476,16 @@ __global__ __launch_bounds__(256) void topk_chunk_wide(const float *__restrict__
         }
     }
     __syncthreads();
+    if (sorted) {
+        const int c = (int)count;  // <= k * EPT
+        int p = 2;
+        while (p < c) p <<= 1;
+        for (int i = c + tid; i < p; i += 256) gathered[i] = 0;
+        __syncthreads();
+        block_sort_desc(gathered, p);
+        for (int i = tid; i < k; i += 256) out[i] = i < c ? gathered[i] : 0;
+        return;
+    }
     if (wave != 0) return;
     const int c = (int)count;
     if (c <= 64) {
@@ -471,18 +546,18 @@ __global__ __launch_bounds__(256) void topk_thresh(const uint64_t *__restrict__ 
 }
 
 // The merge after the fused scoring GEMM (gemm_w8a8_pt<EPI_TOPK>): one workgroup per row
-// takes the k largest (k <= TOPK_SMALL_K) of the count[row] candidates the GEMM kept (keys
-// at key[row*cap ..], their scores at score[row*cap ..], unordered), and writes indices and
+// takes the k largest (k <= KMAX) of the count[row] candidates the GEMM kept (keys at
+// key[row*cap ..], their scores at score[row*cap ..], unordered), and writes indices and
 // scores as topk_merge does. A row with more than cap candidates writes nothing: its
-// caller runs the two-pass path instead. cap <= TOPK_CHUNK.
+// caller runs the two-pass path instead. cap <= 256 * EPT.
+template <int EPT, int KMAX>
 __global__ __launch_bounds__(256) void topk_sink_merge(const unsigned *__restrict__ count,
                                                        const uint64_t *__restrict__ key,
                                                        const float *__restrict__ score_in, int cap, int k,
                                                        int32_t *__restrict__ index, int64_t ldi,
                                                        float *__restrict__ score, int64_t lds_) {
-    constexpr int EPT = TOPK_CHUNK / 256;
-    __shared__ uint64_t lds[256 + EPT * TOPK_SMALL_K + 2];
-    __shared__ uint64_t sorted[TOPK_SMALL_K];
+    __shared__ uint64_t lds[256 + EPT * KMAX + 2];
+    __shared__ uint64_t sorted[KMAX];
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
     const unsigned n = count[row];
@@ -500,17 +575,19 @@ __global__ __launch_bounds__(256) void topk_sink_merge(const unsigned *__restric
         kk[j] = kr[at] & keep;
         sv[j] = sr[at];
     }
-    top_small_k<EPT>(kk, k, sorted, lds);
+    top_small_k<EPT, KMAX>(kk, k, sorted, lds);
     __syncthreads();
     for (int i = tid; i < k; i += 256) {
         const uint64_t s = sorted[i];
         index[row * ldi + i] = s ? (int32_t)topk_index(s) : -1;
         if (!s) score[row * lds_ + i] = __uint_as_float(0x7fc00000u);
     }
-    // each selected key's own f32 score, from the one thread that holds it (keys are unique)
+    // each selected key's own f32 score, from the one thread that holds it (keys are unique;
+    // only keys at or above the k-th selected one can be among them)
+    const uint64_t kth = sorted[k - 1];
 #pragma unroll
     for (int j = 0; j < EPT; ++j)
-        if (kk[j] != 0)
+        if (kk[j] != 0 && kk[j] >= kth)
             for (int i = 0; i < k; ++i)
                 if (kk[j] == sorted[i]) score[row * lds_ + i] = sv[j];
 }
@@ -602,14 +679,17 @@ __global__ __launch_bounds__(256) void topk_merge(const uint64_t *__restrict__ c
     extern __shared__ uint64_t sorted[];
     const int64_t row = blockIdx.x;
     const uint64_t *c = cand + row * m;
-    if (k > TOPK_SMALL_K && k <= TOPK_WIDE_K && m <= 2 * TOPK_CHUNK) {
-        // up to 64 of at most 8192 candidates: top_small_k over them in registers
+    if (k > TOPK_SORT_K && k <= TOPK_WIDE_K && m <= 2 * TOPK_CHUNK) {
+        // up to 64 of at most 8192 candidates: top_small_k over them in registers. Each
+        // thread holds 32 consecutive slots (half of a chunk's list at k = 64): a list is
+        // in descending order, so strided slots would give each thread one rank of many
+        // lists, and the thread maxima a loose bound (thousands of keys gathered).
         constexpr int EPT = 2 * TOPK_CHUNK / 256;
         __shared__ uint64_t wide[256 + EPT * TOPK_WIDE_K + 2];
         uint64_t key[EPT];
 #pragma unroll
         for (int j = 0; j < EPT; ++j) {
-            const int64_t i = threadIdx.x + 256 * j;
+            const int64_t i = (int64_t)threadIdx.x * EPT + j;
             key[j] = c[min(i, m - 1)] & (i < m ? ~0ull : 0ull);  // clamped loads, all in flight
         }
         top_small_k<EPT, TOPK_WIDE_K>(key, k, sorted, wide);
@@ -654,22 +734,7 @@ __global__ __launch_bounds__(256) void topk_merge(const uint64_t *__restrict__ c
             if (i0 + 256 * u < m && kk[u] != 0 && kk[u] >= th) sorted[atomicAdd(&fill, 1u)] = kk[u];  // at most k
     }
     __syncthreads();
-    // bitonic sort of kp keys, descending (the zero padding sinks to the end)
-    for (int size = 2; size <= kp; size <<= 1)
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = threadIdx.x; i < kp; i += 256) {
-                const int j = i ^ stride;
-                if (j > i) {
-                    const uint64_t a = sorted[i], b = sorted[j];
-                    const bool desc = (i & size) == 0;
-                    if (desc ? a < b : a > b) {
-                        sorted[i] = b;
-                        sorted[j] = a;
-                    }
-                }
-            }
-            __syncthreads();
-        }
+    block_sort_desc(sorted, kp);  // the zero padding sinks to the end
     for (int i = threadIdx.x; i < k; i += 256) {
         const uint64_t kk = sorted[i];
         const int64_t col = kk ? topk_index(kk) : -1;

@@ -466,13 +466,14 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight index, const float *queries, 
                     int64_t k, int32_t *hit_index, float *hit_score);
 
 /* How enchip_ann_topk has run on this context: *fused = calls that took the fused route
- * (M >= 8, k <= 32, an index of at least 131072 rows whose dimension
+ * (M >= 8, k <= 64, an index of at least 131072 rows whose dimension
  * padded to 64 is an even multiple of 64, as the tiled GEMM takes it: each query's
  * bound from the k-th best score of the index's first 32768 rows, then one scoring pass
  * that keeps only the scores at or above it, so the M x n scores are never written);
  * *fallbacks = those of them that then ran the two-pass route because some query kept
- * more than 4096 scores (an index ordered so that later rows keep scoring higher). Both
- * routes give identical results. No reference counterpart: a diagnostic. */
+ * more than 4096 scores, or 8192 for k > 32 (an index ordered so that later rows keep
+ * scoring higher). Both routes give identical results. No reference counterpart: a
+ * diagnostic. */
 int enchip_ann_topk_stats(enchip_ctx *ctx, int64_t *fused, int64_t *fallbacks);
 
 /* Caps each growable device scratch buffer of the context at `bytes` (0, the default:

@@ -793,9 +793,11 @@ def test_ann_topk_matches_score_batch_plus_top_hits(ctx, M, N, K, k):
                                         ("ties", 64, 10, 256), ("constant", 40, 5, 256), ("rising", 48, 10, 256),
                                         ("normal", 300, 10, 256), ("normal", 64, 10, 600), ("normal", 40, 10, 500),
                                         ("normal", 16, 10, 384), ("normal", 8, 32, 256), ("ties", 9, 10, 256),
-                                        ("rising", 8, 10, 256)])
+                                        ("rising", 8, 10, 256), ("normal", 64, 64, 256), ("ties", 40, 48, 256),
+                                        ("constant", 40, 40, 256), ("rising", 48, 64, 256), ("normal", 16, 64, 384),
+                                        ("normal", 64, 64, 600)])
 def test_ann_topk_fused_route(ctx, kind, M, k, K):
-    # Above the small-M limit, with k <= 32 and at least 131072 index rows, TopKBatch keeps
+    # Above the small-M limit, with k <= 64 and at least 131072 index rows, TopKBatch keeps
     # the scores on the chip: each query's bound is the k-th best key among the first
     # 32768 rows' scores, one scoring pass (gemm_w8a8_pt's EPI_TOPK epilogue) lists only
     # the scores at or above it, and a merge selects from the lists. Identical to
@@ -811,7 +813,8 @@ def test_ann_topk_fused_route(ctx, kind, M, k, K):
     #     bound is a zero and ties at it break by index, -0 comes back as -0;
     #   constant: all scores equal, so exactly k clear the bound;
     #   rising: scores grow along the index, every row past the sample clears the bound,
-    #     the lists overflow and the call runs the two-pass route instead.
+    #     the lists overflow and the call runs the two-pass route instead;
+    #   k > 32: lists of up to 8192 candidates and their merge's 32-per-thread form.
     N = 150004
     g = workloads.rng(4000 + M + k + K + len(kind))
     q = workloads.activations(g, M, K)

@@ -450,6 +450,16 @@ def other_configs(ctx, torch, stream, ceilings):
             th.append(time.perf_counter() - t0)
         f1, b1 = ctx.ann_topk_stats()
         route = "two-pass" if f1 == f0 else ("fused" if b1 == b0 else "fused, fell back to two-pass")
+        # the same at k = 64, the top of the reference's device range (gpu/anncuda/gemv_w8a8.cu:606-619)
+        t64 = None
+        if M > 1:
+            for _ in range(3):
+                ctx.ann_topk(hidx, qh, 64)
+            t64 = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                ctx.ann_topk(hidx, qh, 64)
+                t64.append(time.perf_counter() - t0)
         nbytes = N * K + M * K + 4 * M + 4 * N + 4 * M * N
         kname = ctx.gemm_kernel_name(hidx, M, 0)
         if "skinny" in kname:  # pre_dev's codes are row-major
@@ -457,6 +467,7 @@ def other_configs(ctx, torch, stream, ceilings):
         out[f"ann_flat_i8_m{M}"] = {
             "top10_us_per_call": t_topk * 1e6,
             "ann_topk_host_us_per_call": float(np.median(th)) * 1e6, "ann_topk_route": route,
+            "ann_topk64_host_us_per_call": float(np.median(t64)) * 1e6 if t64 else None,
             "M": M, "K": K, "N": N, "us_per_call": t * 1e6, "hbm_gbps": nbytes / t / 1e9,
             "frac_hbm_peak": nbytes / t / PEAK_HBM_BPS,
             "frac_measured_read_ceiling": nbytes / t / 1e9 / ceilings["hbm_read_gbps"],
@@ -465,7 +476,7 @@ def other_configs(ctx, torch, stream, ceilings):
                     "bias-free W8A8 scores (enchip_w8a8_pre_dev); bytes = index + queries + scales + M*N f32 scores; "
                     "top10_us_per_call = the same scores plus the device top-10 per query (enchip_topk_rows_dev); "
                     "ann_topk_host_us_per_call = enchip_ann_topk (host queries -> host top-10 hits, wall clock, "
-                    "median), on the route ann_topk_route names"}
+                    "median), on the route ann_topk_route names; ann_topk64_host_us_per_call = the same at k = 64"}
         if M <= 16:
             # the reference's CPU path for the same scores: the C restatement of its AVX2
             # W8A8 linear (oracle/cpu_baseline.c), bias-free, on the host's cores
@@ -1073,6 +1084,9 @@ def compact_result(result: dict, detail_path: str | None = None) -> dict:
         c = oc.get(f"ann_flat_i8_m{m}")
         if c:
             other[f"ann_m{m}_us"] = _r(c.get("us_per_call"))
+            for kk in ("", "64"):
+                if c.get(f"ann_topk{kk}_host_us_per_call") is not None:
+                    other[f"ann_m{m}_topk{kk or '10'}_host_us"] = _r(c[f"ann_topk{kk}_host_us_per_call"])
     q8 = oc.get("matmul_bt_q8_weight_only")
     if q8:
         for k in ("m512_layer_us", "m512_layer_host_us", "m32768_layer_us", "m32768_tflops"):

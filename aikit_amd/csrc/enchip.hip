@@ -1756,6 +1756,10 @@ namespace {
 // Measured on MI355X at n = 2^20 (128 chunks per row), k = 10, per call: 32 rows 57 ->
 // 63 us with the filter, 64 rows 91 -> 81, 256 rows 291 -> 207.
 constexpr int64_t kTopkFilterChunks = 8192;
+// The same floor for the radix stage 1 (k > 64, 4096-score chunks), whose selections cost
+// more: at n = 2^20 (256 chunks per row), k = 100, per call, 16 rows 151 -> 127 us with the
+// filter, 8 rows 126 -> 120, 4 rows 117 either way; 256 rows 847 -> 375.
+constexpr int64_t kTopkFilterChunksRadix = 1024;
 
 // Enqueues the two top-k stages (topk.h) after the caller checked the arguments.
 int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, int64_t n, int64_t k, int32_t *index,
@@ -1776,7 +1780,8 @@ int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, in
     const bool wide = k <= TOPK_WIDE_K;
     const int64_t chunk = wide ? TOPK_WCHUNK : TOPK_CHUNK;
     const int64_t nchunks = std::max<int64_t>(1, (n + chunk - 1) / chunk);
-    const bool filter = wide && nchunks >= 2 * TOPK_SAMPLE_CHUNKS && rows * nchunks >= kTopkFilterChunks;
+    const bool filter =
+        nchunks >= 2 * TOPK_SAMPLE_CHUNKS && rows * nchunks >= (wide ? kTopkFilterChunks : kTopkFilterChunksRadix);
     int rc;
     if ((rc = ensure(c, &c->d_cand, &c->cand_cap, (size_t)(rows * nchunks * k + (filter ? rows : 0)) * sizeof(uint64_t))))
         return rc;
@@ -1786,7 +1791,7 @@ int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, in
     for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
         const int64_t nr = std::min<int64_t>(65535, rows - r0);
         uint64_t *cr = c->d_cand + r0 * nchunks * k;
-        if (filter) {
+        if (filter && wide) {
             hipLaunchKernelGGL(topk_chunk_wide, dim3((unsigned)TOPK_SAMPLE_CHUNKS, (unsigned)nr), dim3(256), 0, s,
                                scores + r0 * ld, ld, n, (int)k, (int)nchunks, cr, 0, (const uint64_t *)nullptr);
             hipLaunchKernelGGL(topk_thresh, dim3((unsigned)((nr + 3) / 4)), dim3(256), 0, s, (const uint64_t *)cr, nr,
@@ -1797,9 +1802,17 @@ int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, in
         } else if (wide) {
             hipLaunchKernelGGL(topk_chunk_wide, dim3((unsigned)nchunks, (unsigned)nr), dim3(256), 0, s, scores + r0 * ld,
                                ld, n, (int)k, (int)nchunks, cr, 0, (const uint64_t *)nullptr);
+        } else if (filter) {
+            hipLaunchKernelGGL(topk_chunk, dim3((unsigned)TOPK_SAMPLE_CHUNKS, (unsigned)nr), dim3(256), 0, s,
+                               scores + r0 * ld, ld, n, (int)k, (int)nchunks, cr, 0, (const uint64_t *)nullptr);
+            hipLaunchKernelGGL(topk_thresh_radix, dim3((unsigned)nr), dim3(256), 0, s, (const uint64_t *)cr,
+                               (int)nchunks, (int)k, thr + r0);
+            hipLaunchKernelGGL(topk_chunk, dim3((unsigned)(nchunks - TOPK_SAMPLE_CHUNKS), (unsigned)nr), dim3(256), 0, s,
+                               scores + r0 * ld, ld, n, (int)k, (int)nchunks, cr, TOPK_SAMPLE_CHUNKS,
+                               (const uint64_t *)(thr + r0));
         } else {
             hipLaunchKernelGGL(topk_chunk, dim3((unsigned)nchunks, (unsigned)nr), dim3(256), 0, s, scores + r0 * ld, ld,
-                               n, (int)k, (int)nchunks, cr);
+                               n, (int)k, (int)nchunks, cr, 0, (const uint64_t *)nullptr);
         }
     }
     for (int64_t r0 = 0; r0 < rows; r0 += kRowChunk) {

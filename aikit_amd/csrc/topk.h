@@ -310,15 +310,19 @@ __device__ void top_small_k(const uint64_t (&key)[EPT], int k, uint64_t *out, ui
     }
 }
 
-// Stage 1 for k > TOPK_WIDE_K. Grid (nchunks, rows), 256 threads. cand[row][chunk][k], 0
-// for unused slots.
+// Stage 1 for k > TOPK_WIDE_K. Grid (nchunks - chunk0, rows), 256 threads; chunk index =
+// chunk0 + blockIdx.x. cand[row][chunk][k], 0 for unused slots. With `thr` (a key per row,
+// 0 for none; topk_thresh_radix), a chunk first lists its keys at or above the row's key
+// and stops there when they are at most k (they are then its only keys that can be among
+// the row's k largest), as topk_chunk_wide does.
 __global__ __launch_bounds__(256) void topk_chunk(const float *__restrict__ scores, int64_t ld, int64_t n, int k,
-                                                  int nchunks, uint64_t *__restrict__ cand) {
+                                                  int nchunks, uint64_t *__restrict__ cand, int chunk0,
+                                                  const uint64_t *__restrict__ thr) {
     constexpr int EPT = TOPK_CHUNK / 256;
     __shared__ unsigned hist[256];
     __shared__ uint64_t bcast[2];
     __shared__ unsigned fill;
-    const int64_t row = blockIdx.y, base = (int64_t)blockIdx.x * TOPK_CHUNK;
+    const int64_t row = blockIdx.y, chunk = chunk0 + (int64_t)blockIdx.x, base = chunk * TOPK_CHUNK;
     const float *p = scores + row * ld;
     uint64_t key[EPT];
     {
@@ -334,7 +338,27 @@ __global__ __launch_bounds__(256) void topk_chunk(const float *__restrict__ scor
             key[j] = i <= last ? topk_key(x[j], i) : 0;
         }
     }
-    uint64_t *out = cand + (row * nchunks + blockIdx.x) * (int64_t)k;
+    uint64_t *out = cand + (row * nchunks + chunk) * (int64_t)k;
+    if (thr != nullptr) {
+        const uint64_t t = thr[row];  // >= 2^32 when set, so padding keys (0) never pass
+        if (t != 0) {
+            if (threadIdx.x == 0) fill = 0;
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < EPT; ++j)
+                if (key[j] >= t) {
+                    const unsigned pos = atomicAdd(&fill, 1u);
+                    if (pos < (unsigned)k) out[pos] = key[j];
+                }
+            __syncthreads();
+            const unsigned total = fill;
+            if (total <= (unsigned)k) {
+                for (int i = (int)total + threadIdx.x; i < k; i += 256) out[i] = 0;
+                return;
+            }
+            __syncthreads();  // every thread has read fill before the selection resets it
+        }
+    }
     const uint64_t th = radix_threshold<EPT>(key, k, hist, bcast);
     if (threadIdx.x == 0) fill = 0;
     __syncthreads();
@@ -663,6 +687,19 @@ __device__ uint64_t radix_threshold_mem(const uint64_t *__restrict__ c, int64_t 
         mask |= (uint64_t)0xff << shift;
     }
     return prefix;
+}
+
+// The row thresholds for topk_chunk (k > TOPK_WIDE_K): the k-th largest of the keys stage 1
+// kept from each row's first TOPK_SAMPLE_CHUNKS chunks, a lower bound of the row's k-th
+// largest key, or 0 when those chunks hold at most k keys. One workgroup per row.
+__global__ __launch_bounds__(256) void topk_thresh_radix(const uint64_t *__restrict__ cand, int nchunks, int k,
+                                                         uint64_t *__restrict__ thr) {
+    __shared__ unsigned hist[256];
+    __shared__ uint64_t bcast[2];
+    const int64_t row = blockIdx.x;
+    const uint64_t t = radix_threshold_mem(cand + row * nchunks * (int64_t)k, (int64_t)TOPK_SAMPLE_CHUNKS * k, k,
+                                           hist, bcast);
+    if (threadIdx.x == 0) thr[row] = t == 1 ? 0 : t;  // 1: at most k keys (a real key is >= 2^32)
 }
 
 // Stage 2. Grid (rows), 256 threads, kp * 8 bytes of dynamic LDS (kp: k rounded up to a

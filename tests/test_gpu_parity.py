@@ -704,19 +704,22 @@ def _fast_top_hits(s, k):
 
 @pytest.mark.parametrize("kind,k", [("normal", 10), ("grid", 10), ("grid", 32), ("normal", 1), ("increasing", 10),
                                     ("decreasing", 10), ("constant", 10), ("nan_head", 10), ("normal", 64),
-                                    ("grid", 48), ("increasing", 64), ("constant", 64), ("nan_head", 40)])
+                                    ("grid", 48), ("increasing", 64), ("constant", 64), ("nan_head", 40),
+                                    ("normal", 100), ("grid", 200), ("increasing", 100), ("constant", 128),
+                                    ("decreasing", 100), ("nan_head", 100)])
 def test_topk_rows_threshold_filter(ctx, kind, k):
     # 64 rows of 2^20 + 3 scores (129 chunks of 8192, the last ragged): stage 1 runs on each
     # row's first 4 chunks, takes the k-th largest of their keys as the row's bound, and the
     # other chunks keep only their keys at or above it when they are at most k. Exact for
     # any data: ties at the bound break by index (grid, constant), a rising row exceeds the
     # bound in every chunk (full selection everywhere), a falling one in none, and rows
-    # whose first chunks are NaN have no bound. For k > 32 the rows but "normal" are 2^20
-    # scores, so the merge's 128 k candidates take its 8192-key register form; "normal"
-    # keeps 129 chunks and the merge's radix form.
+    # whose first chunks are NaN have no bound. For 32 < k <= 64 the rows but "normal" are
+    # 2^20 scores, so the merge's 128 k candidates take its 8192-key register form; "normal"
+    # keeps 129 chunks and the merge's radix form. Past k = 64 the chunks are 4096 scores
+    # (257 per row) and the bound comes from topk_thresh_radix.
     import torch
 
-    rows, n = 64, (1 << 20) + 3 if k <= 32 or kind == "normal" else 1 << 20
+    rows, n = 64, (1 << 20) + 3 if k <= 32 or k > 64 or kind == "normal" else 1 << 20
     g = workloads.rng(1000 + k + len(kind))
     if kind == "normal":
         s = g.standard_normal((rows, n), dtype=np.float32)

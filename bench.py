@@ -436,6 +436,24 @@ def other_configs(ctx, torch, stream, ceilings):
         e1.record(stream)
         torch.cuda.synchronize()
         t_topk = e0.elapsed_time(e1) * 1e-3 / reps
+        # the selection alone at larger k on the same device scores (256 queries): k = 64, the
+        # top of the reference's device range, and k = 100, a retrieve-then-rerank depth
+        t_sel = {}
+        if M == 256:
+            for kb in (10, 64, 100):
+                with torch.cuda.stream(stream):
+                    hib = torch.empty((M, kb), dtype=torch.int32, device="cuda")
+                    hsb = torch.empty((M, kb), dtype=torch.float32, device="cuda")
+                torch.cuda.synchronize()
+                for _ in range(3):
+                    ctx.topk_rows_dev(dst.data_ptr(), N, M, N, kb, hib.data_ptr(), kb, hsb.data_ptr(), kb, sp)
+                e0.record(stream)
+                for _ in range(reps):
+                    ctx.topk_rows_dev(dst.data_ptr(), N, M, N, kb, hib.data_ptr(), kb, hsb.data_ptr(), kb, sp)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                t_sel[kb] = e0.elapsed_time(e1) * 1e3 / reps
+                del hib, hsb
         # TopKBatch through its host entry point (enchip_ann_topk: host queries in, host hits
         # out, synchronous). Above the small-M limit with k <= 32 the selection runs in the
         # scoring pass and the M x N scores are never written (the fused route).
@@ -468,6 +486,7 @@ def other_configs(ctx, torch, stream, ceilings):
             "top10_us_per_call": t_topk * 1e6,
             "ann_topk_host_us_per_call": float(np.median(th)) * 1e6, "ann_topk_route": route,
             "ann_topk64_host_us_per_call": float(np.median(t64)) * 1e6 if t64 else None,
+            "topk_rows_us_per_call": {str(kb): v for kb, v in t_sel.items()} or None,
             "M": M, "K": K, "N": N, "us_per_call": t * 1e6, "hbm_gbps": nbytes / t / 1e9,
             "frac_hbm_peak": nbytes / t / PEAK_HBM_BPS,
             "frac_measured_read_ceiling": nbytes / t / 1e9 / ceilings["hbm_read_gbps"],
@@ -476,7 +495,8 @@ def other_configs(ctx, torch, stream, ceilings):
                     "bias-free W8A8 scores (enchip_w8a8_pre_dev); bytes = index + queries + scales + M*N f32 scores; "
                     "top10_us_per_call = the same scores plus the device top-10 per query (enchip_topk_rows_dev); "
                     "ann_topk_host_us_per_call = enchip_ann_topk (host queries -> host top-10 hits, wall clock, "
-                    "median), on the route ann_topk_route names; ann_topk64_host_us_per_call = the same at k = 64"}
+                    "median), on the route ann_topk_route names; ann_topk64_host_us_per_call = the same at k = 64; "
+                    "topk_rows_us_per_call = enchip_topk_rows_dev alone on the device scores, by k"}
         if M <= 16:
             # the reference's CPU path for the same scores: the C restatement of its AVX2
             # W8A8 linear (oracle/cpu_baseline.c), bias-free, on the host's cores
@@ -1087,6 +1107,8 @@ def compact_result(result: dict, detail_path: str | None = None) -> dict:
             for kk in ("", "64"):
                 if c.get(f"ann_topk{kk}_host_us_per_call") is not None:
                     other[f"ann_m{m}_topk{kk or '10'}_host_us"] = _r(c[f"ann_topk{kk}_host_us_per_call"])
+            for kb, v in (c.get("topk_rows_us_per_call") or {}).items():
+                other[f"ann_m{m}_select{kb}_us"] = _r(v)
     q8 = oc.get("matmul_bt_q8_weight_only")
     if q8:
         for k in ("m512_layer_us", "m512_layer_host_us", "m32768_layer_us", "m32768_tflops"):

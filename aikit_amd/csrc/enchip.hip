@@ -1761,6 +1761,19 @@ constexpr int64_t kTopkFilterChunks = 8192;
 // filter, 8 rows 126 -> 120, 4 rows 117 either way; 256 rows 847 -> 375.
 constexpr int64_t kTopkFilterChunksRadix = 1024;
 
+// The per-row bounds from the first TOPK_SAMPLE_CHUNKS chunks' candidates (cr, nr rows of
+// nchunks * k): topk_thresh's wavefront rounds up to k = TOPK_SORT_K, a sort above.
+void launch_thresh(const uint64_t *cr, int64_t nr, int64_t nchunks, int64_t k, uint64_t *thr, unsigned *zero,
+                   hipStream_t s) {
+    using namespace enchip;
+    if (k > TOPK_SORT_K)
+        hipLaunchKernelGGL(topk_thresh_sorted, dim3((unsigned)nr), dim3(256), 0, s, cr, (int)nchunks, (int)k, thr,
+                           zero);
+    else
+        hipLaunchKernelGGL(topk_thresh, dim3((unsigned)((nr + 3) / 4)), dim3(256), 0, s, cr, nr, (int)nchunks, (int)k,
+                           thr, zero);
+}
+
 // Enqueues the two top-k stages (topk.h) after the caller checked the arguments.
 int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, int64_t n, int64_t k, int32_t *index,
                 int64_t ldi, float *score, int64_t lds, hipStream_t s) {
@@ -1794,8 +1807,7 @@ int launch_topk(enchip_ctx *c, const float *scores, int64_t ld, int64_t rows, in
         if (filter && wide) {
             hipLaunchKernelGGL(topk_chunk_wide, dim3((unsigned)TOPK_SAMPLE_CHUNKS, (unsigned)nr), dim3(256), 0, s,
                                scores + r0 * ld, ld, n, (int)k, (int)nchunks, cr, 0, (const uint64_t *)nullptr);
-            hipLaunchKernelGGL(topk_thresh, dim3((unsigned)((nr + 3) / 4)), dim3(256), 0, s, (const uint64_t *)cr, nr,
-                               (int)nchunks, (int)k, thr + r0, (unsigned *)nullptr);
+            launch_thresh(cr, nr, nchunks, k, thr + r0, nullptr, s);
             hipLaunchKernelGGL(topk_chunk_wide, dim3((unsigned)(nchunks - TOPK_SAMPLE_CHUNKS), (unsigned)nr), dim3(256), 0,
                                s, scores + r0 * ld, ld, n, (int)k, (int)nchunks, cr, TOPK_SAMPLE_CHUNKS,
                                (const uint64_t *)(thr + r0));
@@ -1880,8 +1892,7 @@ int launch_ann_fused(enchip_ctx *c, const Weight &w, int64_t M, int64_t k, hipSt
         hipLaunchKernelGGL(topk_chunk_wide, dim3((unsigned)TOPK_SAMPLE_CHUNKS, (unsigned)nr), dim3(256), 0, s,
                            c->d_dst + r0 * kSinkSample, kSinkSample, kSinkSample, (int)k, TOPK_SAMPLE_CHUNKS, cr, 0,
                            (const uint64_t *)nullptr);
-        hipLaunchKernelGGL(topk_thresh, dim3((unsigned)((nr + 3) / 4)), dim3(256), 0, s, (const uint64_t *)cr, nr,
-                           TOPK_SAMPLE_CHUNKS, (int)k, thr + r0, count + r0);
+        launch_thresh(cr, nr, TOPK_SAMPLE_CHUNKS, k, thr + r0, count + r0, s);
     }
     if ((rc = check_launch(c, "ann_topk sample"))) return rc;
     TopkSink sink;

@@ -543,7 +543,8 @@ __global__ __launch_bounds__(256) void topk_chunk_wide(const float *__restrict__
 // The row thresholds for topk_chunk_wide: the k-th largest of the keys stage 1 kept from
 // each row's first TOPK_SAMPLE_CHUNKS chunks (the k largest of each, so the k-th largest
 // key among all their scores, a lower bound of the row's k-th largest), or 0 when those
-// chunks hold fewer than k keys. One wavefront per row; k <= TOPK_WIDE_K.
+// chunks hold fewer than k keys. One wavefront per row; k <= TOPK_WIDE_K (the host takes
+// topk_thresh_sorted above TOPK_SORT_K).
 __global__ __launch_bounds__(256) void topk_thresh(const uint64_t *__restrict__ cand, int64_t rows, int nchunks, int k,
                                                    uint64_t *__restrict__ thr, unsigned *__restrict__ zero) {
     constexpr int PER_LANE = TOPK_SAMPLE_CHUNKS * TOPK_WIDE_K / 64;
@@ -567,6 +568,26 @@ __global__ __launch_bounds__(256) void topk_thresh(const uint64_t *__restrict__ 
     }
     if (lane == 0) thr[row] = t;
     if (lane == 0 && zero != nullptr) zero[row] = 0;  // the row's TopkSink count
+}
+
+// topk_thresh for k > TOPK_SORT_K: one workgroup per row sorts the row's
+// TOPK_SAMPLE_CHUNKS * k sample keys in LDS (block_sort_desc) and takes the k-th, where k
+// dependent rounds of a wavefront maximum would cost more (k = 64: 18.8 us per 256 rows).
+__global__ __launch_bounds__(256) void topk_thresh_sorted(const uint64_t *__restrict__ cand, int nchunks, int k,
+                                                          uint64_t *__restrict__ thr, unsigned *__restrict__ zero) {
+    __shared__ uint64_t keys[TOPK_SAMPLE_CHUNKS * TOPK_WIDE_K];
+    const int64_t row = blockIdx.x;
+    const uint64_t *c = cand + row * nchunks * (int64_t)k;
+    const int m = TOPK_SAMPLE_CHUNKS * k;  // <= TOPK_SAMPLE_CHUNKS * TOPK_WIDE_K
+    int p = 2;
+    while (p < m) p <<= 1;
+    for (int i = threadIdx.x; i < p; i += 256) keys[i] = i < m ? c[i] : 0;
+    __syncthreads();
+    block_sort_desc(keys, p);
+    if (threadIdx.x == 0) {
+        thr[row] = keys[k - 1];  // 0 when the sample holds fewer than k keys: no threshold
+        if (zero != nullptr) zero[row] = 0;
+    }
 }
 
 // The merge after the fused scoring GEMM (gemm_w8a8_pt<EPI_TOPK>): one workgroup per row

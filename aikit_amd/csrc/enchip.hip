@@ -154,6 +154,10 @@ struct enchip_ctx {
     size_t hit_s_cap = 0;
     // enchip_ann_topk routing (enchip_ann_topk_stats)
     int64_t ann_fused_calls = 0, ann_fallbacks = 0;
+    // Pinned host staging for the host entry points' large copies (upload / download):
+    // two slots of kStageChunk bytes, each fenced by an event recorded after its DMA.
+    char *h_stage = nullptr;
+    hipEvent_t stage_ev[2] = {nullptr, nullptr};
 };
 
 namespace {
@@ -225,6 +229,78 @@ constexpr int64_t kRowChunk = (int64_t)1 << 22;
 bool capturing(hipStream_t s) {
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     return hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
+// Host <-> device copies of the host entry points. From pageable memory the runtime moved
+// 21-37 GB/s host to device and 16-17 GB/s device to host on MI355X (1.5-24 MB), against
+// 43-56 GB/s from pinned memory; a copy into pinned memory followed by the DMA, one after
+// the other, gained nothing. So large copies run through two pinned slots of kStageChunk
+// bytes: the CPU fills (or empties) one slot while the DMA engine moves the other. Device
+// to host from kStageMinDown bytes; host to device, whose pageable rate is better, from
+// kStageMinUp (below it the few chunks hide too little of the per-chunk waits).
+constexpr size_t kStageChunk = (size_t)1 << 20, kStageMinUp = (size_t)4 << 20, kStageMinDown = (size_t)1 << 20;
+
+int ensure_stage(enchip_ctx *c) {
+    if (c->h_stage) return ENCHIP_OK;
+    for (hipEvent_t &e : c->stage_ev)
+        if (!e) HIP_TRY(c, hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    void *p = nullptr;
+    hipError_t e = hipHostMalloc(&p, 2 * kStageChunk, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(c, ENCHIP_ERR_OOM, "hipHostMalloc(%zu): %s", 2 * kStageChunk, hipGetErrorString(e));
+    }
+    c->h_stage = static_cast<char *>(p);
+    return ENCHIP_OK;
+}
+
+// Enqueues the copy of `bytes` from host memory src to device memory dst on s. src may be
+// reused once this returns (every byte is in a pinned slot or already on its way).
+int upload(enchip_ctx *c, void *dst, const void *src, size_t bytes, hipStream_t s) {
+    if (bytes < kStageMinUp) {
+        if (bytes) HIP_TRY(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
+        return ENCHIP_OK;
+    }
+    int rc;
+    if ((rc = ensure_stage(c))) return rc;
+    for (size_t off = 0, i = 0; off < bytes; off += kStageChunk, ++i) {
+        const size_t n = std::min(kStageChunk, bytes - off);
+        char *slot = c->h_stage + (i & 1) * kStageChunk;
+        HIP_TRY(c, hipEventSynchronize(c->stage_ev[i & 1]));  // the slot's last DMA has ended
+        std::memcpy(slot, static_cast<const char *>(src) + off, n);
+        HIP_TRY(c, hipMemcpyAsync(static_cast<char *>(dst) + off, slot, n, hipMemcpyHostToDevice, s));
+        HIP_TRY(c, hipEventRecord(c->stage_ev[i & 1], s));
+    }
+    return ENCHIP_OK;
+}
+
+// Copies `bytes` from device memory src to host memory dst after the work already
+// enqueued on s. A small copy is only enqueued (the caller synchronizes s before it reads
+// dst); a staged one has completed when this returns.
+int download(enchip_ctx *c, void *dst, const void *src, size_t bytes, hipStream_t s) {
+    if (bytes < kStageMinDown) {
+        if (bytes) HIP_TRY(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s));
+        return ENCHIP_OK;
+    }
+    int rc;
+    if ((rc = ensure_stage(c))) return rc;
+    const size_t nch = (bytes + kStageChunk - 1) / kStageChunk;
+    auto chunk = [&](size_t i) { return std::min(kStageChunk, bytes - i * kStageChunk); };
+    auto enqueue = [&](size_t i) -> int {
+        HIP_TRY(c, hipMemcpyAsync(c->h_stage + (i & 1) * kStageChunk, static_cast<const char *>(src) + i * kStageChunk,
+                                  chunk(i), hipMemcpyDeviceToHost, s));
+        HIP_TRY(c, hipEventRecord(c->stage_ev[i & 1], s));
+        return ENCHIP_OK;
+    };
+    for (hipEvent_t e : c->stage_ev) HIP_TRY(c, hipEventSynchronize(e));  // earlier uploads' DMAs
+    if ((rc = enqueue(0))) return rc;
+    for (size_t i = 0; i < nch; ++i) {
+        // the other slot last held chunk i - 1, already copied out
+        if (i + 1 < nch && (rc = enqueue(i + 1))) return rc;
+        HIP_TRY(c, hipEventSynchronize(c->stage_ev[i & 1]));
+        std::memcpy(static_cast<char *>(dst) + i * kStageChunk, c->h_stage + (i & 1) * kStageChunk, chunk(i));
+    }
+    return ENCHIP_OK;
 }
 
 // Orders work about to use the shared scratch on stream s after the scratch's last
@@ -670,6 +746,9 @@ int enchip_close(enchip_ctx *ctx) {
         for (void *p : bufs)
             if (p) (void)hipFree(p);
         if (ctx->scratch_ev) (void)hipEventDestroy(ctx->scratch_ev);
+        for (hipEvent_t e : ctx->stage_ev)
+            if (e) (void)hipEventDestroy(e);
+        if (ctx->h_stage) (void)hipHostFree(ctx->h_stage);
         if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     }
     delete ctx;
@@ -936,11 +1015,11 @@ int enchip_quant_rows(enchip_ctx *ctx, const float *a, int64_t M, int64_t K, int
     if ((rc = ensure(ctx, &ctx->d_aq, &ctx->aq_cap, (size_t)(M * ldq)))) return rc;
     if ((rc = ensure(ctx, &ctx->d_as, &ctx->as_cap, (size_t)M * sizeof(float)))) return rc;
     if ((rc = scratch_wait(ctx, ctx->stream))) return rc;
-    if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = upload(ctx, ctx->d_a, a, (size_t)(M * K) * sizeof(float), ctx->stream))) return rc;
     if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, ldq, ctx->d_as, ctx->stream))) return rc;
     if ((rc = scratch_record(ctx, ctx->stream))) return rc;
-    if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(aq, ctx->d_aq, (size_t)(M * K), hipMemcpyDeviceToHost, ctx->stream));
-    HIP_TRY(ctx, hipMemcpyAsync(ascale, ctx->d_as, (size_t)M * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+    if ((rc = download(ctx, aq, ctx->d_aq, (size_t)(M * K), ctx->stream))) return rc;
+    if ((rc = download(ctx, ascale, ctx->d_as, (size_t)M * sizeof(float), ctx->stream))) return rc;
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     return ENCHIP_OK;
 }
@@ -1171,8 +1250,8 @@ int enchip_w8a8_linear(enchip_ctx *ctx, enchip_weight h, const float *a, int64_t
     if (acc_debug && (rc = ensure(ctx, &ctx->d_acc, &ctx->acc_cap, out_bytes))) return rc;
     hipStream_t s = ctx->stream;
     if ((rc = scratch_wait(ctx, s))) return rc;
-    if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
-    if (bias) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_bias, bias, (size_t)N * sizeof(float), hipMemcpyHostToDevice, s));
+    if ((rc = upload(ctx, ctx->d_a, a, (size_t)(M * K) * sizeof(float), s))) return rc;
+    if (bias && (rc = upload(ctx, ctx->d_bias, bias, (size_t)N * sizeof(float), s))) return rc;
     const bool af = route_af(ctx, *w, M, ctx->d_dst, N) && (!acc_debug || route_af(ctx, *w, M, ctx->d_acc, N));
     if (!acc_debug && fused_small_m(ctx, *w, M, ctx->d_a)) {
         if ((rc = launch_fused_small_m(ctx, *w, ctx->d_a, M, bias ? ctx->d_bias : nullptr, act_code(act), ctx->d_dst,
@@ -1188,8 +1267,8 @@ int enchip_w8a8_linear(enchip_ctx *ctx, enchip_weight h, const float *a, int64_t
         (rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, nullptr, enchip::EPI_I32, ctx->d_acc, N, M, s, af)))
         return rc;
     if ((rc = scratch_record(ctx, s))) return rc;
-    HIP_TRY(ctx, hipMemcpyAsync(dst, ctx->d_dst, out_bytes, hipMemcpyDeviceToHost, s));
-    if (acc_debug) HIP_TRY(ctx, hipMemcpyAsync(acc_debug, ctx->d_acc, out_bytes, hipMemcpyDeviceToHost, s));
+    if ((rc = download(ctx, dst, ctx->d_dst, out_bytes, s))) return rc;
+    if (acc_debug && (rc = download(ctx, acc_debug, ctx->d_acc, out_bytes, s))) return rc;
     HIP_TRY(ctx, hipStreamSynchronize(s));
     return ENCHIP_OK;
 }
@@ -1230,7 +1309,7 @@ int enchip_w8a8_batch(enchip_ctx *ctx, const float *a, int64_t M, int64_t K, con
     if ((rc = ensure_act_scratch(ctx, M, Kp))) return rc;
     hipStream_t s = ctx->stream;
     if ((rc = scratch_wait(ctx, s))) return rc;
-    if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
+    if ((rc = upload(ctx, ctx->d_a, a, (size_t)(M * K) * sizeof(float), s))) return rc;
     // one quantization serves every op, so its layout must suit all of them
     bool af = true;
     for (int i = 0; i < nops; ++i)
@@ -1247,8 +1326,9 @@ int enchip_w8a8_batch(enchip_ctx *ctx, const float *a, int64_t M, int64_t K, con
     }
     if ((rc = scratch_record(ctx, s))) return rc;
     for (int i = 0; i < nops; ++i)
-        HIP_TRY(ctx, hipMemcpyAsync(ops[i].dst, ctx->d_dst + dst_off[(size_t)i],
-                                    (size_t)(M * ws[(size_t)i]->N) * sizeof(float), hipMemcpyDeviceToHost, s));
+        if ((rc = download(ctx, ops[i].dst, ctx->d_dst + dst_off[(size_t)i],
+                           (size_t)(M * ws[(size_t)i]->N) * sizeof(float), s)))
+            return rc;
     HIP_TRY(ctx, hipStreamSynchronize(s));
     return ENCHIP_OK;
 }
@@ -1360,12 +1440,12 @@ int enchip_matmul_bt_f32(enchip_ctx *ctx, const float *a, const float *b, float 
     // operands are uploaded on every call: their contents are never cached (attention
     // rewrites pooled scratch in place between calls, gpu/enccuda/backend_test.go:88-130)
     if (K > 0) {
-        HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
-        HIP_TRY(ctx, hipMemcpyAsync(ctx->d_fb, b, (size_t)(N * K) * sizeof(float), hipMemcpyHostToDevice, s));
+        if ((rc = upload(ctx, ctx->d_a, a, (size_t)(M * K) * sizeof(float), s))) return rc;
+        if ((rc = upload(ctx, ctx->d_fb, b, (size_t)(N * K) * sizeof(float), s))) return rc;
     }
     const enchip_f32_batch one{1, 0, 0, 0};
     if ((rc = launch_matmul_f32(ctx, ctx->d_a, K, ctx->d_fb, K, false, ctx->d_dst, N, M, K, N, one, one, s))) return rc;
-    HIP_TRY(ctx, hipMemcpyAsync(dst, ctx->d_dst, out_bytes, hipMemcpyDeviceToHost, s));
+    if ((rc = download(ctx, dst, ctx->d_dst, out_bytes, s))) return rc;
     HIP_TRY(ctx, hipStreamSynchronize(s));
     return ENCHIP_OK;
 }
@@ -1489,9 +1569,9 @@ int enchip_matmul_bt_q8(enchip_ctx *ctx, enchip_weight h, const float *a, int64_
     if ((rc = ensure(ctx, &ctx->d_dst, &ctx->dst_cap, out_bytes))) return rc;
     hipStream_t s = ctx->stream;
     // the activations are uploaded on every call (gpu/enccuda/backend.go:271-275)
-    if (in_bytes) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, a, in_bytes, hipMemcpyHostToDevice, s));
+    if ((rc = upload(ctx, ctx->d_a, a, in_bytes, s))) return rc;
     if ((rc = launch_matmul_q8w(ctx, *w, ctx->d_a, w->K, ctx->d_dst, w->N, M, s))) return rc;
-    HIP_TRY(ctx, hipMemcpyAsync(dst, ctx->d_dst, out_bytes, hipMemcpyDeviceToHost, s));
+    if ((rc = download(ctx, dst, ctx->d_dst, out_bytes, s))) return rc;
     HIP_TRY(ctx, hipStreamSynchronize(s));
     return ENCHIP_OK;
 }
@@ -1973,7 +2053,7 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int6
     if ((rc = ensure_act_scratch(ctx, M, w->Kp))) return rc;
     hipStream_t s = ctx->stream;
     if ((rc = scratch_wait(ctx, s))) return rc;
-    if (K > 0) HIP_TRY(ctx, hipMemcpyAsync(ctx->d_a, queries, (size_t)(M * K) * sizeof(float), hipMemcpyHostToDevice, s));
+    if ((rc = upload(ctx, ctx->d_a, queries, (size_t)(M * K) * sizeof(float), s))) return rc;
     // the bias-free W8A8 scores (ann/backend.go:25-29), then the selection on the device
     // (d_dst, from the context allocator, is 256-byte aligned: the route does not depend
     // on whether it is allocated yet)

@@ -148,10 +148,11 @@ struct enchip_ctx {
     size_t fb_cap = 0;
     uint64_t *d_cand = nullptr;  // top-k candidates
     size_t cand_cap = 0;
-    int32_t *d_hit_i = nullptr;  // enchip_ann_topk's device results
-    size_t hit_i_cap = 0;
-    float *d_hit_s = nullptr;
-    size_t hit_s_cap = 0;
+    // enchip_ann_topk's device results, one block so that one copy brings them back:
+    // hit indices (int32, M k), hit scores (f32, M k), then the fused route's list sizes
+    // (uint32, M)
+    int32_t *d_hits = nullptr;
+    size_t hits_cap = 0;
     // enchip_ann_topk routing (enchip_ann_topk_stats)
     int64_t ann_fused_calls = 0, ann_fallbacks = 0;
     // Pinned host staging for the host entry points' large copies (upload / download):
@@ -742,7 +743,7 @@ int enchip_close(enchip_ctx *ctx) {
         }
         ctx->weights.clear();
         void *bufs[] = {ctx->d_aq,  ctx->d_as, ctx->d_a,     ctx->d_dst,     ctx->d_bias,
-                        ctx->d_acc, ctx->d_fb, ctx->d_cand, ctx->d_hit_i, ctx->d_hit_s};
+                        ctx->d_acc, ctx->d_fb, ctx->d_cand, ctx->d_hits};
         for (void *p : bufs)
             if (p) (void)hipFree(p);
         if (ctx->scratch_ev) (void)hipEventDestroy(ctx->scratch_ev);
@@ -1950,18 +1951,18 @@ bool ann_fused_ok(const enchip_ctx *c, const Weight &w, int64_t M, int64_t k, bo
 }
 
 // Enqueues steps 1-3 on s for M rows of fragment-major codes in the context scratch
-// (d_aq, d_as), leaving the hits in d_hit_i / d_hit_s and the list sizes (uint32, M) at
-// *counts.
-int launch_ann_fused(enchip_ctx *c, const Weight &w, int64_t M, int64_t k, hipStream_t s, const unsigned **counts) {
+// (d_aq, d_as), leaving the hits at hit_i / hit_s (M x k each) and the list sizes at
+// count (M), all device memory.
+int launch_ann_fused(enchip_ctx *c, const Weight &w, int64_t M, int64_t k, hipStream_t s, int32_t *hit_i,
+                     float *hit_s, unsigned *count) {
     using namespace enchip;
     int rc;
     if ((rc = ensure(c, &c->d_dst, &c->dst_cap, (size_t)(M * kSinkSample) * sizeof(float)))) return rc;
     const int64_t cand_n = M * TOPK_SAMPLE_CHUNKS * k, cap = sink_cap(k);
-    const size_t words = (size_t)(cand_n + M + M * cap) + (size_t)(M * cap + 1) / 2 + (size_t)(M + 1) / 2;
+    const size_t words = (size_t)(cand_n + M + M * cap) + (size_t)(M * cap + 1) / 2;
     if ((rc = ensure(c, &c->d_cand, &c->cand_cap, words * sizeof(uint64_t)))) return rc;
     uint64_t *cand = c->d_cand, *thr = cand + cand_n, *keys = thr + M;
     float *raw = reinterpret_cast<float *>(keys + M * cap);
-    unsigned *count = reinterpret_cast<unsigned *>(raw + M * cap + ((M * cap) & 1));
     Weight sample = w;
     sample.N = sample.Np = kSinkSample;
     if ((rc = launch_gemm(c, sample, c->d_aq, w.Kp, c->d_as, nullptr, EPI_F32, c->d_dst, kSinkSample, M, s, true)))
@@ -2005,13 +2006,39 @@ int launch_ann_fused(enchip_ctx *c, const Weight &w, int64_t M, int64_t k, hipSt
     if (k <= TOPK_SMALL_K)
         hipLaunchKernelGGL((topk_sink_merge<TOPK_CHUNK / 256, TOPK_SMALL_K>), dim3((unsigned)M), dim3(256), 0, s,
                            (const unsigned *)count, (const uint64_t *)keys, (const float *)raw, (int)cap, (int)k,
-                           c->d_hit_i, k, c->d_hit_s, k);
+                           hit_i, k, hit_s, k);
     else
         hipLaunchKernelGGL((topk_sink_merge<2 * TOPK_CHUNK / 256, TOPK_WIDE_K>), dim3((unsigned)M), dim3(256), 0, s,
                            (const unsigned *)count, (const uint64_t *)keys, (const float *)raw, (int)cap, (int)k,
-                           c->d_hit_i, k, c->d_hit_s, k);
-    *counts = count;
+                           hit_i, k, hit_s, k);
     return check_launch(c, "topk_sink_merge");
+}
+
+// Brings back enchip_ann_topk's results after the work enqueued on s: the hits block
+// (d_hits: M k indices, M k scores, then M list sizes when count is given) in one copy,
+// into the pinned staging when it fits a slot, then split into the caller's arrays.
+int fetch_hits(enchip_ctx *c, hipStream_t s, int64_t M, int64_t k, int32_t *hit_index, float *hit_score,
+               unsigned *count) {
+    const size_t n = (size_t)(M * k) * sizeof(int32_t), bytes = 2 * n + (count ? (size_t)M * sizeof(unsigned) : 0);
+    int rc;
+    std::vector<char> big;
+    const char *host;
+    if (bytes <= kStageChunk) {
+        if ((rc = ensure_stage(c))) return rc;
+        for (hipEvent_t e : c->stage_ev) HIP_TRY(c, hipEventSynchronize(e));  // no DMA still reads a slot
+        HIP_TRY(c, hipMemcpyAsync(c->h_stage, c->d_hits, bytes, hipMemcpyDeviceToHost, s));
+        HIP_TRY(c, hipStreamSynchronize(s));
+        host = c->h_stage;
+    } else {
+        big.resize(bytes);
+        if ((rc = download(c, big.data(), c->d_hits, bytes, s))) return rc;
+        HIP_TRY(c, hipStreamSynchronize(s));
+        host = big.data();
+    }
+    std::memcpy(hit_index, host, n);
+    std::memcpy(hit_score, host + n, n);
+    if (count) std::memcpy(count, host + 2 * n, (size_t)M * sizeof(unsigned));
+    return ENCHIP_OK;
 }
 
 }  // namespace
@@ -2048,8 +2075,10 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int6
     HIP_TRY(ctx, hipSetDevice(ctx->device));
     const int64_t K = w->K, N = w->N;
     if ((rc = ensure(ctx, &ctx->d_a, &ctx->a_cap, std::max<size_t>((size_t)(M * K) * sizeof(float), 16)))) return rc;
-    if ((rc = ensure(ctx, &ctx->d_hit_i, &ctx->hit_i_cap, (size_t)(M * k) * sizeof(int32_t)))) return rc;
-    if ((rc = ensure(ctx, &ctx->d_hit_s, &ctx->hit_s_cap, (size_t)(M * k) * sizeof(float)))) return rc;
+    if ((rc = ensure(ctx, &ctx->d_hits, &ctx->hits_cap, (size_t)(2 * M * k + M) * sizeof(int32_t)))) return rc;
+    int32_t *d_hit_i = ctx->d_hits;
+    float *d_hit_s = reinterpret_cast<float *>(d_hit_i + M * k);
+    unsigned *d_count = reinterpret_cast<unsigned *>(d_hit_s + M * k);
     if ((rc = ensure_act_scratch(ctx, M, w->Kp))) return rc;
     hipStream_t s = ctx->stream;
     if ((rc = scratch_wait(ctx, s))) return rc;
@@ -2061,14 +2090,10 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int6
     const bool af = fuse || route_af(ctx, *w, M, nullptr, N);  // the codes' layout, for both routes
     if ((rc = launch_quant(ctx, ctx->d_a, M, K, ctx->d_aq, w->Kp, ctx->d_as, s, af))) return rc;
     if (fuse) {
-        const unsigned *d_count = nullptr;
-        if ((rc = launch_ann_fused(ctx, *w, M, k, s, &d_count))) return rc;
+        if ((rc = launch_ann_fused(ctx, *w, M, k, s, d_hit_i, d_hit_s, d_count))) return rc;
         if ((rc = scratch_record(ctx, s))) return rc;
         std::vector<unsigned> count((size_t)M);
-        HIP_TRY(ctx, hipMemcpyAsync(hit_index, ctx->d_hit_i, (size_t)(M * k) * sizeof(int32_t), hipMemcpyDeviceToHost, s));
-        HIP_TRY(ctx, hipMemcpyAsync(hit_score, ctx->d_hit_s, (size_t)(M * k) * sizeof(float), hipMemcpyDeviceToHost, s));
-        HIP_TRY(ctx, hipMemcpyAsync(count.data(), d_count, (size_t)M * sizeof(unsigned), hipMemcpyDeviceToHost, s));
-        HIP_TRY(ctx, hipStreamSynchronize(s));
+        if ((rc = fetch_hits(ctx, s, M, k, hit_index, hit_score, count.data()))) return rc;
         ++ctx->ann_fused_calls;
         if (*std::max_element(count.begin(), count.end()) <= (unsigned)sink_cap(k)) return ENCHIP_OK;
         ++ctx->ann_fallbacks;  // some row's list overflowed: the two-pass route below
@@ -2076,12 +2101,9 @@ int enchip_ann_topk(enchip_ctx *ctx, enchip_weight h, const float *queries, int6
     if ((rc = ensure(ctx, &ctx->d_dst, &ctx->dst_cap, (size_t)(M * N) * sizeof(float)))) return rc;
     if ((rc = launch_gemm(ctx, *w, ctx->d_aq, w->Kp, ctx->d_as, nullptr, enchip::EPI_F32, ctx->d_dst, N, M, s, af)))
         return rc;
-    if ((rc = launch_topk(ctx, ctx->d_dst, N, M, N, k, ctx->d_hit_i, k, ctx->d_hit_s, k, s))) return rc;
+    if ((rc = launch_topk(ctx, ctx->d_dst, N, M, N, k, d_hit_i, k, d_hit_s, k, s))) return rc;
     if ((rc = scratch_record(ctx, s))) return rc;
-    HIP_TRY(ctx, hipMemcpyAsync(hit_index, ctx->d_hit_i, (size_t)(M * k) * sizeof(int32_t), hipMemcpyDeviceToHost, s));
-    HIP_TRY(ctx, hipMemcpyAsync(hit_score, ctx->d_hit_s, (size_t)(M * k) * sizeof(float), hipMemcpyDeviceToHost, s));
-    HIP_TRY(ctx, hipStreamSynchronize(s));
-    return ENCHIP_OK;
+    return fetch_hits(ctx, s, M, k, hit_index, hit_score, nullptr);
 }
 
 int enchip_ann_topk_stats(enchip_ctx *ctx, int64_t *fused, int64_t *fallbacks) {

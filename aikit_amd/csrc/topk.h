@@ -132,6 +132,10 @@ constexpr int TOPK_WIDE_K = 64;   // up to this k, stage 1 on TOPK_WCHUNK-score 
 // sorted, k = 16 even.
 constexpr int TOPK_SORT_K = 16;
 
+// Keys topk_merge gathers in LDS at the thread-maxima bound before it falls back to the
+// radix select (32 KB).
+constexpr int TOPK_MERGE_POOL = 4096;
+
 // v and the value of the lane a DPP pattern names (every lane has a source lane), larger.
 template <int CTRL>
 __device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v) {
@@ -778,6 +782,67 @@ __global__ __launch_bounds__(256) void topk_merge(const uint64_t *__restrict__ c
             score[row * lds_ + i] = kk ? scores[row * ld + col] : __uint_as_float(0x7fc00000u);
         }
         return;
+    }
+    if (k <= 128) {
+        // The k-th largest of the 256 thread maxima over the candidates bounds the row's k-th
+        // largest key from below; the keys at or above it (a few hundred on mixed lists) are
+        // gathered in LDS and sorted. Two sweeps of the candidates in memory instead of the
+        // radix select's eight. In step j thread t takes slot 256 j + (t + j) % 256: a
+        // wavefront still reads consecutive slots, but a thread meets a different position of
+        // each chunk's list (with t + 256 j alone and k dividing 256, every thread would hold
+        // one list position: the chunks' best keys in a few threads, a loose bound). More
+        // than TOPK_MERGE_POOL keys at the bound take the radix select below. Up to k = 128:
+        // at k = 256 the bound is the least thread maximum and often too loose (measured on
+        // MI355X, 2^20 scores, 64 rows: 273 -> 311 us; k = 100 and 128: 163 -> 118 and 181 -> 126).
+        __shared__ uint64_t mx[256];
+        __shared__ uint64_t pool[TOPK_MERGE_POOL];
+        __shared__ unsigned np;
+        const int64_t steps = (m + 255) / 256;
+        auto sweep = [&](auto &&visit) {
+            for (int64_t j0 = 0; j0 < steps; j0 += 8) {
+                uint64_t kk[8];
+                int64_t at[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int64_t j = j0 + u;
+                    at[u] = 256 * j + ((threadIdx.x + j) & 255);
+                    kk[u] = c[min(at[u], m - 1)];  // clamped, all in flight
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (at[u] < m) visit(kk[u]);
+            }
+        };
+        uint64_t tmax = 0;
+        sweep([&](uint64_t kk) { tmax = kk > tmax ? kk : tmax; });
+        mx[threadIdx.x] = tmax;
+        if (threadIdx.x == 0) np = 0;
+        __syncthreads();
+        block_sort_desc(mx, 256);
+        const uint64_t t = mx[k - 1] != 0 ? mx[k - 1] : 1;  // 1: fewer than k nonzero maxima
+        sweep([&](uint64_t kk) {
+            if (kk != 0 && kk >= t) {
+                const unsigned pos = atomicAdd(&np, 1u);
+                if (pos < (unsigned)TOPK_MERGE_POOL) pool[pos] = kk;
+            }
+        });
+        __syncthreads();
+        const int n = (int)np;
+        if (n <= TOPK_MERGE_POOL) {  // uniform
+            int p = 2;
+            while (p < n) p <<= 1;
+            for (int i = n + threadIdx.x; i < p; i += 256) pool[i] = 0;
+            __syncthreads();
+            block_sort_desc(pool, p);
+            for (int i = threadIdx.x; i < k; i += 256) {
+                const uint64_t kk = i < n ? pool[i] : 0;
+                const int64_t col = kk ? topk_index(kk) : -1;
+                index[row * ldi + i] = (int32_t)col;
+                score[row * lds_ + i] = kk ? scores[row * ld + col] : __uint_as_float(0x7fc00000u);
+            }
+            return;
+        }
+        __syncthreads();  // every thread has read np before the radix select reuses LDS
     }
     const uint64_t th = radix_threshold_mem(c, m, k, hist, bcast);
     for (int i = threadIdx.x; i < kp; i += 256) sorted[i] = 0;

@@ -668,7 +668,8 @@ def _check_topk(hi, hs, scores, k, what):
 
 @pytest.mark.parametrize("rows,n,k", [(3, 10000, 10), (2, 4096, 1024), (5, 1000, 1000), (1, 1, 5), (4, 50000, 100),
                                       (2, 8193, 7), (1, 300000, 64), (2, 0, 5), (3, 70000, 32), (2, 16384, 10),
-                                      (1, 16385, 1), (2, 40000, 33), (3, 70000, 48), (2, 1100003, 64)])
+                                      (1, 16385, 1), (2, 40000, 33), (3, 70000, 48), (2, 1100003, 64),
+                                      (1, 5000000, 10), (2, 2100000, 16)])
 def test_topk_rows_matches_reference_selection(ctx, rows, n, k):
     # FlatI8.topHits' order (score desc, index asc; NaN skipped) on scores full of ties
     # (a coarse grid), signed zeros and NaNs, across chunk boundaries.

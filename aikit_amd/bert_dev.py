@@ -16,7 +16,10 @@ matmul seam, docs/task-native-gpu.md:418-427):
                                         enchip_matmul_bt_f32_dev through an [S, H, L, L] buffer
   out   = W8A8(ctx, Wo) + b             enchip_w8a8_linear_dev
   h     = LN(h + out)                   enchip_residual_layer_norm_dev
-  inter = GELU(W8A8(h, Wi) + b)         enchip_w8a8_linear_dev (fused epilogue)
+  inter = GELU(W8A8(h, Wi) + b)         enchip_w8a8_linear_dev (fused epilogue), or, when
+                                        FFN-down takes fragment-major codes, W8A8(h, Wi) + b
+                                        alone, the GELU applied by FFN-down's quantization
+                                        (enchip_quant_rows_frag_gelu_dev): the same codes
   ffn   = W8A8(inter, Wd) + b           enchip_w8a8_linear_dev
   h     = LN(h + ffn)                   enchip_residual_layer_norm_dev
 
@@ -59,11 +62,12 @@ class DeviceBert:
     """
 
     def __init__(self, ctx: enchip.Context, layers: Sequence[Dict], hidden: int, heads: int, ffn: int,
-                 fused: bool = True, fuse_ln_quant: bool = True):
+                 fused: bool = True, fuse_ln_quant: bool = True, gelu_in_quant: bool = True):
         import torch
 
         self.fused = fused
         self.fuse_ln_quant = fuse_ln_quant
+        self.gelu_in_quant = gelu_in_quant
         self.torch = torch
         self.ctx, self.D, self.H, self.I = ctx, hidden, heads, ffn
         self.hd = hidden // heads
@@ -135,6 +139,15 @@ class DeviceBert:
         if not self.fused or self.hd not in (32, 64):
             return False
         return L <= 512 or self.ctx.attention_products in (enchip.ATT_FLASH_BF16, enchip.ATT_FLASH_F16)
+
+    def gelu_quant_route(self, up_act: int, down: "enchip.Weight", M: int) -> int:
+        """The padded K of FFN-down's codes when FFN-up's GELU moves into FFN-down's
+        quantization (enchip_quant_rows_frag_gelu_dev: FFN-up stores its pre-activations, the
+        quantizer applies the GELU; the same codes, scales and outputs), else 0."""
+        if not self.gelu_in_quant or up_act != enchip.ACT_GELU or down.K % 4 != 0:
+            return 0
+        ok, ldq = self.ctx.frag_route(down, M)
+        return ldq if ok and ldq <= 4096 else 0
 
     def _buffers(self, S: int, L: int):
         key = (S, L)
@@ -213,14 +226,22 @@ class DeviceBert:
             linear("o", w, ctxv, bias, act, out)
             g, s = e["attn_ln"]
             w, bias, act = e["ffn_up"]
+            gq = self.gelu_quant_route(act, e["ffn_down"][0], M)
+            up_act = enchip.ACT_NONE if gq else act
             ldq = ln_then(g, s, out, w, "attn_ln")
             if ldq:
                 self._m("ffn_up.gemm")
-                c.pre_frag_dev(w, codes, ldq, M, ascale, bias.data_ptr(), act, inter.data_ptr(), stream)
+                c.pre_frag_dev(w, codes, ldq, M, ascale, bias.data_ptr(), up_act, inter.data_ptr(), stream)
             else:
-                linear("ffn_up", w, h, bias, act, inter)
+                linear("ffn_up", w, h, bias, up_act, inter)
             w, bias, act = e["ffn_down"]
-            linear("ffn_down", w, inter, bias, act, ffn)
+            if gq:  # inter holds FFN-up's pre-activations: GELU them while quantizing
+                self._m("ffn_down.gelu_quant")
+                c.quant_rows_frag_gelu_dev(inter.data_ptr(), M, w.K, codes, gq, ascale, stream)
+                self._m("ffn_down.gemm")
+                c.pre_frag_dev(w, codes, gq, M, ascale, bias.data_ptr(), act, ffn.data_ptr(), stream)
+            else:
+                linear("ffn_down", w, inter, bias, act, ffn)
             g, s = e["out_ln"]
             nxt = self.handles[li + 1]["qkv"][0] if li + 1 < len(self.handles) else None
             pending = ln_then(g, s, ffn, nxt, "out_ln")

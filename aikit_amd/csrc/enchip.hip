@@ -979,6 +979,44 @@ int enchip_quant_rows_frag_dev(enchip_ctx *ctx, const float *d_a, int64_t M, int
     return launch_quant(ctx, d_a, M, K, d_aq, ldq, d_ascale, s, true);
 }
 
+int enchip_quant_rows_frag_gelu_dev(enchip_ctx *ctx, const float *d_a, int64_t M, int64_t K, int8_t *d_aq,
+                                    int64_t ldq, float *d_ascale, void *stream) {
+    if (!ctx) return ENCHIP_ERR_ARG;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (M < 0 || K <= 0 || K % 4 != 0 || ldq < K || ldq % 64 != 0 || ldq > 256 * 16)
+        return fail(ctx, ENCHIP_ERR_ARG,
+                    "quant_frag_gelu: bad shape M=%lld K=%lld ldq=%lld (K a positive multiple of 4, ldq a multiple of "
+                    "64 with K <= ldq <= 4096)",
+                    (long long)M, (long long)K, (long long)ldq);
+    if (M == 0) return ENCHIP_OK;
+    if (!d_a || !d_aq || !d_ascale) return fail(ctx, ENCHIP_ERR_ARG, "quant_frag_gelu: null pointer");
+    if ((uintptr_t)d_a % 16 != 0 || (uintptr_t)d_aq % 16 != 0)
+        return fail(ctx, ENCHIP_ERR_ARG, "quant_frag_gelu: d_a and d_aq must be 16-byte aligned");
+    HIP_TRY(ctx, hipSetDevice(ctx->device));
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    const int ch = (int)((ldq + 255) / 256), k = (int)K;
+    for (int64_t r0 = 0; r0 < M; r0 += kRowChunk) {
+        const int64_t rows = std::min(kRowChunk, M - r0);
+        const float *a = d_a + r0 * K;
+        int8_t *q = d_aq + r0 * ldq;
+        float *sc = d_ascale + r0;
+        const dim3 grid((unsigned)((rows + 7) / 8)), block(512);
+        switch (ch) {
+#define QGCASE(N)                                                                                    \
+    case N:                                                                                          \
+        hipLaunchKernelGGL(enchip::quant_rows_frag_gelu<N>, grid, block, 0, s, a, q, ldq, sc, rows, k); \
+        break;
+            QGCASE(1) QGCASE(2) QGCASE(3) QGCASE(4) QGCASE(5) QGCASE(6) QGCASE(7) QGCASE(8)
+            QGCASE(9) QGCASE(10) QGCASE(11) QGCASE(12) QGCASE(13) QGCASE(14) QGCASE(15) QGCASE(16)
+#undef QGCASE
+            default: return fail(ctx, ENCHIP_ERR_ARG, "quant_frag_gelu: bad chunk count %d", ch);
+        }
+        int rc = check_launch(ctx, "quant_rows_frag_gelu");
+        if (rc) return rc;
+    }
+    return ENCHIP_OK;
+}
+
 int enchip_w8a8_pre_frag_dev(enchip_ctx *ctx, enchip_weight h, const int8_t *d_aq, int64_t ldq, int64_t M,
                              const float *d_ascale, const float *d_bias, int act, float *d_dst, void *stream) {
     if (!ctx) return ENCHIP_ERR_ARG;

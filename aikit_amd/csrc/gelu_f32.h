@@ -99,11 +99,36 @@ __device__ __forceinline__ float gelu_f32(float x) {
     return 0.5f * x * (1.0f + erf_f32(x * 0.7071067811865476f));
 }
 
+// exp_f32_core without branches, for the erf tail's argument -x*x: bit-identical to
+// exp_f32_core wherever its scaling exponent k is in [-126, 127] (then both return
+// p * 2^k by the same multiply), which holds for every argument the tail uses (x in
+// [1, 4]: k in [-24, -1]). Elsewhere (|x| > ~9.4, NaN) the result is meaningless; the
+// caller discards it (ErfF32 takes its sign branch there, or the value is NaN anyway).
+// The branches of exp_f32_core compile to divergent control flow that serialises the
+// lanes of a tail list; this form lets two list rounds interleave.
+__device__ __forceinline__ float exp_f32_core_tail(float x) {
+    float z = x * 1.4426950408889634f;
+    float t = z + 12582912.0f;
+    float kf = t - 12582912.0f;
+    kf = fminf(fmaxf(kf, -126.0f), 127.0f);  // fmaxf(NaN, -126) = -126: no undefined conversion
+    const int k = (int)kf;
+    float r = x - kf * 0.693145751953125f - kf * 1.428606820309417e-06f;
+    float p = 1.9875691500e-4f;
+    p = p * r + 1.3981999507e-3f;
+    p = p * r + 8.3334519073e-3f;
+    p = p * r + 4.1665795894e-2f;
+    p = p * r + 1.6666665459e-1f;
+    p = p * r + 5.0000001201e-1f;
+    p = p * r * r + r + 1.0f;
+    return p * __uint_as_float((unsigned)(k + 127) << 23);
+}
+
 // gelu_f32 for an argument off ErfF32's series branch (|u| >= 1, u = x * 0.7071067811865476f,
 // or NaN), without branches: the erf tail (1 <= |u| <= 4) is evaluated for every such
 // argument and the sign branch (|u| > 4) selected, by erf_f32's operations on each branch
 // (for |u| > 4 the tail's exp underflows harmlessly, and a NaN takes the tail, as in
-// erf_f32). Branch-free so that several independent arguments interleave. Not for |u| < 1.
+// erf_f32; the tail's exp by exp_f32_core_tail, exact there). Branch-free so that several
+// independent arguments interleave. Not for |u| < 1.
 __device__ __forceinline__ float gelu_f32_offseries(float x) {
     const float u = x * 0.7071067811865476f;
     const float sgn = u < 0 ? -1.0f : 1.0f;
@@ -114,7 +139,7 @@ __device__ __forceinline__ float gelu_f32_offseries(float x) {
     p = p * t + 1.421413741f;
     p = p * t - 0.284496736f;
     p = p * t + 0.254829592f;
-    const float tail = sgn * (1.0f - p * t * exp_f32_core(-ax * ax));
+    const float tail = sgn * (1.0f - p * t * exp_f32_core_tail(-ax * ax));
     return 0.5f * x * (1.0f + (ax > 4 ? sgn : tail));
 }
 

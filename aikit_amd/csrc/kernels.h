@@ -159,6 +159,23 @@ __device__ __forceinline__ int pack_codes(float4 v, float inv) {
     return (c0 & 0xff) | ((c1 & 0xff) << 8) | ((c2 & 0xff) << 16) | ((int)((unsigned)c3 << 24));
 }
 
+// pack_codes for a row whose scale s = maxAbs/127 is a normal float (s >= 2^-126, or
+// +inf): then |v * inv| <= 127 * (1 + 3 * 2^-24) for every finite v of the row, so the
+// rounded value needs no clamp, and v_cvt_i32_f32 turns a NaN into 0 as quant_code does
+// (its float-to-int conversion is written in assembly because a C++ conversion of NaN is
+// undefined). With a subnormal s the quotient can exceed 127, so such rows take
+// pack_codes.
+__device__ __forceinline__ int cvt_i32_f32(float x) {
+    int r;
+    asm volatile("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+__device__ __forceinline__ int pack_codes_normal(float4 v, float inv) {
+    const int c0 = cvt_i32_f32(roundf(v.x * inv)), c1 = cvt_i32_f32(roundf(v.y * inv));
+    const int c2 = cvt_i32_f32(roundf(v.z * inv)), c3 = cvt_i32_f32(roundf(v.w * inv));
+    return (c0 & 0xff) | ((c1 & 0xff) << 8) | ((c2 & 0xff) << 16) | ((int)((unsigned)c3 << 24));
+}
+
 // Row-major codes q[M][ldq], written as packed 32-bit words; columns [K, ldq) zero.
 template <int CH>
 __global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ a,
@@ -234,6 +251,143 @@ __global__ __launch_bounds__(512 / RPW) void quant_rows_frag(const float *__rest
     // piece p = (chunk p / 8, row p % 8): 8 consecutive threads write one whole line
     const int64_t nk32 = ldq >> 5;
     for (int p = threadIdx.x; p < 2 * ldq4; p += NT) {
+        const int c = p >> 3, r2 = p & 7;
+        if (r0 + r2 < M)
+            *reinterpret_cast<int4 *>(q + frag_off(r0 + r2, 16 * (int64_t)c, nk32)) =
+                *reinterpret_cast<const int4 *>(lds + c * CP + r2 * 16);
+    }
+}
+
+// quant_rows_frag of GELUF32(a) (linalg/exp.go:260-263): the codes and scales that
+// quant_rows_frag<CH, 1> writes for rows already passed through the GELU, from the
+// pre-activation rows. For a linear whose input is GELU's output (FFN-down after FFN-up,
+// encoder/bert.go:357-362): FFN-up then runs a bias-only epilogue and this kernel applies
+// the GELU where the rows are read anyway, with many wavefronts per SIMD, where the GEMM's
+// GELU epilogue issues from about one.
+//
+// One wavefront per row, 8 rows per block (the code lines of quant_rows_frag). Each lane
+// evaluates ErfF32's series branch on its 4*CH values without branching (gelu_f32_series4)
+// and keeps the pre-activation of every value that needs another branch (|u| >= 1, or
+// NaN: the tails). The tails are then settled part by part, PG float4 groups at a time:
+// the part goes to a per-wavefront LDS buffer, each lane appends the buffer cells of its
+// tail values to a wave-wide list (a loop over the set bits of its mask, so a lane pays
+// per tail, not per value), the list is evaluated 64 cells at a time by the branch-free
+// gelu_f32_offseries (two rounds interleaved), and the part is read back. A part with no
+// tail in the wavefront is skipped. The list holds every cell of a part, so any number of
+// tails fits. Same bits as gelu_f32 on every value (the series branch by
+// gelu_f32_series4's, every other branch by gelu_f32_offseries's operations), so the
+// codes are quant_rows_frag's of the GELU outputs. The kernel is bound by VALU issue (the
+// series alone is 27 multiplies and adds per value); measured on MI355X at M = 32768,
+// K = 3072, same process, bit-identical: a persistent form that prefetches each
+// wavefront's next row (167 VGPRs, one block per CU) ran 160-295 us against 118-207 for
+// this one, and the series constants held in SGPRs instead of literals 135 against 118.
+//
+// PG: the largest part size (at most CH) that keeps the block's LDS within 80 KB, so two
+// blocks (16 wavefronts) share a CU.
+constexpr int qg_pg(int ch) { return (81920 - 2304 * ch) / 12288 < ch ? (81920 - 2304 * ch) / 12288 : ch; }
+
+template <int CH>
+__global__ __launch_bounds__(512) void quant_rows_frag_gelu(const float *__restrict__ a, int8_t *__restrict__ q,
+                                                            int64_t ldq, float *__restrict__ scale, int64_t M, int K) {
+    constexpr int CP = 144;  // as quant_rows_frag
+    constexpr int PG = qg_pg(CH);
+    constexpr int NPART = (CH + PG - 1) / PG;
+    static_assert(PG >= 1 && 4 * PG <= 32, "a part's tail bits fit one 32-bit word");
+    __shared__ __attribute__((aligned(16))) int8_t lds[16 * CH * CP];
+    __shared__ __attribute__((aligned(16))) float rbuf[8][PG * 256];  // a part of each wavefront's row
+    __shared__ uint16_t tl[8][PG * 256];                              // its tail cells
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t r0 = (int64_t)blockIdx.x * 8;
+    const int64_t row = r0 + wave;
+    const int ldq4 = (int)(ldq >> 2);
+    auto word = [&](int rr, int k4) -> int * { return reinterpret_cast<int *>(lds + (k4 >> 2) * CP + rr * 16 + (k4 & 3) * 4); };
+    float4 v[CH];
+    load_row_raw<CH>(a, min(row, M - 1), K, lane, v);
+    if (row < M) {  // uniform across the wavefront
+        // Series pass: every value by the series branch; tail values keep their input.
+        uint32_t tm[NPART];  // bit 4*(c % PG) + j: value j of float4 c is a tail
+#pragma unroll
+        for (int p = 0; p < NPART; ++p) tm[p] = 0u;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const f32x4v y = {v[c].x, v[c].y, v[c].z, v[c].w};
+            uint32_t t4;
+            const f32x4v gy = gelu_f32_series4(y, t4);
+            v[c] = make_float4(t4 & 1u ? y.x : gy.x, t4 & 2u ? y.y : gy.y, t4 & 4u ? y.z : gy.z, t4 & 8u ? y.w : gy.w);
+            tm[c / PG] |= t4 << (4 * (c % PG));
+        }
+        float *cell = rbuf[wave];  // cell (g * 64 + lane) * 4 + j: value j of the part's float4 g
+        uint16_t *list = tl[wave];
+#pragma unroll
+        for (int p = 0; p < NPART; ++p) {
+            const int c0 = p * PG, ng = (CH - c0) < PG ? (CH - c0) : PG;
+            // each lane's place in the list: a prefix sum of the tail counts, bit-sliced
+            // over ballots (counts up to 4 * PG <= 32 need 6 bits)
+            const int cnt = __builtin_popcount(tm[p]);
+            int excl = 0, total = 0;
+#pragma unroll
+            for (int b = 0; b < 6; ++b) {
+                const uint64_t bm = __builtin_amdgcn_ballot_w64((cnt >> b) & 1);
+                excl += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u)) << b;
+                total += __builtin_popcountll(bm) << b;
+            }
+            if (total == 0) continue;  // uniform
+#pragma unroll
+            for (int g = 0; g < PG; ++g)
+                if (g < ng) *reinterpret_cast<float4 *>(&cell[(g * 64 + lane) * 4]) = v[c0 + g];
+            int pos = excl;
+            for (uint32_t m = tm[p]; m != 0u; m &= m - 1u, ++pos) {
+                const int b = __builtin_ctz(m);
+                list[pos] = (uint16_t)(((b >> 2) * 64 + lane) * 4 + (b & 3));
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            for (int base = 0; base < total; base += 128) {
+                const int e0 = base + lane, e1 = base + 64 + lane;
+                const int i0 = list[min(e0, total - 1)];
+                if (base + 64 < total) {
+                    const int i1 = list[min(e1, total - 1)];
+                    const float g0 = gelu_f32_offseries(cell[i0]);
+                    const float g1 = gelu_f32_offseries(cell[i1]);
+                    if (e0 < total) cell[i0] = g0;
+                    if (e1 < total) cell[i1] = g1;
+                } else if (e0 < total) {
+                    cell[i0] = gelu_f32_offseries(cell[i0]);
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int g = 0; g < PG; ++g)
+                if (g < ng) v[c0 + g] = *reinterpret_cast<const float4 *>(&cell[(g * 64 + lane) * 4]);
+            // the next part's stores to the buffer come after these loads
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        const float m = row_absmax<CH>(v);
+        if (m == 0.0f) {
+#pragma unroll
+            for (int c = 0; c < CH; ++c) *word(wave, lane + 64 * c) = 0;
+            if (lane == 0) scale[row] = 0.0f;
+        } else {
+            const float s = m / 127.0f;
+            const float inv = 1.0f / s;
+            if (s >= 1.17549435e-38f) {  // uniform: the row's scale is a normal float (or +inf)
+#pragma unroll
+                for (int c = 0; c < CH; ++c) *word(wave, lane + 64 * c) = pack_codes_normal(v[c], inv);
+            } else {
+#pragma unroll
+                for (int c = 0; c < CH; ++c) *word(wave, lane + 64 * c) = pack_codes(v[c], inv);
+            }
+            if (lane == 0) scale[row] = s;
+        }
+    }
+    __syncthreads();
+    const int64_t nk32 = ldq >> 5;
+    for (int p = threadIdx.x; p < 2 * ldq4; p += 512) {
         const int c = p >> 3, r2 = p & 7;
         if (r0 + r2 < M)
             *reinterpret_cast<int4 *>(q + frag_off(r0 + r2, 16 * (int64_t)c, nk32)) =

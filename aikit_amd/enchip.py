@@ -46,6 +46,7 @@ _SIGNATURES = {
     "enchip_w8a8_pre_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _i64, _vp, _vp, _int, _vp, _vp]),
     "enchip_w8a8_linear_dev": (_int, [_vp, ctypes.c_uint64, _vp, _i64, _vp, _int, _vp, _vp]),
     "enchip_quant_rows_frag_dev": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "enchip_quant_rows_frag_gelu_dev": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
     "enchip_matmul_bt_f32": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64]),
     "enchip_weight_image_bytes": (_i64, [_i64, _i64]),
     "enchip_topk_rows_dev": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
@@ -332,6 +333,12 @@ class Context:
     def quant_rows_frag_dev(self, d_a: int, M: int, K: int, d_aq: int, ldq: int, d_ascale: int,
                             stream: int = 0) -> None:
         self._check(self._lib.enchip_quant_rows_frag_dev(self._h, d_a, M, K, d_aq, ldq, d_ascale, stream or None))
+
+    def quant_rows_frag_gelu_dev(self, d_a: int, M: int, K: int, d_aq: int, ldq: int, d_ascale: int,
+                                 stream: int = 0) -> None:
+        """quant_rows_frag_dev of GELUF32(d_a), from the pre-activations d_a."""
+        self._check(self._lib.enchip_quant_rows_frag_gelu_dev(self._h, d_a, M, K, d_aq, ldq, d_ascale,
+                                                              stream or None))
 
     def matmul_bt_f32(self, a: np.ndarray, b: np.ndarray) -> np.ndarray:
         """encoder.Backend.MatmulBT (encoder/backend.go:19-28): f32 a[M,K] . b[N,K]^T on the device."""

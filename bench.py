@@ -808,8 +808,14 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
         base = label.split(".")[0]
         if label.endswith(".gemm"):
             K, N, act = lin[base]
+            if base == "ffn_up" and "ffn_down.gelu_quant" in per:
+                act = 0  # the GELU runs in FFN-down's quantization
             u.update(kind="w8a8", ops=2.0 * M * N * K, bytes=float(M * K + N * K + 4 * M + 8 * N + 4 * M * N),
                      kernel=ctx.gemm_kernel_name(wh[base][0], M, act))
+        elif label.endswith(".gelu_quant"):
+            K = lin[base][0]
+            u.update(kind="w8a8", bytes=float(5 * M * K + 4 * M),
+                     kernel=f"enchip::quant_rows_frag_gelu<{((K + 63) // 64 * 64 + 255) // 256}>")
         elif label.endswith(".quant"):
             K = lin[base][0]
             u.update(kind="w8a8", bytes=float(5 * M * K + 4 * M), kernel=quant_kernel_name(K, True))
@@ -844,6 +850,14 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
                                    else 3 * u["ops"] / t / PEAK_BF16_FLOPS)
         table[label] = u
     return table
+
+
+def traffic_key_of(label: str) -> str:
+    """The row of TRAFFIC_PROFILE's table that measured the kernel of an encode label."""
+    base = label.split(".")[0]
+    if label.endswith(".gemm"):
+        return base
+    return ("gelu_quant_" if label.endswith(".gelu_quant") else "quant_") + base
 
 
 def roofline_of(label: str, u: dict, ceilings: dict, traffic_key: str) -> dict:
@@ -1196,17 +1210,22 @@ def main() -> int:
     step_ms_events = sum(u["ms_per_step"] for u in units.values())
     w8a8 = {k: u for k, u in units.items() if u["kind"] == "w8a8"}
     key = max(w8a8, key=lambda k: w8a8[k]["ms_per_step"])
-    traffic_key = key.split(".")[0] if key.endswith(".gemm") else "quant_" + key.split(".")[0]
+    traffic_key = traffic_key_of(key)
     roofline = roofline_of(key, w8a8[key], ceilings, traffic_key)
     u = w8a8[key]
+    gelu_epi = key == "ffn_up.gemm" and "ffn_down.gelu_quant" not in units
     roofline["limiter"] = (
         "VALU issue: the GELU epilogue restates aikit's exact-erf GELUF32 with no FMA (~36 VALU per output in "
         "its branch-free pass), its largest fraction of any roof (roofline.valu); main loops and epilogues "
         "overlap only where a CU's two workgroups are in different phases"
-        if key == "ffn_up.gemm" else "MFMA issue in the main loop" if key.endswith(".gemm") else "HBM")
+        if gelu_epi else
+        "the f32 output stores (4 B per output, most of its bytes) behind the main loop's MFMA issue; no GELU "
+        "in this epilogue (FFN-down's quantization applies it)" if key == "ffn_up.gemm" else
+        "MFMA issue in the main loop" if key.endswith(".gemm") else
+        "HBM, with the exact GELU's VALU work on every element" if key.endswith(".gelu_quant") else "HBM")
     roofline["scope"] = ("the W8A8 path's dominant kernel in the timed encode (by device time per step); "
                          "roofline_step_dominant covers the step's dominant kernel overall")
-    if key == "ffn_up.gemm":
+    if gelu_epi:
         # the third roof of this kernel: its epilogue's f32 VALU work (the exact-erf GELU with
         # no FMA: 36 VALU instructions per output in the branch-free pass, counted in the
         # kernel's gfx950 ISA) against the measured unfused f32 VALU rate
@@ -1236,8 +1255,7 @@ def main() -> int:
     elif dom in w8a8:
         # a W8A8 unit: the same roof as the roofline object (that object itself when the
         # two dominant kernels coincide)
-        rd = roofline if dom == key else roofline_of(
-            dom, ud, ceilings, dom.split(".")[0] if dom.endswith(".gemm") else "quant_" + dom.split(".")[0])
+        rd = roofline if dom == key else roofline_of(dom, ud, ceilings, traffic_key_of(dom))
         step_dom.update({f: rd[f] for f in ("bound", "unit", "achieved", "peak", "frac")})
         if "valu" in rd:
             step_dom["valu_frac"] = rd["valu"]["frac"]

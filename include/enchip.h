@@ -221,6 +221,18 @@ int enchip_w8a8_linear_noalloc_dev(enchip_ctx *ctx, enchip_weight w, const float
 int enchip_quant_rows_frag_dev(enchip_ctx *ctx, const float *d_a, int64_t M, int64_t K,
                                int8_t *d_aq, int64_t ldq, float *d_ascale, void *stream);
 
+/* enchip_quant_rows_frag_dev of GELU(d_a): the codes and scales it would write for the
+ * rows d_a after linalg.GELUF32 (linalg/exp.go:260-263) on every element, computed from
+ * the pre-activations d_a without writing the GELU outputs. Replaces the pair
+ * "W8A8 linear with the GELU epilogue, then quantization of its output" in
+ * encoder/bert.go:357-362 (intermediate = GELU(h Wi^T + bi); output = intermediate Wd^T
+ * + bd): the first linear runs with act = ENCHIP_ACT_NONE and this call quantizes
+ * GELU(its output) for the second, bit-identical to the pair. Requires K % 4 == 0,
+ * ldq <= 4096 (else ENCHIP_ERR_ARG) and 16-byte aligned d_a and d_aq; otherwise the
+ * layout and sizes of enchip_quant_rows_frag_dev. */
+int enchip_quant_rows_frag_gelu_dev(enchip_ctx *ctx, const float *d_a, int64_t M, int64_t K,
+                                    int8_t *d_aq, int64_t ldq, float *d_ascale, void *stream);
+
 /* GEMM + fused epilogue on fragment-major codes from enchip_quant_rows_frag_dev.
  * Returns ENCHIP_ERR_ARG unless enchip_frag_route(ctx, w, M) is 1. Bit-identical to
  * enchip_w8a8_pre_dev / enchip_w8a8_linear_dev on the same activations. */

@@ -328,6 +328,44 @@ def test_device_forward_ln_quant_fusion_is_bit_identical(ctx):
     assert np.array_equal(got[0].view(np.uint32), got[1].view(np.uint32))
 
 
+@pytest.mark.parametrize("up_scale", [1.0, 8.0])
+def test_device_forward_gelu_in_quant_is_bit_identical(ctx, up_scale):
+    # DeviceBert with FFN-up's GELU applied by FFN-down's quantization (the default) and in
+    # FFN-up's epilogue: identical pooled bits. up_scale widens FFN-up's weight scales so
+    # that many pre-activations take ErfF32's tail and sign branches (random-init weights
+    # put ~1% there).
+    import torch
+
+    from aikit_amd import enchip
+    from aikit_amd.bert_dev import DeviceBert
+
+    cfg = workloads.MINILM_L6
+    g = workloads.rng(14)
+    w = model_weights(cfg, seed=104)
+    for lw in w["layers"]:
+        wq, ws, b, act = lw["ffn_up"]
+        lw["ffn_up"] = (wq, (ws * np.float32(up_scale)).astype(np.float32), b, act)
+    S, L, D = cfg.batch, cfg.seq, cfg.hidden
+    h0 = torch.from_numpy(np.concatenate([embeddings_in(g.integers(1000, 30000, size=L), w, cfg)
+                                          for _ in range(S)])).cuda()
+    got = []
+    for gq in (True, False):
+        model = DeviceBert(ctx, w["layers"], D, cfg.heads, cfg.ffn, gelu_in_quant=gq)
+        try:
+            assert bool(model.gelu_quant_route(enchip.ACT_GELU, model.handles[0]["ffn_down"][0], S * L)) == gq
+            h = h0.clone()
+            pooled = torch.empty((S, D), device="cuda")
+            torch.cuda.synchronize()
+            model.embed(h, S, L, pooled)
+            torch.cuda.synchronize()
+            got.append(pooled.cpu().numpy())
+        finally:
+            model.close()
+    say(f"{cfg.name} (FFN-up scales x{up_scale}): GELU in FFN-down's quantization vs in FFN-up, pooled bits equal")
+    assert np.isfinite(got[0]).all()
+    assert np.array_equal(got[0].view(np.uint32), got[1].view(np.uint32))
+
+
 # ------------------------------------------------------------------ full depth at L = 512
 def _cos(a, b):
     a, b = np.asarray(a, np.float64).reshape(-1), np.asarray(b, np.float64).reshape(-1)

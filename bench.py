@@ -852,6 +852,13 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
     return table
 
 
+# VALU lane-operations per element of quant_rows_frag_gelu<12> in the BERT-base encode:
+# SQ_INSTS_VALU = 83,155 wave-instructions per SIMD per launch x 1024 SIMDs x 64 lanes /
+# (32768 x 3072 elements) = 54.1 (series, erf tails, absmax, codes, addressing).
+GELU_QUANT_LANE_OPS = 54
+GELU_QUANT_VALU_SOURCE = "profiles/int8_gemm_clock_mfma_busy_valu_bert_base_xlmr_large.md"
+
+
 def traffic_key_of(label: str) -> str:
     """The row of TRAFFIC_PROFILE's table that measured the kernel of an encode label."""
     base = label.split(".")[0]
@@ -1222,9 +1229,22 @@ def main() -> int:
         "the f32 output stores (4 B per output, most of its bytes) behind the main loop's MFMA issue; no GELU "
         "in this epilogue (FFN-down's quantization applies it)" if key == "ffn_up.gemm" else
         "MFMA issue in the main loop" if key.endswith(".gemm") else
-        "HBM, with the exact GELU's VALU work on every element" if key.endswith(".gelu_quant") else "HBM")
+        "VALU issue: the exact-erf GELU restated with no FMA (27 multiplies and adds per element in the "
+        "series alone) plus the quantization, ~54 VALU lane-ops per element (roofline.valu), at 4 waves per "
+        "SIMD" if key.endswith(".gelu_quant") else "HBM")
     roofline["scope"] = ("the W8A8 path's dominant kernel in the timed encode (by device time per step); "
                          "roofline_step_dominant covers the step's dominant kernel overall")
+    if key.endswith(".gelu_quant"):
+        # its binding roof: VALU lane-operations per element, measured (SQ_INSTS_VALU per
+        # launch x 64 lanes / elements, GELU_QUANT_VALU_SOURCE) against the measured VALU rate
+        elems = cfg.tokens * cfg.ffn
+        valu_ops = float(GELU_QUANT_LANE_OPS) * elems
+        t_l = u["us_per_launch"] * 1e-6
+        roofline["valu"] = {"lane_ops_per_output": GELU_QUANT_LANE_OPS, "outputs_per_launch": elems,
+                            "lane_ops_per_launch": valu_ops, "achieved_t_lane_ops": valu_ops / t_l / 1e12,
+                            "measured_peak_t_lane_ops": ceilings["valu_f32_tops"],
+                            "frac": valu_ops / t_l / 1e12 / ceilings["valu_f32_tops"],
+                            "source": GELU_QUANT_VALU_SOURCE}
     if gelu_epi:
         # the third roof of this kernel: its epilogue's f32 VALU work (the exact-erf GELU with
         # no FMA: 36 VALU instructions per output in the branch-free pass, counted in the

@@ -114,3 +114,38 @@ def test_line_without_cpu_baseline_or_other_configs():
     assert line["cpu_baseline"] is None
     assert "cfg5_pairs_per_s" not in line["other"]
     assert len(json.dumps(line)) <= 4096
+
+
+def test_line_with_the_gelu_quantizer_dominant():
+    # FFN-up's GELU applied by FFN-down's quantizer: the W8A8 path's dominant kernel is then
+    # the quantizer, whose binding roof is VALU issue; the line keeps its valu roof, and
+    # its measured traffic comes from the traffic profile's gelu_quant row.
+    full = canned_result()
+    units = full["encode_kernels"]
+    units["ffn_down.gelu_quant"] = dict(units["ffn_down.quant"], kernel="enchip::quant_rows_frag_gelu<12>",
+                                        us_per_launch=118.8)
+    del units["ffn_down.quant"]
+    full["roofline"] = {"bound": "hbm", "achieved": 4237.0, "peak": 8000.0, "unit": "GB/s", "frac": 0.5297,
+                        "traffic": bench.measured_traffic().get(bench.traffic_key_of("ffn_down.gelu_quant")),
+                        "kernel": "enchip::quant_rows_frag_gelu<12>", "unit_label": "ffn_down.gelu_quant",
+                        "avg_launch_us": 118.8, "alg_bytes_per_launch": 503447552.0, "alg_ops_per_launch": 0.0,
+                        "limiter": "VALU issue", "scope": "s", "traffic_source": bench.TRAFFIC_PROFILE,
+                        "valu": {"lane_ops_per_output": bench.GELU_QUANT_LANE_OPS, "outputs_per_launch": 100663296,
+                                 "lane_ops_per_launch": 5.4e9, "achieved_t_lane_ops": 45.8,
+                                 "measured_peak_t_lane_ops": 59.7, "frac": 0.767}}
+    line = bench.compact_result(full)
+    assert len(json.dumps(line, allow_nan=False)) <= 4096
+    assert line["roofline"]["unit_label"] == "ffn_down.gelu_quant"
+    assert line["roofline"]["valu"]["frac"] == 0.767
+    assert line["roofline"]["valu"]["lane_ops_per_output"] == 54
+    assert line["roofline"]["traffic"] == 503694006  # profiles/bert_base_b64s512_hbm_traffic.md
+    assert line["kernels_us_frac"]["ffn_down.gelu_quant"][0] == 118.8
+
+
+def test_traffic_keys_name_profile_rows():
+    assert bench.traffic_key_of("ffn_up.gemm") == "ffn_up"
+    assert bench.traffic_key_of("o.quant") == "quant_o"
+    assert bench.traffic_key_of("ffn_down.gelu_quant") == "gelu_quant_ffn_down"
+    rows = bench.measured_traffic()
+    for label in ("qkv.gemm", "o.quant", "o.gemm", "ffn_up.gemm", "ffn_down.gelu_quant", "ffn_down.gemm"):
+        assert bench.traffic_key_of(label) in rows, label

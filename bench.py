@@ -922,6 +922,89 @@ def device_forward(ctx, torch, stream, layers_host, cfg, steps: int = 3, warmup:
                     % (steps, warmup, products, tail)}
 
 
+def ffn_gelu_placement(ctx, torch, stream, reps: int = 5) -> dict:
+    """Where FFN-up's exact GELU runs, measured at BERT-base's FFN shape (M = 32768,
+    768 -> 3072 -> the codes of FFN-down's 3072-wide input) over pre-activations of several
+    spreads: the GELU epilogue of FFN-up's GEMM followed by enchip_quant_rows_frag_dev,
+    against a bias-only GEMM followed by enchip_quant_rows_frag_gelu_dev (what the device
+    forward runs for K <= 3072). The weight scales set the pre-activations' standard
+    deviation (int8 codes uniform over +-127 times N(0, 1) activations: ~2031 x the scale);
+    `tails` is the fraction of arguments off ErfF32's series branch. Interleaved, the
+    median of `reps` timings by HIP events on the launch stream; both codes and scales
+    compared bit for bit."""
+    import numpy as np
+
+    from aikit_amd import enchip, workloads
+
+    M, K, N = 32768, 768, 3072
+    sp = stream.cuda_stream
+    hev = HipEvents()
+    g = workloads.rng(5)
+    wq = g.integers(-127, 128, size=(N, K), dtype=np.int8)
+    with torch.cuda.stream(stream):
+        gen = torch.Generator(device="cuda").manual_seed(5)
+        a = torch.randn((M, K), device="cuda", generator=gen)
+        b = torch.from_numpy((g.standard_normal(N) * 0.05).astype(np.float32)).cuda()
+        inter = torch.empty((M, N), device="cuda")
+        s1, s2a, s2b = (torch.empty(M, device="cuda") for _ in range(3))
+    out = {}
+    try:
+        for std in (0.28, 0.55, 1.1, 3.3):
+            ws = (np.float32(std / 2031.0) * g.uniform(0.9, 1.1, N)).astype(np.float32)
+            w = ctx.register_weight(wq, ws)
+            try:
+                ok, ldq = ctx.frag_route(w, M)
+                if not ok:
+                    return {"skipped": "no fragment-major route"}
+                Mp = (M + 127) // 128 * 128
+                with torch.cuda.stream(stream):
+                    q1 = torch.zeros(Mp * ldq, dtype=torch.int8, device="cuda")
+                    q2a = torch.zeros(Mp * N, dtype=torch.int8, device="cuda")
+                    q2b = torch.zeros(Mp * N, dtype=torch.int8, device="cuda")
+                ctx.quant_rows_frag_dev(a.data_ptr(), M, K, q1.data_ptr(), ldq, s1.data_ptr(), sp)
+                legs = {
+                    "gemm_gelu_us": lambda: ctx.pre_frag_dev(w, q1.data_ptr(), ldq, M, s1.data_ptr(), b.data_ptr(),
+                                                             enchip.ACT_GELU, inter.data_ptr(), sp),
+                    "quant_us": lambda: ctx.quant_rows_frag_dev(inter.data_ptr(), M, N, q2a.data_ptr(), N,
+                                                                s2a.data_ptr(), sp),
+                    "gemm_bias_us": lambda: ctx.pre_frag_dev(w, q1.data_ptr(), ldq, M, s1.data_ptr(), b.data_ptr(),
+                                                             enchip.ACT_NONE, inter.data_ptr(), sp),
+                    "gelu_quant_us": lambda: ctx.quant_rows_frag_gelu_dev(inter.data_ptr(), M, N, q2b.data_ptr(), N,
+                                                                          s2b.data_ptr(), sp),
+                }
+                times = {k: [] for k in legs}
+                for rep in range(reps + 1):
+                    evs = []
+                    for k, fn in legs.items():  # in this order: each quantizer reads the GEMM before it
+                        e0, e1 = hev.create(), hev.create()
+                        hev.record(e0, sp)
+                        fn()
+                        hev.record(e1, sp)
+                        evs.append((k, e0, e1))
+                    torch.cuda.synchronize()
+                    if rep:
+                        for k, e0, e1 in evs:
+                            times[k].append(hev.elapsed_ms(e0, e1) * 1e3)
+                    hev.close()
+                pre = inter.cpu().numpy()
+                tails = float(np.mean(~(np.abs(pre * np.float32(0.7071067811865476)) < 1)))
+                same = bool(torch.equal(q2a, q2b)) and bool(torch.equal(s2a.view(torch.int32), s2b.view(torch.int32)))
+                med = {k: float(np.median(v)) for k, v in times.items()}
+                med.update(epilogue_pair_us=med["gemm_gelu_us"] + med["quant_us"],
+                           quantizer_pair_us=med["gemm_bias_us"] + med["gelu_quant_us"], tails=tails,
+                           codes_identical=same)
+                out[str(std)] = med
+                del q1, q2a, q2b
+            finally:
+                ctx.release_weight(w)
+    finally:
+        hev.close()
+    out["note"] = ("FFN-up's GEMM (M 32768, 768 -> 3072) + FFN-down's quantizer: the GELU in the GEMM epilogue "
+                   "(gemm_gelu + quant) vs in the quantizer (gemm_bias + gelu_quant), by pre-activation standard "
+                   "deviation; median of HIP-event timings, interleaved")
+    return out
+
+
 def rerank_device(ctx, torch, stream, steps: int = 2):
     """Config 5: XLM-R-large (24 layers, D 1024, 16 heads, FFN 4096) cross-encoder scoring of
     128 (query, passage) pairs of 512 tokens, random-init weights quantized per channel."""
@@ -1121,6 +1204,12 @@ def compact_result(result: dict, detail_path: str | None = None) -> dict:
             other[f"cfg3_n{n}_frac_hbm"] = _r(c.get("frac_hbm_peak"), 3)
     if "rerank_device_cfg5" in oc:
         other["cfg5_pairs_per_s"] = _r(oc["rerank_device_cfg5"].get("pairs_per_s"))
+    fg = oc.get("ffn_gelu_placement") or {}
+    if fg and "skipped" not in fg:
+        # std: [GELU epilogue + quantizer, bias-only GEMM + GELU quantizer] in us, tail fraction
+        other["ffn_gelu_epi_vs_quant_us"] = {k: [_r(v["epilogue_pair_us"], 4), _r(v["quantizer_pair_us"], 4),
+                                                 _r(v["tails"], 3)]
+                                             for k, v in fg.items() if isinstance(v, dict)}
     for m in ("1", "16", "256"):
         c = oc.get(f"ann_flat_i8_m{m}")
         if c:
@@ -1347,6 +1436,8 @@ def main() -> int:
         log("configs 2 and 3 (isolated linear, small-M GEMV over a rotating > 2x MALL weight set), ann.FlatI8 scoring")
         result["other_configs"] = other_configs(ctx, torch, stream, ceilings)
         result["other_configs"]["weight_registration_cfg4"] = weight_registration(ctx, layers_host)
+        log("FFN-up's GELU: in the GEMM epilogue or in FFN-down's quantizer, by pre-activation spread")
+        result["other_configs"]["ffn_gelu_placement"] = ffn_gelu_placement(ctx, torch, stream)
         log("config 5 cross-encoder rerank resident on the device (XLM-R-large shape, 128 pairs x 512)")
         result["other_configs"]["rerank_device_cfg5"] = rerank_device(ctx, torch, stream)
         log(f"  {result['other_configs']['rerank_device_cfg5']['pairs_per_s']:.1f} pairs/s end to end")

@@ -39,6 +39,11 @@ def canned_result(n_units: int = len(UNITS), long_notes: bool = True) -> dict:
     other["config3_gemv_n3072"] = {"us_per_call": 5.86, "frac_hbm_peak": 0.0566, "note": note}
     other["rerank_device_cfg5"] = {"pairs_per_s": 2443.6, "note": note}
     other["ann_flat_i8_m1"] = {"us_per_call": 59.2, "note": note}
+    other["ffn_gelu_placement"] = {str(sd): {"gemm_gelu_us": 189.7, "quant_us": 82.1, "gemm_bias_us": 118.6,
+                                             "gelu_quant_us": 131.9, "epilogue_pair_us": 271.8123,
+                                             "quantizer_pair_us": 250.5123, "tails": 0.0113, "codes_identical": True}
+                                   for sd in (0.28, 0.55, 1.1, 3.3)}
+    other["ffn_gelu_placement"]["note"] = note
     return {
         "metric": bench.METRIC, "value": 7227.6123456, "unit": "seqs/s", "n_gpus": 1, "steps": 20, "warmup": 3,
         "ms_per_step": 8.8551234, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -95,6 +100,7 @@ def test_line_is_short_and_keeps_the_contract_keys():
     assert line["kernels_us_frac"]["ffn_up.gemm"] == [108.0, 0.17]
     assert line["kernels_us_frac"]["attention"][1] == 0.37
     assert line["other"]["cfg5_pairs_per_s"] == 2444.0
+    assert line["other"]["ffn_gelu_epi_vs_quant_us"]["0.55"] == [271.8, 250.5, 0.0113]
     assert line["measured_ceilings"]["mfma_i8_tops"] == 4288.0
     assert json.loads(text) == line
 

@@ -167,13 +167,31 @@ __device__ __forceinline__ int pack_codes(float4 v, float inv) {
 // pack_codes.
 __device__ __forceinline__ int cvt_i32_f32(float x) {
     int r;
-    asm volatile("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(x));
     return r;
 }
+// math.Round of x for |x| <= 2^22 (here |x| <= 127.00003): trunc(x + copysign(h, x)) with
+// h = 0.5 - 2^-25, one add and one truncation where roundf takes six operations. The sum
+// stays in x's binade (below the next integer), where 2^-25 is under half an ulp: an exact
+// half (n + 0.5) gives n + 1 - 2^-25, which rounds to n + 1 (for n = 0 the tie rounds to the
+// even 1.0), and any x below n + 0.5 (by at least one ulp) gives a sum that rounds below
+// n + 1. NaN stays NaN.
+__device__ __forceinline__ float round_half_away_small(float x) {
+    return __builtin_truncf(x + __builtin_copysignf(__uint_as_float(0x3effffffu), x));
+}
 __device__ __forceinline__ int pack_codes_normal(float4 v, float inv) {
-    const int c0 = cvt_i32_f32(roundf(v.x * inv)), c1 = cvt_i32_f32(roundf(v.y * inv));
-    const int c2 = cvt_i32_f32(roundf(v.z * inv)), c3 = cvt_i32_f32(roundf(v.w * inv));
+    const int c0 = cvt_i32_f32(round_half_away_small(v.x * inv)), c1 = cvt_i32_f32(round_half_away_small(v.y * inv));
+    const int c2 = cvt_i32_f32(round_half_away_small(v.z * inv)), c3 = cvt_i32_f32(round_half_away_small(v.w * inv));
     return (c0 & 0xff) | ((c1 & 0xff) << 8) | ((c2 & 0xff) << 16) | ((int)((unsigned)c3 << 24));
+}
+// absmax_step for values that are never signalling NaNs (results of arithmetic): the IEEE
+// maximum returns the operand that is not a quiet NaN, so max(m, |v|) with m never NaN is
+// `if |v| > m` (equal values have equal bits), in one instruction instead of a compare and
+// a select.
+__device__ __forceinline__ float absmax_step_quiet(float m, float v) {
+    float r;
+    asm("v_max_f32_e64 %0, %1, |%2|" : "=v"(r) : "v"(m), "v"(v));
+    return r;
 }
 
 // Row-major codes q[M][ldq], written as packed 32-bit words; columns [K, ldq) zero.
@@ -261,7 +279,7 @@ __global__ __launch_bounds__(512 / RPW) void quant_rows_frag(const float *__rest
 // quant_rows_frag of GELUF32(a) (linalg/exp.go:260-263): the codes and scales that
 // quant_rows_frag<CH, 1> writes for rows already passed through the GELU, from the
 // pre-activation rows. For a linear whose input is GELU's output (FFN-down after FFN-up,
-// encoder/bert.go:357-362): FFN-up then runs a bias-only epilogue and this kernel applies
+// encoder/bert.go:357-364): FFN-up then runs a bias-only epilogue and this kernel applies
 // the GELU where the rows are read anyway, with many wavefronts per SIMD, where the GEMM's
 // GELU epilogue issues from about one.
 //
@@ -367,7 +385,15 @@ __global__ __launch_bounds__(512) void quant_rows_frag_gelu(const float *__restr
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
-        const float m = row_absmax<CH>(v);
+        float m = 0.0f;  // the GELU values are results of arithmetic: quiet NaNs at most
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            m = absmax_step_quiet(m, v[c].x);
+            m = absmax_step_quiet(m, v[c].y);
+            m = absmax_step_quiet(m, v[c].z);
+            m = absmax_step_quiet(m, v[c].w);
+        }
+        m = wave_absmax(m);
         if (m == 0.0f) {
 #pragma unroll
             for (int c = 0; c < CH; ++c) *word(wave, lane + 64 * c) = 0;

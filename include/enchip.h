@@ -225,7 +225,7 @@ int enchip_quant_rows_frag_dev(enchip_ctx *ctx, const float *d_a, int64_t M, int
  * rows d_a after linalg.GELUF32 (linalg/exp.go:260-263) on every element, computed from
  * the pre-activations d_a without writing the GELU outputs. Replaces the pair
  * "W8A8 linear with the GELU epilogue, then quantization of its output" in
- * encoder/bert.go:357-362 (intermediate = GELU(h Wi^T + bi); output = intermediate Wd^T
+ * encoder/bert.go:357-364 (intermediate = GELU(h Wi^T + bi); output = intermediate Wd^T
  * + bd): the first linear runs with act = ENCHIP_ACT_NONE and this call quantizes
  * GELU(its output) for the second, bit-identical to the pair. Requires K % 4 == 0,
  * ldq <= 4096 (else ENCHIP_ERR_ARG) and 16-byte aligned d_a and d_aq; otherwise the

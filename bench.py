@@ -853,9 +853,9 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
 
 
 # VALU lane-operations per element of quant_rows_frag_gelu<12> in the BERT-base encode:
-# SQ_INSTS_VALU = 83,155 wave-instructions per SIMD per launch x 1024 SIMDs x 64 lanes /
-# (32768 x 3072 elements) = 54.1 (series, erf tails, absmax, codes, addressing).
-GELU_QUANT_LANE_OPS = 54
+# SQ_INSTS_VALU = 77,075 wave-instructions per SIMD per launch x 1024 SIMDs x 64 lanes /
+# (32768 x 3072 elements) = 50.2 (series, erf tails, absmax, codes, addressing).
+GELU_QUANT_LANE_OPS = 50
 GELU_QUANT_VALU_SOURCE = "profiles/int8_gemm_clock_mfma_busy_valu_bert_base_xlmr_large.md"
 
 
@@ -1319,7 +1319,7 @@ def main() -> int:
         "in this epilogue (FFN-down's quantization applies it)" if key == "ffn_up.gemm" else
         "MFMA issue in the main loop" if key.endswith(".gemm") else
         "VALU issue: the exact-erf GELU restated with no FMA (27 multiplies and adds per element in the "
-        "series alone) plus the quantization, ~54 VALU lane-ops per element (roofline.valu), at 4 waves per "
+        "series alone) plus the quantization, ~50 VALU lane-ops per element (roofline.valu), at 4 waves per "
         "SIMD" if key.endswith(".gelu_quant") else "HBM")
     roofline["scope"] = ("the W8A8 path's dominant kernel in the timed encode (by device time per step); "
                          "roofline_step_dominant covers the step's dominant kernel overall")

@@ -143,7 +143,7 @@ def test_line_with_the_gelu_quantizer_dominant():
     assert len(json.dumps(line, allow_nan=False)) <= 4096
     assert line["roofline"]["unit_label"] == "ffn_down.gelu_quant"
     assert line["roofline"]["valu"]["frac"] == 0.767
-    assert line["roofline"]["valu"]["lane_ops_per_output"] == 54
+    assert line["roofline"]["valu"]["lane_ops_per_output"] == bench.GELU_QUANT_LANE_OPS
     assert line["roofline"]["traffic"] == 503694006  # profiles/bert_base_b64s512_hbm_traffic.md
     assert line["kernels_us_frac"]["ffn_down.gelu_quant"][0] == 118.8
 

@@ -17,7 +17,7 @@ matmul seam, docs/task-native-gpu.md:418-427):
   out   = W8A8(ctx, Wo) + b             enchip_w8a8_linear_dev
   h     = LN(h + out)                   enchip_residual_layer_norm_dev
   inter = GELU(W8A8(h, Wi) + b)         enchip_w8a8_linear_dev (fused epilogue), or, when
-                                        FFN-down takes fragment-major codes of K <= 3072,
+                                        FFN-down takes fragment-major codes of K <= 4096,
                                         W8A8(h, Wi) + b alone, the GELU applied by FFN-down's
                                         quantization (enchip_quant_rows_frag_gelu_dev): the
                                         same codes
@@ -141,12 +141,11 @@ class DeviceBert:
             return False
         return L <= 512 or self.ctx.attention_products in (enchip.ATT_FLASH_BF16, enchip.ATT_FLASH_F16)
 
-    # Widest FFN-down input whose GELU moves into the quantization. Measured on MI355X
-    # (rocprofv3 kernel traces of the encodes): BERT-base, K = 3072, FFN-up + quantizer
-    # 176 + 81 -> 108 + 122 us per layer; XLM-R-large, K = 4096, 558 + 223 -> 439 + 464 us,
-    # slower: its rows settle their erf tails in 6 parts against 3 at K = 3072 (the part
-    # buffers that fit two blocks per CU shrink as the row grows).
-    GELU_QUANT_MAX_K = 3072
+    # Widest FFN-down input whose GELU moves into the quantization: every width the
+    # quantizer takes (enchip_quant_rows_frag_gelu_dev: ldq <= 4096). Measured on MI355X,
+    # same process, identical outputs: BERT-base (K = 3072) 8.81 -> 8.52 ms per encode,
+    # XLM-R-large (K = 4096) 53.5 -> 51.8 ms per rerank batch.
+    GELU_QUANT_MAX_K = 4096
 
     def gelu_quant_route(self, up_act: int, down: "enchip.Weight", M: int) -> int:
         """The padded K of FFN-down's codes when FFN-up's GELU moves into FFN-down's

@@ -283,7 +283,8 @@ __global__ __launch_bounds__(512 / RPW) void quant_rows_frag(const float *__rest
 // the GELU where the rows are read anyway, with many wavefronts per SIMD, where the GEMM's
 // GELU epilogue issues from about one.
 //
-// One wavefront per row, 8 rows per block (the code lines of quant_rows_frag). Each lane
+// One wavefront per row, 8 rows per block (the code lines of quant_rows_frag: each line
+// holds 16 codes of each of the block's 8 rows). Each lane
 // evaluates ErfF32's series branch on its 4*CH values without branching (gelu_f32_series4)
 // and keeps the pre-activation of every value that needs another branch (|u| >= 1, or
 // NaN: the tails). The tails are then settled part by part, PG float4 groups at a time:
@@ -300,25 +301,29 @@ __global__ __launch_bounds__(512 / RPW) void quant_rows_frag(const float *__rest
 // wavefront's next row (167 VGPRs, one block per CU) ran 160-295 us against 118-207 for
 // this one, and the series constants held in SGPRs instead of literals 135 against 118.
 //
-// PG: the largest part size (at most CH) that keeps the block's LDS within 80 KB, so two
-// blocks (16 wavefronts) share a CU.
-constexpr int qg_pg(int ch) { return (81920 - 2304 * ch) / 12288 < ch ? (81920 - 2304 * ch) / 12288 : ch; }
+// Each wavefront's LDS region holds its part buffer (PG float4 groups per lane) and, once
+// its tails are settled, its row's codes (CH * 256 bytes), plus a 16-byte pad so that the 8
+// regions start in different banks. PG = 4 keeps the block at 49 KB for any CH <= 16: three
+// blocks (24 wavefronts) share a CU. Measured on MI355X against code staging shared by the
+// block (75 KB, two blocks per CU), M = 32768, K = 3072, same process, bit-identical:
+// 101 / 115 / 138 / 192 against 103 / 127 / 156 / 215 us at 0% / 1% / 20% / 67% tails.
+constexpr int QG_PG = 4;
 
 template <int CH>
 __global__ __launch_bounds__(512) void quant_rows_frag_gelu(const float *__restrict__ a, int8_t *__restrict__ q,
                                                             int64_t ldq, float *__restrict__ scale, int64_t M, int K) {
-    constexpr int CP = 144;  // as quant_rows_frag
-    constexpr int PG = qg_pg(CH);
+    constexpr int PG = QG_PG < CH ? QG_PG : CH;
     constexpr int NPART = (CH + PG - 1) / PG;
     static_assert(PG >= 1 && 4 * PG <= 32, "a part's tail bits fit one 32-bit word");
-    __shared__ __attribute__((aligned(16))) int8_t lds[16 * CH * CP];
-    __shared__ __attribute__((aligned(16))) float rbuf[8][PG * 256];  // a part of each wavefront's row
-    __shared__ uint16_t tl[8][PG * 256];                              // its tail cells
+    constexpr int RB = (PG * 1024 > CH * 256 ? PG * 1024 : CH * 256) + 16;  // bytes per wavefront
+    __shared__ __attribute__((aligned(16))) int8_t lds[8 * RB];  // part buffers, then codes
+    __shared__ uint16_t tl[8][PG * 256];                          // each wavefront's tail cells
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t r0 = (int64_t)blockIdx.x * 8;
     const int64_t row = r0 + wave;
     const int ldq4 = (int)(ldq >> 2);
-    auto word = [&](int rr, int k4) -> int * { return reinterpret_cast<int *>(lds + (k4 >> 2) * CP + rr * 16 + (k4 & 3) * 4); };
+    // the 32-bit word of codes 4*k4 .. 4*k4+3 of block row rr, in that row's own region
+    auto word = [&](int rr, int k4) -> int * { return reinterpret_cast<int *>(lds + rr * RB + k4 * 4); };
     float4 v[CH];
     load_row_raw<CH>(a, min(row, M - 1), K, lane, v);
     if (row < M) {  // uniform across the wavefront
@@ -334,7 +339,8 @@ __global__ __launch_bounds__(512) void quant_rows_frag_gelu(const float *__restr
             v[c] = make_float4(t4 & 1u ? y.x : gy.x, t4 & 2u ? y.y : gy.y, t4 & 4u ? y.z : gy.z, t4 & 8u ? y.w : gy.w);
             tm[c / PG] |= t4 << (4 * (c % PG));
         }
-        float *cell = rbuf[wave];  // cell (g * 64 + lane) * 4 + j: value j of the part's float4 g
+        // cell (g * 64 + lane) * 4 + j: value j of the part's float4 g
+        float *cell = reinterpret_cast<float *>(lds + wave * RB);
         uint16_t *list = tl[wave];
 #pragma unroll
         for (int p = 0; p < NPART; ++p) {
@@ -380,7 +386,7 @@ __global__ __launch_bounds__(512) void quant_rows_frag_gelu(const float *__restr
 #pragma unroll
             for (int g = 0; g < PG; ++g)
                 if (g < ng) v[c0 + g] = *reinterpret_cast<const float4 *>(&cell[(g * 64 + lane) * 4]);
-            // the next part's stores to the buffer come after these loads
+            // the next part's stores to the buffer (or the codes) come after these loads
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -412,12 +418,13 @@ __global__ __launch_bounds__(512) void quant_rows_frag_gelu(const float *__restr
         }
     }
     __syncthreads();
+    // piece p = (chunk p / 8, row p % 8): 8 consecutive threads write one whole line
     const int64_t nk32 = ldq >> 5;
     for (int p = threadIdx.x; p < 2 * ldq4; p += 512) {
         const int c = p >> 3, r2 = p & 7;
         if (r0 + r2 < M)
             *reinterpret_cast<int4 *>(q + frag_off(r0 + r2, 16 * (int64_t)c, nk32)) =
-                *reinterpret_cast<const int4 *>(lds + c * CP + r2 * 16);
+                *reinterpret_cast<const int4 *>(lds + r2 * RB + c * 16);
     }
 }
 

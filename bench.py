@@ -853,8 +853,8 @@ def encode_units(ctx, model, cfg, per: dict, steps: int) -> dict:
 
 
 # VALU lane-operations per element of quant_rows_frag_gelu<12> in the BERT-base encode:
-# SQ_INSTS_VALU = 77,075 wave-instructions per SIMD per launch x 1024 SIMDs x 64 lanes /
-# (32768 x 3072 elements) = 50.2 (series, erf tails, absmax, codes, addressing).
+# SQ_INSTS_VALU = 76,243 wave-instructions per SIMD per launch x 1024 SIMDs x 64 lanes /
+# (32768 x 3072 elements) = 49.6 (series, erf tails, absmax, codes, addressing).
 GELU_QUANT_LANE_OPS = 50
 GELU_QUANT_VALU_SOURCE = "profiles/int8_gemm_clock_mfma_busy_valu_bert_base_xlmr_large.md"
 
